@@ -1,0 +1,193 @@
+"""Benchmark: one VGGT global-attention layer through the block-sparse path on one MI355X.
+
+Workload (the metric's configuration): N = 16 frames x 1374
+tokens = 21,984, H = 16, D = 64, bf16 Q/K/V already resident in HBM, HeSS per-head
+budgets from synthetic (3,24,16) log-normal tables (lambda 0.5, layer 0), sparse_ratio
+0.7. A step is one full layer forward of the hot path: preparation (pool, key mean,
+INT8 Q/K, packed V), pooled map, budgets, selection + LUT, sparse attention with the
+special-query rows dense, output in storage order.
+
+    python bench.py [--steps K] [--warmup W] [--config 1] [--no-cpu-baseline]
+
+Prints one JSON line. value = effective TFLOP/s = 4 N^2 H D / t (dense-equivalent);
+ms_per_step = ms per layer. roofline = the attention kernel's retained-block FLOPs over
+its own HIP-event-timed duration against the INT8 MFMA peak.
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_INT8_TOPS = 5000.0   # MI355X dense INT8 MFMA, TOPS
+PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, GB/s
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=1)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget-s", type=float, default=15.0)
+    ap.add_argument("--no-dense", action="store_true")
+    return ap.parse_args()
+
+
+def retained_flops(nvalid, lut, grid):
+    """Sum over kept (row, key block) of 4*D*rows*cols with true partial sizes."""
+    import numpy as np
+    rows_p = [min(128, grid.T_p - 128 * i) for i in range(grid.q_blk_p)]
+    rows_s = [min(128, grid.T_s - 128 * i) for i in range(grid.q_blk_s)]
+    rows = np.array(rows_p + rows_s, dtype=np.float64)
+    cols = np.array([min(64, grid.Tk - 64 * c) for c in range(grid.kb_tot)], dtype=np.float64)
+    total = 0.0
+    for bh in range(nvalid.shape[0]):
+        for r in range(nvalid.shape[1]):
+            total += rows[r] * cols[lut[bh, r, :nvalid[bh, r]]].sum()
+    return 4.0 * 64 * total
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only "
+                                   "(see DESIGN.md)", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+
+    from ress_amd import budget, kernels, synth
+    from ress_amd.attention import sparse_global_attention
+    from ress_amd.kernels import LayerGrid
+
+    cfg = synth.CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    t0 = time.time()
+    q, k, v, meta = synth.make_layer_qkv(cfg["frames"], corr=cfg["corr"])
+    q, k, v = q.to(dev), k.to(dev), v.to(dev)
+    print(f"[bench] inputs {tuple(q.shape)} generated in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    frames, P, S = meta["frames"], meta["P"], meta["S"]
+    grid = LayerGrid(1, 16, frames, P, S)
+    sr, cdf = cfg["sparse_ratio"], cfg["cdf_threshold"]
+    if cfg["mode"] in ("hess", "ress"):
+        cam, pc = synth.make_hess_tables()
+        bud = budget.HessBudget(cam, pc, lam=0.5)
+    else:
+        bud = budget.UniformBudget()
+    budget_fn = lambda a: bud.num_to_select(0, a, sr, cdf, 1.0)  # noqa: E731
+    out = torch.empty(1, 16, grid.Tk, 64, dtype=torch.float32, device=dev)
+
+    # attention-kernel events: recorded on the stream the kernel is launched on
+    ev = []
+    orig_attn = kernels.sparse_attention
+
+    def timed_attention(*a, **kw):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        r = orig_attn(*a, **kw)
+        e.record()
+        ev.append((s, e))
+        return r
+
+    import ress_amd.attention as attn_mod
+    attn_mod.kernels.sparse_attention = timed_attention
+
+    def step():
+        return sparse_global_attention(q, k, v, grid, budget_fn=budget_fn, out=out)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev.clear()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        res = step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    attn_ms = sum(s.elapsed_time(e) for s, e in ev) / len(ev)
+    attn_mod.kernels.sparse_attention = orig_attn
+
+    # work actually done (same map every step)
+    res = sparse_global_attention(q, k, v, grid, budget_fn=budget_fn, out=out, keep_intermediates=True)
+    torch.cuda.synchronize()
+    lut, nvalid = res.lut.cpu().numpy(), res.nvalid.cpu().numpy()
+    flops_kept = retained_flops(nvalid, lut, grid)
+    N = grid.Tk
+    flops_dense = 4.0 * N * N * 16 * 64
+    sparsity = res.sparsity()
+    achieved = flops_kept / (attn_ms * 1e-3) / 1e12
+
+    # preparation pass (HBM-bound): algorithmic bytes = read Q,K,V + re-read K + write INT8 Q,K + packed V
+    pe_s, pe_e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 20
+    pe_s.record()
+    for _ in range(reps):
+        kernels.prepare_blocks(q, k, v, grid)
+    pe_e.record()
+    torch.cuda.synchronize()
+    prep_ms = pe_s.elapsed_time(pe_e) / reps
+    elems = N * 16 * 64
+    prep_bytes = elems * 2 * 4 + elems * 1 * 2 + elems * 2
+
+    result = {
+        "metric": "ms/global-attn layer + effective TFLOPS, N=21984 H16 D64 @70% sparse, 1 GPU",
+        "value": round(flops_dense / (ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s (effective, dense-equivalent 4*N^2*H*D per layer)",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 QK / bf16 PV / fp32 softmax",
+        "data": "synthetic (seeded smoothed-field Q/K/V, Hilbert order; synthetic HeSS tables)",
+        "config": {"workload": f"BASELINE configs[{args.config}]: one global-attention layer, {cfg['mode']} budget",
+                   "frames": frames, "tokens": N, "heads": 16, "head_dim": 64, "sparse_ratio": sr,
+                   "cdf_threshold": cdf, "realized_sparsity": round(sparsity, 4)},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
+                     "kernel": "k_sparse_attn", "kernel_ms": round(attn_ms, 4),
+                     "retained_flop_per_launch": flops_kept},
+        "prep": {"ms": round(prep_ms, 4), "algorithmic_bytes": prep_bytes,
+                 "achieved_GBs": round(prep_bytes / (prep_ms * 1e-3) / 1e9, 1), "peak_GBs": PEAK_HBM_GBS},
+    }
+
+    if not args.no_dense:
+        qd = q.contiguous()
+        for _ in range(3):
+            F.scaled_dot_product_attention(qd, k, v)
+        torch.cuda.synchronize()
+        ds, de = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ds.record()
+        for _ in range(10):
+            F.scaled_dot_product_attention(qd, k, v)
+        de.record()
+        torch.cuda.synchronize()
+        dense_ms = ds.elapsed_time(de) / 10
+        result["dense_bf16_sdpa_ms"] = round(dense_ms, 4)
+        result["speedup_vs_dense"] = round(dense_ms / ms, 3)
+
+    if not args.no_cpu_baseline:
+        from oracle.cpu_baseline import time_block_masked_sdpa
+        cb = time_block_masked_sdpa(q.cpu(), k.cpu(), v.cpu(), frames, P, S, lut, nvalid, budget_s=args.cpu_budget_s)
+        result["cpu_baseline"] = {
+            "value": round(cb["ms_per_layer"], 1), "unit": "ms/layer", "cores": cb["threads"], "kind": "port",
+            "sample": f"fp32 block-masked SDPA (PyTorch CPU) on {cb['rows_timed']} of {cb['rows_total']} "
+                      f"(head, q-block) rows, {cb['elapsed_s']:.1f}s, extrapolated by kept-block count"}
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,131 @@
+/* libress_hip: MI355X (gfx950) kernels for ReSS / HeSS block-sparse global attention.
+ *
+ * Every entry point is a plain C function: device pointers and sizes in, an int
+ * status out (0 = ok, -1 = bad argument, -2 = launch failure; the message is in
+ * ress_last_error(), thread-local). Nothing here allocates device memory or
+ * synchronises: work is enqueued on `stream` (hipStream_t; 0 = the null stream)
+ * and buffers are owned by the caller. Tensors are row-major; "BH" is batch*heads.
+ * Head dim is 64 throughout. Citations are to the reference repository
+ * (libary753/ReSS) and to the SpargeAttn functions it binds.
+ */
+#ifndef RESS_HIP_H
+#define RESS_HIP_H
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- library ------------------------------------------------------------- */
+const char* ress_last_error(void);
+int ress_abi_version(void);
+
+/* ---- block preparation (prep.hip) ---------------------------------------- */
+
+/* Fused Q/K/V preparation for one ReSS global-attention layer.
+ * Replaces: compute_patch_qkv's patch/special split (src/ress/models/qkv.py:60-68,
+ * tokens.py:8-52), predict_attention's avg pools (src/ress/models/attention.py:90-96),
+ * block_mean_value (attention.py:103-109), km = key.mean(-2) and
+ * per_block_int8(q, k - km) (attention.py:231-233; SpargeAttn quant_per_block with
+ * external/patches/spargeattn.patch:38-41).
+ * q/k/v: bf16 (B,H,frames*P,64) in storage order (per frame S special then P-S patch
+ * tokens), element strides (sB,sH,sT). Outputs:
+ *   q_i8 [BH][qb_p+qb_s][128][64] int8, q_scale [BH][qb_p+qb_s] f32,
+ *   pooled_q [BH][qb_p][64] f32                 qb_p = ceil(T_p/128), qb_s = ceil(T_s/128)
+ *   k_i8 [BH][kb_tot][64][64] int8, k_scale [BH][kb_tot] f32   kb_tot = ceil(frames*P/64)
+ *   pooled_k, pooled_v [BH][kb_p][64] f32       kb_p = ceil(T_p/64) (patch keys only)
+ *   v_pack [BH][kb_tot][4096] bf16, ksum [BH][kb_tot][64] f32, km [BH][64] f32 */
+int ress_prep_qkv(const void* q, const void* k, const void* v, int B, int H, int frames, int P, int S,
+                  long long sqB, long long sqH, long long sqT, long long skB, long long skH, long long skT,
+                  long long svB, long long svH, long long svT, void* q_i8, void* q_scale, void* pooled_q,
+                  void* k_i8, void* k_scale, void* pooled_k, void* pooled_v, void* v_pack, void* ksum,
+                  void* km, hipStream_t stream);
+
+/* Replaces SpargeAttn per_block_int8(q, k) (call site src/ress/models/attention.py:232,
+ * patched Q scale spargeattn.patch:38-41). km [BH][64] optional (NULL = no smoothing).
+ * Outputs in the blocked layouts of ress_prep_qkv; pooled_q [BH][ceil(Tq/128)][64]. */
+int ress_per_block_int8(const void* q, const void* k, const void* km, int B, int H, int Tq, int Tk,
+                        long long sqB, long long sqH, long long sqT, long long skB, long long skH,
+                        long long skT, void* q_i8, void* q_scale, void* k_i8, void* k_scale, void* pooled_q,
+                        hipStream_t stream);
+
+/* Key mean + K/V block pass of a plain (B,H,Tk,64) bf16 sequence (the key mean of
+ * src/ress/models/attention.py:231; block_mean_value attention.py:103-109). */
+int ress_prep_kv_plain(const void* k, const void* v, int B, int H, int Tk, long long skB, long long skH,
+                       long long skT, long long svB, long long svH, long long svT, void* ksum, void* km,
+                       void* pooled_k, void* pooled_v, void* v_pack, hipStream_t stream);
+
+/* ---- pooled map (scores.hip) --------------------------------------------- */
+
+/* Replaces predict_attention's pooled GEMM + softmax (src/ress/models/attention.py:98-100)
+ * and attn_cond = attn_pooled / clamp(rowsum, 1e-6) (attention.py:457,473).
+ * attn_full [BH][q_blk][kb_p], attn_cond [BH][q_blk][n_cand] f32. */
+int ress_pooled_scores(const void* pooled_q, const void* pooled_k, int BH, int q_blk, int kb_p, int n_cand,
+                       float scale, void* attn_full, void* attn_cond, hipStream_t stream);
+
+/* ---- budgets (budget.hip) ------------------------------------------------- */
+
+/* Replaces compute_baseline_num_to_select (src/ress/models/attention.py:268-293):
+ * cdf_threshold < 0 disables the CDF cut, topk < 0 the sparse-ratio floor
+ * (topk = int(k_blk*(1-sr)) in host double arithmetic). out [rows] int32. */
+int ress_baseline_budget(const void* attn_cond, long long rows, int n, float cdf_threshold, int topk,
+                         void* out_counts, hipStream_t stream);
+
+/* Replaces adjust_attention_selection (src/ress/budget/_proportional.py:49-115) as
+ * HessBudget.num_to_select calls it (src/ress/budget/hess.py:92-100), plus a floor.
+ * baseline/out [B][H][q_blk] int32 (may alias); scores_norm [H] f32 or NULL (no
+ * reallocation); iters_out [B][q_blk] int32 or NULL (-1 = did not converge). */
+int ress_head_budget(const void* baseline, int B, int H, int q_blk, const void* scores_norm, double beta,
+                     int max_val, int max_iters, int min_select, void* out_counts, void* iters_out,
+                     hipStream_t stream);
+
+/* ---- selection (select.hip) ------------------------------------------------ */
+
+/* Replaces build_block_mask (src/ress/models/attention.py:147-174) with the
+ * MIN_NUM_TO_SELECT floor (attention.py:525), SpargeAttn block_map_lut_triton
+ * (attention.py:224) and leading attention_sink forcing (spargeattn.patch:61-65).
+ * rank_key [BH][q_blk_sel][n_cand] f32, counts [BH][q_blk_sel] int32; rows
+ * q_blk_sel..q_blk_total-1 are dense. map [BH][q_blk_sel][kb_tot] uint8 (or NULL),
+ * lut [BH][q_blk_total][kb_tot] int32 (ascending kept block indices), nvalid
+ * [BH][q_blk_total] int32. */
+int ress_select_blocks(const void* rank_key, const void* counts, int BH, int q_blk_sel, int q_blk_total,
+                       int n_cand, int kb_tot, int sink_lead, int min_select, void* map, void* lut,
+                       void* nvalid, hipStream_t stream);
+
+/* Replaces SpargeAttn fill_block_map_triton (src/ress/models/attention.py:168):
+ * map[r, sorted_idx[r, :counts[r]]] = 1. map [rows][k] uint8, int64 counts/indices. */
+int ress_fill_block_map(void* map, const void* counts, const void* sorted_idx, long long rows, int k,
+                        hipStream_t stream);
+
+/* Replaces SpargeAttn block_map_lut_triton (src/ress/models/attention.py:224):
+ * map [rows][k] uint8 -> lut [rows][k] int32 (ascending), nvalid [rows]. */
+int ress_block_map_lut(const void* map, long long rows, int k, void* lut, void* nvalid, hipStream_t stream);
+
+/* ---- attention (attn.hip) ----------------------------------------------- */
+
+/* Fused-path attention (src/ress/models/attention.py:404-412 special queries dense,
+ * :625 run_block_sparse_kernel, :652 combine_special_and_patch): inputs from
+ * ress_prep_qkv + ress_select_blocks; out (B,H,frames*P,64) in storage order,
+ * out_dtype 0 f32 / 1 bf16 / 2 f16, element strides soB/soH/soT. */
+int ress_sparse_attn_fwd(const void* q_i8, const void* q_scale, const void* k_i8, const void* k_scale,
+                         const void* v_pack, int v_f16, const void* lut, const void* nvalid, int B, int H,
+                         int frames, int P, int S, float sm_scale, void* out, int out_dtype, long long soB,
+                         long long soH, long long soT, hipStream_t stream);
+
+/* Replaces SpargeAttn qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold
+ * (call src/ress/models/attention.py:238-241) with the same argument meaning; see
+ * attn.hip for the supported flag values. */
+long long ress_qattn_workspace_size(int B, int H, int Tk);
+int ress_qattn_block_sparse_fwd(const void* q_i8, const void* k_i8, const void* v, int v_f16, void* o,
+                                int o_dtype, const void* lut, const void* valid_block_num,
+                                const float* pv_threshold_host, const void* q_scale, const void* k_scale,
+                                int B, int H, int Tq, int Tk, long long svB, long long svH, long long svT,
+                                long long soB, long long soH, long long soT, int tensor_layout, int is_causal,
+                                int qk_quant_gran, float sm_scale, int return_pv_count, void* workspace,
+                                long long workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RESS_HIP_H */

@@ -1,0 +1,378 @@
+/* CPU oracle for the ReSS / HeSS block-sparse global-attention path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This file restates, in plain C on host arrays, the
+ * reference algorithm (libary753/ReSS) for every stage the GPU library implements,
+ * under the same numerics contract (fixed evaluation orders, IEEE division, no
+ * contraction: build with -ffp-contract=off):
+ *   SUM8x  block pooling: per token lane j = t mod 8 a sequential sum over its
+ *          tokens, then ((p0+p1)+(p2+p3))+((p4+p5)+(p6+p7))
+ *   SUM64  row sums: 64 strided sequential partials, then an xor butterfly
+ *   DOT64  sequential fmaf over the 64 dims
+ *   SEQ    sequential sums in index order
+ * Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg use it, and
+ * only as the checker. The product library never links or calls it.
+ *
+ * Tensors are contiguous row-major. bf16 values are passed as uint16_t bit patterns.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+static inline float bf16f(uint16_t b) {
+  uint32_t u = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+static inline uint32_t fbits(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+static inline float bitsf(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+static inline int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+/* ---- exp: Cody-Waite reduction, degree-7 Taylor polynomial (Horner) ---------- */
+float oracle_expf(float x) {
+  if (x != x) return x;
+  if (x > 0x1.62e42ep+6f) return INFINITY;
+  if (x < -0x1.9fe368p+6f) return 0.0f;
+  float n = rintf(x * 0x1.715476p+0f);
+  float r = fmaf(-n, 0x1.62e4p-1f, x);
+  r = fmaf(-n, 0x1.7f7d1cp-20f, r);
+  float p = 0x1.a01a02p-13f;
+  p = fmaf(p, r, 0x1.6c16c2p-10f);
+  p = fmaf(p, r, 0x1.111112p-7f);
+  p = fmaf(p, r, 0x1.555556p-5f);
+  p = fmaf(p, r, 0x1.555556p-3f);
+  p = fmaf(p, r, 0x1p-1f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  int ni = (int)n;
+  if (ni > 127) return (p * 2.0f) * 0x1p127f;
+  if (ni < -126) return (p * bitsf((uint32_t)(ni + 127 + 64) << 23)) * 0x1p-64f;
+  return p * bitsf((uint32_t)(ni + 127) << 23);
+}
+
+/* ---- bf16 rounding (round to nearest even) ------------------------------------ */
+float oracle_round_bf16(float f) {
+  uint32_t u = fbits(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return bitsf(((u >> 16) | 0x40u) << 16);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return bitsf((u >> 16) << 16);
+}
+
+/* ---- order key ------------------------------------------------------------------ */
+static inline uint32_t order_key(float x) {
+  uint32_t u = fbits(x);
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+/* ---- geometry: storage order <-> kernel order ------------------------------------ */
+typedef struct {
+  int P, S, HW, T_p, T_s;
+} tokmap;
+static tokmap mkmap(int frames, int P, int S) {
+  tokmap m = {P, S, P - S, frames * (P - S), frames * S};
+  return m;
+}
+static inline int patch_st(int p, const tokmap* m) { return (p / m->HW) * m->P + m->S + p % m->HW; }
+static inline int special_st(int s, const tokmap* m) { return (s / m->S) * m->P + s % m->S; }
+static inline int key_st(int kk, const tokmap* m) { return kk < m->T_p ? patch_st(kk, m) : special_st(kk - m->T_p, m); }
+
+/* SUM8x over the rows[] (count cnt) of a (tokens, 64) bf16 matrix, for one dim d */
+static float sum8x(const uint16_t* x, const int* rows, int cnt, int d) {
+  float p[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int t = 0; t < cnt; ++t) p[t & 7] = p[t & 7] + bf16f(x[(long long)rows[t] * 64 + d]);
+  return ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+}
+
+/* per-block quantiser: SageAttention quant_per_block (scale = amax/127, round half
+ * away from zero), Q with sm_scale = 1 (external/patches/spargeattn.patch:38-41) */
+static inline int8_t quant(float x, float scale) {
+  if (scale == 0.0f) return 0;
+  float y = x / scale;
+  y = y + (y >= 0.0f ? 0.5f : -0.5f);
+  return (int8_t)(int)y;
+}
+
+/* ---- preparation ------------------------------------------------------------------
+ * Follows src/ress/models/qkv.py:60-68 + tokens.py:8-52 (patch/special split, kernel
+ * key order cat(patch, special), attention.py:405-406), predict_attention's avg pools
+ * (attention.py:90-96; ceil mode, a partial block divided by its valid count),
+ * block_mean_value (attention.py:103-109), km = key.mean(-2) and
+ * per_block_int8(q, k - km) (attention.py:231-233), all in fp32.
+ * q,k,v: (BH, frames*P, 64) bf16. Output layouts as ress_prep_qkv (include/ress_hip.h). */
+void oracle_prep_qkv(const uint16_t* q, const uint16_t* k, const uint16_t* v, int BH, int frames, int P, int S,
+                     int8_t* q_i8, float* q_scale, float* pooled_q, int8_t* k_i8, float* k_scale, float* pooled_k,
+                     float* pooled_v, uint16_t* v_pack, float* ksum, float* km) {
+  tokmap m = mkmap(frames, P, S);
+  const int N = frames * P, Tk = N;
+  const int qbp = cdiv(m.T_p, 128), qbs = cdiv(m.T_s, 128), qbt = qbp + qbs;
+  const int kbt = cdiv(Tk, 64), kbp = cdiv(m.T_p, 64);
+  int rows[128];
+  for (int bh = 0; bh < BH; ++bh) {
+    const uint16_t* qh = q + (long long)bh * N * 64;
+    const uint16_t* kh = k + (long long)bh * N * 64;
+    const uint16_t* vh = v + (long long)bh * N * 64;
+    /* Q blocks */
+    for (int qb = 0; qb < qbt; ++qb) {
+      const int special = qb >= qbp;
+      const int base = special ? (qb - qbp) * 128 : qb * 128;
+      const int cnt = (special ? m.T_s : m.T_p) - base < 128 ? (special ? m.T_s : m.T_p) - base : 128;
+      for (int t = 0; t < cnt; ++t) rows[t] = special ? special_st(base + t, &m) : patch_st(base + t, &m);
+      float amax = 0.0f;
+      for (int t = 0; t < cnt; ++t)
+        for (int d = 0; d < 64; ++d) amax = fmaxf(amax, fabsf(bf16f(qh[(long long)rows[t] * 64 + d])));
+      const float scale = amax / 127.0f;
+      q_scale[(long long)bh * qbt + qb] = scale;
+      if (!special)
+        for (int d = 0; d < 64; ++d)
+          pooled_q[((long long)bh * qbp + qb) * 64 + d] = sum8x(qh, rows, cnt, d) / (float)cnt;
+      int8_t* dst = q_i8 + ((long long)bh * qbt + qb) * 128 * 64;
+      for (int t = 0; t < 128; ++t)
+        for (int d = 0; d < 64; ++d)
+          dst[t * 64 + d] = t < cnt ? quant(bf16f(qh[(long long)rows[t] * 64 + d]), scale) : 0;
+    }
+    /* K/V blocks over the kernel key grid */
+    for (int kb = 0; kb < kbt; ++kb) {
+      const int base = kb * 64;
+      const int cnt = Tk - base < 64 ? Tk - base : 64;
+      int cnt_p = m.T_p - base < 64 ? m.T_p - base : 64;
+      if (cnt_p < 0) cnt_p = 0;
+      for (int t = 0; t < cnt; ++t) rows[t] = key_st(base + t, &m);
+      for (int d = 0; d < 64; ++d) {
+        ksum[((long long)bh * kbt + kb) * 64 + d] = sum8x(kh, rows, cnt, d);
+        if (kb < kbp) {
+          pooled_k[((long long)bh * kbp + kb) * 64 + d] = sum8x(kh, rows, cnt_p, d) / (float)cnt_p;
+          pooled_v[((long long)bh * kbp + kb) * 64 + d] = sum8x(vh, rows, cnt_p, d) / (float)cnt_p;
+        }
+      }
+      uint16_t* vp = v_pack + ((long long)bh * kbt + kb) * 4096;
+      for (int t = 0; t < 64; ++t) {
+        const int u = t & 15;
+        const int pos = (t & ~15) + 8 * ((u >> 2) & 1) + 4 * (u >> 3) + (u & 3);
+        for (int d = 0; d < 64; ++d) vp[d * 64 + pos] = t < cnt ? vh[(long long)rows[t] * 64 + d] : 0;
+      }
+    }
+    /* key mean: SEQ over block sums / Tk */
+    for (int d = 0; d < 64; ++d) {
+      float acc = 0.0f;
+      for (int kb = 0; kb < kbt; ++kb) acc = acc + ksum[((long long)bh * kbt + kb) * 64 + d];
+      km[(long long)bh * 64 + d] = acc / (float)Tk;
+    }
+    /* K quantisation of k - km */
+    for (int kb = 0; kb < kbt; ++kb) {
+      const int base = kb * 64;
+      const int cnt = Tk - base < 64 ? Tk - base : 64;
+      float amax = 0.0f;
+      for (int t = 0; t < cnt; ++t) {
+        const int r = key_st(base + t, &m);
+        for (int d = 0; d < 64; ++d)
+          amax = fmaxf(amax, fabsf(bf16f(kh[(long long)r * 64 + d]) - km[(long long)bh * 64 + d]));
+      }
+      const float scale = amax / 127.0f;
+      k_scale[(long long)bh * kbt + kb] = scale;
+      int8_t* dst = k_i8 + ((long long)bh * kbt + kb) * 4096;
+      for (int t = 0; t < 64; ++t) {
+        const int r = t < cnt ? key_st(base + t, &m) : 0;
+        for (int d = 0; d < 64; ++d)
+          dst[t * 64 + d] = t < cnt ? quant(bf16f(kh[(long long)r * 64 + d]) - km[(long long)bh * 64 + d], scale) : 0;
+      }
+    }
+  }
+}
+
+/* ---- pooled map -----------------------------------------------------------------------
+ * predict_attention's pooled GEMM + softmax (src/ress/models/attention.py:98-100) and
+ * attn_cond = attn_pooled / clamp(rowsum(attn_pooled), 1e-6) (attention.py:457,473). */
+static float sum64(const float* x, int n) {
+  float part[64];
+  for (int l = 0; l < 64; ++l) {
+    float a = 0.0f;
+    for (int i = l; i < n; i += 64) a = a + x[i];
+    part[l] = a;
+  }
+  for (int off = 1; off < 64; off <<= 1) {
+    float nx[64];
+    for (int l = 0; l < 64; ++l) nx[l] = part[l] + part[l ^ off];
+    memcpy(part, nx, sizeof(part));
+  }
+  return part[0];
+}
+
+void oracle_pooled_scores(const float* pooled_q, const float* pooled_k, int BH, int q_blk, int kb_p, int n_cand,
+                          float scale, float* attn_full, float* attn_cond) {
+  float* s = (float*)malloc(sizeof(float) * (kb_p > 0 ? kb_p : 1));
+  for (int bh = 0; bh < BH; ++bh)
+    for (int qb = 0; qb < q_blk; ++qb) {
+      const float* pq = pooled_q + ((long long)bh * q_blk + qb) * 64;
+      float m = -INFINITY;
+      for (int kb = 0; kb < kb_p; ++kb) {
+        const float* pk = pooled_k + ((long long)bh * kb_p + kb) * 64;
+        float acc = 0.0f;
+        for (int d = 0; d < 64; ++d) acc = fmaf(pq[d], pk[d], acc);
+        s[kb] = acc * scale;
+        m = fmaxf(m, s[kb]);
+      }
+      for (int kb = 0; kb < kb_p; ++kb) s[kb] = oracle_expf(s[kb] - m);
+      const float total = sum64(s, kb_p);
+      float* full = attn_full + ((long long)bh * q_blk + qb) * kb_p;
+      for (int kb = 0; kb < kb_p; ++kb) full[kb] = s[kb] / total;
+      float rs = sum64(full, n_cand);
+      rs = fmaxf(rs, 0x1.0c6f7ap-20f);
+      float* cond = attn_cond + ((long long)bh * q_blk + qb) * n_cand;
+      for (int kb = 0; kb < n_cand; ++kb) cond[kb] = full[kb] / rs;
+    }
+  free(s);
+}
+
+/* ---- baseline budget ------------------------------------------------------------------
+ * compute_baseline_num_to_select (src/ress/models/attention.py:268-293): with a CDF
+ * threshold, sort each row descending, SEQ cumsum, count of prefix sums <= fp32(tau)+1e-5
+ * (searchsorted right=True); with a sparse ratio, topk = int(k*(1-sr)) (passed in) and the
+ * larger of the two counts. cdf < 0 / topk < 0 disable the respective cut. */
+static int cmp_desc(const void* a, const void* b) {
+  float x = *(const float*)a, y = *(const float*)b;
+  return (x < y) - (x > y);
+}
+void oracle_baseline_budget(const float* attn_cond, long long rows, int n, float cdf_threshold, int topk, int* out) {
+  float* v = (float*)malloc(sizeof(float) * (n > 0 ? n : 1));
+  const float thr = cdf_threshold + 0x1.4f8b58p-17f;
+  for (long long r = 0; r < rows; ++r) {
+    if (cdf_threshold < 0.0f) {
+      out[r] = topk;
+      continue;
+    }
+    memcpy(v, attn_cond + r * n, sizeof(float) * n);
+    qsort(v, n, sizeof(float), cmp_desc);
+    float c = 0.0f;
+    int count = 0;
+    for (int i = 0; i < n; ++i) {
+      c = c + v[i];
+      if (c <= thr) ++count;
+    }
+    out[r] = count > topk ? count : topk;
+  }
+  free(v);
+}
+
+/* ---- HeSS head reallocation -----------------------------------------------------------
+ * adjust_attention_selection (src/ress/budget/_proportional.py:49-115) with
+ * floor_frac=None, per (batch, q-block) column over heads, fp32, SEQ head sums:
+ * ideal = scores_norm*total; adjusted = (1-beta)*nts + beta*ideal; repeat
+ * {excess = clamp(adj - max, 0); stop if non-finite or sum <= 0; adj = min(adj, max);
+ * w = adj*(adj<max); adj += w/(sum(w)+1e-9)*sum(excess)}; floor(min(adj, max)).
+ * Then the floor min_select. Returns the largest iteration count, or -1 if a column
+ * did not converge within max_iters. */
+int oracle_head_budget(const int* baseline, int B, int H, int q_blk, const float* scores_norm, double beta,
+                       int max_val, int max_iters, int min_select, int* out) {
+  const float omb = (float)(1.0 - beta), bf = (float)beta, maxv = (float)max_val;
+  int worst = 0;
+  float* adj = (float*)malloc(sizeof(float) * H);
+  float* w = (float*)malloc(sizeof(float) * H);
+  for (int b = 0; b < B; ++b)
+    for (int qb = 0; qb < q_blk; ++qb) {
+      const int* base = baseline + (long long)b * H * q_blk + qb;
+      int* dst = out + (long long)b * H * q_blk + qb;
+      if (!scores_norm) {
+        for (int h = 0; h < H; ++h) {
+          int c = base[(long long)h * q_blk];
+          dst[(long long)h * q_blk] = c < min_select ? min_select : c;
+        }
+        continue;
+      }
+      long long total = 0;
+      for (int h = 0; h < H; ++h) total += base[(long long)h * q_blk];
+      for (int h = 0; h < H; ++h) adj[h] = omb * (float)base[(long long)h * q_blk] + bf * (scores_norm[h] * (float)total);
+      int it = 0;
+      for (; it < max_iters; ++it) {
+        float esum = 0.0f;
+        int finite = 1;
+        for (int h = 0; h < H; ++h) {
+          float d = adj[h] - maxv;
+          float ex = d < 0.0f ? 0.0f : d;
+          finite = finite && (ex - ex == 0.0f);
+          esum = esum + ex;
+        }
+        if (!finite || !(esum > 0.0f)) break;
+        float wsum = 0.0f;
+        for (int h = 0; h < H; ++h) {
+          adj[h] = adj[h] > maxv ? maxv : adj[h];
+          w[h] = adj[h] * (adj[h] < maxv ? 1.0f : 0.0f);
+          wsum = wsum + w[h];
+        }
+        const float den = wsum + 0x1.12e0bep-30f;
+        for (int h = 0; h < H; ++h) adj[h] = adj[h] + (w[h] / den) * esum;
+      }
+      if (it >= max_iters) worst = -1;
+      else if (worst >= 0 && it > worst) worst = it;
+      for (int h = 0; h < H; ++h) {
+        float a = adj[h] > maxv ? maxv : adj[h];
+        int c = (int)floorf(a);
+        dst[(long long)h * q_blk] = c < min_select ? min_select : c;
+      }
+    }
+  free(adj);
+  free(w);
+  return worst;
+}
+
+/* ---- selection --------------------------------------------------------------------------
+ * build_block_mask (src/ress/models/attention.py:147-174): keep the top max(n, min_select)
+ * (at most n_cand) candidates of each row, order (value desc, index asc) -- brute force by
+ * sorting indices -- then the trailing sink columns (always kept) and any leading
+ * attention_sink columns (external/patches/spargeattn.patch:61-65). LUT = ascending kept
+ * columns (block_map_lut_triton, attention.py:224). Rows q_blk_sel..q_blk_total-1 are dense. */
+static const float* g_keys;
+static int cmp_rank(const void* a, const void* b) {
+  int i = *(const int*)a, j = *(const int*)b;
+  uint32_t ki = order_key(g_keys[i]), kj = order_key(g_keys[j]);
+  if (ki != kj) return ki > kj ? -1 : 1;
+  return (i > j) - (i < j);
+}
+void oracle_select_blocks(const float* rank_key, const int* counts, int BH, int q_blk_sel, int q_blk_total,
+                          int n_cand, int kb_tot, int sink_lead, int min_select, uint8_t* map, int* lut, int* nvalid) {
+  int* idx = (int*)malloc(sizeof(int) * (n_cand > 0 ? n_cand : 1));
+  uint8_t* keep = (uint8_t*)malloc(kb_tot);
+  for (int bh = 0; bh < BH; ++bh)
+    for (int qb = 0; qb < q_blk_total; ++qb) {
+      if (qb >= q_blk_sel) {
+        for (int c = 0; c < kb_tot; ++c) keep[c] = 1;
+      } else {
+        const long long srow = (long long)bh * q_blk_sel + qb;
+        int n = counts[srow];
+        n = n < min_select ? min_select : n;
+        n = n < 0 ? 0 : (n > n_cand ? n_cand : n);
+        g_keys = rank_key + srow * n_cand;
+        for (int i = 0; i < n_cand; ++i) idx[i] = i;
+        qsort(idx, n_cand, sizeof(int), cmp_rank);
+        memset(keep, 0, kb_tot);
+        for (int i = 0; i < n; ++i) keep[idx[i]] = 1;
+        for (int c = n_cand; c < kb_tot; ++c) keep[c] = 1;
+        for (int c = 0; c < sink_lead && c < kb_tot; ++c) keep[c] = 1;
+        if (map) memcpy(map + srow * kb_tot, keep, kb_tot);
+      }
+      const long long lrow = (long long)bh * q_blk_total + qb;
+      int pos = 0;
+      for (int c = 0; c < kb_tot; ++c)
+        if (keep[c]) lut[lrow * kb_tot + pos++] = c;
+      nvalid[lrow] = pos;
+    }
+  free(idx);
+  free(keep);
+}
+
+/* vectorised helpers for tests */
+void oracle_expf_array(const float* x, float* y, long long n) {
+  for (long long i = 0; i < n; ++i) y[i] = oracle_expf(x[i]);
+}
+void oracle_round_bf16_array(const float* x, float* y, long long n) {
+  for (long long i = 0; i < n; ++i) y[i] = oracle_round_bf16(x[i]);
+}

@@ -1,0 +1,308 @@
+"""The block-sparse global-attention forward (reference src/ress/models/attention.py).
+
+`ress_attention_forward` is the drop-in replacement of a global block's attention
+forward. Its hot path, `sparse_global_attention`, runs on the GPU kernels only:
+
+    prepare_blocks     pool Q/K/V, key mean, per-block INT8 Q/K, packed V   (prep.hip)
+    pooled_scores      pooled softmax attn_full, renormalised attn_cond      (scores.hip)
+    budget_fn          per-(head, q-block) counts                            (budget.hip)
+    rank key           attn_cond, or ReSS restore-swap / projected / random
+    select_blocks      top-n + sinks -> final_map, LUT                       (select.hip)
+    sparse_attention   INT8 QK^T / bf16 PV over the LUT, special rows dense  (attn.hip)
+
+No step falls back to the CPU or to a dense PyTorch path.
+"""
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from ress_amd import _lib, kernels
+from ress_amd import criterion as _criterion
+from ress_amd.kernels import KS_K, KS_Q, LayerGrid
+from ress_amd.qkv import combine_special_and_patch, compute_qkv, get_patch_tokens, get_special_tokens, project_out
+
+KBLK = 64
+MIN_NUM_TO_SELECT = 2  # floor on real key blocks per query row (reference attention.py:40-42)
+
+_RANDOM_SEED = 20260826  # block_criterion="random" (reference attention.py:177-196)
+_random_gens = {}
+
+
+def _random_gen(device):
+    gen = _random_gens.get(device)
+    if gen is None:
+        gen = torch.Generator(device=device).manual_seed(_RANDOM_SEED)
+        _random_gens[device] = gen
+    return gen
+
+
+@dataclass
+class AttentionAux:
+    """Per-layer auxiliary values (reference attention.py:246-265)."""
+
+    attn_pooled: torch.Tensor = None
+    v_bar: torch.Tensor = None
+    attn_full: torch.Tensor = None
+    v_bar_full: torch.Tensor = None
+    n_cand: int = None
+    q_patch: torch.Tensor = None
+    shape: dict = None
+    sparsity: float = None
+    output: torch.Tensor = None
+
+
+@dataclass
+class LayerResult:
+    out: torch.Tensor              # (B, H, frames*P, 64) storage order
+    attn_full: torch.Tensor = None
+    attn_cond: torch.Tensor = None
+    v_bar_full: torch.Tensor = None
+    final_map: torch.Tensor = None
+    counts: torch.Tensor = None
+    lut: torch.Tensor = None
+    nvalid: torch.Tensor = None
+    blocks: kernels.Blocks = None
+
+    def sparsity(self):
+        """Realized sparsity 1 - mean(final_map), sinks included (reference
+        attention.py:242). Synchronises with the device."""
+        if self.final_map is None:
+            return 0.0
+        return 1.0 - self.final_map.float().mean().item()
+
+
+def _rank_key(block_criterion, attn_cond, attn_full, v_bar_full, counts, grid, M, hd):
+    if block_criterion == "probability":
+        return attn_cond
+    if block_criterion == "random":
+        return torch.rand(attn_cond.shape, device=attn_cond.device, dtype=torch.float32,
+                          generator=_random_gen(attn_cond.device))
+    from ress_amd import projected as _projected
+    if block_criterion == "projected":
+        if M is None:
+            raise AssertionError("block_criterion='projected' requires bake_and_attach_M(model) first (self.M)")
+        return _projected.projected_score(attn_full, v_bar_full, M, n_cand=grid.n_cand)
+    if _criterion.is_restore_swap(block_criterion):
+        spec = _criterion.parse_restore_swap(block_criterion)
+        if spec.use_wo:
+            if M is None:
+                raise AssertionError(f"block_criterion={block_criterion!r} requires bake_and_attach_M(model) first")
+        else:
+            M = torch.eye(hd, device=attn_full.device, dtype=torch.float32).expand(grid.H, hd, hd)
+        return _projected.restore_swap_rank_by(
+            attn_full, v_bar_full, M, counts, n_cand=grid.n_cand, n_iters=spec.n_iters, track_best=spec.track_best,
+            big_dtype=spec.big_dtype, restore_frac=spec.restore_frac, decay=spec.decay, maximize=spec.maximize,
+            invert_cut=spec.invert_cut)
+    raise ValueError(block_criterion)
+
+
+def sparse_global_attention(q, k, v, grid, *, num_to_select=None, budget_fn=None, perhead_budget_fn=None,
+                            joint_select_fn=None, block_criterion="probability", M=None, out=None,
+                            out_dtype=torch.float32, keep_intermediates=False):
+    """One layer's block-sparse global attention on the GPU.
+
+    q, k, v: bf16 (B, H, frames*P, 64) in storage order (per frame S special then P-S
+    patch tokens). Patch queries attend to the selected key blocks plus the trailing
+    special blocks; special queries attend densely (reference attention.py:404-412,
+    446-491, 510-581, 625). Returns a LayerResult whose `out` is (B, H, frames*P, 64)
+    in storage order."""
+    blocks = kernels.prepare_blocks(q, k, v, grid)
+    attn_full, attn_cond = kernels.pooled_scores(blocks)
+    v_bar_full = blocks.pooled_v.view(grid.B, grid.H, grid.kb_p, 64)
+    counts = None
+    final_map = None
+    if joint_select_fn is not None:
+        final_map = joint_select_fn(attn_cond, v_bar_full[..., :grid.n_cand, :], grid.sink_blocks)
+        lut, nvalid = kernels.lut_from_map(final_map, grid)
+    else:
+        if perhead_budget_fn is not None:
+            counts = perhead_budget_fn(attn_cond, v_bar_full[..., :grid.n_cand, :])
+        elif budget_fn is not None:
+            counts = budget_fn(attn_cond)
+        else:
+            counts = num_to_select
+        if counts is None:
+            raise AssertionError("num_to_select (or budget_fn/perhead_budget_fn) required unless dense=True "
+                                 "or joint_select_fn is given")
+        if not torch.is_tensor(counts):
+            counts = torch.full((grid.B, grid.H, grid.q_blk_p), int(counts), dtype=torch.int32, device=q.device)
+        counts = counts.reshape(grid.B, grid.H, grid.q_blk_p)
+        rank = _rank_key(block_criterion, attn_cond, attn_full, v_bar_full,
+                         counts.clamp(min=min(MIN_NUM_TO_SELECT, grid.n_cand)) if block_criterion != "probability"
+                         else counts, grid, M, 64)
+        final_map, lut, nvalid = kernels.select_blocks(rank, counts, grid, min(MIN_NUM_TO_SELECT, grid.n_cand))
+    o = kernels.sparse_attention(blocks, lut, nvalid, out=out, out_dtype=out_dtype)
+    res = LayerResult(out=o, final_map=final_map)
+    if keep_intermediates:
+        res.attn_full, res.attn_cond, res.v_bar_full = attn_full, attn_cond, v_bar_full
+        res.counts, res.lut, res.nvalid, res.blocks = counts, lut, nvalid, blocks
+    return res
+
+
+def _dense_storage(q, k, v, shp):
+    """Exact SDPA of every query over cat(patch, special) keys (reference attention.py:404-412,
+    484-486), written back in storage order."""
+    N, P, S = shp["N"], shp["P"], shp["S"]
+    kp, ks = get_patch_tokens(k, N, P, S), get_special_tokens(k, N, P, S)
+    vp, vs = get_patch_tokens(v, N, P, S), get_special_tokens(v, N, P, S)
+    key = kp if ks is None else torch.cat([kp, ks], dim=-2)
+    value = vp if vs is None else torch.cat([vp, vs], dim=-2)
+    xp = F.scaled_dot_product_attention(get_patch_tokens(q, N, P, S), key, value)
+    qs = get_special_tokens(q, N, P, S)
+    xs = None if qs is None else F.scaled_dot_product_attention(qs, key, value)
+    return combine_special_and_patch(xs, xp, shp)
+
+
+def ress_attention_forward(self, x, pos, num_to_select=None, budget_fn=None, perhead_budget_fn=None,
+                           joint_select_fn=None, block_criterion="probability", pool_mode="avg",
+                           num_special_tokens=5, num_heads=16, shape=None, aux_store=None, aux_full=True,
+                           dense=False, retain_output_grad=False, pooled_fallback=False, protect_own_frame=False):
+    """Replacement forward of a global-attention block (reference attention.py:296-659),
+    same arguments and return value: (B, N*P, dim) after the W_O projection."""
+    if pool_mode != "avg":
+        raise NotImplementedError("only avg pooling (the reference default) is implemented")
+    if protect_own_frame:
+        raise NotImplementedError("protect_own_frame is not implemented")
+    q, k, v, shp = compute_qkv(self, x, pos, num_special_tokens=num_special_tokens, num_heads=num_heads,
+                               shape=shape)
+    B, N, P, hd, nh, S = shp["B"], shp["N"], shp["P"], shp["head_dim"], shp["num_heads"], shp["S"]
+    if hd != 64:
+        raise ValueError(f"head_dim {hd} unsupported (the kernels are written for 64)")
+    grid = LayerGrid(B=B, H=nh, frames=N, P=P, S=S)
+    res = None
+    if dense:
+        x_out = _dense_storage(q, k, v, shp).float()
+        sparsity = 0.0
+    else:
+        qb, kbf, vbf = (t.to(torch.bfloat16) for t in (q, k, v))
+        res = sparse_global_attention(
+            qb, kbf, vbf, grid, num_to_select=num_to_select, budget_fn=budget_fn, perhead_budget_fn=perhead_budget_fn,
+            joint_select_fn=joint_select_fn, block_criterion=block_criterion, M=getattr(self, "M", None),
+            keep_intermediates=aux_store is not None and aux_full)
+        x_out = res.out
+        sparsity = res.sparsity() if aux_store is not None else None
+    if aux_store is not None:
+        if aux_full and res is not None:
+            aux_store["value"] = AttentionAux(
+                attn_pooled=res.attn_full[..., :grid.n_cand], v_bar=res.v_bar_full[..., :grid.n_cand, :],
+                attn_full=res.attn_full, v_bar_full=res.v_bar_full, n_cand=grid.n_cand,
+                q_patch=get_patch_tokens(q, N, P, S), shape=shp, sparsity=sparsity)
+        else:
+            aux_store["value"] = AttentionAux(shape=shp, sparsity=sparsity)
+    if retain_output_grad and x_out.requires_grad:
+        x_out.retain_grad()
+    if aux_store is not None and aux_full:
+        aux_store["value"].output = x_out
+    return project_out(self, x_out.to(x.dtype) if x.dtype != x_out.dtype else x_out, B, N, P, nh, hd)
+
+
+# ---------------------------------------------------------------------------
+# Reference-compatible standalone helpers (plain sequences, GPU kernels)
+# ---------------------------------------------------------------------------
+
+def _plain_pools(query, key):
+    B, nh, Tq, C = query.shape
+    Tk = key.shape[-2]
+    if C != 64:
+        raise ValueError("head_dim must be 64")
+    dev = query.device
+    q = query.to(torch.bfloat16)
+    k = key.to(torch.bfloat16)
+    nq, nk = -(-Tq // KS_Q), -(-Tk // KS_K)
+    BH = B * nh
+    q_i8 = torch.empty(BH, nq, KS_Q, 64, dtype=torch.int8, device=dev)
+    q_scale = torch.empty(BH, nq, device=dev)
+    k_i8 = torch.empty(BH, nk, KS_K, 64, dtype=torch.int8, device=dev)
+    k_scale = torch.empty(BH, nk, device=dev)
+    pooled_q = torch.empty(BH, nq, 64, device=dev)
+    P = _lib.ptr
+    _lib.call("ress_per_block_int8", P(q), P(k), None, B, nh, Tq, Tk, *q.stride()[:3], *k.stride()[:3], P(q_i8),
+              P(q_scale), P(k_i8), P(k_scale), P(pooled_q), _lib.stream_handle(dev))
+    ksum = torch.empty(BH, nk, 64, device=dev)
+    km = torch.empty(BH, 64, device=dev)
+    pooled_k = torch.empty(BH, nk, 64, device=dev)
+    pooled_v = torch.empty(BH, nk, 64, device=dev)
+    v_pack = torch.empty(BH, nk, 4096, dtype=torch.bfloat16, device=dev)
+    _lib.call("ress_prep_kv_plain", P(k), P(k), B, nh, Tk, *k.stride()[:3], *k.stride()[:3], P(ksum), P(km),
+              P(pooled_k), P(pooled_v), P(v_pack), _lib.stream_handle(dev))
+    return pooled_q, pooled_k, (B, nh, nq, nk)
+
+
+def predict_attention(query, key, ks_q=KS_Q, ks_k=KS_K, pool_mode="avg"):
+    """Pooled block map softmax(pool(Q) pool(K)^T / sqrt(C)) (reference attention.py:82-100).
+    query (B, nh, Tq, 64), key (B, nh, Tk, 64) -> (B, nh, ceil(Tq/128), ceil(Tk/64)) fp32."""
+    if (ks_q, ks_k, pool_mode) != (KS_Q, KS_K, "avg"):
+        raise NotImplementedError("the kernels pool with 128/64 averages")
+    pooled_q, pooled_k, (B, nh, nq, nk) = _plain_pools(query, key)
+    dev = query.device
+    full = torch.empty(B, nh, nq, nk, device=dev)
+    cond = torch.empty(B, nh, nq, nk, device=dev)
+    _lib.call("ress_pooled_scores", _lib.ptr(pooled_q), _lib.ptr(pooled_k), B * nh, nq, nk, nk,
+              1.0 / math.sqrt(64), _lib.ptr(full), _lib.ptr(cond), _lib.stream_handle(dev))
+    return full
+
+
+def block_mean_value(value, ks_k=KS_K):
+    """Per-64-key-block mean of V (reference attention.py:103-109): (B, nh, Tk, 64) ->
+    (B, nh, ceil(Tk/64), 64) fp32."""
+    if ks_k != KS_K:
+        raise NotImplementedError("block size is 64")
+    B, nh, Tk, C = value.shape
+    v = value.to(torch.bfloat16)
+    dev = v.device
+    nk = -(-Tk // KS_K)
+    BH = B * nh
+    ksum = torch.empty(BH, nk, 64, device=dev)
+    km = torch.empty(BH, 64, device=dev)
+    pk = torch.empty(BH, nk, 64, device=dev)
+    pv = torch.empty(BH, nk, 64, device=dev)
+    vp = torch.empty(BH, nk, 4096, dtype=torch.bfloat16, device=dev)
+    _lib.call("ress_prep_kv_plain", _lib.ptr(v), _lib.ptr(v), B, nh, Tk, *v.stride()[:3], *v.stride()[:3],
+              _lib.ptr(ksum), _lib.ptr(km), _lib.ptr(pk), _lib.ptr(pv), _lib.ptr(vp), _lib.stream_handle(dev))
+    return pv.view(B, nh, nk, 64)
+
+
+def build_block_mask(pooled_score, num_to_select, sink_blocks, rank_by=None):
+    """Top num_to_select of each row by (rank_by or pooled_score), ties to the lowest
+    index, plus `sink_blocks` trailing all-True columns (reference attention.py:147-174).
+    Returns (B, nh, q_blk, k_blk + sink_blocks) bool."""
+    key = pooled_score if rank_by is None else rank_by
+    B, nh, q_blk, k_blk = key.shape
+    grid_cols = k_blk + sink_blocks
+    dev = key.device
+    fmap = torch.empty(B, nh, q_blk, grid_cols, dtype=torch.uint8, device=dev)
+    lut = torch.empty(B * nh, q_blk, grid_cols, dtype=torch.int32, device=dev)
+    nvalid = torch.empty(B * nh, q_blk, dtype=torch.int32, device=dev)
+    rk = key.float().contiguous()
+    cn = num_to_select.to(torch.int32).contiguous()
+    _lib.call("ress_select_blocks", _lib.ptr(rk), _lib.ptr(cn), B * nh, q_blk, q_blk, k_blk, grid_cols, 0, 0,
+              _lib.ptr(fmap), _lib.ptr(lut), _lib.ptr(nvalid), _lib.stream_handle(dev))
+    return fmap.bool()
+
+
+def compute_baseline_num_to_select(pooled_score, sparse_ratio=None, cdf_threshold=None, eps=1e-5):
+    from ress_amd.budget import compute_baseline_num_to_select as _c
+    return _c(pooled_score, sparse_ratio, cdf_threshold, eps)
+
+
+def run_block_sparse_kernel(query, key, value, final_map, dtype=torch.float16, out_dtype=torch.float32):
+    """Reference attention.py:217-243 on the GPU kernels: LUT of final_map, key mean,
+    per-block INT8 Q and K - km, block-sparse attention. query (B,nh,Tq,64), key/value
+    (B,nh,Tk,64), final_map (B,nh,ceil(Tq/128),ceil(Tk/64)). Returns (o, sparsity)."""
+    from ress_amd import sparge
+    B, nh, Tq, C = query.shape
+    q = query.contiguous().to(torch.bfloat16)
+    k = key.contiguous().to(torch.bfloat16)
+    v = value.contiguous().to(dtype)
+    lut, valid_block_num = sparge.block_map_lut_triton(final_map)
+    km = sparge.key_mean(k)
+    q_int8, q_scale, k_int8, k_scale = sparge.per_block_int8(q, k, km=km)
+    o = torch.empty(B, nh, Tq, C, dtype=out_dtype, device=q.device)
+    sparge.qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold(
+        q_int8, k_int8, v, o, lut, valid_block_num, sparge.hyperparameter_check(1e10, nh, q.device), q_scale,
+        k_scale, 1, 0, 1, 1.0 / math.sqrt(C), 0)
+    sparsity = 1 - final_map.float().mean().item()
+    return o, sparsity

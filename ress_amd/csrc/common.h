@@ -1,0 +1,169 @@
+// Shared device-side definitions for libress_hip (gfx950 / CDNA4).
+//
+// Numerics contract. Every kernel that feeds a block map (pooling, the pooled
+// softmax, the CDF budget, the HeSS reallocation, top-k selection, restore-swap)
+// fixes its floating-point evaluation order so that the result is a pure
+// function of the inputs. The orders are:
+//
+//   SUM8x(T)   block pooling over T tokens with 8 token lanes:
+//              p_j = ((0 + x[j]) + x[8+j]) + x[16+j] ...   for j = 0..7
+//              (only the block's valid tokens, in increasing token order)
+//              total = ((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7))
+//   SUM64(n)   row sums: p_l = sequential sum of x[i] for i = l, l+64, l+128 ...
+//              for l = 0..63, then a butterfly: at offsets 1,2,4,8,16,32 every
+//              partial becomes partial[l] + partial[l ^ off].
+//   DOT64      pooled dot products: acc = fmaf(a[d], b[d], acc), d = 0..63, from 0.
+//   SEQ        sequential sums in index order (CDF prefix sums, HeSS head sums,
+//              the key mean over blocks).
+//
+// Division and square root are IEEE correctly rounded (hipcc's default
+// -fhip-fp32-correctly-rounded-divide-sqrt), and every file is compiled with
+// -ffp-contract=off so no multiply-add is fused unless written as fmaf().
+// ress_expf is Cody-Waite argument reduction plus a degree-7 Taylor polynomial
+// evaluated by Horner's rule; it is written out here (not the device libm) so
+// its bits are fixed.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define RESS_API extern "C" __attribute__((visibility("default")))
+
+// ---- error reporting (defined in capi.hip) --------------------------------
+void ress_set_error(const char* fmt, ...);
+
+#define RESS_REQUIRE(cond, ...)        \
+  do {                                 \
+    if (!(cond)) {                     \
+      ress_set_error(__VA_ARGS__);     \
+      return -1;                       \
+    }                                  \
+  } while (0)
+
+#define RESS_LAUNCHED(name)                                                   \
+  do {                                                                        \
+    hipError_t _e = hipGetLastError();                                        \
+    if (_e != hipSuccess) {                                                   \
+      ress_set_error("%s: launch failed: %s", name, hipGetErrorString(_e));   \
+      return -2;                                                              \
+    }                                                                         \
+  } while (0)
+
+// ---- geometry --------------------------------------------------------------
+// Token layout of one (batch, head) sequence as the backbone produces it:
+// frames of P tokens, the first S of each frame special (camera/register),
+// the remaining HW patch tokens. The kernels address tokens in "kernel order":
+// patch tokens first (frame-major), then special tokens (frame-major), which is
+// the reference's cat([k_patch, k_special]) (attention.py:405-406). S == 0 is the
+// plain full-sequence layout (kernel order == storage order).
+struct TokenMap {
+  int P;    // tokens per frame in storage
+  int S;    // special tokens per frame
+  int HW;   // patch tokens per frame (P - S)
+  int T_p;  // total patch tokens (frames * HW)
+  int T_s;  // total special tokens (frames * S)
+};
+
+__device__ __forceinline__ int patch_to_storage(int p, const TokenMap& m) {
+  int f = p / m.HW;
+  return f * m.P + m.S + (p - f * m.HW);
+}
+__device__ __forceinline__ int special_to_storage(int s, const TokenMap& m) {
+  int f = s / m.S;
+  return f * m.P + (s - f * m.S);
+}
+// kernel key index -> storage index
+__device__ __forceinline__ int key_to_storage(int kk, const TokenMap& m) {
+  return kk < m.T_p ? patch_to_storage(kk, m) : special_to_storage(kk - m.T_p, m);
+}
+
+// ---- bf16 ------------------------------------------------------------------
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ void unpack_bf16x8(const uint4& r, float x[8]) {
+  x[0] = bf16_lo(r.x); x[1] = bf16_hi(r.x);
+  x[2] = bf16_lo(r.y); x[3] = bf16_hi(r.y);
+  x[4] = bf16_lo(r.z); x[5] = bf16_hi(r.z);
+  x[6] = bf16_lo(r.w); x[7] = bf16_hi(r.w);
+}
+// fp32 -> bf16, round to nearest even (NaN kept quiet)
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ float round_bf16(float f) {
+  return __uint_as_float(f32_to_bf16_bits(f) << 16);
+}
+
+// ---- exp -------------------------------------------------------------------
+// e^x = 2^n * e^r, n = rint(x*log2(e)), r = x - n*ln2 (two-constant Cody-Waite
+// split of ln2), e^r by the Taylor series to degree 7 (|r| <= 0.347 keeps the
+// truncation error below 0.05 ulp).
+__device__ __forceinline__ float ress_expf(float x) {
+  if (x != x) return x;
+  if (x > 0x1.62e42ep+6f) return __builtin_huge_valf();
+  if (x < -0x1.9fe368p+6f) return 0.0f;
+  float n = rintf(x * 0x1.715476p+0f);
+  float r = fmaf(-n, 0x1.62e4p-1f, x);
+  r = fmaf(-n, 0x1.7f7d1cp-20f, r);
+  float p = 0x1.a01a02p-13f;
+  p = fmaf(p, r, 0x1.6c16c2p-10f);
+  p = fmaf(p, r, 0x1.111112p-7f);
+  p = fmaf(p, r, 0x1.555556p-5f);
+  p = fmaf(p, r, 0x1.555556p-3f);
+  p = fmaf(p, r, 0x1p-1f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  int ni = (int)n;
+  if (ni > 127) return (p * 2.0f) * 0x1p127f;
+  if (ni < -126) return (p * __int_as_float((ni + 127 + 64) << 23)) * 0x1p-64f;
+  return p * __int_as_float((ni + 127) << 23);
+}
+
+// ---- order keys ------------------------------------------------------------
+// Order-preserving fp32 -> uint32 (unsigned compare == float compare; -0 == +0;
+// NaN above +inf).
+__device__ __forceinline__ uint32_t order_key(float x) {
+  uint32_t u = __float_as_uint(x);
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// ---- per-block int8 quantiser ---------------------------------------------
+// scale = amax/127; q = trunc(x/scale + 0.5*sign) (round half away from zero),
+// the published SageAttention per-block rule. A block whose amax is 0 has scale
+// 0 and all-zero codes.
+__device__ __forceinline__ int quant_i8(float x, float scale) {
+  if (scale == 0.0f) return 0;
+  float y = x / scale;
+  y = y + (y >= 0.0f ? 0.5f : -0.5f);
+  return (int)y;
+}
+
+// ---- wave reductions (wave64) ---------------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+// the SUM64 butterfly over 64 lane partials
+__device__ __forceinline__ float sum64_tree(float v) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v = v + __shfl_xor(v, off, 64);
+  return v;
+}
+// the SUM8x tree over token lanes j = lane>>3 (lane bits 3..5)
+__device__ __forceinline__ float sum8_tree(float v) {
+  v = v + __shfl_xor(v, 8, 64);
+  v = v + __shfl_xor(v, 16, 64);
+  v = v + __shfl_xor(v, 32, 64);
+  return v;
+}
+
+__host__ __device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }

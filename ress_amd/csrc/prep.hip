@@ -1,0 +1,321 @@
+// Block preparation: mean pooling, per-block INT8 quantisation of Q and K, and
+// packing of V into the attention kernel's MFMA-ready layout.
+//
+// Replaces, for the block-sparse path:
+//   * predict_attention's avg_pool1d of Q (128) and K (64), ceil mode, a partial
+//     block divided by its valid count  (reference src/ress/models/attention.py:82-100)
+//   * block_mean_value's pool of V (64)                     (attention.py:103-109)
+//   * km = key.mean(dim=-2) and per_block_int8(q, k - km)   (attention.py:231-233,
+//     SpargeAttn quant_per_block with external/patches/spargeattn.patch:38-41:
+//     Q is quantised with sm_scale = 1)
+//
+// One wave (64 lanes) per (block, batch*head). Lane l owns dims 8*(l&7)..+7 of
+// token lane j = l>>3; a block of T tokens is read in T/8 coalesced 1 KiB rows.
+#include "common.h"
+
+struct Strides {  // element strides of a (B, H, T, D) tensor in any layout
+  long long b, h, t;
+  int H;
+};
+__device__ __forceinline__ long long bh_offset(int bh, const Strides& s) {
+  return (long long)(bh / s.H) * s.b + (long long)(bh % s.H) * s.h;
+}
+
+// ----------------------------------------------------------------------------
+// Q blocks: kernel q-blocks 0..q_blk_p-1 hold patch queries, q_blk_p.. the
+// special queries. Writes q_i8 [BH][q_blk_total][128][64], q_scale [BH][q_blk_total]
+// and, for patch blocks, pooled_q [BH][q_blk_p][64].
+__global__ __launch_bounds__(64) void k_prep_q(const uint16_t* __restrict__ q, Strides sq, TokenMap m,
+                                               int q_blk_p, int q_blk_total, int8_t* __restrict__ q_i8,
+                                               float* __restrict__ q_scale, float* __restrict__ pooled_q) {
+  const int qb = blockIdx.x, bh = blockIdx.y, lane = threadIdx.x;
+  const int j = lane >> 3, dg = lane & 7;
+  const bool special = qb >= q_blk_p;
+  const int base = special ? (qb - q_blk_p) * 128 : qb * 128;
+  const int cnt = min(128, (special ? m.T_s : m.T_p) - base);
+  const uint16_t* src = q + bh_offset(bh, sq) + dg * 8;
+
+  uint4 raw[16];
+  float acc[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int t = 8 * i + j;
+    raw[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (t < cnt) {
+      const int tok = special ? special_to_storage(base + t, m) : patch_to_storage(base + t, m);
+      raw[i] = *reinterpret_cast<const uint4*>(src + (long long)tok * sq.t);
+      float x[8];
+      unpack_bf16x8(raw[i], x);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        acc[c] = acc[c] + x[c];
+        amax = fmaxf(amax, fabsf(x[c]));
+      }
+    }
+  }
+  amax = wave_max(amax);
+  const float scale = amax / 127.0f;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) acc[c] = sum8_tree(acc[c]);
+  if (!special && j == 0) {
+    float* pq = pooled_q + ((long long)bh * q_blk_p + qb) * 64 + dg * 8;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) pq[c] = acc[c] / (float)cnt;
+  }
+  if (lane == 0) q_scale[(long long)bh * q_blk_total + qb] = scale;
+  int8_t* dst = q_i8 + (((long long)bh * q_blk_total + qb) * 128) * 64 + dg * 8;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float x[8];
+    unpack_bf16x8(raw[i], x);
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w0 |= ((uint32_t)(quant_i8(x[c], scale) & 0xff)) << (8 * c);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w1 |= ((uint32_t)(quant_i8(x[4 + c], scale) & 0xff)) << (8 * c);
+    *reinterpret_cast<uint2*>(dst + (8 * i + j) * 64) = make_uint2(w0, w1);
+  }
+}
+
+// ----------------------------------------------------------------------------
+// K/V blocks over the kernel key grid (patch keys then special keys).
+//  ksum   [BH][kb_tot][64]  full-block K sums (SUM8x), for the key mean
+//  pooled_k [BH][kb_p][64]  patch-only K means (the scoring grid)
+//  pooled_v [BH][kb_p][64]  patch-only V means (ReSS's v_bar)
+//  v_pack [BH][kb_tot][64 dims][64 keys]  bf16, keys permuted inside every group of
+//         16 as 0-3,8-11,4-7,12-15 so that one 16-byte read per lane is an MFMA
+//         operand; keys past the sequence end are zero.
+__global__ __launch_bounds__(64) void k_prep_kv(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                                                Strides sk, Strides sv, TokenMap m, int Tk, int kb_tot, int kb_p,
+                                                float* __restrict__ ksum, float* __restrict__ pooled_k,
+                                                float* __restrict__ pooled_v, uint16_t* __restrict__ v_pack) {
+  __shared__ uint16_t vt[64 * 64];
+  const int kb = blockIdx.x, bh = blockIdx.y, lane = threadIdx.x;
+  const int j = lane >> 3, dg = lane & 7;
+  const int base = kb * 64;
+  const int cnt = min(64, Tk - base);
+  const int cnt_p = min(64, m.T_p - base);  // <= 0 past the patch keys
+  const uint16_t* ksrc = k + bh_offset(bh, sk) + dg * 8;
+  const uint16_t* vsrc = v + bh_offset(bh, sv) + dg * 8;
+
+  float ka[8], kp[8], vp[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) ka[c] = kp[c] = vp[c] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int t = 8 * i + j;
+    uint4 rv = make_uint4(0u, 0u, 0u, 0u);
+    if (t < cnt) {
+      const int tok = key_to_storage(base + t, m);
+      const uint4 rk = *reinterpret_cast<const uint4*>(ksrc + (long long)tok * sk.t);
+      rv = *reinterpret_cast<const uint4*>(vsrc + (long long)tok * sv.t);
+      float xk[8], xv[8];
+      unpack_bf16x8(rk, xk);
+      unpack_bf16x8(rv, xv);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) ka[c] = ka[c] + xk[c];
+      if (t < cnt_p) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          kp[c] = kp[c] + xk[c];
+          vp[c] = vp[c] + xv[c];
+        }
+      }
+    }
+    // transpose into LDS: vt[dim][perm(key)]
+    const int u = t & 15;
+    const int pos = (t & ~15) + 8 * ((u >> 2) & 1) + 4 * (u >> 3) + (u & 3);
+    const uint32_t w[4] = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      vt[(dg * 8 + 2 * c) * 64 + pos] = (uint16_t)(w[c] & 0xffffu);
+      vt[(dg * 8 + 2 * c + 1) * 64 + pos] = (uint16_t)(w[c] >> 16);
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    ka[c] = sum8_tree(ka[c]);
+    kp[c] = sum8_tree(kp[c]);
+    vp[c] = sum8_tree(vp[c]);
+  }
+  if (j == 0) {
+    float* ks = ksum + ((long long)bh * kb_tot + kb) * 64 + dg * 8;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) ks[c] = ka[c];
+    if (kb < kb_p) {
+      float* pk = pooled_k + ((long long)bh * kb_p + kb) * 64 + dg * 8;
+      float* pv = pooled_v + ((long long)bh * kb_p + kb) * 64 + dg * 8;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        pk[c] = kp[c] / (float)cnt_p;
+        pv[c] = vp[c] / (float)cnt_p;
+      }
+    }
+  }
+  __syncthreads();
+  // 8 KiB out, 128 B per lane
+  uint4* dst = reinterpret_cast<uint4*>(v_pack + ((long long)bh * kb_tot + kb) * 4096);
+  const uint4* s4 = reinterpret_cast<const uint4*>(vt);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dst[i * 64 + lane] = s4[i * 64 + lane];
+}
+
+// key mean over all Tk keys: km[d] = SEQ-sum of the block sums / Tk
+__global__ __launch_bounds__(64) void k_key_mean(const float* __restrict__ ksum, int kb_tot, int Tk,
+                                                 float* __restrict__ km) {
+  const int bh = blockIdx.x, d = threadIdx.x;
+  const float* s = ksum + (long long)bh * kb_tot * 64 + d;
+  float acc = 0.0f;
+  for (int b = 0; b < kb_tot; ++b) acc = acc + s[(long long)b * 64];
+  km[(long long)bh * 64 + d] = acc / (float)Tk;
+}
+
+// K quantisation after smoothing: x = k - km (fp32), per 64-key block.
+// k_i8 [BH][kb_tot][64 keys][64], k_scale [BH][kb_tot]. km may be null (no smoothing).
+__global__ __launch_bounds__(64) void k_quant_k(const uint16_t* __restrict__ k, Strides sk, TokenMap m, int Tk,
+                                                int kb_tot, const float* __restrict__ km, int8_t* __restrict__ k_i8,
+                                                float* __restrict__ k_scale) {
+  const int kb = blockIdx.x, bh = blockIdx.y, lane = threadIdx.x;
+  const int j = lane >> 3, dg = lane & 7;
+  const int base = kb * 64;
+  const int cnt = min(64, Tk - base);
+  const uint16_t* src = k + bh_offset(bh, sk) + dg * 8;
+  float mean[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) mean[c] = km ? km[(long long)bh * 64 + dg * 8 + c] : 0.0f;
+  float x[8][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int t = 8 * i + j;
+    uint4 r = make_uint4(0u, 0u, 0u, 0u);
+    if (t < cnt) r = *reinterpret_cast<const uint4*>(src + (long long)key_to_storage(base + t, m) * sk.t);
+    unpack_bf16x8(r, x[i]);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      x[i][c] = (t < cnt) ? x[i][c] - mean[c] : 0.0f;
+      amax = fmaxf(amax, fabsf(x[i][c]));
+    }
+  }
+  amax = wave_max(amax);
+  const float scale = amax / 127.0f;
+  if (lane == 0) k_scale[(long long)bh * kb_tot + kb] = scale;
+  int8_t* dst = k_i8 + ((long long)bh * kb_tot + kb) * 4096 + dg * 8;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w0 |= ((uint32_t)(quant_i8(x[i][c], scale) & 0xff)) << (8 * c);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w1 |= ((uint32_t)(quant_i8(x[i][4 + c], scale) & 0xff)) << (8 * c);
+    *reinterpret_cast<uint2*>(dst + (8 * i + j) * 64) = make_uint2(w0, w1);
+  }
+}
+
+// ============================================================================
+// C ABI
+// ============================================================================
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+static TokenMap make_map(int frames, int P, int S) {
+  TokenMap m;
+  m.P = P;
+  m.S = S;
+  m.HW = P - S;
+  m.T_p = frames * (P - S);
+  m.T_s = frames * S;
+  return m;
+}
+
+// Fused preparation of one layer's Q/K/V for the ReSS forward (reference
+// attention.py:398-491 + 226-233). Inputs are the backbone's bf16 Q/K/V in storage
+// order with element strides (sB, sH, sT); D = 64 with unit stride.
+RESS_API int ress_prep_qkv(const void* q, const void* k, const void* v, int B, int H, int frames, int P, int S,
+                           long long sqB, long long sqH, long long sqT, long long skB, long long skH, long long skT,
+                           long long svB, long long svH, long long svT, void* q_i8, void* q_scale, void* pooled_q,
+                           void* k_i8, void* k_scale, void* pooled_k, void* pooled_v, void* v_pack, void* ksum,
+                           void* km, hipStream_t stream) {
+  RESS_REQUIRE(B > 0 && H > 0 && frames > 0 && P > S && S >= 0, "ress_prep_qkv: bad geometry B=%d H=%d F=%d P=%d S=%d",
+               B, H, frames, P, S);
+  RESS_REQUIRE(q && k && v && q_i8 && q_scale && pooled_q && k_i8 && k_scale && pooled_k && pooled_v && v_pack && ksum &&
+                   km,
+               "ress_prep_qkv: null pointer");
+  RESS_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(v_pack) && aligned16(q_i8) && aligned16(k_i8),
+               "ress_prep_qkv: tensors must be 16-byte aligned");
+  RESS_REQUIRE(sqT % 8 == 0 && skT % 8 == 0 && svT % 8 == 0 && sqH % 8 == 0 && skH % 8 == 0 && svH % 8 == 0 &&
+                   sqB % 8 == 0 && skB % 8 == 0 && svB % 8 == 0,
+               "ress_prep_qkv: strides must be multiples of 8 elements");
+  TokenMap m = make_map(frames, P, S);
+  const int Tk = frames * P;
+  const int BH = B * H;
+  const int q_blk_p = cdiv(m.T_p, 128), q_blk_s = cdiv(m.T_s, 128);
+  const int kb_tot = cdiv(Tk, 64), kb_p = cdiv(m.T_p, 64);
+  Strides sq{sqB, sqH, sqT, H}, sk{skB, skH, skT, H}, sv{svB, svH, svT, H};
+  hipLaunchKernelGGL(k_prep_q, dim3(q_blk_p + q_blk_s, BH), dim3(64), 0, stream, (const uint16_t*)q, sq, m, q_blk_p,
+                     q_blk_p + q_blk_s, (int8_t*)q_i8, (float*)q_scale, (float*)pooled_q);
+  RESS_LAUNCHED("k_prep_q");
+  hipLaunchKernelGGL(k_prep_kv, dim3(kb_tot, BH), dim3(64), 0, stream, (const uint16_t*)k, (const uint16_t*)v, sk, sv,
+                     m, Tk, kb_tot, kb_p, (float*)ksum, (float*)pooled_k, (float*)pooled_v, (uint16_t*)v_pack);
+  RESS_LAUNCHED("k_prep_kv");
+  hipLaunchKernelGGL(k_key_mean, dim3(BH), dim3(64), 0, stream, (const float*)ksum, kb_tot, Tk, (float*)km);
+  RESS_LAUNCHED("k_key_mean");
+  hipLaunchKernelGGL(k_quant_k, dim3(kb_tot, BH), dim3(64), 0, stream, (const uint16_t*)k, sk, m, Tk, kb_tot,
+                     (const float*)km, (int8_t*)k_i8, (float*)k_scale);
+  RESS_LAUNCHED("k_quant_k");
+  return 0;
+}
+
+// Mirror of SpargeAttn's per_block_int8(q, k) as the reference calls it
+// (attention.py:232, with the patched Q scale of spargeattn.patch:38-41): plain
+// sequences of Tq / Tk tokens, Q blocks of 128, K blocks of 64, optional key mean
+// km [B*H][64] subtracted from K first (null = none). Outputs use the attention
+// kernel's blocked layout: q_i8 [BH][ceil(Tq/128)][128][64],
+// k_i8 [BH][ceil(Tk/64)][64][64], scales [BH][nblk].
+RESS_API int ress_per_block_int8(const void* q, const void* k, const void* km, int B, int H, int Tq, int Tk,
+                                 long long sqB, long long sqH, long long sqT, long long skB, long long skH,
+                                 long long skT, void* q_i8, void* q_scale, void* k_i8, void* k_scale, void* pooled_q,
+                                 hipStream_t stream) {
+  RESS_REQUIRE(B > 0 && H > 0 && Tq > 0 && Tk > 0, "ress_per_block_int8: bad geometry");
+  RESS_REQUIRE(q && k && q_i8 && q_scale && k_i8 && k_scale && pooled_q, "ress_per_block_int8: null pointer");
+  RESS_REQUIRE(aligned16(q) && aligned16(k) && aligned16(q_i8) && aligned16(k_i8),
+               "ress_per_block_int8: tensors must be 16-byte aligned");
+  RESS_REQUIRE(sqT % 8 == 0 && skT % 8 == 0 && sqH % 8 == 0 && skH % 8 == 0 && sqB % 8 == 0 && skB % 8 == 0,
+               "ress_per_block_int8: strides must be multiples of 8 elements");
+  const int BH = B * H;
+  TokenMap mq = make_map(1, Tq, 0), mk = make_map(1, Tk, 0);
+  Strides sq{sqB, sqH, sqT, H}, sk{skB, skH, skT, H};
+  const int nq = cdiv(Tq, 128), nk = cdiv(Tk, 64);
+  hipLaunchKernelGGL(k_prep_q, dim3(nq, BH), dim3(64), 0, stream, (const uint16_t*)q, sq, mq, nq, nq, (int8_t*)q_i8,
+                     (float*)q_scale, (float*)pooled_q);
+  RESS_LAUNCHED("k_prep_q");
+  hipLaunchKernelGGL(k_quant_k, dim3(nk, BH), dim3(64), 0, stream, (const uint16_t*)k, sk, mk, Tk, nk,
+                     (const float*)km, (int8_t*)k_i8, (float*)k_scale);
+  RESS_LAUNCHED("k_quant_k");
+  return 0;
+}
+
+// Key mean of a plain (B,H,Tk,64) bf16 tensor (reference attention.py:231), via the
+// same SUM8x block sums and SEQ block order as the fused path. ksum is workspace
+// [BH][ceil(Tk/64)][64] fp32; the pooled/packed outputs of the block pass go to
+// pooled_k [BH][ceil(Tk/64)][64], pooled_v (same) and v_pack [BH][ceil(Tk/64)][4096] bf16.
+RESS_API int ress_prep_kv_plain(const void* k, const void* v, int B, int H, int Tk, long long skB, long long skH,
+                                long long skT, long long svB, long long svH, long long svT, void* ksum, void* km,
+                                void* pooled_k, void* pooled_v, void* v_pack, hipStream_t stream) {
+  RESS_REQUIRE(B > 0 && H > 0 && Tk > 0, "ress_prep_kv_plain: bad geometry");
+  RESS_REQUIRE(k && v && ksum && km && pooled_k && pooled_v && v_pack, "ress_prep_kv_plain: null pointer");
+  RESS_REQUIRE(aligned16(k) && aligned16(v) && aligned16(v_pack), "ress_prep_kv_plain: tensors must be 16-byte aligned");
+  RESS_REQUIRE(skT % 8 == 0 && svT % 8 == 0 && skH % 8 == 0 && svH % 8 == 0 && skB % 8 == 0 && svB % 8 == 0,
+               "ress_prep_kv_plain: strides must be multiples of 8 elements");
+  const int BH = B * H, nk = cdiv(Tk, 64);
+  TokenMap mk = make_map(1, Tk, 0);
+  Strides sk{skB, skH, skT, H}, sv{svB, svH, svT, H};
+  hipLaunchKernelGGL(k_prep_kv, dim3(nk, BH), dim3(64), 0, stream, (const uint16_t*)k, (const uint16_t*)v, sk, sv, mk,
+                     Tk, nk, nk, (float*)ksum, (float*)pooled_k, (float*)pooled_v, (uint16_t*)v_pack);
+  RESS_LAUNCHED("k_prep_kv");
+  hipLaunchKernelGGL(k_key_mean, dim3(BH), dim3(64), 0, stream, (const float*)ksum, nk, Tk, (float*)km);
+  RESS_LAUNCHED("k_key_mean");
+  return 0;
+}

@@ -1,0 +1,245 @@
+"""Thin tensor-level wrappers over the libress_hip C ABI, plus the layer geometry.
+
+Every function here takes device tensors, allocates its outputs with torch (the
+caching allocator, so steady-state calls do not reach hipMalloc) and enqueues the
+kernels on torch's current stream. Nothing here synchronises with the host.
+"""
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from ress_amd import _lib
+
+KS_Q = 128  # query block (reference src/ress/models/attention.py:37)
+KS_K = 64   # key block (attention.py:38-39)
+HEAD_DIM = 64
+
+
+def _cdiv(a, b):
+    return -(-a // b)
+
+
+@dataclass(frozen=True)
+class LayerGrid:
+    """Block geometry of one global-attention layer (reference attention.py:446-491).
+
+    Storage order per (batch, head): `frames` frames of `P` tokens, the first `S` of
+    each special. Kernel key order is cat(patch, special); query blocks are the patch
+    blocks followed by the special blocks (dense rows)."""
+
+    B: int
+    H: int
+    frames: int
+    P: int
+    S: int
+    sink_protect: bool = True
+
+    @property
+    def BH(self):
+        return self.B * self.H
+
+    @property
+    def T_p(self):
+        return self.frames * (self.P - self.S)
+
+    @property
+    def T_s(self):
+        return self.frames * self.S
+
+    @property
+    def Tk(self):
+        return self.frames * self.P
+
+    @property
+    def q_blk_p(self):
+        return _cdiv(self.T_p, KS_Q)
+
+    @property
+    def q_blk_s(self):
+        return _cdiv(self.T_s, KS_Q)
+
+    @property
+    def q_blk_total(self):
+        return self.q_blk_p + self.q_blk_s
+
+    @property
+    def kb_p(self):
+        """Width of the pooled map (patch keys only, ceil)."""
+        return _cdiv(self.T_p, KS_K)
+
+    @property
+    def kb_tot(self):
+        """Kernel key-block grid over cat(patch, special)."""
+        return _cdiv(self.Tk, KS_K)
+
+    @property
+    def n_cand(self):
+        """Droppable candidate blocks: only blocks holding patch keys exclusively
+        when special tokens exist (attention.py:453-456)."""
+        if self.S > 0 and self.sink_protect:
+            return self.T_p // KS_K
+        return _cdiv(self.T_p, KS_K)
+
+    @property
+    def sink_blocks(self):
+        return self.kb_tot - self.n_cand
+
+
+@dataclass
+class Blocks:
+    """Output of the preparation pass (see ress_prep_qkv)."""
+
+    grid: LayerGrid
+    q_i8: torch.Tensor
+    q_scale: torch.Tensor
+    pooled_q: torch.Tensor
+    k_i8: torch.Tensor
+    k_scale: torch.Tensor
+    pooled_k: torch.Tensor
+    pooled_v: torch.Tensor
+    v_pack: torch.Tensor
+    ksum: torch.Tensor
+    km: torch.Tensor
+
+
+def _check_qkv(t, name, grid):
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a device tensor (the block-sparse path runs only on the GPU)")
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16, got {t.dtype}")
+    if t.dim() != 4 or t.shape[0] != grid.B or t.shape[1] != grid.H or t.shape[2] != grid.Tk or t.shape[3] != HEAD_DIM:
+        raise ValueError(f"{name} must be (B,H,frames*P,64) = ({grid.B},{grid.H},{grid.Tk},64), got {tuple(t.shape)}")
+    if t.stride(3) != 1:
+        raise ValueError(f"{name} must have a unit-stride head dim")
+
+
+def prepare_blocks(q, k, v, grid):
+    """Pool, quantise and pack one layer's Q/K/V (bf16, storage order)."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _check_qkv(t, n, grid)
+    dev = q.device
+    BH = grid.BH
+    e = lambda *s, dt=torch.float32: torch.empty(*s, dtype=dt, device=dev)  # noqa: E731
+    b = Blocks(
+        grid=grid,
+        q_i8=e(BH, grid.q_blk_total, KS_Q, HEAD_DIM, dt=torch.int8),
+        q_scale=e(BH, grid.q_blk_total),
+        pooled_q=e(BH, grid.q_blk_p, HEAD_DIM),
+        k_i8=e(BH, grid.kb_tot, KS_K, HEAD_DIM, dt=torch.int8),
+        k_scale=e(BH, grid.kb_tot),
+        pooled_k=e(BH, grid.kb_p, HEAD_DIM),
+        pooled_v=e(BH, grid.kb_p, HEAD_DIM),
+        v_pack=e(BH, grid.kb_tot, 4096, dt=torch.bfloat16),
+        ksum=e(BH, grid.kb_tot, HEAD_DIM),
+        km=e(BH, HEAD_DIM),
+    )
+    P = _lib.ptr
+    _lib.call(
+        "ress_prep_qkv", P(q), P(k), P(v), grid.B, grid.H, grid.frames, grid.P, grid.S,
+        *q.stride()[:3], *k.stride()[:3], *v.stride()[:3],
+        P(b.q_i8), P(b.q_scale), P(b.pooled_q), P(b.k_i8), P(b.k_scale), P(b.pooled_k), P(b.pooled_v),
+        P(b.v_pack), P(b.ksum), P(b.km), _lib.stream_handle(dev))
+    return b
+
+
+def pooled_scores(blocks):
+    """(attn_full, attn_cond): the pooled softmax over the kb_p patch key blocks and its
+    renormalisation over the n_cand candidates, both (B,H,q_blk_p,*) fp32."""
+    g = blocks.grid
+    dev = blocks.pooled_q.device
+    full = torch.empty(g.B, g.H, g.q_blk_p, g.kb_p, dtype=torch.float32, device=dev)
+    cond = torch.empty(g.B, g.H, g.q_blk_p, g.n_cand, dtype=torch.float32, device=dev)
+    _lib.call("ress_pooled_scores", _lib.ptr(blocks.pooled_q), _lib.ptr(blocks.pooled_k), g.BH, g.q_blk_p, g.kb_p,
+              g.n_cand, 1.0 / math.sqrt(HEAD_DIM), _lib.ptr(full), _lib.ptr(cond), _lib.stream_handle(dev))
+    return full, cond
+
+
+def topk_from_ratio(k_blk, sparse_ratio):
+    """int(k_blk * (1 - sparse_ratio)) in Python double arithmetic (attention.py:287)."""
+    return int(k_blk * (1 - sparse_ratio))
+
+
+def baseline_budget(attn_pooled, sparse_ratio=None, cdf_threshold=None):
+    """compute_baseline_num_to_select (attention.py:268-293) on the GPU. Returns int32
+    counts shaped attn_pooled.shape[:-1]."""
+    if sparse_ratio is None and cdf_threshold is None:
+        raise AssertionError("at least one of sparse_ratio/cdf_threshold required")
+    if not attn_pooled.is_cuda or attn_pooled.dtype != torch.float32:
+        raise RuntimeError("baseline_budget takes an fp32 device tensor")
+    ap = attn_pooled.contiguous()
+    k_blk = ap.shape[-1]
+    rows = ap.numel() // k_blk if k_blk else 0
+    out = torch.empty(ap.shape[:-1], dtype=torch.int32, device=ap.device)
+    topk = topk_from_ratio(k_blk, sparse_ratio) if sparse_ratio is not None else -1
+    cdf = float(cdf_threshold) if cdf_threshold is not None else -1.0
+    _lib.call("ress_baseline_budget", _lib.ptr(ap), rows, k_blk, cdf, topk, _lib.ptr(out),
+              _lib.stream_handle(ap.device))
+    return out
+
+
+def head_budget(baseline, scores_norm, beta, max_val, max_iters=1000, min_select=0, iters_out=None):
+    """adjust_attention_selection (src/ress/budget/_proportional.py:49-115) on the GPU.
+    baseline (B,H,q_blk) int32; scores_norm (H,) fp32 device tensor or None."""
+    if baseline.dtype != torch.int32:
+        baseline = baseline.to(torch.int32)
+    baseline = baseline.contiguous()
+    B, H, q_blk = baseline.shape
+    out = torch.empty_like(baseline)
+    _lib.call("ress_head_budget", _lib.ptr(baseline), B, H, q_blk, _lib.ptr(scores_norm), float(beta), int(max_val),
+              int(max_iters), int(min_select), _lib.ptr(out), _lib.ptr(iters_out), _lib.stream_handle(baseline.device))
+    return out
+
+
+def select_blocks(rank_key, counts, grid, min_select, sink_lead=0, want_map=True):
+    """Top-n selection + sinks + LUT. rank_key (B,H,q_blk_p,n_cand) fp32, counts
+    (B,H,q_blk_p) int. Returns (final_map uint8 (B,H,q_blk_p,kb_tot) or None, lut, nvalid)."""
+    dev = rank_key.device
+    rk = rank_key.contiguous()
+    if rk.dtype != torch.float32:
+        rk = rk.float()
+    cn = counts.to(torch.int32).contiguous()
+    fmap = (torch.empty(grid.B, grid.H, grid.q_blk_p, grid.kb_tot, dtype=torch.uint8, device=dev)
+            if want_map else None)
+    lut = torch.empty(grid.BH, grid.q_blk_total, grid.kb_tot, dtype=torch.int32, device=dev)
+    nvalid = torch.empty(grid.BH, grid.q_blk_total, dtype=torch.int32, device=dev)
+    _lib.call("ress_select_blocks", _lib.ptr(rk), _lib.ptr(cn), grid.BH, grid.q_blk_p, grid.q_blk_total, grid.n_cand,
+              grid.kb_tot, int(sink_lead), int(min_select), _lib.ptr(fmap), _lib.ptr(lut), _lib.ptr(nvalid),
+              _lib.stream_handle(dev))
+    return fmap, lut, nvalid
+
+
+def lut_from_map(final_map, grid):
+    """LUT of an externally built final_map (B,H,q_blk_p,kb_tot) bool, plus the dense
+    special rows (block_map_lut_triton, attention.py:224)."""
+    dev = final_map.device
+    m = final_map.to(torch.uint8).contiguous()
+    lut = torch.empty(grid.BH, grid.q_blk_total, grid.kb_tot, dtype=torch.int32, device=dev)
+    nvalid = torch.empty(grid.BH, grid.q_blk_total, dtype=torch.int32, device=dev)
+    # dense rows first via an empty selection, then the map rows
+    _lib.call("ress_select_blocks", None, None, grid.BH, 0, grid.q_blk_total, grid.n_cand, grid.kb_tot, 0, 0, None,
+              _lib.ptr(lut), _lib.ptr(nvalid), _lib.stream_handle(dev))
+    if grid.q_blk_p:
+        lut_p = torch.empty(grid.BH, grid.q_blk_p, grid.kb_tot, dtype=torch.int32, device=dev)
+        nv_p = torch.empty(grid.BH, grid.q_blk_p, dtype=torch.int32, device=dev)
+        _lib.call("ress_block_map_lut", _lib.ptr(m), grid.BH * grid.q_blk_p, grid.kb_tot, _lib.ptr(lut_p),
+                  _lib.ptr(nv_p), _lib.stream_handle(dev))
+        lut[:, :grid.q_blk_p] = lut_p
+        nvalid[:, :grid.q_blk_p] = nv_p
+    return lut, nvalid
+
+
+def sparse_attention(blocks, lut, nvalid, out=None, out_dtype=torch.float32):
+    """Block-sparse attention over the prepared blocks; returns (B,H,frames*P,64) in
+    storage order (patch rows sparse, special rows dense)."""
+    g = blocks.grid
+    dev = blocks.q_i8.device
+    if out is None:
+        out = torch.empty(g.B, g.H, g.Tk, HEAD_DIM, dtype=out_dtype, device=dev)
+    code = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[out.dtype]
+    _lib.call("ress_sparse_attn_fwd", _lib.ptr(blocks.q_i8), _lib.ptr(blocks.q_scale), _lib.ptr(blocks.k_i8),
+              _lib.ptr(blocks.k_scale), _lib.ptr(blocks.v_pack), 0, _lib.ptr(lut), _lib.ptr(nvalid), g.B, g.H,
+              g.frames, g.P, g.S, 1.0 / math.sqrt(HEAD_DIM), _lib.ptr(out), code, *out.stride()[:3],
+              _lib.stream_handle(dev))
+    return out

@@ -1,0 +1,74 @@
+"""Q/K/V projection, qk-norm and RoPE for a VGGT-family attention module, and the
+output projection (reference src/ress/models/qkv.py:25-87, tokens.py:8-52).
+
+Unlike the reference, Q/K/V stay in storage order (B, nh, frames*P, hd): the patch /
+special split happens inside the GPU preparation pass (no `.contiguous()` copies), and
+the attention kernel writes its output back in storage order.
+"""
+
+import torch
+
+
+def grid_shape(x, pos, num_special_tokens=5, num_heads=16, shape=None):
+    """(B, N frames, P tokens/frame, H, W, S, hd) of one global-attention input
+    (reference qkv.py:44-58: H/W from the +1-shifted positions, or an explicit
+    {"N","H","W"} override)."""
+    B, NP, dim = x.shape
+    S = num_special_tokens
+    if shape is not None:
+        H, W, N = shape["H"], shape["W"], shape["N"]
+    else:
+        H = int(pos[0].max(0).values[0])
+        W = int(pos[0].max(0).values[1])
+        N = NP // (H * W + S)
+    P = H * W + S
+    if N * P != NP:
+        raise AssertionError(f"token split mismatch: N={N} x P={P} (= H*W+S = {H}*{W}+{S}) != {NP} tokens")
+    return {"B": B, "N": N, "P": P, "head_dim": dim // num_heads, "num_heads": num_heads, "H": H, "W": W, "S": S}
+
+
+def compute_qkv(self, x, pos, num_special_tokens=5, num_heads=16, shape=None):
+    """(q, k, v, shape): each (B, nh, N*P, hd) in storage order, after q_norm/k_norm and
+    RoPE -- reference qkv.py:60-68 without the split."""
+    shp = grid_shape(x, pos, num_special_tokens, num_heads, shape)
+    B, NP, _ = x.shape
+    nh, hd = shp["num_heads"], shp["head_dim"]
+    qkv = self.qkv(x).reshape(B, NP, 3, nh, hd).permute(2, 0, 3, 1, 4)
+    q, k, v = qkv.unbind(0)
+    q, k = self.q_norm(q), self.k_norm(k)
+    if getattr(self, "rope", None) is not None:
+        q = self.rope(q, pos)
+        k = self.rope(k, pos)
+    return q, k, v, shp
+
+
+def get_patch_tokens(x, N, P, S):
+    """(..., N*P, C) -> (..., N*(P-S), C) patch tokens, frame-major (reference tokens.py:8-30)."""
+    assert x.shape[-2] == N * P
+    lead, C = x.shape[:-2], x.shape[-1]
+    return x.view(*lead, N, P, C)[..., S:, :].reshape(*lead, N * (P - S), C)
+
+
+def get_special_tokens(x, N, P, S):
+    """(..., N*P, C) -> (..., N*S, C) special tokens or None (reference tokens.py:33-52)."""
+    assert x.shape[-2] == N * P
+    if S == 0:
+        return None
+    lead, C = x.shape[:-2], x.shape[-1]
+    return x.view(*lead, N, P, C)[..., :S, :].reshape(*lead, N * S, C)
+
+
+def combine_special_and_patch(x_special, x_patch, shape):
+    """Inverse split (reference qkv.py:71-81): (B,nh,N*S,hd) + (B,nh,N*(P-S),hd) ->
+    (B,nh,N*P,hd)."""
+    B, N, P, hd, nh, S = (shape[k] for k in ("B", "N", "P", "head_dim", "num_heads", "S"))
+    xp = x_patch.reshape(B, nh, N, P - S, hd)
+    x = xp if x_special is None else torch.cat([x_special.reshape(B, nh, N, S, hd), xp], dim=-2)
+    return x.reshape(B, nh, N * P, hd)
+
+
+def project_out(self, x, B, N, P, nh, hd):
+    """W_O projection (reference qkv.py:84-87)."""
+    x = x.transpose(1, 2).reshape(B, N * P, nh * hd)
+    x = self.proj(x)
+    return self.proj_drop(x)

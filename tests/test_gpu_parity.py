@@ -1,0 +1,219 @@
+"""GPU parity: every HIP stage against the CPU oracle on the same inputs.
+
+Block maps, budgets, LUTs, INT8 codes, scales and pooled values are compared bit for
+bit; the attention output against the fp32 block-masked softmax reference with
+max-abs <= 2e-2 and cosine >= 0.999."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import reference as ref
+from pipeline_oracle import oracle_layer, row_sample
+from ress_amd import budget, kernels, synth
+from ress_amd.attention import sparse_global_attention
+from ress_amd.kernels import LayerGrid
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-2
+MIN_COS = 0.999
+
+
+def _np(t):
+    t = t.detach().cpu()
+    if t.dtype == torch.bfloat16:
+        return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def _bits_equal(a, b):
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    assert a.shape == b.shape, (a.shape, b.shape)
+    if a.dtype == np.float32:
+        return np.array_equal(a.view(np.uint32), b.astype(np.float32).view(np.uint32))
+    return np.array_equal(a, b)
+
+
+def _rand_layer(frames, P, S, H, seed):
+    g = torch.Generator().manual_seed(seed)
+    mk = lambda s: torch.randn(1, H, frames * P, 64, generator=g).mul(s).to(torch.bfloat16)  # noqa: E731
+    return mk(1.0), mk(1.3), mk(0.7)
+
+
+SHAPES = [
+    ("vggt_f4", None),            # BASELINE configs[0] geometry, synthetic field
+    ("ragged", (3, 203, 5, 2)),   # partial q/k blocks, straddling special block
+    ("plain", (1, 320, 0, 3)),    # no special tokens
+    ("tiny", (2, 40, 5, 1)),      # fewer tokens than one q block
+]
+
+
+@pytest.fixture(scope="module", params=SHAPES, ids=[s[0] for s in SHAPES])
+def layer(request, dev):
+    name, spec = request.param
+    if spec is None:
+        q, k, v, meta = synth.make_layer_qkv(4)
+        frames, P, S, H = meta["frames"], meta["P"], meta["S"], 16
+    else:
+        frames, P, S, H = spec
+        q, k, v = _rand_layer(frames, P, S, H, seed=len(name))
+    print(f"[layer {name}] frames={frames} P={P} S={S} H={H}", flush=True)
+    return name, q, k, v, frames, P, S, H
+
+
+def test_prep_bit_exact(layer, dev):
+    name, q, k, v, frames, P, S, H = layer
+    g = LayerGrid(1, H, frames, P, S)
+    blocks = kernels.prepare_blocks(q.to(dev), k.to(dev), v.to(dev), g)
+    torch.cuda.synchronize()
+    o = oracle.prep_qkv(q, k, v, frames, P, S)
+    for field in ("q_i8", "q_scale", "pooled_q", "k_i8", "k_scale", "pooled_k", "pooled_v", "ksum", "km"):
+        assert _bits_equal(_np(getattr(blocks, field)), o[field]), field
+    assert _bits_equal(_np(blocks.v_pack), o["v_pack"])
+
+
+def test_pooled_scores_bit_exact(layer, dev):
+    name, q, k, v, frames, P, S, H = layer
+    g = LayerGrid(1, H, frames, P, S)
+    blocks = kernels.prepare_blocks(q.to(dev), k.to(dev), v.to(dev), g)
+    full, cond = kernels.pooled_scores(blocks)
+    o = oracle.prep_qkv(q, k, v, frames, P, S)
+    ofull, ocond = oracle.pooled_scores(o["pooled_q"], o["pooled_k"], g.n_cand)
+    assert _bits_equal(_np(full).reshape(ofull.shape), ofull)
+    assert _bits_equal(_np(cond).reshape(ocond.shape), ocond)
+
+
+@pytest.mark.parametrize("sr,cdf", [(0.5, 0.9), (None, 0.9), (0.7, None), (0.2, 0.5)])
+def test_baseline_budget_bit_exact(sr, cdf, dev):
+    rng = np.random.default_rng(7)
+    a = rng.dirichlet(np.full(342, 0.2), size=(1, 16, 40)).astype(np.float32)
+    a[0, 0, 0] = np.float32(1 / 342)
+    got = budget.compute_baseline_num_to_select(torch.from_numpy(a).to(dev), sr, cdf)
+    want = oracle.baseline_budget(a, sr, cdf)
+    assert np.array_equal(_np(got), want)
+
+
+def test_head_budget_bit_exact(dev):
+    rng = np.random.default_rng(8)
+    cam, pc = synth.make_hess_tables()
+    hb = budget.HessBudget(cam, pc, lam=0.5)
+    for layer_idx in (0, 5, 23):
+        base = rng.integers(0, 342, size=(1, 16, 50)).astype(np.int32)
+        base[0, 3] = 340  # force caps
+        got = kernels.head_budget(torch.from_numpy(base).to(dev), hb._scores_norm(layer_idx, dev), 1.0, 342)
+        want, it = oracle.head_budget(base, oracle.scores_norm_seq(hb.head_scores[layer_idx].numpy()), 1.0, 342)
+        assert it >= 0
+        assert np.array_equal(_np(got), want)
+    # host-side normalisation equals the oracle's
+    assert np.array_equal(budget.scores_norm(hb.head_scores[3]), oracle.scores_norm_seq(hb.head_scores[3].numpy()))
+
+
+def test_head_budget_non_convergence_is_reported(dev):
+    base = torch.full((1, 4, 1), 50, dtype=torch.int32, device=dev)
+    with pytest.raises(RuntimeError, match="did not converge"):
+        budget.adjust_attention_selection(base, torch.tensor([8.0, 1.0, 1.0, 1.0]), 1.0, 60, max_iters=1, check=True)
+    out = budget.adjust_attention_selection(base, torch.tensor([8.0, 1.0, 1.0, 1.0]), 1.0, 60, check=True)
+    want, _ = oracle.head_budget(np.full((1, 4, 1), 50, np.int32), oracle.scores_norm_seq(np.array([8, 1, 1, 1.0])),
+                                 1.0, 60)
+    assert np.array_equal(_np(out), want)
+
+
+@pytest.mark.parametrize("n_cand,kb_tot,sink_lead", [(342, 344, 0), (85, 86, 0), (64, 64, 5), (1, 3, 0), (700, 710, 22)])
+def test_select_bit_exact_with_ties(n_cand, kb_tot, sink_lead, dev):
+    rng = np.random.default_rng(n_cand)
+    BH, q_sel, q_tot = 4, 11, 12
+    keys = rng.integers(0, 7, size=(BH, q_sel, n_cand)).astype(np.float32) * np.float32(0.125)
+    keys[0, 1] = rng.random(n_cand).astype(np.float32)
+    counts = rng.integers(-2, n_cand + 3, size=(BH, q_sel)).astype(np.int32)
+    counts[0, :3] = [0, 1, n_cand]
+    g = LayerGrid(1, BH, 1, 64, 0)  # only BH / shapes are used below
+    dev_keys = torch.from_numpy(keys).to(dev)
+    fmap = torch.empty(BH, q_sel, kb_tot, dtype=torch.uint8, device=dev)
+    lut = torch.empty(BH, q_tot, kb_tot, dtype=torch.int32, device=dev)
+    nv = torch.empty(BH, q_tot, dtype=torch.int32, device=dev)
+    from ress_amd import _lib
+    _lib.call("ress_select_blocks", _lib.ptr(dev_keys), _lib.ptr(torch.from_numpy(counts).to(dev)), BH, q_sel, q_tot,
+              n_cand, kb_tot, sink_lead, 2, _lib.ptr(fmap), _lib.ptr(lut), _lib.ptr(nv), _lib.stream_handle(dev))
+    omap, olut, onv = oracle.select_blocks(keys, counts, q_tot, kb_tot, sink_lead=sink_lead, min_select=2)
+    assert np.array_equal(_np(fmap), omap)
+    assert np.array_equal(_np(nv), onv)
+    l = _np(lut)
+    for b in range(BH):
+        for r in range(q_tot):
+            assert np.array_equal(l[b, r, :onv[b, r]], olut[b, r, :onv[b, r]])
+    del g
+
+
+def _check_attention(out, q, k, v, frames, P, S, lut, nvalid, rows):
+    o = out.float().cpu()
+    refs = ref.masked_attention_rows(q, k, v, frames, P, S, lut, nvalid, rows)
+    worst, cos_min = 0.0, 1.0
+    for (bh, qb), (tok, r) in refs.items():
+        got = o.reshape(-1, o.shape[2], 64)[bh, torch.from_numpy(tok)]
+        err = (got - r).abs().max().item()
+        cos = torch.nn.functional.cosine_similarity(got.flatten(), r.flatten(), dim=0).item()
+        worst, cos_min = max(worst, err), min(cos_min, cos)
+    assert worst <= ATOL, worst
+    assert cos_min >= MIN_COS, cos_min
+    return worst, cos_min
+
+
+def test_attention_matches_fp32_masked_softmax(layer, dev):
+    name, q, k, v, frames, P, S, H = layer
+    g = LayerGrid(1, H, frames, P, S)
+    o = oracle_layer(q, k, v, frames, P, S, sparse_ratio=0.5, cdf_threshold=0.9, H=H)
+    blocks = kernels.prepare_blocks(q.to(dev), k.to(dev), v.to(dev), g)
+    lut = torch.from_numpy(o["lut"].reshape(g.BH, g.q_blk_total, g.kb_tot)).to(dev)
+    nv = torch.from_numpy(o["nvalid"]).to(dev)
+    out = kernels.sparse_attention(blocks, lut, nv)
+    torch.cuda.synchronize()
+    rows = row_sample(o["nvalid"], 12 if name == "vggt_f4" else 30)
+    w, c = _check_attention(out, q, k, v, frames, P, S, o["lut"], o["nvalid"], rows)
+    print(f"[{name}] attention max-abs {w:.3e} min-cos {c:.6f}")
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+def test_attention_low_precision_outputs(out_dtype, dev):
+    frames, P, S, H = 2, 200, 4, 2
+    q, k, v = _rand_layer(frames, P, S, H, seed=11)
+    g = LayerGrid(1, H, frames, P, S)
+    o = oracle_layer(q, k, v, frames, P, S, sparse_ratio=0.5, H=H)
+    blocks = kernels.prepare_blocks(q.to(dev), k.to(dev), v.to(dev), g)
+    lut = torch.from_numpy(o["lut"]).to(dev)
+    nv = torch.from_numpy(o["nvalid"]).to(dev)
+    out32 = kernels.sparse_attention(blocks, lut, nv)
+    out = kernels.sparse_attention(blocks, lut, nv, out_dtype=out_dtype)
+    assert out.dtype == out_dtype
+    assert torch.allclose(out.float(), out32.to(out_dtype).float(), rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("cfg", ["sparse_vggt_f4", "hess_f16"])
+def test_layer_pipeline_matches_oracle(cfg, dev):
+    if cfg == "sparse_vggt_f4":
+        frames, sr, cdf, hess = 4, 0.5, 0.9, False
+    else:
+        frames, sr, cdf, hess = 16, 0.7, None, True
+    q, k, v, meta = synth.make_layer_qkv(frames)
+    P, S = meta["P"], meta["S"]
+    g = LayerGrid(1, 16, frames, P, S)
+    if hess:
+        cam, pc = synth.make_hess_tables()
+        bud = budget.HessBudget(cam, pc, lam=0.5)
+        head_scores = bud.head_scores[0].numpy()
+    else:
+        bud = budget.UniformBudget()
+        head_scores = None
+    res = sparse_global_attention(q.to(dev), k.to(dev), v.to(dev), g,
+                                  budget_fn=lambda a: bud.num_to_select(0, a, sr, cdf, 1.0), keep_intermediates=True)
+    torch.cuda.synchronize()
+    o = oracle_layer(q, k, v, frames, P, S, sparse_ratio=sr, cdf_threshold=cdf, head_scores=head_scores)
+    assert np.array_equal(_np(res.counts).reshape(o["counts"].shape), o["counts"])
+    assert np.array_equal(_np(res.final_map).reshape(o["map"].shape), o["map"])
+    assert np.array_equal(_np(res.nvalid), o["nvalid"])
+    sparsity = res.sparsity()
+    print(f"[{cfg}] realized sparsity {sparsity:.4f}")
+    rows = row_sample(o["nvalid"], 10)
+    w, c = _check_attention(res.out, q, k, v, frames, P, S, o["lut"], o["nvalid"], rows)
+    print(f"[{cfg}] attention max-abs {w:.3e} min-cos {c:.6f}")

@@ -1,0 +1,68 @@
+"""The C-ABI library loads and exports every entry point include/ress_hip.h declares, with
+the argument counts the ctypes binding uses. CPU only (no kernel is launched)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from ress_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ress_hip.h")
+
+
+def _declarations():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"^\s*(?:const\s+)?[a-z ]+\*?\s*(ress_\w+)\s*\(([^;]*?)\)\s*;", text, flags=re.M | re.S):
+        args = m.group(2).strip()
+        decls[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return decls
+
+
+@pytest.fixture(scope="module")
+def library():
+    if not os.path.exists(_lib.LIB_PATH):
+        from ress_amd.build import build_library
+        build_library()
+    return _lib.lib()
+
+
+def test_header_declares_entry_points():
+    decls = _declarations()
+    assert len(decls) >= 14
+    assert "ress_sparse_attn_fwd" in decls and "ress_qattn_block_sparse_fwd" in decls
+
+
+def test_every_declared_symbol_is_exported(library):
+    for name in _declarations():
+        assert hasattr(library, name), name
+        assert isinstance(getattr(library, name), ctypes._CFuncPtr)
+
+
+def test_binding_argument_counts_match_header(library):
+    decls = _declarations()
+    for name, sig in _lib._SIGS.items():
+        assert name in decls, f"{name} bound but not declared"
+        assert len(sig) == decls[name], (name, len(sig), decls[name])
+    assert set(_lib.exported_symbols()) == set(decls)
+
+
+def test_abi_version_and_error_string(library):
+    assert library.ress_abi_version() == 1
+    assert isinstance(library.ress_last_error(), bytes)
+
+
+def test_argument_validation_without_a_gpu(library):
+    # bad geometry is rejected on the host before any launch
+    rc = library.ress_pooled_scores(None, None, 0, 0, 0, 0, ctypes.c_float(0.125), None, None, None)
+    assert rc == -1
+    assert b"bad geometry" in library.ress_last_error()
+    rc = library.ress_baseline_budget(None, 4, 10, ctypes.c_float(-1.0), -1, None, None)
+    assert rc == -1 and b"at least one" in library.ress_last_error()
+    rc = library.ress_qattn_block_sparse_fwd(*([None] * 3), 0, None, 0, None, None, None, None, None, 1, 1, 128, 64,
+                                             0, 0, 0, 0, 0, 0, 0, 0, 1, ctypes.c_float(0.125), 0, None, 0, None)
+    assert rc == -1 and b"tensor_layout" in library.ress_last_error()
