@@ -35,12 +35,14 @@ int ress_abi_version(void);
  *   pooled_q [BH][qb_p][64] f32                 qb_p = ceil(T_p/128), qb_s = ceil(T_s/128)
  *   k_i8 [BH][kb_tot][64][64] int8, k_scale [BH][kb_tot] f32   kb_tot = ceil(frames*P/64)
  *   pooled_k, pooled_v [BH][kb_p][64] f32       kb_p = ceil(T_p/64) (patch keys only)
- *   v_pack [BH][kb_tot][4096] bf16, ksum [BH][kb_tot][64] f32, km [BH][64] f32 */
+ *   v_pack [BH][kb_tot][4096] bf16, ksum [BH][kb_tot][64] f32, km [BH][64] f32
+ *   q_lo / k_lo (optional, layouts of q_i8 / k_i8): split-INT8 residual codes, x ~
+ *   scale*hi + scale/254*lo, used by ress_sparse_attn_fwd for a two-term INT8 QK^T. */
 int ress_prep_qkv(const void* q, const void* k, const void* v, int B, int H, int frames, int P, int S,
                   long long sqB, long long sqH, long long sqT, long long skB, long long skH, long long skT,
-                  long long svB, long long svH, long long svT, void* q_i8, void* q_scale, void* pooled_q,
-                  void* k_i8, void* k_scale, void* pooled_k, void* pooled_v, void* v_pack, void* ksum,
-                  void* km, hipStream_t stream);
+                  long long svB, long long svH, long long svT, void* q_i8, void* q_lo, void* q_scale,
+                  void* pooled_q, void* k_i8, void* k_lo, void* k_scale, void* pooled_k, void* pooled_v,
+                  void* v_pack, void* ksum, void* km, hipStream_t stream);
 
 /* Replaces SpargeAttn per_block_int8(q, k) (call site src/ress/models/attention.py:232,
  * patched Q scale spargeattn.patch:38-41). km [BH][64] optional (NULL = no smoothing).
@@ -107,11 +109,12 @@ int ress_block_map_lut(const void* map, long long rows, int k, void* lut, void* 
 /* Fused-path attention (src/ress/models/attention.py:404-412 special queries dense,
  * :625 run_block_sparse_kernel, :652 combine_special_and_patch): inputs from
  * ress_prep_qkv + ress_select_blocks; out (B,H,frames*P,64) in storage order,
- * out_dtype 0 f32 / 1 bf16 / 2 f16, element strides soB/soH/soT. */
-int ress_sparse_attn_fwd(const void* q_i8, const void* q_scale, const void* k_i8, const void* k_scale,
-                         const void* v_pack, int v_f16, const void* lut, const void* nvalid, int B, int H,
-                         int frames, int P, int S, float sm_scale, void* out, int out_dtype, long long soB,
-                         long long soH, long long soT, hipStream_t stream);
+ * out_dtype 0 f32 / 1 bf16 / 2 f16, element strides soB/soH/soT. q_lo/k_lo both NULL: the
+ * reference's single-term per-block INT8 QK^T; both set: the two-term split product. */
+int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void* q_scale, const void* k_i8,
+                         const void* k_lo, const void* k_scale, const void* v_pack, int v_f16, const void* lut,
+                         const void* nvalid, int B, int H, int frames, int P, int S, float sm_scale, void* out,
+                         int out_dtype, long long soB, long long soH, long long soT, hipStream_t stream);
 
 /* Replaces SpargeAttn qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold
  * (call src/ress/models/attention.py:238-241) with the same argument meaning; see

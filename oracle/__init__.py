@@ -69,9 +69,11 @@ def prep_qkv(q, k, v, frames, P, S):
     kbt, kbp = -(-N // 64), -(-T_p // 64)
     out = dict(
         q_i8=np.zeros((BH, qbp + qbs, 128, 64), np.int8),
+        q_lo=np.zeros((BH, qbp + qbs, 128, 64), np.int8),
         q_scale=np.zeros((BH, qbp + qbs), np.float32),
         pooled_q=np.zeros((BH, qbp, 64), np.float32),
         k_i8=np.zeros((BH, kbt, 64, 64), np.int8),
+        k_lo=np.zeros((BH, kbt, 64, 64), np.int8),
         k_scale=np.zeros((BH, kbt), np.float32),
         pooled_k=np.zeros((BH, kbp, 64), np.float32),
         pooled_v=np.zeros((BH, kbp, 64), np.float32),
@@ -80,7 +82,8 @@ def prep_qkv(q, k, v, frames, P, S):
         km=np.zeros((BH, 64), np.float32),
     )
     lib().oracle_prep_qkv(_p(qu), _p(ku), _p(vu), BH, frames, P, S, *[_p(out[n]) for n in (
-        "q_i8", "q_scale", "pooled_q", "k_i8", "k_scale", "pooled_k", "pooled_v", "v_pack", "ksum", "km")])
+        "q_i8", "q_lo", "q_scale", "pooled_q", "k_i8", "k_lo", "k_scale", "pooled_k", "pooled_v", "v_pack", "ksum",
+        "km")])
     return out
 
 

@@ -101,6 +101,11 @@ static inline int8_t quant(float x, float scale) {
   y = y + (y >= 0.0f ? 0.5f : -0.5f);
   return (int8_t)(int)y;
 }
+/* split-INT8 residual code: x ~ scale*hi + (scale/254)*lo, residual fmaf(-scale, hi, x) */
+static inline int8_t quant_lo(float x, float scale, int8_t hi) {
+  if (scale == 0.0f) return 0;
+  return quant(fmaf(-scale, (float)hi, x), scale / 254.0f);
+}
 
 /* ---- preparation ------------------------------------------------------------------
  * Follows src/ress/models/qkv.py:60-68 + tokens.py:8-52 (patch/special split, kernel
@@ -110,8 +115,8 @@ static inline int8_t quant(float x, float scale) {
  * per_block_int8(q, k - km) (attention.py:231-233), all in fp32.
  * q,k,v: (BH, frames*P, 64) bf16. Output layouts as ress_prep_qkv (include/ress_hip.h). */
 void oracle_prep_qkv(const uint16_t* q, const uint16_t* k, const uint16_t* v, int BH, int frames, int P, int S,
-                     int8_t* q_i8, float* q_scale, float* pooled_q, int8_t* k_i8, float* k_scale, float* pooled_k,
-                     float* pooled_v, uint16_t* v_pack, float* ksum, float* km) {
+                     int8_t* q_i8, int8_t* q_lo, float* q_scale, float* pooled_q, int8_t* k_i8, int8_t* k_lo,
+                     float* k_scale, float* pooled_k, float* pooled_v, uint16_t* v_pack, float* ksum, float* km) {
   tokmap m = mkmap(frames, P, S);
   const int N = frames * P, Tk = N;
   const int qbp = cdiv(m.T_p, 128), qbs = cdiv(m.T_s, 128), qbt = qbp + qbs;
@@ -136,9 +141,13 @@ void oracle_prep_qkv(const uint16_t* q, const uint16_t* k, const uint16_t* v, in
         for (int d = 0; d < 64; ++d)
           pooled_q[((long long)bh * qbp + qb) * 64 + d] = sum8x(qh, rows, cnt, d) / (float)cnt;
       int8_t* dst = q_i8 + ((long long)bh * qbt + qb) * 128 * 64;
+      int8_t* dlo = q_lo + ((long long)bh * qbt + qb) * 128 * 64;
       for (int t = 0; t < 128; ++t)
-        for (int d = 0; d < 64; ++d)
-          dst[t * 64 + d] = t < cnt ? quant(bf16f(qh[(long long)rows[t] * 64 + d]), scale) : 0;
+        for (int d = 0; d < 64; ++d) {
+          const float x = t < cnt ? bf16f(qh[(long long)rows[t] * 64 + d]) : 0.0f;
+          dst[t * 64 + d] = quant(x, scale);
+          dlo[t * 64 + d] = quant_lo(x, scale, dst[t * 64 + d]);
+        }
     }
     /* K/V blocks over the kernel key grid */
     for (int kb = 0; kb < kbt; ++kb) {
@@ -180,10 +189,14 @@ void oracle_prep_qkv(const uint16_t* q, const uint16_t* k, const uint16_t* v, in
       const float scale = amax / 127.0f;
       k_scale[(long long)bh * kbt + kb] = scale;
       int8_t* dst = k_i8 + ((long long)bh * kbt + kb) * 4096;
+      int8_t* dlo = k_lo + ((long long)bh * kbt + kb) * 4096;
       for (int t = 0; t < 64; ++t) {
         const int r = t < cnt ? key_st(base + t, &m) : 0;
-        for (int d = 0; d < 64; ++d)
-          dst[t * 64 + d] = t < cnt ? quant(bf16f(kh[(long long)r * 64 + d]) - km[(long long)bh * 64 + d], scale) : 0;
+        for (int d = 0; d < 64; ++d) {
+          const float x = t < cnt ? bf16f(kh[(long long)r * 64 + d]) - km[(long long)bh * 64 + d] : 0.0f;
+          dst[t * 64 + d] = quant(x, scale);
+          dlo[t * 64 + d] = quant_lo(x, scale, dst[t * 64 + d]);
+        }
       }
     }
   }

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(_HERE, "libress_hip.so")
 
 # argument codes: p = pointer, i = int, l = long long, f = float, d = double, s = stream
 _SIGS = {
-    "ress_prep_qkv": "pppiiiii" + "lllllllll" + "pppppppppp" + "s",
+    "ress_prep_qkv": "pppiiiii" + "lllllllll" + "pppppppppppp" + "s",
     "ress_per_block_int8": "pppiiii" + "llllll" + "ppppp" + "s",
     "ress_prep_kv_plain": "ppiii" + "llllll" + "ppppp" + "s",
     "ress_pooled_scores": "ppiiiifpp" + "s",
@@ -24,7 +24,7 @@ _SIGS = {
     "ress_select_blocks": "ppiiiiiiippp" + "s",
     "ress_fill_block_map": "ppplI" + "s",
     "ress_block_map_lut": "plipp" + "s",
-    "ress_sparse_attn_fwd": "pppppippiiiiifpillls",
+    "ress_sparse_attn_fwd": "pppppppippiiiiifpillls",
     "ress_qattn_block_sparse_fwd": "pppipipppppiiiilllllliiifipls",
 }
 _CT = {

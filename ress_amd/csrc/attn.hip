@@ -28,6 +28,8 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
 struct AttnArgs {
   const int8_t* q_i8;      // [BH][q_blk_total][128][64]
+  const int8_t* q_lo;      // split-INT8 residual codes (same layout) or null
+  const int8_t* k_lo;      // split-INT8 residual codes [BH][kb_tot][64][64] or null
   const float* q_scale;    // [BH][q_blk_total]
   const int8_t* k_i8;      // [BH][kb_tot][64][64]
   const float* k_scale;    // [BH][kb_tot]
@@ -64,9 +66,13 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   }
 }
 
-template <bool V_F16, int OUT>
+// SPLIT: two-term INT8 Q and K (x ~ s*hi + s/254*lo). S = 254*(Qhi.Khi) + (Qhi.Klo + Qlo.Khi)
+// in int32 (the lo.lo term, below 2^-16 relative, is dropped), 3 INT8 MFMAs per tile.
+template <bool SPLIT, bool V_F16, int OUT>
 __global__ __launch_bounds__(256, 2) void k_sparse_attn(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint4 smem[2][768];  // per stage: K 4 KiB + V 8 KiB
+  constexpr int KCH = SPLIT ? 512 : 256;  // 16-byte chunks of K per stage (hi [+ lo])
+  constexpr int STAGE = KCH + 512;        // + V 8 KiB
+  __shared__ __attribute__((aligned(16))) uint4 smem[2][STAGE];
 
   // ---- XCD-major work mapping -------------------------------------------
   const int x = blockIdx.x;
@@ -93,9 +99,16 @@ __global__ __launch_bounds__(256, 2) void k_sparse_attn(AttnArgs a) {
   const int8_t* qsrc = a.q_i8 + (row * 128 + 32 * w + qi) * 64 + 16 * g;
   const v4i qa0 = *reinterpret_cast<const v4i*>(qsrc);
   const v4i qa1 = *reinterpret_cast<const v4i*>(qsrc + 32);
-  const float qs = a.q_scale[row] * a.sm_scale_log2e;
+  v4i ql0, ql1;
+  if constexpr (SPLIT) {
+    const int8_t* qlsrc = a.q_lo + (row * 128 + 32 * w + qi) * 64 + 16 * g;
+    ql0 = *reinterpret_cast<const v4i*>(qlsrc);
+    ql1 = *reinterpret_cast<const v4i*>(qlsrc + 32);
+  }
+  const float qs = a.q_scale[row] * a.sm_scale_log2e * (SPLIT ? (1.0f / 254.0f) : 1.0f);
   const float* ksc = a.k_scale + (long long)bh * a.kb_tot;
   const uint4* kbase_p = reinterpret_cast<const uint4*>(a.k_i8 + (long long)bh * a.kb_tot * 4096);
+  const uint4* klbase_p = SPLIT ? reinterpret_cast<const uint4*>(a.k_lo + (long long)bh * a.kb_tot * 4096) : nullptr;
   const uint4* vbase_p = reinterpret_cast<const uint4*>(a.v_pack + (long long)bh * a.kb_tot * 4096);
 
   float m_run = -__builtin_huge_valf(), l_run = 0.0f;
@@ -103,15 +116,17 @@ __global__ __launch_bounds__(256, 2) void k_sparse_attn(AttnArgs a) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) o0[r] = o1[r] = 0.0f;
 
-  uint4 r0, r1, r2;
+  uint4 r0, r1, r2, r3;
   if (nv > 0) {
     const int kb = lut[0];
     r0 = kbase_p[(long long)kb * 256 + tid];
+    if constexpr (SPLIT) r3 = klbase_p[(long long)kb * 256 + tid];
     r1 = vbase_p[(long long)kb * 512 + tid];
     r2 = vbase_p[(long long)kb * 512 + 256 + tid];
     smem[0][tid] = r0;
-    smem[0][256 + tid] = r1;
-    smem[0][512 + tid] = r2;
+    if constexpr (SPLIT) smem[0][256 + tid] = r3;
+    smem[0][KCH + tid] = r1;
+    smem[0][KCH + 256 + tid] = r2;
   }
   __syncthreads();
 
@@ -122,11 +137,13 @@ __global__ __launch_bounds__(256, 2) void k_sparse_attn(AttnArgs a) {
     if (more) {
       const int kn = lut[it + 1];
       r0 = kbase_p[(long long)kn * 256 + tid];
+      if constexpr (SPLIT) r3 = klbase_p[(long long)kn * 256 + tid];
       r1 = vbase_p[(long long)kn * 512 + tid];
       r2 = vbase_p[(long long)kn * 512 + 256 + tid];
     }
     const int8_t* sk = reinterpret_cast<const int8_t*>(&smem[buf][0]);
-    const uint16_t* sv = reinterpret_cast<const uint16_t*>(&smem[buf][256]);
+    const int8_t* skl = sk + 4096;
+    const uint16_t* sv = reinterpret_cast<const uint16_t*>(&smem[buf][KCH]);
 
     // ---- S^T = K . Q^T --------------------------------------------------
     v16i s0, s1;
@@ -141,6 +158,28 @@ __global__ __launch_bounds__(256, 2) void k_sparse_attn(AttnArgs a) {
       s0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k01, qa1, s0, 0, 0, 0);
       s1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k10, qa0, s1, 0, 0, 0);
       s1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k11, qa1, s1, 0, 0, 0);
+      if constexpr (SPLIT) {
+        v16i b0, b1;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) b0[r] = b1[r] = 0;
+        const v4i l00 = *reinterpret_cast<const v4i*>(skl + qi * 64 + 16 * g);
+        const v4i l01 = *reinterpret_cast<const v4i*>(skl + qi * 64 + 32 + 16 * g);
+        const v4i l10 = *reinterpret_cast<const v4i*>(skl + (32 + qi) * 64 + 16 * g);
+        const v4i l11 = *reinterpret_cast<const v4i*>(skl + (32 + qi) * 64 + 32 + 16 * g);
+        b0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k00, ql0, b0, 0, 0, 0);
+        b0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k01, ql1, b0, 0, 0, 0);
+        b0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(l00, qa0, b0, 0, 0, 0);
+        b0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(l01, qa1, b0, 0, 0, 0);
+        b1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k10, ql0, b1, 0, 0, 0);
+        b1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k11, ql1, b1, 0, 0, 0);
+        b1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(l10, qa0, b1, 0, 0, 0);
+        b1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(l11, qa1, b1, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          s0[r] = s0[r] * 254 + b0[r];
+          s1[r] = s1[r] * 254 + b1[r];
+        }
+      }
     }
 
     // ---- online softmax (exp2 domain) -----------------------------------
@@ -194,8 +233,9 @@ __global__ __launch_bounds__(256, 2) void k_sparse_attn(AttnArgs a) {
 
     if (more) {
       smem[buf ^ 1][tid] = r0;
-      smem[buf ^ 1][256 + tid] = r1;
-      smem[buf ^ 1][512 + tid] = r2;
+      if constexpr (SPLIT) smem[buf ^ 1][256 + tid] = r3;
+      smem[buf ^ 1][KCH + tid] = r1;
+      smem[buf ^ 1][KCH + 256 + tid] = r2;
     }
     __syncthreads();
   }
@@ -260,31 +300,36 @@ __global__ __launch_bounds__(64) void k_pack_v(const uint16_t* __restrict__ v, l
 // ============================================================================
 // C ABI
 // ============================================================================
-template <bool V_F16>
+template <bool SPLIT, bool V_F16>
 static int launch_attn(const AttnArgs& a, int out_dtype, hipStream_t stream) {
   const int per_xcd = ((a.BH + 7) / 8) * a.q_blk_total;
   const dim3 grid(8 * per_xcd), block(256);
   switch (out_dtype) {
-    case OUT_F32: hipLaunchKernelGGL((k_sparse_attn<V_F16, OUT_F32>), grid, block, 0, stream, a); break;
-    case OUT_BF16: hipLaunchKernelGGL((k_sparse_attn<V_F16, OUT_BF16>), grid, block, 0, stream, a); break;
-    default: hipLaunchKernelGGL((k_sparse_attn<V_F16, OUT_F16>), grid, block, 0, stream, a); break;
+    case OUT_F32: hipLaunchKernelGGL((k_sparse_attn<SPLIT, V_F16, OUT_F32>), grid, block, 0, stream, a); break;
+    case OUT_BF16: hipLaunchKernelGGL((k_sparse_attn<SPLIT, V_F16, OUT_BF16>), grid, block, 0, stream, a); break;
+    default: hipLaunchKernelGGL((k_sparse_attn<SPLIT, V_F16, OUT_F16>), grid, block, 0, stream, a); break;
   }
   RESS_LAUNCHED("k_sparse_attn");
   return 0;
 }
 
-static int attn_common(const void* q_i8, const void* q_scale, const void* k_i8, const void* k_scale, const void* v_pack,
-                       int v_f16, const void* lut, const void* nvalid, int B, int H, TokenMap m, int Tk, float sm_scale,
-                       void* out, int out_dtype, long long soB, long long soH, long long soT, hipStream_t stream) {
+static int attn_common(const void* q_i8, const void* q_lo, const void* q_scale, const void* k_i8, const void* k_lo,
+                       const void* k_scale, const void* v_pack, int v_f16, const void* lut, const void* nvalid, int B,
+                       int H, TokenMap m, int Tk, float sm_scale, void* out, int out_dtype, long long soB,
+                       long long soH, long long soT, hipStream_t stream) {
   RESS_REQUIRE(q_i8 && q_scale && k_i8 && k_scale && v_pack && lut && nvalid && out, "sparse attention: null pointer");
-  RESS_REQUIRE(((uintptr_t)q_i8 & 15u) == 0 && ((uintptr_t)k_i8 & 15u) == 0 && ((uintptr_t)v_pack & 15u) == 0,
-               "sparse attention: q_i8/k_i8/v_pack must be 16-byte aligned");
+  RESS_REQUIRE((q_lo == nullptr) == (k_lo == nullptr), "sparse attention: give both q_lo and k_lo, or neither");
+  RESS_REQUIRE(((uintptr_t)q_i8 & 15u) == 0 && ((uintptr_t)k_i8 & 15u) == 0 && ((uintptr_t)v_pack & 15u) == 0 &&
+                   ((uintptr_t)q_lo & 15u) == 0 && ((uintptr_t)k_lo & 15u) == 0,
+               "sparse attention: q_i8/q_lo/k_i8/k_lo/v_pack must be 16-byte aligned");
   RESS_REQUIRE(out_dtype >= 0 && out_dtype <= 2, "sparse attention: out_dtype must be 0 (f32), 1 (bf16) or 2 (f16)");
   const int align = out_dtype == OUT_F32 ? 16 : 8;
   RESS_REQUIRE(((uintptr_t)out % align) == 0 && soT % 4 == 0 && soH % 4 == 0 && soB % 4 == 0,
                "sparse attention: output must be %d-byte aligned with strides a multiple of 4", align);
   AttnArgs a;
   a.q_i8 = (const int8_t*)q_i8;
+  a.q_lo = (const int8_t*)q_lo;
+  a.k_lo = (const int8_t*)k_lo;
   a.q_scale = (const float*)q_scale;
   a.k_i8 = (const int8_t*)k_i8;
   a.k_scale = (const float*)k_scale;
@@ -303,18 +348,21 @@ static int attn_common(const void* q_i8, const void* q_scale, const void* k_i8, 
   a.Tk = Tk;
   a.sm_scale_log2e = sm_scale * 1.4426950408889634f;
   a.m = m;
-  return v_f16 ? launch_attn<true>(a, out_dtype, stream) : launch_attn<false>(a, out_dtype, stream);
+  if (q_lo) return v_f16 ? launch_attn<true, true>(a, out_dtype, stream) : launch_attn<true, false>(a, out_dtype, stream);
+  return v_f16 ? launch_attn<false, true>(a, out_dtype, stream) : launch_attn<false, false>(a, out_dtype, stream);
 }
 
 // Fused-path attention over the ReSS token split: queries are the patch tokens
 // (q-blocks 0..ceil(T_p/128)-1, sparse LUT rows) then the special tokens (dense
 // rows); keys are cat(patch, special). The output is written in storage order
 // (B,H,frames*P,64) with element strides soB/soH/soT, i.e. the reference's
-// combine_special_and_patch (src/ress/models/qkv.py:71-81) is fused in.
-RESS_API int ress_sparse_attn_fwd(const void* q_i8, const void* q_scale, const void* k_i8, const void* k_scale,
-                                  const void* v_pack, int v_f16, const void* lut, const void* nvalid, int B, int H,
-                                  int frames, int P, int S, float sm_scale, void* out, int out_dtype, long long soB,
-                                  long long soH, long long soT, hipStream_t stream) {
+// combine_special_and_patch (src/ress/models/qkv.py:71-81) is fused in. With q_lo/k_lo
+// (split-INT8 residual codes from ress_prep_qkv) QK^T is evaluated as a two-term INT8
+// product; without them it is the single-term per-block INT8 product of the reference.
+RESS_API int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void* q_scale, const void* k_i8,
+                                  const void* k_lo, const void* k_scale, const void* v_pack, int v_f16, const void* lut,
+                                  const void* nvalid, int B, int H, int frames, int P, int S, float sm_scale, void* out,
+                                  int out_dtype, long long soB, long long soH, long long soT, hipStream_t stream) {
   RESS_REQUIRE(B > 0 && H > 0 && frames > 0 && P > S && S >= 0, "ress_sparse_attn_fwd: bad geometry");
   TokenMap m;
   m.P = P;
@@ -322,8 +370,8 @@ RESS_API int ress_sparse_attn_fwd(const void* q_i8, const void* q_scale, const v
   m.HW = P - S;
   m.T_p = frames * (P - S);
   m.T_s = frames * S;
-  return attn_common(q_i8, q_scale, k_i8, k_scale, v_pack, v_f16, lut, nvalid, B, H, m, frames * P, sm_scale, out,
-                     out_dtype, soB, soH, soT, stream);
+  return attn_common(q_i8, q_lo, q_scale, k_i8, k_lo, k_scale, v_pack, v_f16, lut, nvalid, B, H, m, frames * P,
+                     sm_scale, out, out_dtype, soB, soH, soT, stream);
 }
 
 RESS_API long long ress_qattn_workspace_size(int B, int H, int Tk) {
@@ -371,6 +419,6 @@ RESS_API int ress_qattn_block_sparse_fwd(const void* q_i8, const void* k_i8, con
   m.HW = Tq;
   m.T_p = Tq;
   m.T_s = 0;
-  return attn_common(q_i8, q_scale, k_i8, k_scale, workspace, v_f16, lut, valid_block_num, B, H, m, Tk, sm_scale, o,
-                     o_dtype, soB, soH, soT, stream);
+  return attn_common(q_i8, nullptr, q_scale, k_i8, nullptr, k_scale, workspace, v_f16, lut, valid_block_num, B, H, m,
+                     Tk, sm_scale, o, o_dtype, soB, soH, soT, stream);
 }

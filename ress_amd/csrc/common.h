@@ -140,6 +140,13 @@ __device__ __forceinline__ int quant_i8(float x, float scale) {
   y = y + (y >= 0.0f ? 0.5f : -0.5f);
   return (int)y;
 }
+// Two-term ("split") INT8: x ~ scale*hi + (scale/254)*lo. hi is the per-block code
+// above; lo quantises the exact residual fmaf(-scale, hi, x) (|r| <= scale/2) with the
+// scale scale/254, so |lo| <= 127.
+__device__ __forceinline__ int quant_i8_lo(float x, float scale, int hi) {
+  if (scale == 0.0f) return 0;
+  return quant_i8(fmaf(-scale, (float)hi, x), scale / 254.0f);
+}
 
 // ---- wave reductions (wave64) ---------------------------------------------
 __device__ __forceinline__ float wave_max(float v) {

@@ -13,6 +13,29 @@
 // token lane j = l>>3; a block of T tokens is read in T/8 coalesced 1 KiB rows.
 #include "common.h"
 
+__device__ __forceinline__ uint2 pack_i8x8(const int c[8]) {
+  uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w0 |= ((uint32_t)(c[i] & 0xff)) << (8 * i);
+    w1 |= ((uint32_t)(c[4 + i] & 0xff)) << (8 * i);
+  }
+  return make_uint2(w0, w1);
+}
+
+// hi (and, if lo_dst is set, split lo) codes of 8 values -> two 8-byte stores
+__device__ __forceinline__ void store_codes(const float x[8], float scale, int8_t* hi_dst, int8_t* lo_dst) {
+  int hi[8], lo[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) hi[c] = quant_i8(x[c], scale);
+  *reinterpret_cast<uint2*>(hi_dst) = pack_i8x8(hi);
+  if (lo_dst) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) lo[c] = quant_i8_lo(x[c], scale, hi[c]);
+    *reinterpret_cast<uint2*>(lo_dst) = pack_i8x8(lo);
+  }
+}
+
 struct Strides {  // element strides of a (B, H, T, D) tensor in any layout
   long long b, h, t;
   int H;
@@ -27,7 +50,8 @@ __device__ __forceinline__ long long bh_offset(int bh, const Strides& s) {
 // and, for patch blocks, pooled_q [BH][q_blk_p][64].
 __global__ __launch_bounds__(64) void k_prep_q(const uint16_t* __restrict__ q, Strides sq, TokenMap m,
                                                int q_blk_p, int q_blk_total, int8_t* __restrict__ q_i8,
-                                               float* __restrict__ q_scale, float* __restrict__ pooled_q) {
+                                               int8_t* __restrict__ q_lo, float* __restrict__ q_scale,
+                                               float* __restrict__ pooled_q) {
   const int qb = blockIdx.x, bh = blockIdx.y, lane = threadIdx.x;
   const int j = lane >> 3, dg = lane & 7;
   const bool special = qb >= q_blk_p;
@@ -66,17 +90,13 @@ __global__ __launch_bounds__(64) void k_prep_q(const uint16_t* __restrict__ q, S
     for (int c = 0; c < 8; ++c) pq[c] = acc[c] / (float)cnt;
   }
   if (lane == 0) q_scale[(long long)bh * q_blk_total + qb] = scale;
-  int8_t* dst = q_i8 + (((long long)bh * q_blk_total + qb) * 128) * 64 + dg * 8;
+  const long long off = (((long long)bh * q_blk_total + qb) * 128) * 64 + dg * 8;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     float x[8];
     unpack_bf16x8(raw[i], x);
-    uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) w0 |= ((uint32_t)(quant_i8(x[c], scale) & 0xff)) << (8 * c);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) w1 |= ((uint32_t)(quant_i8(x[4 + c], scale) & 0xff)) << (8 * c);
-    *reinterpret_cast<uint2*>(dst + (8 * i + j) * 64) = make_uint2(w0, w1);
+    const int r = (8 * i + j) * 64;
+    store_codes(x, scale, q_i8 + off + r, q_lo ? q_lo + off + r : nullptr);
   }
 }
 
@@ -177,7 +197,7 @@ __global__ __launch_bounds__(64) void k_key_mean(const float* __restrict__ ksum,
 // k_i8 [BH][kb_tot][64 keys][64], k_scale [BH][kb_tot]. km may be null (no smoothing).
 __global__ __launch_bounds__(64) void k_quant_k(const uint16_t* __restrict__ k, Strides sk, TokenMap m, int Tk,
                                                 int kb_tot, const float* __restrict__ km, int8_t* __restrict__ k_i8,
-                                                float* __restrict__ k_scale) {
+                                                int8_t* __restrict__ k_lo, float* __restrict__ k_scale) {
   const int kb = blockIdx.x, bh = blockIdx.y, lane = threadIdx.x;
   const int j = lane >> 3, dg = lane & 7;
   const int base = kb * 64;
@@ -203,15 +223,11 @@ __global__ __launch_bounds__(64) void k_quant_k(const uint16_t* __restrict__ k, 
   amax = wave_max(amax);
   const float scale = amax / 127.0f;
   if (lane == 0) k_scale[(long long)bh * kb_tot + kb] = scale;
-  int8_t* dst = k_i8 + ((long long)bh * kb_tot + kb) * 4096 + dg * 8;
+  const long long off = ((long long)bh * kb_tot + kb) * 4096 + dg * 8;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) w0 |= ((uint32_t)(quant_i8(x[i][c], scale) & 0xff)) << (8 * c);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) w1 |= ((uint32_t)(quant_i8(x[i][4 + c], scale) & 0xff)) << (8 * c);
-    *reinterpret_cast<uint2*>(dst + (8 * i + j) * 64) = make_uint2(w0, w1);
+    const int r = (8 * i + j) * 64;
+    store_codes(x[i], scale, k_i8 + off + r, k_lo ? k_lo + off + r : nullptr);
   }
 }
 
@@ -232,18 +248,20 @@ static TokenMap make_map(int frames, int P, int S) {
 
 // Fused preparation of one layer's Q/K/V for the ReSS forward (reference
 // attention.py:398-491 + 226-233). Inputs are the backbone's bf16 Q/K/V in storage
-// order with element strides (sB, sH, sT); D = 64 with unit stride.
+// order with element strides (sB, sH, sT); D = 64 with unit stride. q_lo/k_lo (same
+// layouts as q_i8/k_i8) receive the split-INT8 residual codes, or are null.
 RESS_API int ress_prep_qkv(const void* q, const void* k, const void* v, int B, int H, int frames, int P, int S,
                            long long sqB, long long sqH, long long sqT, long long skB, long long skH, long long skT,
-                           long long svB, long long svH, long long svT, void* q_i8, void* q_scale, void* pooled_q,
-                           void* k_i8, void* k_scale, void* pooled_k, void* pooled_v, void* v_pack, void* ksum,
-                           void* km, hipStream_t stream) {
+                           long long svB, long long svH, long long svT, void* q_i8, void* q_lo, void* q_scale,
+                           void* pooled_q, void* k_i8, void* k_lo, void* k_scale, void* pooled_k, void* pooled_v,
+                           void* v_pack, void* ksum, void* km, hipStream_t stream) {
   RESS_REQUIRE(B > 0 && H > 0 && frames > 0 && P > S && S >= 0, "ress_prep_qkv: bad geometry B=%d H=%d F=%d P=%d S=%d",
                B, H, frames, P, S);
   RESS_REQUIRE(q && k && v && q_i8 && q_scale && pooled_q && k_i8 && k_scale && pooled_k && pooled_v && v_pack && ksum &&
                    km,
                "ress_prep_qkv: null pointer");
-  RESS_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(v_pack) && aligned16(q_i8) && aligned16(k_i8),
+  RESS_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(v_pack) && aligned16(q_i8) && aligned16(k_i8) &&
+                   aligned16(q_lo) && aligned16(k_lo),
                "ress_prep_qkv: tensors must be 16-byte aligned");
   RESS_REQUIRE(sqT % 8 == 0 && skT % 8 == 0 && svT % 8 == 0 && sqH % 8 == 0 && skH % 8 == 0 && svH % 8 == 0 &&
                    sqB % 8 == 0 && skB % 8 == 0 && svB % 8 == 0,
@@ -255,7 +273,7 @@ RESS_API int ress_prep_qkv(const void* q, const void* k, const void* v, int B, i
   const int kb_tot = cdiv(Tk, 64), kb_p = cdiv(m.T_p, 64);
   Strides sq{sqB, sqH, sqT, H}, sk{skB, skH, skT, H}, sv{svB, svH, svT, H};
   hipLaunchKernelGGL(k_prep_q, dim3(q_blk_p + q_blk_s, BH), dim3(64), 0, stream, (const uint16_t*)q, sq, m, q_blk_p,
-                     q_blk_p + q_blk_s, (int8_t*)q_i8, (float*)q_scale, (float*)pooled_q);
+                     q_blk_p + q_blk_s, (int8_t*)q_i8, (int8_t*)q_lo, (float*)q_scale, (float*)pooled_q);
   RESS_LAUNCHED("k_prep_q");
   hipLaunchKernelGGL(k_prep_kv, dim3(kb_tot, BH), dim3(64), 0, stream, (const uint16_t*)k, (const uint16_t*)v, sk, sv,
                      m, Tk, kb_tot, kb_p, (float*)ksum, (float*)pooled_k, (float*)pooled_v, (uint16_t*)v_pack);
@@ -263,7 +281,7 @@ RESS_API int ress_prep_qkv(const void* q, const void* k, const void* v, int B, i
   hipLaunchKernelGGL(k_key_mean, dim3(BH), dim3(64), 0, stream, (const float*)ksum, kb_tot, Tk, (float*)km);
   RESS_LAUNCHED("k_key_mean");
   hipLaunchKernelGGL(k_quant_k, dim3(kb_tot, BH), dim3(64), 0, stream, (const uint16_t*)k, sk, m, Tk, kb_tot,
-                     (const float*)km, (int8_t*)k_i8, (float*)k_scale);
+                     (const float*)km, (int8_t*)k_i8, (int8_t*)k_lo, (float*)k_scale);
   RESS_LAUNCHED("k_quant_k");
   return 0;
 }
@@ -289,10 +307,10 @@ RESS_API int ress_per_block_int8(const void* q, const void* k, const void* km, i
   Strides sq{sqB, sqH, sqT, H}, sk{skB, skH, skT, H};
   const int nq = cdiv(Tq, 128), nk = cdiv(Tk, 64);
   hipLaunchKernelGGL(k_prep_q, dim3(nq, BH), dim3(64), 0, stream, (const uint16_t*)q, sq, mq, nq, nq, (int8_t*)q_i8,
-                     (float*)q_scale, (float*)pooled_q);
+                     (int8_t*)nullptr, (float*)q_scale, (float*)pooled_q);
   RESS_LAUNCHED("k_prep_q");
   hipLaunchKernelGGL(k_quant_k, dim3(nk, BH), dim3(64), 0, stream, (const uint16_t*)k, sk, mk, Tk, nk,
-                     (const float*)km, (int8_t*)k_i8, (float*)k_scale);
+                     (const float*)km, (int8_t*)k_i8, (int8_t*)nullptr, (float*)k_scale);
   RESS_LAUNCHED("k_quant_k");
   return 0;
 }

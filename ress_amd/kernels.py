@@ -93,9 +93,11 @@ class Blocks:
 
     grid: LayerGrid
     q_i8: torch.Tensor
+    q_lo: torch.Tensor  # split-INT8 residual codes, or None
     q_scale: torch.Tensor
     pooled_q: torch.Tensor
     k_i8: torch.Tensor
+    k_lo: torch.Tensor
     k_scale: torch.Tensor
     pooled_k: torch.Tensor
     pooled_v: torch.Tensor
@@ -115,8 +117,10 @@ def _check_qkv(t, name, grid):
         raise ValueError(f"{name} must have a unit-stride head dim")
 
 
-def prepare_blocks(q, k, v, grid):
-    """Pool, quantise and pack one layer's Q/K/V (bf16, storage order)."""
+def prepare_blocks(q, k, v, grid, split=True):
+    """Pool, quantise and pack one layer's Q/K/V (bf16, storage order). split=True also
+    writes the split-INT8 residual codes (two-term QK^T in the attention kernel);
+    split=False gives the reference's single-term per-block INT8 only."""
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
         _check_qkv(t, n, grid)
     dev = q.device
@@ -125,9 +129,11 @@ def prepare_blocks(q, k, v, grid):
     b = Blocks(
         grid=grid,
         q_i8=e(BH, grid.q_blk_total, KS_Q, HEAD_DIM, dt=torch.int8),
+        q_lo=e(BH, grid.q_blk_total, KS_Q, HEAD_DIM, dt=torch.int8) if split else None,
         q_scale=e(BH, grid.q_blk_total),
         pooled_q=e(BH, grid.q_blk_p, HEAD_DIM),
         k_i8=e(BH, grid.kb_tot, KS_K, HEAD_DIM, dt=torch.int8),
+        k_lo=e(BH, grid.kb_tot, KS_K, HEAD_DIM, dt=torch.int8) if split else None,
         k_scale=e(BH, grid.kb_tot),
         pooled_k=e(BH, grid.kb_p, HEAD_DIM),
         pooled_v=e(BH, grid.kb_p, HEAD_DIM),
@@ -139,8 +145,8 @@ def prepare_blocks(q, k, v, grid):
     _lib.call(
         "ress_prep_qkv", P(q), P(k), P(v), grid.B, grid.H, grid.frames, grid.P, grid.S,
         *q.stride()[:3], *k.stride()[:3], *v.stride()[:3],
-        P(b.q_i8), P(b.q_scale), P(b.pooled_q), P(b.k_i8), P(b.k_scale), P(b.pooled_k), P(b.pooled_v),
-        P(b.v_pack), P(b.ksum), P(b.km), _lib.stream_handle(dev))
+        P(b.q_i8), P(b.q_lo), P(b.q_scale), P(b.pooled_q), P(b.k_i8), P(b.k_lo), P(b.k_scale), P(b.pooled_k),
+        P(b.pooled_v), P(b.v_pack), P(b.ksum), P(b.km), _lib.stream_handle(dev))
     return b
 
 
@@ -238,8 +244,9 @@ def sparse_attention(blocks, lut, nvalid, out=None, out_dtype=torch.float32):
     if out is None:
         out = torch.empty(g.B, g.H, g.Tk, HEAD_DIM, dtype=out_dtype, device=dev)
     code = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[out.dtype]
-    _lib.call("ress_sparse_attn_fwd", _lib.ptr(blocks.q_i8), _lib.ptr(blocks.q_scale), _lib.ptr(blocks.k_i8),
-              _lib.ptr(blocks.k_scale), _lib.ptr(blocks.v_pack), 0, _lib.ptr(lut), _lib.ptr(nvalid), g.B, g.H,
+    _lib.call("ress_sparse_attn_fwd", _lib.ptr(blocks.q_i8), _lib.ptr(blocks.q_lo), _lib.ptr(blocks.q_scale),
+              _lib.ptr(blocks.k_i8), _lib.ptr(blocks.k_lo), _lib.ptr(blocks.k_scale), _lib.ptr(blocks.v_pack), 0,
+              _lib.ptr(lut), _lib.ptr(nvalid), g.B, g.H,
               g.frames, g.P, g.S, 1.0 / math.sqrt(HEAD_DIM), _lib.ptr(out), code, *out.stride()[:3],
               _lib.stream_handle(dev))
     return out

@@ -27,6 +27,7 @@ def oracle_layer(q, k, v, frames, P, S, sparse_ratio=None, cdf_threshold=None, h
 def row_sample(nvalid, n, seed=0):
     """A few (bh, qb) rows: first, last, the dense rows, and random ones."""
     BH, qt = nvalid.shape
+    n = min(n, BH * qt)
     rng = np.random.default_rng(seed)
     rows = {(0, 0), (BH - 1, qt - 1), (0, qt - 1)}
     while len(rows) < n:

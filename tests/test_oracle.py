@@ -147,6 +147,20 @@ def test_quantisation_rule_and_roundtrip(small_layer):
             assert np.array_equal(o["k_i8"][bh, kb, :x.shape[0]], _sage_quant(x, scale))
 
 
+def test_split_codes_bound_the_residual(small_layer):
+    q, k, v, frames, P, S, o = small_layer
+    for hi, lo, sc in ((o["q_i8"], o["q_lo"], o["q_scale"]), (o["k_i8"], o["k_lo"], o["k_scale"])):
+        assert np.abs(lo.astype(np.int32)).max() <= 127
+    qp, _ = ref.split_tokens(q.float(), frames, P, S)
+    x = qp[0, 0, :128].numpy()
+    s = o["q_scale"][0, 0]
+    approx = s * o["q_i8"][0, 0].astype(np.float64) + (s / 254) * o["q_lo"][0, 0].astype(np.float64)
+    err = np.abs(x - approx)
+    assert err.max() <= s / 508 * 1.001 + 1e-12
+    # the two-term code is ~254x finer than the single term
+    assert err.max() < np.abs(x - s * o["q_i8"][0, 0]).max() / 100
+
+
 def test_zero_block_quantises_to_zero():
     q = torch.zeros(1, 1, 256, 64, dtype=torch.bfloat16)
     k = _rand_bf16((1, 1, 256, 64), 5)
