@@ -110,11 +110,13 @@ int ress_block_map_lut(const void* map, long long rows, int k, void* lut, void* 
  * :625 run_block_sparse_kernel, :652 combine_special_and_patch): inputs from
  * ress_prep_qkv + ress_select_blocks; out (B,H,frames*P,64) in storage order,
  * out_dtype 0 f32 / 1 bf16 / 2 f16, element strides soB/soH/soT. q_lo/k_lo both NULL: the
- * reference's single-term per-block INT8 QK^T; both set: the two-term split product. */
+ * reference's single-term per-block INT8 QK^T; both set: the two-term split product.
+ * sched: 32 int32 of device workspace (the persistent kernel's row schedule). */
 int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void* q_scale, const void* k_i8,
                          const void* k_lo, const void* k_scale, const void* v_pack, int v_f16, const void* lut,
                          const void* nvalid, int B, int H, int frames, int P, int S, float sm_scale, void* out,
-                         int out_dtype, long long soB, long long soH, long long soT, hipStream_t stream);
+                         int out_dtype, long long soB, long long soH, long long soT, void* sched,
+                         hipStream_t stream);
 
 /* Replaces SpargeAttn qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold
  * (call src/ress/models/attention.py:238-241) with the same argument meaning; see

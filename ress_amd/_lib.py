@@ -24,7 +24,7 @@ _SIGS = {
     "ress_select_blocks": "ppiiiiiiippp" + "s",
     "ress_fill_block_map": "ppplI" + "s",
     "ress_block_map_lut": "plipp" + "s",
-    "ress_sparse_attn_fwd": "pppppppippiiiiifpillls",
+    "ress_sparse_attn_fwd": "pppppppippiiiiifpilllps",
     "ress_qattn_block_sparse_fwd": "pppipipppppiiiilllllliiifipls",
 }
 _CT = {

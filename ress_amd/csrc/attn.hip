@@ -9,10 +9,10 @@
 //   O[q] = sum_k softmax_k( q_scale*k_scale*sm_scale * (Q8[q] . K8[k]) ) V[k]
 //
 // Work item = (batch*head, 128-query block); 256 threads = 4 waves of 32 queries.
-// Per kept 64-key block:
-//   S^T (64 keys x 32 queries) = K8 . Q8^T     4 x v_mfma_i32_32x32x32_i8
+// Per kept 64-key block, as two 32-key tiles:
+//   S^T (32 keys x 32 queries) = K8 . Q8^T     2 x v_mfma_i32_32x32x32_i8 (6 when split)
 //   online softmax in the exp2 domain, scale folded into one fma per score
-//   O^T (64 dims x 32 queries) += V^T . P^T    8 x v_mfma_f32_32x32x16_{bf16,f16}
+//   O^T (64 dims x 32 queries) += V^T . P^T    4 x v_mfma_f32_32x32x16_{bf16,f16}
 // The S^T accumulator layout puts one query per lane, so P feeds the PV MFMA from
 // registers; V is pre-packed (prep.hip) with keys permuted to match. K/V tiles are
 // double-buffered in LDS. Work items are mapped XCD-major: hardware workgroup x runs
@@ -41,6 +41,7 @@ struct AttnArgs {
   int H, BH;
   int q_blk_p, q_blk_total, kb_tot, Tk;
   float sm_scale_log2e;
+  int* sched;  // RESS_SCHED_INTS ints of workspace written by k_attn_schedule
   TokenMap m;  // query rows: patch blocks via patch_to_storage, the rest via special_to_storage
 };
 
@@ -66,188 +67,314 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   }
 }
 
+// LDS layout of one stage: K hi tile (4 KiB, 64 rows x 4 chunks of 16 B), [K lo
+// tile], V^T tile (8 KiB, 64 rows x 8 chunks). Chunks are XOR-swizzled so that the
+// b128 reads of any 8 or 16 consecutive lanes (consecutive rows, same logical chunk)
+// fall in distinct bank groups:
+//   K: chunk c of row r at 4r + (c ^ (((r >> 1) ^ (r >> 3)) & 3))
+//   V: chunk c of row r at 8r + (c ^ ((r ^ (r >> 3)) & 7))
+__device__ __forceinline__ int k_slot(int r, int c) { return 4 * r + (c ^ (((r >> 1) ^ (r >> 3)) & 3)); }
+__device__ __forceinline__ int v_slot(int r, int c) { return 8 * r + (c ^ ((r ^ (r >> 3)) & 7)); }
+
+// 16 bytes per lane, global -> LDS without a register round trip (gfx950
+// global_load_lds_dwordx4): lane i of the wave writes lds_base + 16*i, lds_base uniform.
+__device__ __forceinline__ void gl_lds16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)src,
+                                   (void __attribute__((address_space(3)))*)lds_base, 16, 0, 0);
+}
+__device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+template <bool V_F16>
+__device__ __forceinline__ uint32_t cvt_pair(float a, float b) {
+  const v2f x = {a, b};
+  if constexpr (V_F16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, v2h));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, v2bf));
+}
+// a.x + a.y of a packed 16-bit pair accumulated in fp32
+template <bool V_F16>
+__device__ __forceinline__ float dot2_acc(uint32_t p, float acc) {
+  if constexpr (V_F16) {
+    const v2h ones = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, p), ones, acc, false);
+  } else {
+    const v2bf ones = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, p), ones, acc, false);
+  }
+}
+
+// Reductions over the lane pair (l, l^32) that share a query row, without LDS:
+// v_permlane32_swap exchanges the two 32-lane halves.
+__device__ __forceinline__ int pair_max(int x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return max((int)r[0], (int)r[1]);
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return __int_as_float((int)r[0]) + __int_as_float((int)r[1]);
+}
+
+// ---- work schedule ---------------------------------------------------------
+// Rows are items in head-major order (per head: its dense special rows, then its
+// patch rows). The schedule cuts the item list into 8 contiguous ranges of equal
+// work (kept blocks + a fixed per-row cost), one per XCD, so each XCD walks few
+// heads (their K/V stay in its L2) and all XCDs finish together.
+//   sched[0..8]   range bounds (sched[j] .. sched[j+1]-1 belong to XCD j)
+//   sched[16..23] per-XCD next-item counters (atomically advanced by the kernel)
+#define RESS_SCHED_INTS 32
+#define RESS_ROW_COST 2
+
+__device__ __forceinline__ void item_to_row(int i, int q_blk_p, int q_blk_total, int& bh, int& qb) {
+  bh = i / q_blk_total;
+  const int r = i - bh * q_blk_total;
+  const int qs = q_blk_total - q_blk_p;
+  qb = r < qs ? q_blk_p + r : r - qs;
+}
+
+__global__ __launch_bounds__(1024) void k_attn_schedule(const int* __restrict__ nvalid, int BH, int q_blk_p,
+                                                        int q_blk_total, int* __restrict__ sched) {
+  __shared__ long long part[1024];
+  const int tid = threadIdx.x;
+  const int n = BH * q_blk_total;
+  const int per = (n + 1023) / 1024;
+  const int i0 = min(n, tid * per), i1 = min(n, i0 + per);
+  long long s = 0;
+  for (int i = i0; i < i1; ++i) {
+    int bh, qb;
+    item_to_row(i, q_blk_p, q_blk_total, bh, qb);
+    s += nvalid[(long long)bh * q_blk_total + qb] + RESS_ROW_COST;
+  }
+  part[tid] = s;
+  if (tid < 9) sched[tid] = tid == 0 ? 0 : n;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {  // inclusive scan
+    const long long v = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  const long long W = part[1023];
+  long long run = part[tid] - s;  // exclusive prefix of this thread's first item
+  long long prev = -1;            // exclusive prefix of item i-1
+  if (i0 > 0 && i0 < n) {
+    int bh, qb;
+    item_to_row(i0 - 1, q_blk_p, q_blk_total, bh, qb);
+    prev = run - (nvalid[(long long)bh * q_blk_total + qb] + RESS_ROW_COST);
+  }
+  for (int i = i0; i < i1; ++i) {
+    // item i starts range j if its exclusive prefix is the first to reach j*W/8
+    for (int j = 1; j < 8; ++j)
+      if (run * 8 >= (long long)j * W && prev * 8 < (long long)j * W) sched[j] = i;
+    int bh, qb;
+    item_to_row(i, q_blk_p, q_blk_total, bh, qb);
+    prev = run;
+    run += nvalid[(long long)bh * q_blk_total + qb] + RESS_ROW_COST;
+  }
+  __syncthreads();
+  if (tid < 8) sched[16 + tid] = sched[tid];
+}
+
+// The running max is moved (and O, l rescaled) only when a row's block max exceeds it
+// by more than this many log2 units, so P stays below 2^8; the final O / l is exact.
+#define RESS_RESCALE_LOG2 8.0f
+
+// One 32-key tile t of the current K/V stage: S^T tile, running max with lazy rescale,
+// P = exp2(S*c - m), O^T += V^T P^T. nkt = valid keys in the tile (MASK only).
+template <bool SPLIT, bool V_F16, bool MASK>
+__device__ __forceinline__ void attn_tile(const uint4* __restrict__ sk, const uint4* __restrict__ sv, int t, int nkt,
+                                          float c, int ka, int kb2, const v4i& qa0, const v4i& qa1, const v4i& ql0,
+                                          const v4i& ql1, int g, int qi, float& m_run, float& l_run, v16f& o0,
+                                          v16f& o1) {
+  const v4i kx0 = __builtin_bit_cast(v4i, sk[ka]);
+  const v4i kx1 = __builtin_bit_cast(v4i, sk[kb2]);
+  v16i sacc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) sacc[r] = 0;
+  sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kx0, qa0, sacc, 0, 0, 0);
+  sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kx1, qa1, sacc, 0, 0, 0);
+  if constexpr (SPLIT) {
+    // S = 254*(hi.hi) + hi.lo + lo.hi in one accumulator: scale the hi.hi partial
+    // (|hi.hi| <= 64*127*127 < 2^23, so a 24-bit multiply is exact), then let the
+    // cross-term MFMAs accumulate on top of it.
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sacc[r] = __mul24(sacc[r], 254);
+    const v4i lx0 = __builtin_bit_cast(v4i, sk[256 + ka]);
+    const v4i lx1 = __builtin_bit_cast(v4i, sk[256 + kb2]);
+    sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kx0, ql0, sacc, 0, 0, 0);
+    sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kx1, ql1, sacc, 0, 0, 0);
+    sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(lx0, qa0, sacc, 0, 0, 0);
+    sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(lx1, qa1, sacc, 0, 0, 0);
+  }
+  // register r is key 32t + 8(r/4) + 4g + r%4 of the block
+  if constexpr (MASK) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      if (8 * (r >> 2) + 4 * g + (r & 3) >= nkt) sacc[r] = -2147483647 - 1;
+  }
+  int mx = max(sacc[0], sacc[1]);
+#pragma unroll
+  for (int r = 2; r < 16; r += 2) mx = max(mx, max(sacc[r], sacc[r + 1]));
+  mx = pair_max(mx);
+  const float bmax = (float)mx * c;
+  const bool need = bmax > m_run + RESS_RESCALE_LOG2;
+  if (__any(need)) {
+    const float m_new = need ? bmax : m_run;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    m_run = m_new;
+    l_run *= alpha;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      o0[r] *= alpha;
+      o1[r] *= alpha;
+    }
+  }
+  const float nm = -m_run;
+  float p[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) p[r] = __builtin_amdgcn_exp2f(fmaf((float)sacc[r], c, nm));
+  if constexpr (MASK) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      if (8 * (r >> 2) + 4 * g + (r & 3) >= nkt) p[r] = 0.0f;
+  }
+  // O^T += V^T . P^T: MFMA s = 2t + h covers keys 16s..16s+15, registers 8h..8h+7. The
+  // row sum accumulates the same rounded P the MFMA consumes.
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint4 pb;
+    pb.x = cvt_pair<V_F16>(p[8 * h + 0], p[8 * h + 1]);
+    pb.y = cvt_pair<V_F16>(p[8 * h + 2], p[8 * h + 3]);
+    pb.z = cvt_pair<V_F16>(p[8 * h + 4], p[8 * h + 5]);
+    pb.w = cvt_pair<V_F16>(p[8 * h + 6], p[8 * h + 7]);
+    l_run = dot2_acc<V_F16>(pb.x, l_run);
+    l_run = dot2_acc<V_F16>(pb.y, l_run);
+    l_run = dot2_acc<V_F16>(pb.z, l_run);
+    l_run = dot2_acc<V_F16>(pb.w, l_run);
+    const int sidx = 2 * t + h;
+    const uint4 va0 = sv[v_slot(qi, 2 * sidx + g)];
+    const uint4 va1 = sv[v_slot(32 + qi, 2 * sidx + g)];
+    o0 = pv_mfma<V_F16>(va0, pb, o0);
+    o1 = pv_mfma<V_F16>(va1, pb, o1);
+  }
+}
+
 // SPLIT: two-term INT8 Q and K (x ~ s*hi + s/254*lo). S = 254*(Qhi.Khi) + (Qhi.Klo + Qlo.Khi)
 // in int32 (the lo.lo term, below 2^-16 relative, is dropped), 3 INT8 MFMAs per tile.
-template <bool SPLIT, bool V_F16, int OUT>
-__global__ __launch_bounds__(256, 2) void k_sparse_attn(AttnArgs a) {
-  constexpr int KCH = SPLIT ? 512 : 256;  // 16-byte chunks of K per stage (hi [+ lo])
-  constexpr int STAGE = KCH + 512;        // + V 8 KiB
-  __shared__ __attribute__((aligned(16))) uint4 smem[2][STAGE];
-
-  // ---- XCD-major work mapping -------------------------------------------
-  const int x = blockIdx.x;
-  const int xcd = x & 7, u = x >> 3;
-  const int nh = (a.BH - xcd + 7) >> 3;  // heads whose rows this XCD runs
-  const int q_blk_s = a.q_blk_total - a.q_blk_p;
-  int bh, qb;
-  if (u < nh * q_blk_s) {  // dense (special-query) rows first: they are the longest
-    bh = xcd + 8 * (u / q_blk_s);
-    qb = a.q_blk_p + u % q_blk_s;
-  } else {
-    const int v = u - nh * q_blk_s;
-    const int hi = v / a.q_blk_p;
-    if (hi >= nh) return;
-    bh = xcd + 8 * hi;
-    qb = v - hi * a.q_blk_p;
-  }
-
+template <bool SPLIT, bool V_F16, int OUT, int KCH, int STAGE>
+__device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __restrict__ lut_all,
+                                                const int* __restrict__ nvalid, const float* __restrict__ k_scale,
+                                                uint4* __restrict__ s0, uint4* __restrict__ s1, int bh, int qb) {
   const long long row = (long long)bh * a.q_blk_total + qb;
-  const int nv = a.nvalid[row];
-  const int* lut = a.lut + row * a.kb_tot;
+  const int nv = nvalid[row];
+  const int* lut = lut_all + row * a.kb_tot;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, qi = l & 31;
 
   const int8_t* qsrc = a.q_i8 + (row * 128 + 32 * w + qi) * 64 + 16 * g;
   const v4i qa0 = *reinterpret_cast<const v4i*>(qsrc);
   const v4i qa1 = *reinterpret_cast<const v4i*>(qsrc + 32);
-  v4i ql0, ql1;
+  v4i ql0 = qa0, ql1 = qa1;  // residual codes (SPLIT only)
   if constexpr (SPLIT) {
     const int8_t* qlsrc = a.q_lo + (row * 128 + 32 * w + qi) * 64 + 16 * g;
     ql0 = *reinterpret_cast<const v4i*>(qlsrc);
     ql1 = *reinterpret_cast<const v4i*>(qlsrc + 32);
   }
   const float qs = a.q_scale[row] * a.sm_scale_log2e * (SPLIT ? (1.0f / 254.0f) : 1.0f);
-  const float* ksc = a.k_scale + (long long)bh * a.kb_tot;
-  const uint4* kbase_p = reinterpret_cast<const uint4*>(a.k_i8 + (long long)bh * a.kb_tot * 4096);
-  const uint4* klbase_p = SPLIT ? reinterpret_cast<const uint4*>(a.k_lo + (long long)bh * a.kb_tot * 4096) : nullptr;
-  const uint4* vbase_p = reinterpret_cast<const uint4*>(a.v_pack + (long long)bh * a.kb_tot * 4096);
+  const float* ksc = k_scale + (long long)bh * a.kb_tot;
+
+  // Stage loads are LDS-DMA: lane l of wave w fills the 16-byte slots 64w+l (K hi, K lo)
+  // and 128w+l, 128w+64+l (V), so it fetches the global chunk that the swizzle places
+  // there (the XOR swizzle is its own inverse).
+  const int kslot = 64 * w + l;
+  const int ksrc = 16 * (4 * (kslot >> 2) + ((kslot & 3) ^ ((((kslot >> 2) >> 1) ^ ((kslot >> 2) >> 3)) & 3)));
+  const int vslot0 = 128 * w + l, vslot1 = vslot0 + 64;
+  const int vsrc0 = 16 * (8 * (vslot0 >> 3) + ((vslot0 & 7) ^ (((vslot0 >> 3) ^ (vslot0 >> 6)) & 7)));
+  const int vsrc1 = 16 * (8 * (vslot1 >> 3) + ((vslot1 & 7) ^ (((vslot1 >> 3) ^ (vslot1 >> 6)) & 7)));
+  const char* kblk0 = reinterpret_cast<const char*>(a.k_i8) + (long long)bh * a.kb_tot * 4096;
+  const char* klblk0 = SPLIT ? reinterpret_cast<const char*>(a.k_lo) + (long long)bh * a.kb_tot * 4096 : nullptr;
+  const char* vblk0 = reinterpret_cast<const char*>(a.v_pack) + (long long)bh * a.kb_tot * 8192;
+  auto stage_load = [&](uint4* stage, int kb) {
+    char* base = reinterpret_cast<char*>(stage);
+    gl_lds16(kblk0 + (long long)kb * 4096 + ksrc, base + 1024 * w);
+    if constexpr (SPLIT) gl_lds16(klblk0 + (long long)kb * 4096 + ksrc, base + 4096 + 1024 * w);
+    gl_lds16(vblk0 + (long long)kb * 8192 + vsrc0, base + 16 * KCH + 2048 * w);
+    gl_lds16(vblk0 + (long long)kb * 8192 + vsrc1, base + 16 * KCH + 2048 * w + 1024);
+  };
+  // LDS sources of this lane's MFMA operands
+  const int ks00 = k_slot(qi, g), ks01 = k_slot(qi, 2 + g);
+  const int ks10 = k_slot(32 + qi, g), ks11 = k_slot(32 + qi, 2 + g);
 
   float m_run = -__builtin_huge_valf(), l_run = 0.0f;
   v16f o0, o1;
 #pragma unroll
   for (int r = 0; r < 16; ++r) o0[r] = o1[r] = 0.0f;
 
-  uint4 r0, r1, r2, r3;
-  if (nv > 0) {
-    const int kb = lut[0];
-    r0 = kbase_p[(long long)kb * 256 + tid];
-    if constexpr (SPLIT) r3 = klbase_p[(long long)kb * 256 + tid];
-    r1 = vbase_p[(long long)kb * 512 + tid];
-    r2 = vbase_p[(long long)kb * 512 + 256 + tid];
-    smem[0][tid] = r0;
-    if constexpr (SPLIT) smem[0][256 + tid] = r3;
-    smem[0][KCH + tid] = r1;
-    smem[0][KCH + 256 + tid] = r2;
-  }
+  if (nv > 0) stage_load(s0, lut[0]);
+  wait_lds_dma();
   __syncthreads();
 
-  for (int it = 0; it < nv; ++it) {
-    const int buf = it & 1;
-    const int kb = lut[it];
-    const bool more = it + 1 < nv;
-    if (more) {
-      const int kn = lut[it + 1];
-      r0 = kbase_p[(long long)kn * 256 + tid];
-      if constexpr (SPLIT) r3 = klbase_p[(long long)kn * 256 + tid];
-      r1 = vbase_p[(long long)kn * 512 + tid];
-      r2 = vbase_p[(long long)kn * 512 + 256 + tid];
-    }
-    const int8_t* sk = reinterpret_cast<const int8_t*>(&smem[buf][0]);
-    const int8_t* skl = sk + 4096;
-    const uint16_t* sv = reinterpret_cast<const uint16_t*>(&smem[buf][KCH]);
+  // the block index and scale of the next iteration are loaded one iteration ahead
+  int kb = nv > 0 ? lut[0] : 0;
+  float c = nv > 0 ? qs * ksc[kb] : 0.0f;
+  // Only the sequence's last key block can be partial; LUTs are ascending, so if it is
+  // kept it is the last entry. Full blocks run the unmasked loop, the partial one is
+  // peeled off after it.
+  const bool tail_partial = nv > 0 && (a.Tk & 63) != 0 && lut[nv - 1] == a.kb_tot - 1;
+  const int nv_full = nv - (tail_partial ? 1 : 0);
 
-    // ---- S^T = K . Q^T --------------------------------------------------
-    v16i s0, s1;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s0[r] = s1[r] = 0;
-    {
-      const v4i k00 = *reinterpret_cast<const v4i*>(sk + qi * 64 + 16 * g);
-      const v4i k01 = *reinterpret_cast<const v4i*>(sk + qi * 64 + 32 + 16 * g);
-      const v4i k10 = *reinterpret_cast<const v4i*>(sk + (32 + qi) * 64 + 16 * g);
-      const v4i k11 = *reinterpret_cast<const v4i*>(sk + (32 + qi) * 64 + 32 + 16 * g);
-      s0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k00, qa0, s0, 0, 0, 0);
-      s0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k01, qa1, s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k10, qa0, s1, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k11, qa1, s1, 0, 0, 0);
-      if constexpr (SPLIT) {
-        v16i b0, b1;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) b0[r] = b1[r] = 0;
-        const v4i l00 = *reinterpret_cast<const v4i*>(skl + qi * 64 + 16 * g);
-        const v4i l01 = *reinterpret_cast<const v4i*>(skl + qi * 64 + 32 + 16 * g);
-        const v4i l10 = *reinterpret_cast<const v4i*>(skl + (32 + qi) * 64 + 16 * g);
-        const v4i l11 = *reinterpret_cast<const v4i*>(skl + (32 + qi) * 64 + 32 + 16 * g);
-        b0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k00, ql0, b0, 0, 0, 0);
-        b0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k01, ql1, b0, 0, 0, 0);
-        b0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(l00, qa0, b0, 0, 0, 0);
-        b0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(l01, qa1, b0, 0, 0, 0);
-        b1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k10, ql0, b1, 0, 0, 0);
-        b1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k11, ql1, b1, 0, 0, 0);
-        b1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(l10, qa0, b1, 0, 0, 0);
-        b1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(l11, qa1, b1, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          s0[r] = s0[r] * 254 + b0[r];
-          s1[r] = s1[r] * 254 + b1[r];
-        }
-      }
+  // One kept block: stage the next block into `nxt` (LDS-DMA, in flight during the
+  // compute), consume `cur`. The two stages are distinct LDS objects and the loop is
+  // unrolled by two, so the compiler can see the DMA never writes the stage being read
+  // and does not wait for it before the LDS reads.
+  auto step = [&](const uint4* cur, uint4* nxt, int it) {
+    int kn = 0;
+    float cn = 0.0f;
+    if (it + 1 < nv) {
+      kn = lut[it + 1];
+      cn = qs * ksc[kn];
+      stage_load(nxt, kn);
     }
-
-    // ---- online softmax (exp2 domain) -----------------------------------
-    // lane holds query qi; register r of tile t is key 32t + 8(r/4) + 4g + r%4
-    const float c = qs * ksc[kb];
-    const int key0 = kb * 64;
-    const int nk = min(64, a.Tk - key0);
-    int imax = -2147483647 - 1;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int kr = 8 * (r >> 2) + 4 * g + (r & 3);
-      if (kr < nk) imax = max(imax, s0[r]);
-      if (kr + 32 < nk) imax = max(imax, s1[r]);
-    }
-    imax = max(imax, __shfl_xor(imax, 32, 64));
-    const float m_new = fmaxf(m_run, (float)imax * c);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    float p0[16], p1[16];
-    float psum = 0.0f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int kr = 8 * (r >> 2) + 4 * g + (r & 3);
-      p0[r] = kr < nk ? __builtin_amdgcn_exp2f(fmaf((float)s0[r], c, -m_new)) : 0.0f;
-      p1[r] = kr + 32 < nk ? __builtin_amdgcn_exp2f(fmaf((float)s1[r], c, -m_new)) : 0.0f;
-      psum += p0[r] + p1[r];
-    }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      o0[r] *= alpha;
-      o1[r] *= alpha;
-    }
-
-    // ---- O^T += V^T . P^T -----------------------------------------------
-    // MFMA s covers keys 16s..16s+15: tile s/2, registers 8(s%2)..+7
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const float* ps = (s < 2) ? p0 : p1;
-      const int rb = 8 * (s & 1);
-      uint4 pb;
-      pb.x = pack2<V_F16>(ps[rb + 0], ps[rb + 1]);
-      pb.y = pack2<V_F16>(ps[rb + 2], ps[rb + 3]);
-      pb.z = pack2<V_F16>(ps[rb + 4], ps[rb + 5]);
-      pb.w = pack2<V_F16>(ps[rb + 6], ps[rb + 7]);
-      const uint4 va0 = *reinterpret_cast<const uint4*>(sv + qi * 64 + 16 * s + 8 * g);
-      const uint4 va1 = *reinterpret_cast<const uint4*>(sv + (32 + qi) * 64 + 16 * s + 8 * g);
-      o0 = pv_mfma<V_F16>(va0, pb, o0);
-      o1 = pv_mfma<V_F16>(va1, pb, o1);
-    }
-
-    if (more) {
-      smem[buf ^ 1][tid] = r0;
-      if constexpr (SPLIT) smem[buf ^ 1][256 + tid] = r3;
-      smem[buf ^ 1][KCH + tid] = r1;
-      smem[buf ^ 1][KCH + 256 + tid] = r2;
-    }
+    const uint4* sk = cur;
+    const uint4* sv = cur + KCH;
+    // Each 64-key block is consumed as two 32-key tiles, each a full online-softmax step
+    // (S^T tile -> running max -> P -> O^T += V^T P^T), keeping one 16-register S
+    // accumulator live.
+    attn_tile<SPLIT, V_F16, false>(sk, sv, 0, 32, c, ks00, ks01, qa0, qa1, ql0, ql1, g, qi, m_run, l_run, o0, o1);
+    attn_tile<SPLIT, V_F16, false>(sk, sv, 1, 32, c, ks10, ks11, qa0, qa1, ql0, ql1, g, qi, m_run, l_run, o0, o1);
+    kb = kn;
+    c = cn;
+    wait_lds_dma();
     __syncthreads();
+  };
+  int it = 0;
+  for (; it + 2 <= nv_full; it += 2) {
+    step(s0, s1, it);
+    step(s1, s0, it + 1);
+  }
+  if (it < nv_full) {
+    step(s0, s1, it);
+    ++it;
+  }
+  if (tail_partial) {  // kb / c already hold the last block's index and scale
+    const uint4* cur = (it & 1) ? s1 : s0;
+    const uint4* sk = cur;
+    const uint4* sv = cur + KCH;
+    const int nk = a.Tk - kb * 64;
+    attn_tile<SPLIT, V_F16, true>(sk, sv, 0, nk, c, ks00, ks01, qa0, qa1, ql0, ql1, g, qi, m_run, l_run, o0, o1);
+    attn_tile<SPLIT, V_F16, true>(sk, sv, 1, nk - 32, c, ks10, ks11, qa0, qa1, ql0, ql1, g, qi, m_run, l_run, o0, o1);
+    __syncthreads();  // the next row's prologue overwrites this stage
   }
 
   // ---- epilogue ------------------------------------------------------------
-  const float lt = l_run + __shfl_xor(l_run, 32, 64);
+  const float lt = pair_sum(l_run);
   const float inv = (nv > 0 && lt > 0.0f) ? 1.0f / lt : 0.0f;
   const bool special = qb >= a.q_blk_p;
   const int qbase = special ? (qb - a.q_blk_p) * 128 : qb * 128;
   const int cnt_q = min(128, (special ? a.m.T_s : a.m.T_p) - qbase);
   const int qrow = 32 * w + qi;
-  if (qrow >= cnt_q) return;
+  if (qrow >= cnt_q) return;  // this row function only; the caller's loop continues
   const int tok = special ? special_to_storage(qbase + qrow, a.m) : patch_to_storage(qbase + qrow, a.m);
   const long long off = (long long)(bh / a.H) * a.soB + (long long)(bh % a.H) * a.soH + (long long)tok * a.soT;
 #pragma unroll
@@ -266,6 +393,31 @@ __global__ __launch_bounds__(256, 2) void k_sparse_attn(AttnArgs a) {
             make_uint2(pack2<F16>(y0, y1), pack2<F16>(y2, y3));
       }
     }
+  }
+}
+
+template <bool SPLIT, bool V_F16, int OUT>
+__global__ __launch_bounds__(256, 3) void k_sparse_attn(AttnArgs a, const int* __restrict__ lut,
+                                                        const int* __restrict__ nvalid,
+                                                        const float* __restrict__ k_scale) {
+  constexpr int KCH = SPLIT ? 512 : 256;  // 16-byte chunks of K per stage (hi [+ lo])
+  constexpr int STAGE = KCH + 512;        // + V 8 KiB
+  __shared__ __attribute__((aligned(16))) uint4 stage0[STAGE];
+  __shared__ __attribute__((aligned(16))) uint4 stage1[STAGE];
+  __shared__ int s_item;
+
+  // ---- persistent loop over this XCD's range of rows ------------------------
+  const int xcd = blockIdx.x & 7;
+  const int item_end = a.sched[xcd + 1];
+  for (;;) {
+    if (threadIdx.x == 0) s_item = atomicAdd(&a.sched[16 + xcd], 1);
+    __syncthreads();
+    const int item = __builtin_amdgcn_readfirstlane(s_item);
+    __syncthreads();
+    if (item >= item_end) break;
+    int bh, qb;
+    item_to_row(item, a.q_blk_p, a.q_blk_total, bh, qb);
+    sparse_attn_row<SPLIT, V_F16, OUT, KCH, STAGE>(a, lut, nvalid, k_scale, stage0, stage1, bh, qb);
   }
 }
 
@@ -300,14 +452,29 @@ __global__ __launch_bounds__(64) void k_pack_v(const uint16_t* __restrict__ v, l
 // ============================================================================
 // C ABI
 // ============================================================================
+static int g_cu_count[64];
+
 template <bool SPLIT, bool V_F16>
 static int launch_attn(const AttnArgs& a, int out_dtype, hipStream_t stream) {
-  const int per_xcd = ((a.BH + 7) / 8) * a.q_blk_total;
-  const dim3 grid(8 * per_xcd), block(256);
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (g_cu_count[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    g_cu_count[dev] = cus;
+  }
+  hipLaunchKernelGGL(k_attn_schedule, dim3(1), dim3(1024), 0, stream, a.nvalid, a.BH, a.q_blk_p, a.q_blk_total,
+                     a.sched);
+  RESS_LAUNCHED("k_attn_schedule");
+  // persistent: 3 resident workgroups per CU, a multiple of the 8 XCDs
+  const dim3 grid(8 * ((3 * g_cu_count[dev] + 7) / 8)), block(256);
   switch (out_dtype) {
-    case OUT_F32: hipLaunchKernelGGL((k_sparse_attn<SPLIT, V_F16, OUT_F32>), grid, block, 0, stream, a); break;
-    case OUT_BF16: hipLaunchKernelGGL((k_sparse_attn<SPLIT, V_F16, OUT_BF16>), grid, block, 0, stream, a); break;
-    default: hipLaunchKernelGGL((k_sparse_attn<SPLIT, V_F16, OUT_F16>), grid, block, 0, stream, a); break;
+    case OUT_F32: hipLaunchKernelGGL((k_sparse_attn<SPLIT, V_F16, OUT_F32>), grid, block, 0, stream, a, a.lut, a.nvalid,
+                                          a.k_scale); break;
+    case OUT_BF16: hipLaunchKernelGGL((k_sparse_attn<SPLIT, V_F16, OUT_BF16>), grid, block, 0, stream, a, a.lut, a.nvalid,
+                                          a.k_scale); break;
+    default: hipLaunchKernelGGL((k_sparse_attn<SPLIT, V_F16, OUT_F16>), grid, block, 0, stream, a, a.lut, a.nvalid,
+                                          a.k_scale); break;
   }
   RESS_LAUNCHED("k_sparse_attn");
   return 0;
@@ -316,8 +483,9 @@ static int launch_attn(const AttnArgs& a, int out_dtype, hipStream_t stream) {
 static int attn_common(const void* q_i8, const void* q_lo, const void* q_scale, const void* k_i8, const void* k_lo,
                        const void* k_scale, const void* v_pack, int v_f16, const void* lut, const void* nvalid, int B,
                        int H, TokenMap m, int Tk, float sm_scale, void* out, int out_dtype, long long soB,
-                       long long soH, long long soT, hipStream_t stream) {
-  RESS_REQUIRE(q_i8 && q_scale && k_i8 && k_scale && v_pack && lut && nvalid && out, "sparse attention: null pointer");
+                       long long soH, long long soT, void* sched, hipStream_t stream) {
+  RESS_REQUIRE(q_i8 && q_scale && k_i8 && k_scale && v_pack && lut && nvalid && out && sched,
+               "sparse attention: null pointer");
   RESS_REQUIRE((q_lo == nullptr) == (k_lo == nullptr), "sparse attention: give both q_lo and k_lo, or neither");
   RESS_REQUIRE(((uintptr_t)q_i8 & 15u) == 0 && ((uintptr_t)k_i8 & 15u) == 0 && ((uintptr_t)v_pack & 15u) == 0 &&
                    ((uintptr_t)q_lo & 15u) == 0 && ((uintptr_t)k_lo & 15u) == 0,
@@ -347,6 +515,7 @@ static int attn_common(const void* q_i8, const void* q_lo, const void* q_scale, 
   a.kb_tot = cdiv(Tk, 64);
   a.Tk = Tk;
   a.sm_scale_log2e = sm_scale * 1.4426950408889634f;
+  a.sched = (int*)sched;
   a.m = m;
   if (q_lo) return v_f16 ? launch_attn<true, true>(a, out_dtype, stream) : launch_attn<true, false>(a, out_dtype, stream);
   return v_f16 ? launch_attn<false, true>(a, out_dtype, stream) : launch_attn<false, false>(a, out_dtype, stream);
@@ -359,10 +528,12 @@ static int attn_common(const void* q_i8, const void* q_lo, const void* q_scale, 
 // combine_special_and_patch (src/ress/models/qkv.py:71-81) is fused in. With q_lo/k_lo
 // (split-INT8 residual codes from ress_prep_qkv) QK^T is evaluated as a two-term INT8
 // product; without them it is the single-term per-block INT8 product of the reference.
+// sched: RESS_SCHED_INTS (32) int32 of device workspace for the row schedule.
 RESS_API int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void* q_scale, const void* k_i8,
                                   const void* k_lo, const void* k_scale, const void* v_pack, int v_f16, const void* lut,
                                   const void* nvalid, int B, int H, int frames, int P, int S, float sm_scale, void* out,
-                                  int out_dtype, long long soB, long long soH, long long soT, hipStream_t stream) {
+                                  int out_dtype, long long soB, long long soH, long long soT, void* sched,
+                                  hipStream_t stream) {
   RESS_REQUIRE(B > 0 && H > 0 && frames > 0 && P > S && S >= 0, "ress_sparse_attn_fwd: bad geometry");
   TokenMap m;
   m.P = P;
@@ -371,11 +542,13 @@ RESS_API int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void
   m.T_p = frames * (P - S);
   m.T_s = frames * S;
   return attn_common(q_i8, q_lo, q_scale, k_i8, k_lo, k_scale, v_pack, v_f16, lut, nvalid, B, H, m, frames * P,
-                     sm_scale, out, out_dtype, soB, soH, soT, stream);
+                     sm_scale, out, out_dtype, soB, soH, soT, sched, stream);
 }
 
+static long long qattn_vpack_bytes(int B, int H, int Tk) { return (long long)B * H * cdiv(Tk, 64) * 4096 * 2; }
+
 RESS_API long long ress_qattn_workspace_size(int B, int H, int Tk) {
-  return (long long)B * H * cdiv(Tk, 64) * 4096 * 2;
+  return qattn_vpack_bytes(B, H, Tk) + RESS_SCHED_INTS * 4;
 }
 
 // Mirror of SpargeAttn's qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold
@@ -386,7 +559,7 @@ RESS_API long long ress_qattn_workspace_size(int B, int H, int Tk) {
 // q_scale [B*H][ceil(Tq/128)], k_scale [B*H][ceil(Tk/64)]; o (B,H,Tq,64) with strides.
 // Supported: tensor_layout 1 (HND), is_causal 0, qk_quant_gran 1 (per block),
 // return_pv_count 0, pv_threshold disabled (>= 1e9, the reference passes 1e10).
-// workspace: ress_qattn_workspace_size(B,H,Tk) bytes for the packed V.
+// workspace: ress_qattn_workspace_size(B,H,Tk) bytes (packed V + the row schedule).
 RESS_API int ress_qattn_block_sparse_fwd(const void* q_i8, const void* k_i8, const void* v, int v_f16, void* o,
                                          int o_dtype, const void* lut, const void* valid_block_num,
                                          const float* pv_threshold_host, const void* q_scale, const void* k_scale,
@@ -420,5 +593,5 @@ RESS_API int ress_qattn_block_sparse_fwd(const void* q_i8, const void* k_i8, con
   m.T_p = Tq;
   m.T_s = 0;
   return attn_common(q_i8, nullptr, q_scale, k_i8, nullptr, k_scale, workspace, v_f16, lut, valid_block_num, B, H, m,
-                     Tk, sm_scale, o, o_dtype, soB, soH, soT, stream);
+                     Tk, sm_scale, o, o_dtype, soB, soH, soT, (char*)workspace + qattn_vpack_bytes(B, H, Tk), stream);
 }

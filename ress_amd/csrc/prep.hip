@@ -183,13 +183,22 @@ __global__ __launch_bounds__(64) void k_prep_kv(const uint16_t* __restrict__ k, 
   for (int i = 0; i < 8; ++i) dst[i * 64 + lane] = s4[i * 64 + lane];
 }
 
-// key mean over all Tk keys: km[d] = SEQ-sum of the block sums / Tk
+// key mean over all Tk keys: km[d] = SEQ-sum of the block sums / Tk. The loads are
+// issued 16 at a time so the serial add chain is not a chain of memory latencies.
 __global__ __launch_bounds__(64) void k_key_mean(const float* __restrict__ ksum, int kb_tot, int Tk,
                                                  float* __restrict__ km) {
   const int bh = blockIdx.x, d = threadIdx.x;
   const float* s = ksum + (long long)bh * kb_tot * 64 + d;
   float acc = 0.0f;
-  for (int b = 0; b < kb_tot; ++b) acc = acc + s[(long long)b * 64];
+  int b = 0;
+  for (; b + 16 <= kb_tot; b += 16) {
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = s[(long long)(b + j) * 64];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc = acc + v[j];
+  }
+  for (; b < kb_tot; ++b) acc = acc + s[(long long)b * 64];
   km[(long long)bh * 64 + d] = acc / (float)Tk;
 }
 

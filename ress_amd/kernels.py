@@ -244,9 +244,10 @@ def sparse_attention(blocks, lut, nvalid, out=None, out_dtype=torch.float32):
     if out is None:
         out = torch.empty(g.B, g.H, g.Tk, HEAD_DIM, dtype=out_dtype, device=dev)
     code = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[out.dtype]
+    sched = torch.empty(32, dtype=torch.int32, device=dev)
     _lib.call("ress_sparse_attn_fwd", _lib.ptr(blocks.q_i8), _lib.ptr(blocks.q_lo), _lib.ptr(blocks.q_scale),
               _lib.ptr(blocks.k_i8), _lib.ptr(blocks.k_lo), _lib.ptr(blocks.k_scale), _lib.ptr(blocks.v_pack), 0,
               _lib.ptr(lut), _lib.ptr(nvalid), g.B, g.H,
-              g.frames, g.P, g.S, 1.0 / math.sqrt(HEAD_DIM), _lib.ptr(out), code, *out.stride()[:3],
+              g.frames, g.P, g.S, 1.0 / math.sqrt(HEAD_DIM), _lib.ptr(out), code, *out.stride()[:3], _lib.ptr(sched),
               _lib.stream_handle(dev))
     return out

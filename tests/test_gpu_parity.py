@@ -222,3 +222,25 @@ def test_layer_pipeline_matches_oracle(cfg, dev):
     rows = row_sample(o["nvalid"], 10)
     w, c = _check_attention(res.out, q, k, v, frames, P, S, o["lut"], o["nvalid"], rows)
     print(f"[{cfg}] attention max-abs {w:.3e} min-cos {c:.6f}")
+
+
+@pytest.mark.parametrize("B,H,frames", [(2, 16, 3), (1, 5, 2), (1, 1, 1)])
+def test_attention_writes_every_row(B, H, frames, dev):
+    """The persistent row schedule covers every (batch, head, q-block) exactly once:
+    a NaN-filled output has no NaN left, and rows match the per-row fp32 reference."""
+    P, S = 203, 5
+    g = torch.Generator().manual_seed(B * 100 + H)
+    mk = lambda: torch.randn(B, H, frames * P, 64, generator=g).to(torch.bfloat16)  # noqa: E731
+    q, k, v = mk(), mk(), mk()
+    grid = LayerGrid(B, H, frames, P, S)
+    blocks = kernels.prepare_blocks(q.to(dev), k.to(dev), v.to(dev), grid)
+    rng = np.random.default_rng(1)
+    keys = torch.from_numpy(rng.random((B, H, grid.q_blk_p, grid.n_cand)).astype(np.float32)).to(dev)
+    counts = torch.from_numpy(rng.integers(0, grid.n_cand + 1, (B, H, grid.q_blk_p)).astype(np.int32)).to(dev)
+    _, lut, nv = kernels.select_blocks(keys, counts, grid, 2)
+    out = torch.full((B, H, grid.Tk, 64), float("nan"), device=dev)
+    kernels.sparse_attention(blocks, lut, nv, out=out)
+    torch.cuda.synchronize()
+    assert not torch.isnan(out).any()
+    rows = row_sample(nv.cpu().numpy(), 12)
+    _check_attention(out, q, k, v, frames, P, S, lut.cpu().numpy(), nv.cpu().numpy(), rows)
