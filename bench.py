@@ -37,7 +37,26 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=15.0)
     ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="run one plain device copy of this many MiB first (PMC traffic calibration)")
     return ap.parse_args()
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel`, from the committed PMC summary (profiles/), or None.
+
+    The summary holds FETCH_SIZE and WRITE_SIZE per dispatch, each divided by what the
+    same counter read for a plain copy of known size; its 'traffic_bytes_per_launch'
+    line is the sum."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_config1_pmc_traffic.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        return None
+    return None
 
 
 def retained_flops(nvalid, lut, grid):
@@ -73,6 +92,13 @@ def main():
     t0 = time.time()
     q, k, v, meta = synth.make_layer_qkv(cfg["frames"], corr=cfg["corr"])
     q, k, v = q.to(dev), k.to(dev), v.to(dev)
+    if args.calib_copy_mib:
+        src = torch.empty(args.calib_copy_mib << 18, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     print(f"[bench] inputs {tuple(q.shape)} generated in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
     frames, P, S = meta["frames"], meta["P"], meta["S"]
     grid = LayerGrid(1, 16, frames, P, S)
@@ -157,7 +183,7 @@ def main():
                    "frames": frames, "tokens": N, "heads": 16, "head_dim": 64, "sparse_ratio": sr,
                    "cdf_threshold": cdf, "realized_sparsity": round(sparsity, 4)},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": measured_traffic("k_sparse_attn"),
                      "kernel": "k_sparse_attn", "kernel_ms": round(attn_ms, 4),
                      "retained_flop_per_launch": flops_kept},
         "prep": {"ms": round(prep_ms, 4), "algorithmic_bytes": prep_bytes,
