@@ -3,15 +3,17 @@
 Workload (the metric's configuration): N = 16 frames x 1374
 tokens = 21,984, H = 16, D = 64, bf16 Q/K/V already resident in HBM, HeSS per-head
 budgets from synthetic (3,24,16) log-normal tables (lambda 0.5, layer 0), sparse_ratio
-0.7. A step is one full layer forward of the hot path: preparation (pool, key mean,
-INT8 Q/K, packed V), pooled map, budgets, selection + LUT, sparse attention with the
+0.7. A step is one full layer forward of the hot path: preparation (pools, packed
+K/V or INT8 codes), pooled map, budgets, selection + LUT, sparse attention with the
 special-query rows dense, output in storage order.
 
     python bench.py [--steps K] [--warmup W] [--config 1] [--no-cpu-baseline]
 
 Prints one JSON line. value = effective TFLOP/s = 4 N^2 H D / t (dense-equivalent);
 ms_per_step = ms per layer. roofline = the attention kernel's retained-block FLOPs over
-its own HIP-event-timed duration against the INT8 MFMA peak.
+its own HIP-event-timed duration against the dense MFMA peak of its arithmetic (QK^T
+half at the bf16 or INT8 rate, PV half at the bf16 rate); frac_of_int8_peak prices the
+same FLOPs against the INT8 peak.
 """
 
 import argparse
@@ -25,7 +27,15 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_INT8_TOPS = 5000.0   # MI355X dense INT8 MFMA, TOPS
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, GB/s
+
+
+def mfma_peak(qk_mode):
+    """Dense MFMA peak for the retained FLOPs, half of which are QK^T and half PV (bf16):
+    QK^T at the bf16 or INT8 rate, harmonic combination of the two halves."""
+    qk = PEAK_BF16_TFLOPS if qk_mode == "bf16" else PEAK_INT8_TOPS
+    return 1.0 / (0.5 / qk + 0.5 / PEAK_BF16_TFLOPS)
 
 
 def parse():
@@ -37,6 +47,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=15.0)
     ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--qk-mode", default="bf16", choices=["bf16", "i8x2", "i8"],
+                    help="QK^T operands of the attention kernel (bf16 inputs, two-term or single-term INT8)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run one plain device copy of this many MiB first (PMC traffic calibration)")
     return ap.parse_args()
@@ -127,7 +139,7 @@ def main():
     attn_mod.kernels.sparse_attention = timed_attention
 
     def step():
-        return sparse_global_attention(q, k, v, grid, budget_fn=budget_fn, out=out)
+        return sparse_global_attention(q, k, v, grid, budget_fn=budget_fn, out=out, qk_mode=args.qk_mode)
 
     for _ in range(args.warmup):
         step()
@@ -145,7 +157,8 @@ def main():
     attn_mod.kernels.sparse_attention = orig_attn
 
     # work actually done (same map every step)
-    res = sparse_global_attention(q, k, v, grid, budget_fn=budget_fn, out=out, keep_intermediates=True)
+    res = sparse_global_attention(q, k, v, grid, budget_fn=budget_fn, out=out, keep_intermediates=True,
+                                  qk_mode=args.qk_mode)
     torch.cuda.synchronize()
     lut, nvalid = res.lut.cpu().numpy(), res.nvalid.cpu().numpy()
     flops_kept = retained_flops(nvalid, lut, grid)
@@ -154,17 +167,20 @@ def main():
     sparsity = res.sparsity()
     achieved = flops_kept / (attn_ms * 1e-3) / 1e12
 
-    # preparation pass (HBM-bound): algorithmic bytes = read Q,K,V + re-read K + write INT8 Q,K + packed V
+    # preparation pass (HBM-bound). Algorithmic bytes, in units of one (N,H,64) tensor's
+    # element count: bf16 reads Q,K,V (6) and writes packed K,V (4); the INT8 modes read
+    # Q,K,V and K again (8) and write the codes (2 per term) and packed V (2).
     pe_s, pe_e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     reps = 20
     pe_s.record()
     for _ in range(reps):
-        kernels.prepare_blocks(q, k, v, grid)
+        kernels.prepare_blocks(q, k, v, grid, mode=args.qk_mode)
     pe_e.record()
     torch.cuda.synchronize()
     prep_ms = pe_s.elapsed_time(pe_e) / reps
     elems = N * 16 * 64
-    prep_bytes = elems * 2 * 4 + elems * 1 * 2 + elems * 2
+    prep_bytes = elems * {"bf16": 10, "i8x2": 14, "i8": 12}[args.qk_mode]
+    peak = mfma_peak(args.qk_mode)
 
     result = {
         "metric": "ms/global-attn layer + effective TFLOPS, N=21984 H16 D64 @70% sparse, 1 GPU",
@@ -177,13 +193,15 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 QK / bf16 PV / fp32 softmax",
+        "dtype": {"bf16": "bf16 QK", "i8x2": "two-term int8 QK", "i8": "int8 QK"}[args.qk_mode]
+                 + " / bf16 PV / fp32 softmax",
         "data": "synthetic (seeded smoothed-field Q/K/V, Hilbert order; synthetic HeSS tables)",
         "config": {"workload": f"BASELINE configs[{args.config}]: one global-attention layer, {cfg['mode']} budget",
                    "frames": frames, "tokens": N, "heads": 16, "head_dim": 64, "sparse_ratio": sr,
-                   "cdf_threshold": cdf, "realized_sparsity": round(sparsity, 4)},
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": measured_traffic("k_sparse_attn"),
+                   "cdf_threshold": cdf, "realized_sparsity": round(sparsity, 4), "qk_mode": args.qk_mode},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": round(peak, 1), "unit": "TFLOP/s",
+                     "frac": round(achieved / peak, 4), "traffic": measured_traffic(f"k_sparse_attn_{args.qk_mode}"),
+                     "frac_of_int8_peak": round(achieved / PEAK_INT8_TOPS, 4),
                      "kernel": "k_sparse_attn", "kernel_ms": round(attn_ms, 4),
                      "retained_flop_per_launch": flops_kept},
         "prep": {"ms": round(prep_ms, 4), "algorithmic_bytes": prep_bytes,

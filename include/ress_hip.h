@@ -37,12 +37,15 @@ int ress_abi_version(void);
  *   pooled_k, pooled_v [BH][kb_p][64] f32       kb_p = ceil(T_p/64) (patch keys only)
  *   v_pack [BH][kb_tot][4096] bf16, ksum [BH][kb_tot][64] f32, km [BH][64] f32
  *   q_lo / k_lo (optional, layouts of q_i8 / k_i8): split-INT8 residual codes, x ~
- *   scale*hi + scale/254*lo, used by ress_sparse_attn_fwd for a two-term INT8 QK^T. */
+ *   scale*hi + scale/254*lo, used by ress_sparse_attn_fwd for a two-term INT8 QK^T.
+ *   k_pack [BH][kb_tot][64][64] bf16 (optional): the K blocks for ress_sparse_attn_fwd_bf16.
+ * q_i8 = k_i8 = NULL selects the bf16 operands: only pooled_q/k/v, v_pack and k_pack
+ * (required) are written; q_lo, q_scale, k_lo, k_scale, ksum, km are unused. */
 int ress_prep_qkv(const void* q, const void* k, const void* v, int B, int H, int frames, int P, int S,
                   long long sqB, long long sqH, long long sqT, long long skB, long long skH, long long skT,
                   long long svB, long long svH, long long svT, void* q_i8, void* q_lo, void* q_scale,
                   void* pooled_q, void* k_i8, void* k_lo, void* k_scale, void* pooled_k, void* pooled_v,
-                  void* v_pack, void* ksum, void* km, hipStream_t stream);
+                  void* v_pack, void* k_pack, void* ksum, void* km, hipStream_t stream);
 
 /* Replaces SpargeAttn per_block_int8(q, k) (call site src/ress/models/attention.py:232,
  * patched Q scale spargeattn.patch:38-41). km [BH][64] optional (NULL = no smoothing).
@@ -117,6 +120,15 @@ int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void* q_scale
                          const void* nvalid, int B, int H, int frames, int P, int S, float sm_scale, void* out,
                          int out_dtype, long long soB, long long soH, long long soT, void* sched,
                          hipStream_t stream);
+
+/* The fused-path attention of ress_sparse_attn_fwd (same reference lines) with QK^T on
+ * the bf16 inputs (fp32 accumulation) instead of INT8 codes: q is the layer's bf16
+ * (B,H,frames*P,64) query tensor in storage order with element strides sqB/sqH/sqT,
+ * k_pack and v_pack come from ress_prep_qkv. sched: 32 int32 of device workspace. */
+int ress_sparse_attn_fwd_bf16(const void* q, long long sqB, long long sqH, long long sqT, const void* k_pack,
+                              const void* v_pack, const void* lut, const void* nvalid, int B, int H, int frames,
+                              int P, int S, float sm_scale, void* out, int out_dtype, long long soB, long long soH,
+                              long long soT, void* sched, hipStream_t stream);
 
 /* Replaces SpargeAttn qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold
  * (call src/ress/models/attention.py:238-241) with the same argument meaning; see

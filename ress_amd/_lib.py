@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(_HERE, "libress_hip.so")
 
 # argument codes: p = pointer, i = int, l = long long, f = float, d = double, s = stream
 _SIGS = {
-    "ress_prep_qkv": "pppiiiii" + "lllllllll" + "pppppppppppp" + "s",
+    "ress_prep_qkv": "pppiiiii" + "lllllllll" + "ppppppppppppp" + "s",
     "ress_per_block_int8": "pppiiii" + "llllll" + "ppppp" + "s",
     "ress_prep_kv_plain": "ppiii" + "llllll" + "ppppp" + "s",
     "ress_pooled_scores": "ppiiiifpp" + "s",
@@ -25,6 +25,7 @@ _SIGS = {
     "ress_fill_block_map": "ppplI" + "s",
     "ress_block_map_lut": "plipp" + "s",
     "ress_sparse_attn_fwd": "pppppppippiiiiifpilllps",
+    "ress_sparse_attn_fwd_bf16": "plllpppp" + "iiiiif" + "pi" + "lll" + "ps",
     "ress_qattn_block_sparse_fwd": "pppipipppppiiiilllllliiifipls",
 }
 _CT = {

@@ -3,12 +3,14 @@
 `ress_attention_forward` is the drop-in replacement of a global block's attention
 forward. Its hot path, `sparse_global_attention`, runs on the GPU kernels only:
 
-    prepare_blocks     pool Q/K/V, key mean, per-block INT8 Q/K, packed V   (prep.hip)
+    prepare_blocks     pool Q/K/V, packed K/V (bf16 mode) or key mean +
+                       per-block INT8 Q/K codes (INT8 modes)                 (prep.hip)
     pooled_scores      pooled softmax attn_full, renormalised attn_cond      (scores.hip)
     budget_fn          per-(head, q-block) counts                            (budget.hip)
     rank key           attn_cond, or ReSS restore-swap / projected / random
     select_blocks      top-n + sinks -> final_map, LUT                       (select.hip)
-    sparse_attention   INT8 QK^T / bf16 PV over the LUT, special rows dense  (attn.hip)
+    sparse_attention   QK^T (bf16 or INT8), online softmax, bf16 PV over the
+                       LUT, special rows dense                               (attn.hip)
 
 No step falls back to the CPU or to a dense PyTorch path.
 """
@@ -26,6 +28,11 @@ from ress_amd.qkv import combine_special_and_patch, compute_qkv, get_patch_token
 
 KBLK = 64
 MIN_NUM_TO_SELECT = 2  # floor on real key blocks per query row (reference attention.py:40-42)
+
+# QK^T operands of the attention kernel. bf16 is exact in the inputs and the fastest;
+# the INT8 modes reproduce the reference's SpargeAttn quantiser ("i8") or refine it
+# with a second code per element ("i8x2").
+DEFAULT_QK_MODE = "bf16"
 
 _RANDOM_SEED = 20260826  # block_criterion="random" (reference attention.py:177-196)
 _random_gens = {}
@@ -101,15 +108,16 @@ def _rank_key(block_criterion, attn_cond, attn_full, v_bar_full, counts, grid, M
 
 def sparse_global_attention(q, k, v, grid, *, num_to_select=None, budget_fn=None, perhead_budget_fn=None,
                             joint_select_fn=None, block_criterion="probability", M=None, out=None,
-                            out_dtype=torch.float32, keep_intermediates=False):
+                            out_dtype=torch.float32, keep_intermediates=False, qk_mode=None):
     """One layer's block-sparse global attention on the GPU.
 
     q, k, v: bf16 (B, H, frames*P, 64) in storage order (per frame S special then P-S
     patch tokens). Patch queries attend to the selected key blocks plus the trailing
     special blocks; special queries attend densely (reference attention.py:404-412,
-    446-491, 510-581, 625). Returns a LayerResult whose `out` is (B, H, frames*P, 64)
-    in storage order."""
-    blocks = kernels.prepare_blocks(q, k, v, grid)
+    446-491, 510-581, 625). qk_mode: the QK^T operands, "bf16" (default), "i8x2" or
+    "i8" (see kernels.Blocks); the block map does not depend on it. Returns a
+    LayerResult whose `out` is (B, H, frames*P, 64) in storage order."""
+    blocks = kernels.prepare_blocks(q, k, v, grid, mode=qk_mode or DEFAULT_QK_MODE)
     attn_full, attn_cond = kernels.pooled_scores(blocks)
     v_bar_full = blocks.pooled_v.view(grid.B, grid.H, grid.kb_p, 64)
     counts = None

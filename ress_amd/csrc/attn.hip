@@ -34,6 +34,9 @@ struct AttnArgs {
   const int8_t* k_i8;      // [BH][kb_tot][64][64]
   const float* k_scale;    // [BH][kb_tot]
   const uint16_t* v_pack;  // [BH][kb_tot][64 dims][64 permuted keys]
+  const uint16_t* q_bf;    // QK_BF16: the bf16 queries, (B,H,T,64) storage order, strides sqB/sqH/sqT
+  long long sqB, sqH, sqT;
+  const uint16_t* k_pack;  // QK_BF16: [BH][kb_tot][64 keys][64] bf16
   const int* lut;          // [BH][q_blk_total][kb_tot]
   const int* nvalid;       // [BH][q_blk_total]
   void* out;
@@ -181,44 +184,98 @@ __global__ __launch_bounds__(1024) void k_attn_schedule(const int* __restrict__ 
 // by more than this many log2 units, so P stays below 2^8; the final O / l is exact.
 #define RESS_RESCALE_LOG2 8.0f
 
+// QK^T operand modes.
+//  QK_I8    single-term per-block INT8 (the reference's SpargeAttn quantiser)
+//  QK_I8X2  two-term INT8, x ~ s*hi + s/254*lo: S = 254*(hi.hi) + hi.lo + lo.hi in
+//           int32 (the lo.lo term, below 2^-16 relative, is dropped)
+//  QK_BF16  the bf16 inputs themselves, fp32 accumulation
+enum { QK_I8 = 0, QK_I8X2 = 1, QK_BF16 = 2 };
+
+// Q operand of one lane (query qi, half g), four 16-byte registers:
+//   INT8 modes: [0],[1] = hi codes of dims 16g..16g+15 and 32+16g..; [2],[3] = lo codes
+//   QK_BF16:    [j] = dims 16j+8g .. 16j+8g+7
+// K operand LDS slots of one lane for tile t (key 32t+qi):
+//   INT8 modes: ks[0], ks[1] = hi chunks g and 2+g (lo chunks at +256 slots)
+//   QK_BF16:    ks[j] = chunk 2j+g of the 128-byte key row
+template <int QK>
+__device__ __forceinline__ void k_slots(int row, int g, int ks[4]) {
+  if constexpr (QK == QK_BF16) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ks[j] = v_slot(row, 2 * j + g);
+  } else {
+    ks[0] = k_slot(row, g);
+    ks[1] = k_slot(row, 2 + g);
+    ks[2] = ks[3] = 0;
+  }
+}
+
+__device__ __forceinline__ float pair_maxf(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return fmaxf(__int_as_float((int)r[0]), __int_as_float((int)r[1]));
+}
+
 // One 32-key tile t of the current K/V stage: S^T tile, running max with lazy rescale,
 // P = exp2(S*c - m), O^T += V^T P^T. nkt = valid keys in the tile (MASK only).
-template <bool SPLIT, bool V_F16, bool MASK>
+template <int QK, bool V_F16, bool MASK>
 __device__ __forceinline__ void attn_tile(const uint4* __restrict__ sk, const uint4* __restrict__ sv, int t, int nkt,
-                                          float c, int ka, int kb2, const v4i& qa0, const v4i& qa1, const v4i& ql0,
-                                          const v4i& ql1, int g, int qi, float& m_run, float& l_run, v16f& o0,
-                                          v16f& o1) {
-  const v4i kx0 = __builtin_bit_cast(v4i, sk[ka]);
-  const v4i kx1 = __builtin_bit_cast(v4i, sk[kb2]);
-  v16i sacc;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) sacc[r] = 0;
-  sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kx0, qa0, sacc, 0, 0, 0);
-  sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kx1, qa1, sacc, 0, 0, 0);
-  if constexpr (SPLIT) {
-    // S = 254*(hi.hi) + hi.lo + lo.hi in one accumulator: scale the hi.hi partial
-    // (|hi.hi| <= 64*127*127 < 2^23, so a 24-bit multiply is exact), then let the
-    // cross-term MFMAs accumulate on top of it.
-#pragma unroll
-    for (int r = 0; r < 16; ++r) sacc[r] = __mul24(sacc[r], 254);
-    const v4i lx0 = __builtin_bit_cast(v4i, sk[256 + ka]);
-    const v4i lx1 = __builtin_bit_cast(v4i, sk[256 + kb2]);
-    sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kx0, ql0, sacc, 0, 0, 0);
-    sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kx1, ql1, sacc, 0, 0, 0);
-    sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(lx0, qa0, sacc, 0, 0, 0);
-    sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(lx1, qa1, sacc, 0, 0, 0);
-  }
+                                          float c, const int (&ks)[4], const uint4 (&qv)[4], int g, int qi,
+                                          float& m_run, float& l_run, v16f& o0, v16f& o1) {
   // register r is key 32t + 8(r/4) + 4g + r%4 of the block
-  if constexpr (MASK) {
+  float s[16];
+  float bmax;
+  if constexpr (QK == QK_BF16) {
+    v16f sacc;
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
-      if (8 * (r >> 2) + 4 * g + (r & 3) >= nkt) sacc[r] = -2147483647 - 1;
+    for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, sk[ks[j]]),
+                                                     __builtin_bit_cast(v8bf, qv[j]), sacc, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = sacc[r];
+    if constexpr (MASK) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (8 * (r >> 2) + 4 * g + (r & 3) >= nkt) s[r] = -__builtin_huge_valf();
+    }
+    float mx = fmaxf(s[0], s[1]);
+#pragma unroll
+    for (int r = 2; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[r], s[r + 1]));
+    bmax = pair_maxf(mx) * c;
+  } else {
+    const v4i kx0 = __builtin_bit_cast(v4i, sk[ks[0]]);
+    const v4i kx1 = __builtin_bit_cast(v4i, sk[ks[1]]);
+    const v4i qa0 = __builtin_bit_cast(v4i, qv[0]), qa1 = __builtin_bit_cast(v4i, qv[1]);
+    v16i sacc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sacc[r] = 0;
+    sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kx0, qa0, sacc, 0, 0, 0);
+    sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kx1, qa1, sacc, 0, 0, 0);
+    if constexpr (QK == QK_I8X2) {
+      // scale the hi.hi partial (|hi.hi| <= 64*127*127 < 2^23, so a 24-bit multiply is
+      // exact), then let the cross-term MFMAs accumulate on top of it
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[r] = __mul24(sacc[r], 254);
+      const v4i lx0 = __builtin_bit_cast(v4i, sk[256 + ks[0]]);
+      const v4i lx1 = __builtin_bit_cast(v4i, sk[256 + ks[1]]);
+      const v4i ql0 = __builtin_bit_cast(v4i, qv[2]), ql1 = __builtin_bit_cast(v4i, qv[3]);
+      sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kx0, ql0, sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kx1, ql1, sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(lx0, qa0, sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(lx1, qa1, sacc, 0, 0, 0);
+    }
+    if constexpr (MASK) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (8 * (r >> 2) + 4 * g + (r & 3) >= nkt) sacc[r] = -2147483647 - 1;
+    }
+    int mx = max(sacc[0], sacc[1]);
+#pragma unroll
+    for (int r = 2; r < 16; r += 2) mx = max(mx, max(sacc[r], sacc[r + 1]));
+    bmax = (float)pair_max(mx) * c;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = (float)sacc[r];
   }
-  int mx = max(sacc[0], sacc[1]);
-#pragma unroll
-  for (int r = 2; r < 16; r += 2) mx = max(mx, max(sacc[r], sacc[r + 1]));
-  mx = pair_max(mx);
-  const float bmax = (float)mx * c;
   const bool need = bmax > m_run + RESS_RESCALE_LOG2;
   if (__any(need)) {
     const float m_new = need ? bmax : m_run;
@@ -234,7 +291,7 @@ __device__ __forceinline__ void attn_tile(const uint4* __restrict__ sk, const ui
   const float nm = -m_run;
   float p[16];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) p[r] = __builtin_amdgcn_exp2f(fmaf((float)sacc[r], c, nm));
+  for (int r = 0; r < 16; ++r) p[r] = __builtin_amdgcn_exp2f(fmaf(s[r], c, nm));
   if constexpr (MASK) {
 #pragma unroll
     for (int r = 0; r < 16; ++r)
@@ -261,50 +318,88 @@ __device__ __forceinline__ void attn_tile(const uint4* __restrict__ sk, const ui
   }
 }
 
-// SPLIT: two-term INT8 Q and K (x ~ s*hi + s/254*lo). S = 254*(Qhi.Khi) + (Qhi.Klo + Qlo.Khi)
-// in int32 (the lo.lo term, below 2^-16 relative, is dropped), 3 INT8 MFMAs per tile.
-template <bool SPLIT, bool V_F16, int OUT, int KCH, int STAGE>
+// K chunks (16 B) per stage: INT8 hi 256 [+ lo 256]; bf16 512.
+template <int QK>
+struct StageShape {
+  static constexpr int KCH = QK == QK_I8 ? 256 : 512;
+  static constexpr int STAGE = KCH + 512;  // + V^T 8 KiB
+};
+
+template <int QK, bool V_F16, int OUT>
 __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __restrict__ lut_all,
                                                 const int* __restrict__ nvalid, const float* __restrict__ k_scale,
                                                 uint4* __restrict__ s0, uint4* __restrict__ s1, int bh, int qb) {
+  constexpr int KCH = StageShape<QK>::KCH;
   const long long row = (long long)bh * a.q_blk_total + qb;
   const int nv = nvalid[row];
   const int* lut = lut_all + row * a.kb_tot;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, qi = l & 31;
+  const bool special = qb >= a.q_blk_p;
+  const int qbase = special ? (qb - a.q_blk_p) * 128 : qb * 128;
+  const int cnt_q = min(128, (special ? a.m.T_s : a.m.T_p) - qbase);
+  const int qrow = 32 * w + qi;
 
-  const int8_t* qsrc = a.q_i8 + (row * 128 + 32 * w + qi) * 64 + 16 * g;
-  const v4i qa0 = *reinterpret_cast<const v4i*>(qsrc);
-  const v4i qa1 = *reinterpret_cast<const v4i*>(qsrc + 32);
-  v4i ql0 = qa0, ql1 = qa1;  // residual codes (SPLIT only)
-  if constexpr (SPLIT) {
-    const int8_t* qlsrc = a.q_lo + (row * 128 + 32 * w + qi) * 64 + 16 * g;
-    ql0 = *reinterpret_cast<const v4i*>(qlsrc);
-    ql1 = *reinterpret_cast<const v4i*>(qlsrc + 32);
+  uint4 qv[4];
+  float qs;  // this row's logit scale (times log2 e); INT8 modes multiply in k_scale per block
+  if constexpr (QK == QK_BF16) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qv[j] = make_uint4(0u, 0u, 0u, 0u);
+    if (qrow < cnt_q) {
+      const int tok = special ? special_to_storage(qbase + qrow, a.m) : patch_to_storage(qbase + qrow, a.m);
+      const uint16_t* src = a.q_bf + (long long)(bh / a.H) * a.sqB + (long long)(bh % a.H) * a.sqH +
+                            (long long)tok * a.sqT + 8 * g;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qv[j] = *reinterpret_cast<const uint4*>(src + 16 * j);
+    }
+    qs = a.sm_scale_log2e;
+  } else {
+    const int8_t* qsrc = a.q_i8 + (row * 128 + qrow) * 64 + 16 * g;
+    qv[0] = *reinterpret_cast<const uint4*>(qsrc);
+    qv[1] = *reinterpret_cast<const uint4*>(qsrc + 32);
+    qv[2] = qv[0];
+    qv[3] = qv[1];
+    if constexpr (QK == QK_I8X2) {
+      const int8_t* qlsrc = a.q_lo + (row * 128 + qrow) * 64 + 16 * g;
+      qv[2] = *reinterpret_cast<const uint4*>(qlsrc);
+      qv[3] = *reinterpret_cast<const uint4*>(qlsrc + 32);
+    }
+    qs = a.q_scale[row] * a.sm_scale_log2e * (QK == QK_I8X2 ? (1.0f / 254.0f) : 1.0f);
   }
-  const float qs = a.q_scale[row] * a.sm_scale_log2e * (SPLIT ? (1.0f / 254.0f) : 1.0f);
   const float* ksc = k_scale + (long long)bh * a.kb_tot;
+  auto block_scale = [&](int kb) -> float {
+    if constexpr (QK == QK_BF16) return qs;
+    else return qs * ksc[kb];
+  };
 
-  // Stage loads are LDS-DMA: lane l of wave w fills the 16-byte slots 64w+l (K hi, K lo)
-  // and 128w+l, 128w+64+l (V), so it fetches the global chunk that the swizzle places
-  // there (the XOR swizzle is its own inverse).
+  // Stage loads are LDS-DMA: lane l of wave w fills 16-byte slots 64w+l (INT8 K hi, K lo)
+  // or 128w+l, 128w+64+l (bf16 K, V), so it fetches the global chunk that the swizzle
+  // places there (the XOR swizzles are their own inverse).
   const int kslot = 64 * w + l;
   const int ksrc = 16 * (4 * (kslot >> 2) + ((kslot & 3) ^ ((((kslot >> 2) >> 1) ^ ((kslot >> 2) >> 3)) & 3)));
   const int vslot0 = 128 * w + l, vslot1 = vslot0 + 64;
   const int vsrc0 = 16 * (8 * (vslot0 >> 3) + ((vslot0 & 7) ^ (((vslot0 >> 3) ^ (vslot0 >> 6)) & 7)));
   const int vsrc1 = 16 * (8 * (vslot1 >> 3) + ((vslot1 & 7) ^ (((vslot1 >> 3) ^ (vslot1 >> 6)) & 7)));
-  const char* kblk0 = reinterpret_cast<const char*>(a.k_i8) + (long long)bh * a.kb_tot * 4096;
-  const char* klblk0 = SPLIT ? reinterpret_cast<const char*>(a.k_lo) + (long long)bh * a.kb_tot * 4096 : nullptr;
+  const char* kblk0 = QK == QK_BF16 ? reinterpret_cast<const char*>(a.k_pack) + (long long)bh * a.kb_tot * 8192
+                                    : reinterpret_cast<const char*>(a.k_i8) + (long long)bh * a.kb_tot * 4096;
+  const char* klblk0 =
+      QK == QK_I8X2 ? reinterpret_cast<const char*>(a.k_lo) + (long long)bh * a.kb_tot * 4096 : nullptr;
   const char* vblk0 = reinterpret_cast<const char*>(a.v_pack) + (long long)bh * a.kb_tot * 8192;
   auto stage_load = [&](uint4* stage, int kb) {
     char* base = reinterpret_cast<char*>(stage);
-    gl_lds16(kblk0 + (long long)kb * 4096 + ksrc, base + 1024 * w);
-    if constexpr (SPLIT) gl_lds16(klblk0 + (long long)kb * 4096 + ksrc, base + 4096 + 1024 * w);
+    if constexpr (QK == QK_BF16) {
+      gl_lds16(kblk0 + (long long)kb * 8192 + vsrc0, base + 2048 * w);
+      gl_lds16(kblk0 + (long long)kb * 8192 + vsrc1, base + 2048 * w + 1024);
+    } else {
+      gl_lds16(kblk0 + (long long)kb * 4096 + ksrc, base + 1024 * w);
+      if constexpr (QK == QK_I8X2) gl_lds16(klblk0 + (long long)kb * 4096 + ksrc, base + 4096 + 1024 * w);
+    }
     gl_lds16(vblk0 + (long long)kb * 8192 + vsrc0, base + 16 * KCH + 2048 * w);
     gl_lds16(vblk0 + (long long)kb * 8192 + vsrc1, base + 16 * KCH + 2048 * w + 1024);
   };
-  // LDS sources of this lane's MFMA operands
-  const int ks00 = k_slot(qi, g), ks01 = k_slot(qi, 2 + g);
-  const int ks10 = k_slot(32 + qi, g), ks11 = k_slot(32 + qi, 2 + g);
+  // LDS sources of this lane's K operands, per tile
+  int ks0[4], ks1[4];
+  k_slots<QK>(qi, g, ks0);
+  k_slots<QK>(32 + qi, g, ks1);
 
   float m_run = -__builtin_huge_valf(), l_run = 0.0f;
   v16f o0, o1;
@@ -317,7 +412,7 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
 
   // the block index and scale of the next iteration are loaded one iteration ahead
   int kb = nv > 0 ? lut[0] : 0;
-  float c = nv > 0 ? qs * ksc[kb] : 0.0f;
+  float c = nv > 0 ? block_scale(kb) : 0.0f;
   // Only the sequence's last key block can be partial; LUTs are ascending, so if it is
   // kept it is the last entry. Full blocks run the unmasked loop, the partial one is
   // peeled off after it.
@@ -333,16 +428,14 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
     float cn = 0.0f;
     if (it + 1 < nv) {
       kn = lut[it + 1];
-      cn = qs * ksc[kn];
+      cn = block_scale(kn);
       stage_load(nxt, kn);
     }
-    const uint4* sk = cur;
-    const uint4* sv = cur + KCH;
     // Each 64-key block is consumed as two 32-key tiles, each a full online-softmax step
     // (S^T tile -> running max -> P -> O^T += V^T P^T), keeping one 16-register S
     // accumulator live.
-    attn_tile<SPLIT, V_F16, false>(sk, sv, 0, 32, c, ks00, ks01, qa0, qa1, ql0, ql1, g, qi, m_run, l_run, o0, o1);
-    attn_tile<SPLIT, V_F16, false>(sk, sv, 1, 32, c, ks10, ks11, qa0, qa1, ql0, ql1, g, qi, m_run, l_run, o0, o1);
+    attn_tile<QK, V_F16, false>(cur, cur + KCH, 0, 32, c, ks0, qv, g, qi, m_run, l_run, o0, o1);
+    attn_tile<QK, V_F16, false>(cur, cur + KCH, 1, 32, c, ks1, qv, g, qi, m_run, l_run, o0, o1);
     kb = kn;
     c = cn;
     wait_lds_dma();
@@ -359,21 +452,15 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
   }
   if (tail_partial) {  // kb / c already hold the last block's index and scale
     const uint4* cur = (it & 1) ? s1 : s0;
-    const uint4* sk = cur;
-    const uint4* sv = cur + KCH;
     const int nk = a.Tk - kb * 64;
-    attn_tile<SPLIT, V_F16, true>(sk, sv, 0, nk, c, ks00, ks01, qa0, qa1, ql0, ql1, g, qi, m_run, l_run, o0, o1);
-    attn_tile<SPLIT, V_F16, true>(sk, sv, 1, nk - 32, c, ks10, ks11, qa0, qa1, ql0, ql1, g, qi, m_run, l_run, o0, o1);
+    attn_tile<QK, V_F16, true>(cur, cur + KCH, 0, nk, c, ks0, qv, g, qi, m_run, l_run, o0, o1);
+    attn_tile<QK, V_F16, true>(cur, cur + KCH, 1, nk - 32, c, ks1, qv, g, qi, m_run, l_run, o0, o1);
     __syncthreads();  // the next row's prologue overwrites this stage
   }
 
   // ---- epilogue ------------------------------------------------------------
   const float lt = pair_sum(l_run);
   const float inv = (nv > 0 && lt > 0.0f) ? 1.0f / lt : 0.0f;
-  const bool special = qb >= a.q_blk_p;
-  const int qbase = special ? (qb - a.q_blk_p) * 128 : qb * 128;
-  const int cnt_q = min(128, (special ? a.m.T_s : a.m.T_p) - qbase);
-  const int qrow = 32 * w + qi;
   if (qrow >= cnt_q) return;  // this row function only; the caller's loop continues
   const int tok = special ? special_to_storage(qbase + qrow, a.m) : patch_to_storage(qbase + qrow, a.m);
   const long long off = (long long)(bh / a.H) * a.soB + (long long)(bh % a.H) * a.soH + (long long)tok * a.soT;
@@ -396,12 +483,11 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
   }
 }
 
-template <bool SPLIT, bool V_F16, int OUT>
+template <int QK, bool V_F16, int OUT>
 __global__ __launch_bounds__(256, 3) void k_sparse_attn(AttnArgs a, const int* __restrict__ lut,
                                                         const int* __restrict__ nvalid,
                                                         const float* __restrict__ k_scale) {
-  constexpr int KCH = SPLIT ? 512 : 256;  // 16-byte chunks of K per stage (hi [+ lo])
-  constexpr int STAGE = KCH + 512;        // + V 8 KiB
+  constexpr int STAGE = StageShape<QK>::STAGE;
   __shared__ __attribute__((aligned(16))) uint4 stage0[STAGE];
   __shared__ __attribute__((aligned(16))) uint4 stage1[STAGE];
   __shared__ int s_item;
@@ -417,7 +503,7 @@ __global__ __launch_bounds__(256, 3) void k_sparse_attn(AttnArgs a, const int* _
     if (item >= item_end) break;
     int bh, qb;
     item_to_row(item, a.q_blk_p, a.q_blk_total, bh, qb);
-    sparse_attn_row<SPLIT, V_F16, OUT, KCH, STAGE>(a, lut, nvalid, k_scale, stage0, stage1, bh, qb);
+    sparse_attn_row<QK, V_F16, OUT>(a, lut, nvalid, k_scale, stage0, stage1, bh, qb);
   }
 }
 
@@ -454,7 +540,7 @@ __global__ __launch_bounds__(64) void k_pack_v(const uint16_t* __restrict__ v, l
 // ============================================================================
 static int g_cu_count[64];
 
-template <bool SPLIT, bool V_F16>
+template <int QK, bool V_F16>
 static int launch_attn(const AttnArgs& a, int out_dtype, hipStream_t stream) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
@@ -469,38 +555,33 @@ static int launch_attn(const AttnArgs& a, int out_dtype, hipStream_t stream) {
   // persistent: 3 resident workgroups per CU, a multiple of the 8 XCDs
   const dim3 grid(8 * ((3 * g_cu_count[dev] + 7) / 8)), block(256);
   switch (out_dtype) {
-    case OUT_F32: hipLaunchKernelGGL((k_sparse_attn<SPLIT, V_F16, OUT_F32>), grid, block, 0, stream, a, a.lut, a.nvalid,
-                                          a.k_scale); break;
-    case OUT_BF16: hipLaunchKernelGGL((k_sparse_attn<SPLIT, V_F16, OUT_BF16>), grid, block, 0, stream, a, a.lut, a.nvalid,
-                                          a.k_scale); break;
-    default: hipLaunchKernelGGL((k_sparse_attn<SPLIT, V_F16, OUT_F16>), grid, block, 0, stream, a, a.lut, a.nvalid,
-                                          a.k_scale); break;
+    case OUT_F32:
+      hipLaunchKernelGGL((k_sparse_attn<QK, V_F16, OUT_F32>), grid, block, 0, stream, a, a.lut, a.nvalid, a.k_scale);
+      break;
+    case OUT_BF16:
+      hipLaunchKernelGGL((k_sparse_attn<QK, V_F16, OUT_BF16>), grid, block, 0, stream, a, a.lut, a.nvalid, a.k_scale);
+      break;
+    default:
+      hipLaunchKernelGGL((k_sparse_attn<QK, V_F16, OUT_F16>), grid, block, 0, stream, a, a.lut, a.nvalid, a.k_scale);
+      break;
   }
   RESS_LAUNCHED("k_sparse_attn");
   return 0;
 }
 
-static int attn_common(const void* q_i8, const void* q_lo, const void* q_scale, const void* k_i8, const void* k_lo,
-                       const void* k_scale, const void* v_pack, int v_f16, const void* lut, const void* nvalid, int B,
-                       int H, TokenMap m, int Tk, float sm_scale, void* out, int out_dtype, long long soB,
-                       long long soH, long long soT, void* sched, hipStream_t stream) {
-  RESS_REQUIRE(q_i8 && q_scale && k_i8 && k_scale && v_pack && lut && nvalid && out && sched,
-               "sparse attention: null pointer");
-  RESS_REQUIRE((q_lo == nullptr) == (k_lo == nullptr), "sparse attention: give both q_lo and k_lo, or neither");
-  RESS_REQUIRE(((uintptr_t)q_i8 & 15u) == 0 && ((uintptr_t)k_i8 & 15u) == 0 && ((uintptr_t)v_pack & 15u) == 0 &&
-                   ((uintptr_t)q_lo & 15u) == 0 && ((uintptr_t)k_lo & 15u) == 0,
-               "sparse attention: q_i8/q_lo/k_i8/k_lo/v_pack must be 16-byte aligned");
+static bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Shared argument checks and fields; the QK operands are filled in by the caller.
+static int attn_args(AttnArgs& a, const void* v_pack, const void* lut, const void* nvalid, int B, int H, TokenMap m,
+                     int Tk, float sm_scale, void* out, int out_dtype, long long soB, long long soH, long long soT,
+                     void* sched) {
+  RESS_REQUIRE(v_pack && lut && nvalid && out && sched, "sparse attention: null pointer");
+  RESS_REQUIRE(al16(v_pack), "sparse attention: v_pack must be 16-byte aligned");
   RESS_REQUIRE(out_dtype >= 0 && out_dtype <= 2, "sparse attention: out_dtype must be 0 (f32), 1 (bf16) or 2 (f16)");
   const int align = out_dtype == OUT_F32 ? 16 : 8;
   RESS_REQUIRE(((uintptr_t)out % align) == 0 && soT % 4 == 0 && soH % 4 == 0 && soB % 4 == 0,
                "sparse attention: output must be %d-byte aligned with strides a multiple of 4", align);
-  AttnArgs a;
-  a.q_i8 = (const int8_t*)q_i8;
-  a.q_lo = (const int8_t*)q_lo;
-  a.k_lo = (const int8_t*)k_lo;
-  a.q_scale = (const float*)q_scale;
-  a.k_i8 = (const int8_t*)k_i8;
-  a.k_scale = (const float*)k_scale;
+  a = AttnArgs{};
   a.v_pack = (const uint16_t*)v_pack;
   a.lut = (const int*)lut;
   a.nvalid = (const int*)nvalid;
@@ -517,8 +598,38 @@ static int attn_common(const void* q_i8, const void* q_lo, const void* q_scale, 
   a.sm_scale_log2e = sm_scale * 1.4426950408889634f;
   a.sched = (int*)sched;
   a.m = m;
-  if (q_lo) return v_f16 ? launch_attn<true, true>(a, out_dtype, stream) : launch_attn<true, false>(a, out_dtype, stream);
-  return v_f16 ? launch_attn<false, true>(a, out_dtype, stream) : launch_attn<false, false>(a, out_dtype, stream);
+  return 0;
+}
+
+static int attn_common(const void* q_i8, const void* q_lo, const void* q_scale, const void* k_i8, const void* k_lo,
+                       const void* k_scale, const void* v_pack, int v_f16, const void* lut, const void* nvalid, int B,
+                       int H, TokenMap m, int Tk, float sm_scale, void* out, int out_dtype, long long soB,
+                       long long soH, long long soT, void* sched, hipStream_t stream) {
+  RESS_REQUIRE(q_i8 && q_scale && k_i8 && k_scale, "sparse attention: null pointer");
+  RESS_REQUIRE((q_lo == nullptr) == (k_lo == nullptr), "sparse attention: give both q_lo and k_lo, or neither");
+  RESS_REQUIRE(al16(q_i8) && al16(k_i8) && al16(q_lo) && al16(k_lo),
+               "sparse attention: q_i8/q_lo/k_i8/k_lo must be 16-byte aligned");
+  AttnArgs a;
+  if (attn_args(a, v_pack, lut, nvalid, B, H, m, Tk, sm_scale, out, out_dtype, soB, soH, soT, sched)) return -1;
+  a.q_i8 = (const int8_t*)q_i8;
+  a.q_lo = (const int8_t*)q_lo;
+  a.k_lo = (const int8_t*)k_lo;
+  a.q_scale = (const float*)q_scale;
+  a.k_i8 = (const int8_t*)k_i8;
+  a.k_scale = (const float*)k_scale;
+  if (q_lo)
+    return v_f16 ? launch_attn<QK_I8X2, true>(a, out_dtype, stream) : launch_attn<QK_I8X2, false>(a, out_dtype, stream);
+  return v_f16 ? launch_attn<QK_I8, true>(a, out_dtype, stream) : launch_attn<QK_I8, false>(a, out_dtype, stream);
+}
+
+static TokenMap layer_map(int frames, int P, int S) {
+  TokenMap m;
+  m.P = P;
+  m.S = S;
+  m.HW = P - S;
+  m.T_p = frames * (P - S);
+  m.T_s = frames * S;
+  return m;
 }
 
 // Fused-path attention over the ReSS token split: queries are the patch tokens
@@ -535,14 +646,33 @@ RESS_API int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void
                                   int out_dtype, long long soB, long long soH, long long soT, void* sched,
                                   hipStream_t stream) {
   RESS_REQUIRE(B > 0 && H > 0 && frames > 0 && P > S && S >= 0, "ress_sparse_attn_fwd: bad geometry");
-  TokenMap m;
-  m.P = P;
-  m.S = S;
-  m.HW = P - S;
-  m.T_p = frames * (P - S);
-  m.T_s = frames * S;
-  return attn_common(q_i8, q_lo, q_scale, k_i8, k_lo, k_scale, v_pack, v_f16, lut, nvalid, B, H, m, frames * P,
-                     sm_scale, out, out_dtype, soB, soH, soT, sched, stream);
+  return attn_common(q_i8, q_lo, q_scale, k_i8, k_lo, k_scale, v_pack, v_f16, lut, nvalid, B, H,
+                     layer_map(frames, P, S), frames * P, sm_scale, out, out_dtype, soB, soH, soT, sched, stream);
+}
+
+// The same fused-path attention with QK^T on the bf16 inputs themselves (fp32
+// accumulation): q is the layer's bf16 query tensor (B,H,frames*P,64) in storage order
+// with element strides sqB/sqH/sqT, k_pack the bf16 key blocks ress_prep_qkv writes,
+// v_pack its packed bf16 V. No quantisation error enters the logits; the online
+// softmax, P rounding and PV product are those of ress_sparse_attn_fwd.
+RESS_API int ress_sparse_attn_fwd_bf16(const void* q, long long sqB, long long sqH, long long sqT, const void* k_pack,
+                                       const void* v_pack, const void* lut, const void* nvalid, int B, int H,
+                                       int frames, int P, int S, float sm_scale, void* out, int out_dtype,
+                                       long long soB, long long soH, long long soT, void* sched, hipStream_t stream) {
+  RESS_REQUIRE(B > 0 && H > 0 && frames > 0 && P > S && S >= 0, "ress_sparse_attn_fwd_bf16: bad geometry");
+  RESS_REQUIRE(q && k_pack, "ress_sparse_attn_fwd_bf16: null pointer");
+  RESS_REQUIRE(al16(q) && al16(k_pack) && sqT % 8 == 0 && sqH % 8 == 0 && sqB % 8 == 0,
+               "ress_sparse_attn_fwd_bf16: q/k_pack must be 16-byte aligned, q strides a multiple of 8");
+  AttnArgs a;
+  if (attn_args(a, v_pack, lut, nvalid, B, H, layer_map(frames, P, S), frames * P, sm_scale, out, out_dtype, soB, soH,
+                soT, sched))
+    return -1;
+  a.q_bf = (const uint16_t*)q;
+  a.sqB = sqB;
+  a.sqH = sqH;
+  a.sqT = sqT;
+  a.k_pack = (const uint16_t*)k_pack;
+  return launch_attn<QK_BF16, false>(a, out_dtype, stream);
 }
 
 static long long qattn_vpack_bytes(int B, int H, int Tk) { return (long long)B * H * cdiv(Tk, 64) * 4096 * 2; }

@@ -80,8 +80,6 @@ __global__ __launch_bounds__(64) void k_prep_q(const uint16_t* __restrict__ q, S
       }
     }
   }
-  amax = wave_max(amax);
-  const float scale = amax / 127.0f;
 #pragma unroll
   for (int c = 0; c < 8; ++c) acc[c] = sum8_tree(acc[c]);
   if (!special && j == 0) {
@@ -89,6 +87,9 @@ __global__ __launch_bounds__(64) void k_prep_q(const uint16_t* __restrict__ q, S
 #pragma unroll
     for (int c = 0; c < 8; ++c) pq[c] = acc[c] / (float)cnt;
   }
+  if (!q_i8) return;  // pooling only (the bf16 attention operands read Q directly)
+  amax = wave_max(amax);
+  const float scale = amax / 127.0f;
   if (lane == 0) q_scale[(long long)bh * q_blk_total + qb] = scale;
   const long long off = (((long long)bh * q_blk_total + qb) * 128) * 64 + dg * 8;
 #pragma unroll
@@ -102,7 +103,8 @@ __global__ __launch_bounds__(64) void k_prep_q(const uint16_t* __restrict__ q, S
 
 // ----------------------------------------------------------------------------
 // K/V blocks over the kernel key grid (patch keys then special keys).
-//  ksum   [BH][kb_tot][64]  full-block K sums (SUM8x), for the key mean
+//  ksum   [BH][kb_tot][64]  full-block K sums (SUM8x), for the key mean (or null)
+//  k_pack [BH][kb_tot][64 keys][64] bf16 row-major K blocks (or null)
 //  pooled_k [BH][kb_p][64]  patch-only K means (the scoring grid)
 //  pooled_v [BH][kb_p][64]  patch-only V means (ReSS's v_bar)
 //  v_pack [BH][kb_tot][64 dims][64 keys]  bf16, keys permuted inside every group of
@@ -111,7 +113,8 @@ __global__ __launch_bounds__(64) void k_prep_q(const uint16_t* __restrict__ q, S
 __global__ __launch_bounds__(64) void k_prep_kv(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                                                 Strides sk, Strides sv, TokenMap m, int Tk, int kb_tot, int kb_p,
                                                 float* __restrict__ ksum, float* __restrict__ pooled_k,
-                                                float* __restrict__ pooled_v, uint16_t* __restrict__ v_pack) {
+                                                float* __restrict__ pooled_v, uint16_t* __restrict__ v_pack,
+                                                uint16_t* __restrict__ k_pack) {
   __shared__ uint16_t vt[64 * 64];
   const int kb = blockIdx.x, bh = blockIdx.y, lane = threadIdx.x;
   const int j = lane >> 3, dg = lane & 7;
@@ -127,10 +130,10 @@ __global__ __launch_bounds__(64) void k_prep_kv(const uint16_t* __restrict__ k, 
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int t = 8 * i + j;
-    uint4 rv = make_uint4(0u, 0u, 0u, 0u);
+    uint4 rv = make_uint4(0u, 0u, 0u, 0u), rk = rv;
     if (t < cnt) {
       const int tok = key_to_storage(base + t, m);
-      const uint4 rk = *reinterpret_cast<const uint4*>(ksrc + (long long)tok * sk.t);
+      rk = *reinterpret_cast<const uint4*>(ksrc + (long long)tok * sk.t);
       rv = *reinterpret_cast<const uint4*>(vsrc + (long long)tok * sv.t);
       float xk[8], xv[8];
       unpack_bf16x8(rk, xk);
@@ -145,6 +148,8 @@ __global__ __launch_bounds__(64) void k_prep_kv(const uint16_t* __restrict__ k, 
         }
       }
     }
+    if (k_pack)  // row-major bf16 K block, zero past the sequence end
+      *reinterpret_cast<uint4*>(k_pack + (((long long)bh * kb_tot + kb) * 64 + t) * 64 + dg * 8) = rk;
     // transpose into LDS: vt[dim][perm(key)]
     const int u = t & 15;
     const int pos = (t & ~15) + 8 * ((u >> 2) & 1) + 4 * (u >> 3) + (u & 3);
@@ -162,9 +167,11 @@ __global__ __launch_bounds__(64) void k_prep_kv(const uint16_t* __restrict__ k, 
     vp[c] = sum8_tree(vp[c]);
   }
   if (j == 0) {
-    float* ks = ksum + ((long long)bh * kb_tot + kb) * 64 + dg * 8;
+    if (ksum) {
+      float* ks = ksum + ((long long)bh * kb_tot + kb) * 64 + dg * 8;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) ks[c] = ka[c];
+      for (int c = 0; c < 8; ++c) ks[c] = ka[c];
+    }
     if (kb < kb_p) {
       float* pk = pooled_k + ((long long)bh * kb_p + kb) * 64 + dg * 8;
       float* pv = pooled_v + ((long long)bh * kb_p + kb) * 64 + dg * 8;
@@ -257,20 +264,28 @@ static TokenMap make_map(int frames, int P, int S) {
 
 // Fused preparation of one layer's Q/K/V for the ReSS forward (reference
 // attention.py:398-491 + 226-233). Inputs are the backbone's bf16 Q/K/V in storage
-// order with element strides (sB, sH, sT); D = 64 with unit stride. q_lo/k_lo (same
-// layouts as q_i8/k_i8) receive the split-INT8 residual codes, or are null.
+// order with element strides (sB, sH, sT); D = 64 with unit stride.
+//  * INT8 operands (q_i8 and k_i8 set): codes, scales, key mean; q_lo/k_lo (same
+//    layouts as q_i8/k_i8) receive the split-INT8 residual codes, or are null.
+//  * bf16 operands (q_i8 and k_i8 null): only the pools, v_pack and k_pack are
+//    written; q_lo, q_scale, k_lo, k_scale, ksum and km are unused (may be null).
+// k_pack [BH][kb_tot][64 keys][64] bf16 (keys in kernel order, zero-padded) is
+// written whenever it is non-null.
 RESS_API int ress_prep_qkv(const void* q, const void* k, const void* v, int B, int H, int frames, int P, int S,
                            long long sqB, long long sqH, long long sqT, long long skB, long long skH, long long skT,
                            long long svB, long long svH, long long svT, void* q_i8, void* q_lo, void* q_scale,
                            void* pooled_q, void* k_i8, void* k_lo, void* k_scale, void* pooled_k, void* pooled_v,
-                           void* v_pack, void* ksum, void* km, hipStream_t stream) {
+                           void* v_pack, void* k_pack, void* ksum, void* km, hipStream_t stream) {
   RESS_REQUIRE(B > 0 && H > 0 && frames > 0 && P > S && S >= 0, "ress_prep_qkv: bad geometry B=%d H=%d F=%d P=%d S=%d",
                B, H, frames, P, S);
-  RESS_REQUIRE(q && k && v && q_i8 && q_scale && pooled_q && k_i8 && k_scale && pooled_k && pooled_v && v_pack && ksum &&
-                   km,
-               "ress_prep_qkv: null pointer");
+  RESS_REQUIRE(q && k && v && pooled_q && pooled_k && pooled_v && v_pack, "ress_prep_qkv: null pointer");
+  const bool quant = q_i8 != nullptr;
+  RESS_REQUIRE((q_i8 == nullptr) == (k_i8 == nullptr), "ress_prep_qkv: give both q_i8 and k_i8, or neither");
+  RESS_REQUIRE(!quant || (q_scale && k_scale && ksum && km), "ress_prep_qkv: INT8 operands need q_scale, k_scale, ksum, km");
+  RESS_REQUIRE(quant || k_pack, "ress_prep_qkv: bf16 operands need k_pack");
+  RESS_REQUIRE(quant || (!q_lo && !k_lo), "ress_prep_qkv: q_lo/k_lo need the INT8 operands");
   RESS_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(v_pack) && aligned16(q_i8) && aligned16(k_i8) &&
-                   aligned16(q_lo) && aligned16(k_lo),
+                   aligned16(q_lo) && aligned16(k_lo) && aligned16(k_pack),
                "ress_prep_qkv: tensors must be 16-byte aligned");
   RESS_REQUIRE(sqT % 8 == 0 && skT % 8 == 0 && svT % 8 == 0 && sqH % 8 == 0 && skH % 8 == 0 && svH % 8 == 0 &&
                    sqB % 8 == 0 && skB % 8 == 0 && svB % 8 == 0,
@@ -281,12 +296,16 @@ RESS_API int ress_prep_qkv(const void* q, const void* k, const void* v, int B, i
   const int q_blk_p = cdiv(m.T_p, 128), q_blk_s = cdiv(m.T_s, 128);
   const int kb_tot = cdiv(Tk, 64), kb_p = cdiv(m.T_p, 64);
   Strides sq{sqB, sqH, sqT, H}, sk{skB, skH, skT, H}, sv{svB, svH, svT, H};
-  hipLaunchKernelGGL(k_prep_q, dim3(q_blk_p + q_blk_s, BH), dim3(64), 0, stream, (const uint16_t*)q, sq, m, q_blk_p,
-                     q_blk_p + q_blk_s, (int8_t*)q_i8, (int8_t*)q_lo, (float*)q_scale, (float*)pooled_q);
+  // without codes only the patch blocks (the pooled ones) have work
+  hipLaunchKernelGGL(k_prep_q, dim3(quant ? q_blk_p + q_blk_s : q_blk_p, BH), dim3(64), 0, stream, (const uint16_t*)q,
+                     sq, m, q_blk_p, q_blk_p + q_blk_s, (int8_t*)q_i8, (int8_t*)q_lo, (float*)q_scale,
+                     (float*)pooled_q);
   RESS_LAUNCHED("k_prep_q");
   hipLaunchKernelGGL(k_prep_kv, dim3(kb_tot, BH), dim3(64), 0, stream, (const uint16_t*)k, (const uint16_t*)v, sk, sv,
-                     m, Tk, kb_tot, kb_p, (float*)ksum, (float*)pooled_k, (float*)pooled_v, (uint16_t*)v_pack);
+                     m, Tk, kb_tot, kb_p, (float*)(quant ? ksum : nullptr), (float*)pooled_k, (float*)pooled_v,
+                     (uint16_t*)v_pack, (uint16_t*)k_pack);
   RESS_LAUNCHED("k_prep_kv");
+  if (!quant) return 0;
   hipLaunchKernelGGL(k_key_mean, dim3(BH), dim3(64), 0, stream, (const float*)ksum, kb_tot, Tk, (float*)km);
   RESS_LAUNCHED("k_key_mean");
   hipLaunchKernelGGL(k_quant_k, dim3(kb_tot, BH), dim3(64), 0, stream, (const uint16_t*)k, sk, m, Tk, kb_tot,
@@ -340,7 +359,8 @@ RESS_API int ress_prep_kv_plain(const void* k, const void* v, int B, int H, int 
   TokenMap mk = make_map(1, Tk, 0);
   Strides sk{skB, skH, skT, H}, sv{svB, svH, svT, H};
   hipLaunchKernelGGL(k_prep_kv, dim3(nk, BH), dim3(64), 0, stream, (const uint16_t*)k, (const uint16_t*)v, sk, sv, mk,
-                     Tk, nk, nk, (float*)ksum, (float*)pooled_k, (float*)pooled_v, (uint16_t*)v_pack);
+                     Tk, nk, nk, (float*)ksum, (float*)pooled_k, (float*)pooled_v, (uint16_t*)v_pack,
+                     (uint16_t*)nullptr);
   RESS_LAUNCHED("k_prep_kv");
   hipLaunchKernelGGL(k_key_mean, dim3(BH), dim3(64), 0, stream, (const float*)ksum, nk, Tk, (float*)km);
   RESS_LAUNCHED("k_key_mean");

@@ -87,13 +87,22 @@ class LayerGrid:
         return self.kb_tot - self.n_cand
 
 
+QK_MODES = ("bf16", "i8x2", "i8")
+
+
 @dataclass
 class Blocks:
-    """Output of the preparation pass (see ress_prep_qkv)."""
+    """Output of the preparation pass (see ress_prep_qkv). `mode` names the QK^T
+    operands the attention kernel will use:
+      "bf16"  the bf16 inputs themselves (q, k_pack); no codes are written
+      "i8x2"  two-term INT8 codes (q_i8 + q_lo, k_i8 + k_lo) with per-block scales
+      "i8"    the reference's single-term per-block INT8 codes (q_i8, k_i8)"""
 
     grid: LayerGrid
+    mode: str
+    q: torch.Tensor  # the bf16 queries (storage order), read directly in "bf16" mode
     q_i8: torch.Tensor
-    q_lo: torch.Tensor  # split-INT8 residual codes, or None
+    q_lo: torch.Tensor
     q_scale: torch.Tensor
     pooled_q: torch.Tensor
     k_i8: torch.Tensor
@@ -102,6 +111,7 @@ class Blocks:
     pooled_k: torch.Tensor
     pooled_v: torch.Tensor
     v_pack: torch.Tensor
+    k_pack: torch.Tensor
     ksum: torch.Tensor
     km: torch.Tensor
 
@@ -117,36 +127,43 @@ def _check_qkv(t, name, grid):
         raise ValueError(f"{name} must have a unit-stride head dim")
 
 
-def prepare_blocks(q, k, v, grid, split=True):
-    """Pool, quantise and pack one layer's Q/K/V (bf16, storage order). split=True also
-    writes the split-INT8 residual codes (two-term QK^T in the attention kernel);
-    split=False gives the reference's single-term per-block INT8 only."""
+def prepare_blocks(q, k, v, grid, mode="bf16", split=None):
+    """Pool and pack one layer's Q/K/V (bf16, storage order) for the attention mode
+    `mode` (see Blocks). `split` is the older spelling: True = "i8x2", False = "i8"."""
+    if split is not None:
+        mode = "i8x2" if split else "i8"
+    if mode not in QK_MODES:
+        raise ValueError(f"mode must be one of {QK_MODES}, got {mode!r}")
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
         _check_qkv(t, n, grid)
     dev = q.device
     BH = grid.BH
+    quant = mode != "bf16"
     e = lambda *s, dt=torch.float32: torch.empty(*s, dtype=dt, device=dev)  # noqa: E731
     b = Blocks(
         grid=grid,
-        q_i8=e(BH, grid.q_blk_total, KS_Q, HEAD_DIM, dt=torch.int8),
-        q_lo=e(BH, grid.q_blk_total, KS_Q, HEAD_DIM, dt=torch.int8) if split else None,
-        q_scale=e(BH, grid.q_blk_total),
+        mode=mode,
+        q=q,
+        q_i8=e(BH, grid.q_blk_total, KS_Q, HEAD_DIM, dt=torch.int8) if quant else None,
+        q_lo=e(BH, grid.q_blk_total, KS_Q, HEAD_DIM, dt=torch.int8) if mode == "i8x2" else None,
+        q_scale=e(BH, grid.q_blk_total) if quant else None,
         pooled_q=e(BH, grid.q_blk_p, HEAD_DIM),
-        k_i8=e(BH, grid.kb_tot, KS_K, HEAD_DIM, dt=torch.int8),
-        k_lo=e(BH, grid.kb_tot, KS_K, HEAD_DIM, dt=torch.int8) if split else None,
-        k_scale=e(BH, grid.kb_tot),
+        k_i8=e(BH, grid.kb_tot, KS_K, HEAD_DIM, dt=torch.int8) if quant else None,
+        k_lo=e(BH, grid.kb_tot, KS_K, HEAD_DIM, dt=torch.int8) if mode == "i8x2" else None,
+        k_scale=e(BH, grid.kb_tot) if quant else None,
         pooled_k=e(BH, grid.kb_p, HEAD_DIM),
         pooled_v=e(BH, grid.kb_p, HEAD_DIM),
         v_pack=e(BH, grid.kb_tot, 4096, dt=torch.bfloat16),
-        ksum=e(BH, grid.kb_tot, HEAD_DIM),
-        km=e(BH, HEAD_DIM),
+        k_pack=None if quant else e(BH, grid.kb_tot, KS_K, HEAD_DIM, dt=torch.bfloat16),
+        ksum=e(BH, grid.kb_tot, HEAD_DIM) if quant else None,
+        km=e(BH, HEAD_DIM) if quant else None,
     )
     P = _lib.ptr
     _lib.call(
         "ress_prep_qkv", P(q), P(k), P(v), grid.B, grid.H, grid.frames, grid.P, grid.S,
         *q.stride()[:3], *k.stride()[:3], *v.stride()[:3],
         P(b.q_i8), P(b.q_lo), P(b.q_scale), P(b.pooled_q), P(b.k_i8), P(b.k_lo), P(b.k_scale), P(b.pooled_k),
-        P(b.pooled_v), P(b.v_pack), P(b.ksum), P(b.km), _lib.stream_handle(dev))
+        P(b.pooled_v), P(b.v_pack), P(b.k_pack), P(b.ksum), P(b.km), _lib.stream_handle(dev))
     return b
 
 
@@ -240,14 +257,19 @@ def sparse_attention(blocks, lut, nvalid, out=None, out_dtype=torch.float32):
     """Block-sparse attention over the prepared blocks; returns (B,H,frames*P,64) in
     storage order (patch rows sparse, special rows dense)."""
     g = blocks.grid
-    dev = blocks.q_i8.device
+    dev = blocks.pooled_q.device
     if out is None:
         out = torch.empty(g.B, g.H, g.Tk, HEAD_DIM, dtype=out_dtype, device=dev)
     code = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[out.dtype]
     sched = torch.empty(32, dtype=torch.int32, device=dev)
-    _lib.call("ress_sparse_attn_fwd", _lib.ptr(blocks.q_i8), _lib.ptr(blocks.q_lo), _lib.ptr(blocks.q_scale),
-              _lib.ptr(blocks.k_i8), _lib.ptr(blocks.k_lo), _lib.ptr(blocks.k_scale), _lib.ptr(blocks.v_pack), 0,
-              _lib.ptr(lut), _lib.ptr(nvalid), g.B, g.H,
-              g.frames, g.P, g.S, 1.0 / math.sqrt(HEAD_DIM), _lib.ptr(out), code, *out.stride()[:3], _lib.ptr(sched),
-              _lib.stream_handle(dev))
+    P = _lib.ptr
+    sm = 1.0 / math.sqrt(HEAD_DIM)
+    if blocks.mode == "bf16":
+        _lib.call("ress_sparse_attn_fwd_bf16", P(blocks.q), *blocks.q.stride()[:3], P(blocks.k_pack),
+                  P(blocks.v_pack), P(lut), P(nvalid), g.B, g.H, g.frames, g.P, g.S, sm, P(out), code,
+                  *out.stride()[:3], P(sched), _lib.stream_handle(dev))
+    else:
+        _lib.call("ress_sparse_attn_fwd", P(blocks.q_i8), P(blocks.q_lo), P(blocks.q_scale), P(blocks.k_i8),
+                  P(blocks.k_lo), P(blocks.k_scale), P(blocks.v_pack), 0, P(lut), P(nvalid), g.B, g.H,
+                  g.frames, g.P, g.S, sm, P(out), code, *out.stride()[:3], P(sched), _lib.stream_handle(dev))
     return out

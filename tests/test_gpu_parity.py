@@ -66,12 +66,30 @@ def layer(request, dev):
 def test_prep_bit_exact(layer, dev):
     name, q, k, v, frames, P, S, H = layer
     g = LayerGrid(1, H, frames, P, S)
-    blocks = kernels.prepare_blocks(q.to(dev), k.to(dev), v.to(dev), g)
+    blocks = kernels.prepare_blocks(q.to(dev), k.to(dev), v.to(dev), g, mode="i8x2")
     torch.cuda.synchronize()
     o = oracle.prep_qkv(q, k, v, frames, P, S)
     for field in ("q_i8", "q_lo", "q_scale", "pooled_q", "k_i8", "k_lo", "k_scale", "pooled_k", "pooled_v", "ksum", "km"):
         assert _bits_equal(_np(getattr(blocks, field)), o[field]), field
     assert _bits_equal(_np(blocks.v_pack), o["v_pack"])
+
+
+def test_prep_bf16_operands(layer, dev):
+    """bf16 mode: the pools and v_pack equal the INT8 modes' (oracle) bit for bit, and
+    k_pack is K in kernel key order cat(patch, special), zero-padded to whole blocks."""
+    name, q, k, v, frames, P, S, H = layer
+    g = LayerGrid(1, H, frames, P, S)
+    blocks = kernels.prepare_blocks(q.to(dev), k.to(dev), v.to(dev), g, mode="bf16")
+    torch.cuda.synchronize()
+    assert blocks.q_i8 is None and blocks.k_i8 is None
+    o = oracle.prep_qkv(q, k, v, frames, P, S)
+    for field in ("pooled_q", "pooled_k", "pooled_v", "v_pack"):
+        assert _bits_equal(_np(getattr(blocks, field)), o[field]), field
+    kp, ks = ref.split_tokens(k, frames, P, S)
+    keys = kp if ks is None else torch.cat([kp, ks], dim=-2)
+    want = torch.zeros(H, g.kb_tot * 64, 64, dtype=torch.bfloat16)
+    want[:, :g.Tk] = keys[0]
+    assert np.array_equal(_np(blocks.k_pack).reshape(H, -1, 64), _np(want))
 
 
 def test_pooled_scores_bit_exact(layer, dev):
@@ -160,27 +178,29 @@ def _check_attention(out, q, k, v, frames, P, S, lut, nvalid, rows):
     return worst, cos_min
 
 
-def test_attention_matches_fp32_masked_softmax(layer, dev):
+@pytest.mark.parametrize("mode", ["bf16", "i8x2"])
+def test_attention_matches_fp32_masked_softmax(layer, mode, dev):
     name, q, k, v, frames, P, S, H = layer
     g = LayerGrid(1, H, frames, P, S)
     o = oracle_layer(q, k, v, frames, P, S, sparse_ratio=0.5, cdf_threshold=0.9, H=H)
-    blocks = kernels.prepare_blocks(q.to(dev), k.to(dev), v.to(dev), g)
+    blocks = kernels.prepare_blocks(q.to(dev), k.to(dev), v.to(dev), g, mode=mode)
     lut = torch.from_numpy(o["lut"].reshape(g.BH, g.q_blk_total, g.kb_tot)).to(dev)
     nv = torch.from_numpy(o["nvalid"]).to(dev)
     out = kernels.sparse_attention(blocks, lut, nv)
     torch.cuda.synchronize()
     rows = row_sample(o["nvalid"], 12 if name == "vggt_f4" else 30)
     w, c = _check_attention(out, q, k, v, frames, P, S, o["lut"], o["nvalid"], rows)
-    print(f"[{name}] attention max-abs {w:.3e} min-cos {c:.6f}")
+    print(f"[{name} {mode}] attention max-abs {w:.3e} min-cos {c:.6f}")
 
 
+@pytest.mark.parametrize("mode", ["bf16", "i8x2"])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
-def test_attention_low_precision_outputs(out_dtype, dev):
+def test_attention_low_precision_outputs(out_dtype, mode, dev):
     frames, P, S, H = 2, 200, 4, 2
     q, k, v = _rand_layer(frames, P, S, H, seed=11)
     g = LayerGrid(1, H, frames, P, S)
     o = oracle_layer(q, k, v, frames, P, S, sparse_ratio=0.5, H=H)
-    blocks = kernels.prepare_blocks(q.to(dev), k.to(dev), v.to(dev), g)
+    blocks = kernels.prepare_blocks(q.to(dev), k.to(dev), v.to(dev), g, mode=mode)
     lut = torch.from_numpy(o["lut"]).to(dev)
     nv = torch.from_numpy(o["nvalid"]).to(dev)
     out32 = kernels.sparse_attention(blocks, lut, nv)
@@ -194,8 +214,8 @@ def test_attention_low_precision_outputs(out_dtype, dev):
         assert torch.allclose(out.float(), out32, rtol=2.0 ** -10, atol=2.0 ** -24)
 
 
-@pytest.mark.parametrize("cfg", ["sparse_vggt_f4", "hess_f16"])
-def test_layer_pipeline_matches_oracle(cfg, dev):
+@pytest.mark.parametrize("cfg,mode", [("sparse_vggt_f4", "bf16"), ("hess_f16", "bf16"), ("hess_f16", "i8x2")])
+def test_layer_pipeline_matches_oracle(cfg, mode, dev):
     if cfg == "sparse_vggt_f4":
         frames, sr, cdf, hess = 4, 0.5, 0.9, False
     else:
@@ -211,7 +231,8 @@ def test_layer_pipeline_matches_oracle(cfg, dev):
         bud = budget.UniformBudget()
         head_scores = None
     res = sparse_global_attention(q.to(dev), k.to(dev), v.to(dev), g,
-                                  budget_fn=lambda a: bud.num_to_select(0, a, sr, cdf, 1.0), keep_intermediates=True)
+                                  budget_fn=lambda a: bud.num_to_select(0, a, sr, cdf, 1.0), keep_intermediates=True,
+                                  qk_mode=mode)
     torch.cuda.synchronize()
     o = oracle_layer(q, k, v, frames, P, S, sparse_ratio=sr, cdf_threshold=cdf, head_scores=head_scores)
     assert np.array_equal(_np(res.counts).reshape(o["counts"].shape), o["counts"])
@@ -221,11 +242,12 @@ def test_layer_pipeline_matches_oracle(cfg, dev):
     print(f"[{cfg}] realized sparsity {sparsity:.4f}")
     rows = row_sample(o["nvalid"], 10)
     w, c = _check_attention(res.out, q, k, v, frames, P, S, o["lut"], o["nvalid"], rows)
-    print(f"[{cfg}] attention max-abs {w:.3e} min-cos {c:.6f}")
+    print(f"[{cfg} {mode}] attention max-abs {w:.3e} min-cos {c:.6f}")
 
 
+@pytest.mark.parametrize("mode", ["bf16", "i8x2"])
 @pytest.mark.parametrize("B,H,frames", [(2, 16, 3), (1, 5, 2), (1, 1, 1)])
-def test_attention_writes_every_row(B, H, frames, dev):
+def test_attention_writes_every_row(B, H, frames, mode, dev):
     """The persistent row schedule covers every (batch, head, q-block) exactly once:
     a NaN-filled output has no NaN left, and rows match the per-row fp32 reference."""
     P, S = 203, 5
@@ -233,7 +255,7 @@ def test_attention_writes_every_row(B, H, frames, dev):
     mk = lambda: torch.randn(B, H, frames * P, 64, generator=g).to(torch.bfloat16)  # noqa: E731
     q, k, v = mk(), mk(), mk()
     grid = LayerGrid(B, H, frames, P, S)
-    blocks = kernels.prepare_blocks(q.to(dev), k.to(dev), v.to(dev), grid)
+    blocks = kernels.prepare_blocks(q.to(dev), k.to(dev), v.to(dev), grid, mode=mode)
     rng = np.random.default_rng(1)
     keys = torch.from_numpy(rng.random((B, H, grid.q_blk_p, grid.n_cand)).astype(np.float32)).to(dev)
     counts = torch.from_numpy(rng.integers(0, grid.n_cand + 1, (B, H, grid.q_blk_p)).astype(np.int32)).to(dev)
