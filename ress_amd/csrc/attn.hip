@@ -14,11 +14,13 @@
 //   online softmax in the exp2 domain, scale folded into one fma per score
 //   O^T (64 dims x 32 queries) += V^T . P^T    4 x v_mfma_f32_32x32x16_{bf16,f16}
 // The S^T accumulator layout puts one query per lane, so P feeds the PV MFMA from
-// registers; V is pre-packed (prep.hip) with keys permuted to match. K/V tiles are
-// double-buffered in LDS. Work items are mapped XCD-major: hardware workgroup x runs
+// registers; V is pre-packed (prep.hip) with keys permuted to match. K/V tiles go
+// through three LDS stages filled by LDS-DMA two blocks ahead. Work items are mapped XCD-major: hardware workgroup x runs
 // on XCD x%8, and consecutive workgroups of one XCD walk the rows of one head so
 // that head's K/V stay in that XCD's L2.
 #include "common.h"
+
+#include <type_traits>
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -86,6 +88,22 @@ __device__ __forceinline__ void gl_lds16(const void* src, void* lds_base) {
                                    (void __attribute__((address_space(3)))*)lds_base, 16, 0, 0);
 }
 __device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Barrier between pipeline steps. __syncthreads() would also wait for every outstanding
+// global access (vmcnt(0)), i.e. for the DMA just started two blocks ahead. Here the
+// DMA the next step reads has been waited for explicitly (wait_lds_dma_but), this
+// wave's LDS reads are complete (lgkmcnt(0)), and the empty asm statements keep the
+// compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// all but the newest N vector-memory operations of this wave complete (loads retire in
+// issue order): waits for older stages while the newest stage's DMA stays in flight
+template <int N>
+__device__ __forceinline__ void wait_lds_dma_but() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
@@ -214,15 +232,13 @@ __device__ __forceinline__ float pair_maxf(float x) {
   return fmaxf(__int_as_float((int)r[0]), __int_as_float((int)r[1]));
 }
 
-// One 32-key tile t of the current K/V stage: S^T tile, running max with lazy rescale,
-// P = exp2(S*c - m), O^T += V^T P^T. nkt = valid keys in the tile (MASK only).
-template <int QK, bool V_F16, bool MASK>
-__device__ __forceinline__ void attn_tile(const uint4* __restrict__ sk, const uint4* __restrict__ sv, int t, int nkt,
-                                          float c, const int (&ks)[4], const uint4 (&qv)[4], int g, int qi,
-                                          float& m_run, float& l_run, v16f& o0, v16f& o1) {
-  // register r is key 32t + 8(r/4) + 4g + r%4 of the block
-  float s[16];
-  float bmax;
+// S^T for one 32-key tile (keys 32t.. of the stage) as floats, plus the tile's max
+// score (in S units). Register r is key 32t + 8(r/4) + 4g + r%4 of the block.
+// nkt = valid keys in the tile (MASK only): masked scores are -inf (bf16) or the
+// lowest int (INT8), which exp2 maps to 0.
+template <int QK, bool MASK>
+__device__ __forceinline__ void qk_tile(const uint4* __restrict__ sk, int nkt, const int (&ks)[4],
+                                        const uint4 (&qv)[4], int g, float (&s)[16], float& tmax) {
   if constexpr (QK == QK_BF16) {
     v16f sacc;
 #pragma unroll
@@ -238,10 +254,16 @@ __device__ __forceinline__ void attn_tile(const uint4* __restrict__ sk, const ui
       for (int r = 0; r < 16; ++r)
         if (8 * (r >> 2) + 4 * g + (r & 3) >= nkt) s[r] = -__builtin_huge_valf();
     }
-    float mx = fmaxf(s[0], s[1]);
-#pragma unroll
-    for (int r = 2; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[r], s[r + 1]));
-    bmax = pair_maxf(mx) * c;
+    // two max chains; with NaNs excluded (this file is built with -fno-honor-nans: the
+    // scores are finite, or -inf for masked keys) each pair of fmaxf becomes one
+    // v_max3_f32 with no NaN-quieting of the MFMA results
+    float ma = fmaxf(fmaxf(s[0], s[1]), s[2]), mb = fmaxf(fmaxf(s[8], s[9]), s[10]);
+    ma = fmaxf(fmaxf(ma, s[3]), s[4]);
+    mb = fmaxf(fmaxf(mb, s[11]), s[12]);
+    ma = fmaxf(fmaxf(ma, s[5]), s[6]);
+    mb = fmaxf(fmaxf(mb, s[13]), s[14]);
+    ma = fmaxf(fmaxf(ma, s[7]), mb);
+    tmax = fmaxf(ma, s[15]);
   } else {
     const v4i kx0 = __builtin_bit_cast(v4i, sk[ks[0]]);
     const v4i kx1 = __builtin_bit_cast(v4i, sk[ks[1]]);
@@ -272,23 +294,16 @@ __device__ __forceinline__ void attn_tile(const uint4* __restrict__ sk, const ui
     int mx = max(sacc[0], sacc[1]);
 #pragma unroll
     for (int r = 2; r < 16; r += 2) mx = max(mx, max(sacc[r], sacc[r + 1]));
-    bmax = (float)pair_max(mx) * c;
+    tmax = (float)mx;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = (float)sacc[r];
   }
-  const bool need = bmax > m_run + RESS_RESCALE_LOG2;
-  if (__any(need)) {
-    const float m_new = need ? bmax : m_run;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    m_run = m_new;
-    l_run *= alpha;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      o0[r] *= alpha;
-      o1[r] *= alpha;
-    }
-  }
-  const float nm = -m_run;
+}
+
+// P = exp2(S*c - m) for one tile, row sum, O^T += V^T P^T (2 MFMAs per output half).
+template <bool V_F16, bool MASK>
+__device__ __forceinline__ void pv_tile(const uint4* __restrict__ sv, int t, int nkt, const float (&s)[16], float c,
+                                        float nm, int g, int qi, float& l_run, v16f& o0, v16f& o1) {
   float p[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) p[r] = __builtin_amdgcn_exp2f(fmaf(s[r], c, nm));
@@ -297,8 +312,8 @@ __device__ __forceinline__ void attn_tile(const uint4* __restrict__ sk, const ui
     for (int r = 0; r < 16; ++r)
       if (8 * (r >> 2) + 4 * g + (r & 3) >= nkt) p[r] = 0.0f;
   }
-  // O^T += V^T . P^T: MFMA s = 2t + h covers keys 16s..16s+15, registers 8h..8h+7. The
-  // row sum accumulates the same rounded P the MFMA consumes.
+  // MFMA s = 2t + h covers keys 16s..16s+15, registers 8h..8h+7. The row sum
+  // accumulates the same rounded P the MFMA consumes.
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     uint4 pb;
@@ -318,18 +333,148 @@ __device__ __forceinline__ void attn_tile(const uint4* __restrict__ sk, const ui
   }
 }
 
+// INT8 modes: one 64-key block as two 32-key online-softmax steps (S^T tile -> running
+// max with lazy rescale -> P -> O^T += V^T P^T), one S accumulator live at a time.
+template <int QK, bool V_F16, bool MASK>
+__device__ __forceinline__ void attn_block_i8(const uint4* __restrict__ stage, int kch, int nk, float c,
+                                              const int (&ks0)[4], const int (&ks1)[4], const uint4 (&qv)[4], int g,
+                                              int qi, float& m_run, float& l_run, v16f& o0, v16f& o1) {
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    float sc[16], tmax;
+    qk_tile<QK, MASK>(stage, nk - 32 * t, t ? ks1 : ks0, qv, g, sc, tmax);
+    const float bmax = (float)pair_max((int)tmax) * c;
+    const bool need = bmax > m_run + RESS_RESCALE_LOG2;
+    if (__any(need)) {
+      const float m_new = need ? bmax : m_run;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        o0[r] *= alpha;
+        o1[r] *= alpha;
+      }
+    }
+    pv_tile<V_F16, MASK>(stage + kch, t, nk - 32 * t, sc, c, -m_run, g, qi, l_run, o0, o1);
+  }
+}
+
+// bf16 mode: one 64-key block, with its LDS traffic issued ahead of use. All eight K
+// operand reads and tile 0's four V reads go out first (LDS returns in order, so each
+// MFMA waits only for its own operand), both tiles' S^T MFMAs follow, then one
+// running-max update per block with lazy rescale, and P = exp2(S*c - m) with PV per
+// tile (tile 1's V reads issued under tile 0's PV).
+template <bool MASK>
+__device__ __forceinline__ void attn_block_bf16(const uint4* __restrict__ stage, int kch, int nk, float c,
+                                                const int (&ks0)[4], const int (&ks1)[4], const uint4 (&qv)[4], int g,
+                                                int qi, float& m_run, float& l_run, v16f& o0, v16f& o1) {
+  const uint4* sv = stage + kch;
+  uint4 k0[4], k1[4], v0[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) k0[j] = stage[ks0[j]];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) k1[j] = stage[ks1[j]];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    v0[2 * h] = sv[v_slot(qi, 2 * h + g)];
+    v0[2 * h + 1] = sv[v_slot(32 + qi, 2 * h + g)];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  v16f a0, a1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) a0[r] = a1[r] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    a0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, k0[j]), __builtin_bit_cast(v8bf, qv[j]), a0,
+                                                 0, 0, 0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    a1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, k1[j]), __builtin_bit_cast(v8bf, qv[j]), a1,
+                                                 0, 0, 0);
+  float s0[16], s1[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    s0[r] = a0[r];
+    s1[r] = a1[r];
+  }
+  if constexpr (MASK) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = 8 * (r >> 2) + 4 * g + (r & 3);
+      if (key >= nk) s0[r] = -__builtin_huge_valf();
+      if (key + 32 >= nk) s1[r] = -__builtin_huge_valf();
+    }
+  }
+  // max over the lane's 32 scores; with NaNs excluded (this file is built with
+  // -fno-honor-nans: scores are finite, or -inf for masked keys) pairs of fmaxf become
+  // v_max3_f32 with no NaN-quieting of the MFMA results
+  float ma = fmaxf(fmaxf(s0[0], s0[1]), s0[2]), mb = fmaxf(fmaxf(s1[0], s1[1]), s1[2]);
+#pragma unroll
+  for (int r = 3; r < 15; r += 2) {
+    ma = fmaxf(fmaxf(ma, s0[r]), s0[r + 1]);
+    mb = fmaxf(fmaxf(mb, s1[r]), s1[r + 1]);
+  }
+  ma = fmaxf(fmaxf(ma, s0[15]), s1[15]);
+  const float bmax = pair_maxf(fmaxf(ma, mb)) * c;
+  const bool need = bmax > m_run + RESS_RESCALE_LOG2;
+  if (__any(need)) {
+    const float m_new = need ? bmax : m_run;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    m_run = m_new;
+    l_run *= alpha;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      o0[r] *= alpha;
+      o1[r] *= alpha;
+    }
+  }
+  const float nm = -m_run;
+  // P tile t, row sum, O^T += V^T P^T; register r is key 32t + 8(r/4) + 4g + r%4
+  auto pv = [&](const float (&sc)[16], const uint4 (&vv)[4]) {
+    float p[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = __builtin_amdgcn_exp2f(fmaf(sc[r], c, nm));
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint4 pb;
+      pb.x = cvt_pair<false>(p[8 * h + 0], p[8 * h + 1]);
+      pb.y = cvt_pair<false>(p[8 * h + 2], p[8 * h + 3]);
+      pb.z = cvt_pair<false>(p[8 * h + 4], p[8 * h + 5]);
+      pb.w = cvt_pair<false>(p[8 * h + 6], p[8 * h + 7]);
+      l_run = dot2_acc<false>(pb.x, l_run);
+      l_run = dot2_acc<false>(pb.y, l_run);
+      l_run = dot2_acc<false>(pb.z, l_run);
+      l_run = dot2_acc<false>(pb.w, l_run);
+      o0 = pv_mfma<false>(vv[2 * h], pb, o0);
+      o1 = pv_mfma<false>(vv[2 * h + 1], pb, o1);
+    }
+  };
+  pv(s0, v0);
+  uint4 v1[4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    v1[2 * h] = sv[v_slot(qi, 4 + 2 * h + g)];
+    v1[2 * h + 1] = sv[v_slot(32 + qi, 4 + 2 * h + g)];
+  }
+  pv(s1, v1);
+}
+
 // K chunks (16 B) per stage: INT8 hi 256 [+ lo 256]; bf16 512.
 template <int QK>
 struct StageShape {
   static constexpr int KCH = QK == QK_I8 ? 256 : 512;
   static constexpr int STAGE = KCH + 512;  // + V^T 8 KiB
+  static constexpr int DMA = QK == QK_I8 ? 3 : 4;  // LDS-DMA instructions per lane per stage
 };
 
 template <int QK, bool V_F16, int OUT>
 __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __restrict__ lut_all,
                                                 const int* __restrict__ nvalid, const float* __restrict__ k_scale,
-                                                uint4* __restrict__ s0, uint4* __restrict__ s1, int bh, int qb) {
+                                                uint4* __restrict__ s0, uint4* __restrict__ s1,
+                                                uint4* __restrict__ s2, int bh, int qb) {
   constexpr int KCH = StageShape<QK>::KCH;
+  constexpr int DMA = StageShape<QK>::DMA;
   const long long row = (long long)bh * a.q_blk_total + qb;
   const int nv = nvalid[row];
   const int* lut = lut_all + row * a.kb_tot;
@@ -339,8 +484,8 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
   const int cnt_q = min(128, (special ? a.m.T_s : a.m.T_p) - qbase);
   const int qrow = 32 * w + qi;
 
-  uint4 qv[4];
-  float qs;  // this row's logit scale (times log2 e); INT8 modes multiply in k_scale per block
+  uint4 qv[4];  // Q operand (see k_slots)
+  float qs;     // this row's logit scale (times log2 e); INT8 modes multiply in k_scale per block
   if constexpr (QK == QK_BF16) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) qv[j] = make_uint4(0u, 0u, 0u, 0u);
@@ -401,17 +546,35 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
   k_slots<QK>(qi, g, ks0);
   k_slots<QK>(32 + qi, g, ks1);
 
-  float m_run = -__builtin_huge_valf(), l_run = 0.0f;
+  float m_run = -__builtin_huge_valf(), l_run = 0.0f;  // running max (log2 units), row sum
   v16f o0, o1;
 #pragma unroll
   for (int r = 0; r < 16; ++r) o0[r] = o1[r] = 0.0f;
+  auto block = [&](const uint4* cur, int nk, float cb, auto mask_tag) {
+    constexpr bool M = decltype(mask_tag)::value;
+    if constexpr (QK == QK_BF16)
+      attn_block_bf16<M>(cur, KCH, nk, cb, ks0, ks1, qv, g, qi, m_run, l_run, o0, o1);
+    else
+      attn_block_i8<QK, V_F16, M>(cur, KCH, nk, cb, ks0, ks1, qv, g, qi, m_run, l_run, o0, o1);
+  };
 
+  // Three stages: block i lives in stage i % 3 and is fetched two steps ahead, so each
+  // DMA has two blocks of compute to land in.
   if (nv > 0) stage_load(s0, lut[0]);
-  wait_lds_dma();
+  if (nv > 1) {
+    stage_load(s1, lut[1]);
+    wait_lds_dma_but<DMA>();
+  } else {
+    wait_lds_dma();
+  }
   __syncthreads();
 
-  // the block index and scale of the next iteration are loaded one iteration ahead
+  // LUT entries are read two steps before their DMA is issued (kb1, kb2 = blocks it+1,
+  // it+2 at the start of step it), so no step waits on a scalar load; the scale of the
+  // next block is read one step ahead.
   int kb = nv > 0 ? lut[0] : 0;
+  int kb1 = nv > 1 ? lut[1] : 0;
+  int kb2 = nv > 2 ? lut[2] : 0;
   float c = nv > 0 ? block_scale(kb) : 0.0f;
   // Only the sequence's last key block can be partial; LUTs are ascending, so if it is
   // kept it is the last entry. Full blocks run the unmasked loop, the partial one is
@@ -419,42 +582,40 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
   const bool tail_partial = nv > 0 && (a.Tk & 63) != 0 && lut[nv - 1] == a.kb_tot - 1;
   const int nv_full = nv - (tail_partial ? 1 : 0);
 
-  // One kept block: stage the next block into `nxt` (LDS-DMA, in flight during the
-  // compute), consume `cur`. The two stages are distinct LDS objects and the loop is
-  // unrolled by two, so the compiler can see the DMA never writes the stage being read
-  // and does not wait for it before the LDS reads.
-  auto step = [&](const uint4* cur, uint4* nxt, int it) {
-    int kn = 0;
-    float cn = 0.0f;
-    if (it + 1 < nv) {
-      kn = lut[it + 1];
-      cn = block_scale(kn);
-      stage_load(nxt, kn);
-    }
-    // Each 64-key block is consumed as two 32-key tiles, each a full online-softmax step
-    // (S^T tile -> running max -> P -> O^T += V^T P^T), keeping one 16-register S
-    // accumulator live.
-    attn_tile<QK, V_F16, false>(cur, cur + KCH, 0, 32, c, ks0, qv, g, qi, m_run, l_run, o0, o1);
-    attn_tile<QK, V_F16, false>(cur, cur + KCH, 1, 32, c, ks1, qv, g, qi, m_run, l_run, o0, o1);
-    kb = kn;
+  // One kept block: start the DMA of block it+2 into `ahead`, consume `cur`, then wait
+  // for block it+1 (the newest DMA may stay in flight). The stages are distinct LDS
+  // objects and the loop is unrolled by three, so the compiler can see that no DMA
+  // writes the stage being read and does not wait for it before the LDS reads. The
+  // stage `ahead` was last read in step it-1, which every wave has left (barrier).
+  auto step = [&](const uint4* cur, uint4* ahead, int it) {
+    const bool fetch = it + 2 < nv;
+    if (fetch) stage_load(ahead, kb2);
+    const float cn = it + 1 < nv ? block_scale(kb1) : 0.0f;
+    block(cur, 64, c, std::false_type{});
+    // issued after the block's LDS reads, so their waits do not include this load
+    __builtin_amdgcn_sched_barrier(0);
+    const int kb3 = it + 3 < nv ? lut[it + 3] : 0;
+    kb = kb1;
+    kb1 = kb2;
+    kb2 = kb3;
     c = cn;
-    wait_lds_dma();
-    __syncthreads();
+    if (fetch) wait_lds_dma_but<DMA>();
+    else wait_lds_dma();
+    stage_barrier();
   };
   int it = 0;
-  for (; it + 2 <= nv_full; it += 2) {
-    step(s0, s1, it);
+  for (; it + 3 <= nv_full; it += 3) {
+    step(s0, s2, it);
     step(s1, s0, it + 1);
+    step(s2, s1, it + 2);
   }
-  if (it < nv_full) {
-    step(s0, s1, it);
-    ++it;
-  }
+  if (it < nv_full) step(s0, s2, it++);
+  if (it < nv_full) step(s1, s0, it++);
   if (tail_partial) {  // kb / c already hold the last block's index and scale
-    const uint4* cur = (it & 1) ? s1 : s0;
+    const int st = it % 3;
+    const uint4* cur = st == 0 ? s0 : (st == 1 ? s1 : s2);
     const int nk = a.Tk - kb * 64;
-    attn_tile<QK, V_F16, true>(cur, cur + KCH, 0, nk, c, ks0, qv, g, qi, m_run, l_run, o0, o1);
-    attn_tile<QK, V_F16, true>(cur, cur + KCH, 1, nk - 32, c, ks1, qv, g, qi, m_run, l_run, o0, o1);
+    block(cur, nk, c, std::true_type{});
     __syncthreads();  // the next row's prologue overwrites this stage
   }
 
@@ -483,13 +644,20 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
   }
 }
 
+// Resident workgroups per CU (= waves per SIMD).
+template <int QK>
+struct Occupancy {
+  static constexpr int value = QK == QK_BF16 ? 2 : 3;
+};
+
 template <int QK, bool V_F16, int OUT>
-__global__ __launch_bounds__(256, 3) void k_sparse_attn(AttnArgs a, const int* __restrict__ lut,
+__global__ __launch_bounds__(256, Occupancy<QK>::value) void k_sparse_attn(AttnArgs a, const int* __restrict__ lut,
                                                         const int* __restrict__ nvalid,
                                                         const float* __restrict__ k_scale) {
   constexpr int STAGE = StageShape<QK>::STAGE;
   __shared__ __attribute__((aligned(16))) uint4 stage0[STAGE];
   __shared__ __attribute__((aligned(16))) uint4 stage1[STAGE];
+  __shared__ __attribute__((aligned(16))) uint4 stage2[STAGE];
   __shared__ int s_item;
 
   // ---- persistent loop over this XCD's range of rows ------------------------
@@ -503,7 +671,7 @@ __global__ __launch_bounds__(256, 3) void k_sparse_attn(AttnArgs a, const int* _
     if (item >= item_end) break;
     int bh, qb;
     item_to_row(item, a.q_blk_p, a.q_blk_total, bh, qb);
-    sparse_attn_row<QK, V_F16, OUT>(a, lut, nvalid, k_scale, stage0, stage1, bh, qb);
+    sparse_attn_row<QK, V_F16, OUT>(a, lut, nvalid, k_scale, stage0, stage1, stage2, bh, qb);
   }
 }
 
@@ -552,8 +720,8 @@ static int launch_attn(const AttnArgs& a, int out_dtype, hipStream_t stream) {
   hipLaunchKernelGGL(k_attn_schedule, dim3(1), dim3(1024), 0, stream, a.nvalid, a.BH, a.q_blk_p, a.q_blk_total,
                      a.sched);
   RESS_LAUNCHED("k_attn_schedule");
-  // persistent: 3 resident workgroups per CU, a multiple of the 8 XCDs
-  const dim3 grid(8 * ((3 * g_cu_count[dev] + 7) / 8)), block(256);
+  // persistent: Occupancy<QK> resident workgroups per CU, a multiple of the 8 XCDs
+  const dim3 grid(8 * ((Occupancy<QK>::value * g_cu_count[dev] + 7) / 8)), block(256);
   switch (out_dtype) {
     case OUT_F32:
       hipLaunchKernelGGL((k_sparse_attn<QK, V_F16, OUT_F32>), grid, block, 0, stream, a, a.lut, a.nvalid, a.k_scale);
