@@ -107,6 +107,22 @@ int ress_fill_block_map(void* map, const void* counts, const void* sorted_idx, l
  * map [rows][k] uint8 -> lut [rows][k] int32 (ascending), nvalid [rows]. */
 int ress_block_map_lut(const void* map, long long rows, int k, void* lut, void* nvalid, hipStream_t stream);
 
+/* ---- ReSS restore-swap (ress_swap.hip) ------------------------------------ */
+
+/* Replaces restore_swap_rank_by (src/ress/scoring/projected.py:395-1058) with its fused
+ * round body (src/ress/scoring/fused_round.py, fused_topm.py), as ress_attention_forward
+ * calls it for the restore_swap* criteria (src/ress/models/attention.py:545-566).
+ * A [BH][q_blk][kb_p] pooled map (attn_full), V [BH][kb_p][64] block means (v_bar_full),
+ * M [H][64][64] (head bh % H), nts [BH][q_blk] kept budgets. Out: rank_key
+ * [BH][q_blk][n_cand] = 1 kept / 0 dropped (its top-nts is the keep set), obj [BH][q_blk]
+ * (optional) J of the returned set, s_out [BH][q_blk][n_cand] (optional) the scores
+ * s = P*sqrt(d^T M d). flags: 1 bf16 k-wide tensors, 2 track_best, 4 maximize, 8
+ * invert_cut, 16 renormalize off. kb_p <= 2048. */
+long long ress_restore_swap_workspace_size(int BH, int kb_p, int n_cand);
+int ress_restore_swap(const void* A, const void* V, const void* M, const void* nts, int BH, int H, int q_blk, int kb_p,
+                      int n_cand, int n_iters, double restore_frac, double decay, int flags, void* rank_key, void* obj,
+                      void* s_out, void* workspace, long long workspace_bytes, hipStream_t stream);
+
 /* ---- attention (attn.hip) ----------------------------------------------- */
 
 /* Fused-path attention (src/ress/models/attention.py:404-412 special queries dense,

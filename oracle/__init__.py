@@ -157,3 +157,25 @@ def round_bf16_array(x):
     y = np.empty_like(a)
     lib().oracle_round_bf16_array(_p(a), _p(y), ctypes.c_longlong(a.size))
     return y
+
+
+RS_BF16, RS_TRACK_BEST, RS_MAXIMIZE, RS_INVERT_CUT, RS_NO_RENORM = 1, 2, 4, 8, 16
+
+
+def restore_swap(A, V, M, nts, n_cand, n_iters=5, restore_frac=0.5, decay=0.5, big_bf16=True, track_best=True,
+                 maximize=False, invert_cut=False, renormalize=True, want_s=False):
+    """ReSS restore-swap keep sets. A (H,q_blk,kb_p) f32, V (H,kb_p,64) f32, M (H,64,64) f32,
+    nts (H,q_blk) int. Returns (keep (H,q_blk,n_cand) uint8, J (H,q_blk) f32[, s])."""
+    A = np.ascontiguousarray(A, np.float32)
+    V = np.ascontiguousarray(V, np.float32)
+    M = np.ascontiguousarray(M, np.float32)
+    nts = np.ascontiguousarray(nts, np.int32)
+    H, q_blk, kb_p = A.shape
+    keep = np.zeros((H, q_blk, n_cand), np.uint8)
+    obj = np.zeros((H, q_blk), np.float32)
+    s = np.zeros((H, q_blk, n_cand), np.float32) if want_s else None
+    flags = ((RS_BF16 if big_bf16 else 0) | (RS_TRACK_BEST if track_best else 0) | (RS_MAXIMIZE if maximize else 0)
+             | (RS_INVERT_CUT if invert_cut else 0) | (0 if renormalize else RS_NO_RENORM))
+    lib().oracle_restore_swap(_p(A), _p(V), _p(M), _p(nts), H, q_blk, kb_p, n_cand, n_iters,
+                              ctypes.c_double(restore_frac), ctypes.c_double(decay), flags, _p(keep), _p(obj), _p(s))
+    return (keep, obj, s) if want_s else (keep, obj)

@@ -389,3 +389,250 @@ void oracle_expf_array(const float* x, float* y, long long n) {
 void oracle_round_bf16_array(const float* x, float* y, long long n) {
   for (long long i = 0; i < n; ++i) y[i] = oracle_round_bf16(x[i]);
 }
+
+/* ---- ReSS restore-swap ---------------------------------------------------------------
+ * restore_swap_rank_by (src/ress/scoring/projected.py:395-1058) with the round body of
+ * scoring/fused_round.py:_round_kernel (kept-mass-normalised objective J = ||g||^2_M / K^2,
+ * drift compensate) and fused_topm's exact top-m (ties to the lowest index). One (head,
+ * query-block) row at a time; rows are independent.
+ *
+ * Numerics. `big` (flag RS_BF16) is the dtype of the k-wide tensors: every value the
+ * reference stores in bf16 is rounded here (bf), at the same points (quadratic_deviation
+ * projected.py:259-288, dense_reference :313-356, the round :903-947, fused_round.py
+ * :176-226). The reference leaves GEMM / sum accumulation orders to torch-CUDA; this
+ * restatement fixes them: every dot product and sum is a sequential fp32 chain in index
+ * order (fmaf for products, plain adds for sums of rounded terms), the same order the GPU
+ * kernel uses.
+ *
+ * A [H][q_blk][kb_p]  pooled map over the patch key blocks (attn_full), fp32
+ * V [H][kb_p][64]     block-mean values (v_bar_full), fp32
+ * M [H][64][64]       M_h = W_O^h^T W_O^h (identity for the _nowo recipes), fp32
+ * nts [H][q_blk]      kept budget per row (after the min-2 floor)
+ * keep [H][q_blk][n_cand]  out: 1 = kept candidate
+ * obj  [H][q_blk]     out (optional): J of the returned set (fp32, this order)
+ * s_out [H][q_blk][n_cand] out (optional): s = P*sqrt(d^T M d) (the rank_by base)
+ * flags: 1 bf16 k-wide tensors, 2 track_best, 4 maximize, 8 invert_cut, 16 renormalize
+ * off (the cut ranks s instead of s/(1-P)). Returns 0. */
+#define RS_BF16 1
+#define RS_TRACK_BEST 2
+#define RS_MAXIMIZE 4
+#define RS_INVERT_CUT 8
+#define RS_NO_RENORM 16
+
+static inline float rs_bf(float x, int big) { return big ? oracle_round_bf16(x) : x; }
+/* fused_topm's order key: sign-bit flip for non-negatives, complement for negatives */
+static inline uint32_t rs_key(float x) {
+  uint32_t u = fbits(x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+static const uint32_t* g_rs_keys;
+static int cmp_rs(const void* a, const void* b) {
+  int i = *(const int*)a, j = *(const int*)b;
+  if (g_rs_keys[i] != g_rs_keys[j]) return g_rs_keys[i] > g_rs_keys[j] ? -1 : 1;
+  return (i > j) - (i < j);
+}
+/* top-m of key among valid (ties: lowest index) -> sel[] = 1 */
+static void rs_top_m(const float* q, const uint8_t* valid, int n, int m, uint8_t* sel, uint32_t* keys, int* idx) {
+  int c = 0;
+  for (int i = 0; i < n; ++i) {
+    sel[i] = 0;
+    keys[i] = rs_key(q[i]);
+    if (valid[i]) idx[c++] = i;
+  }
+  g_rs_keys = keys;
+  qsort(idx, c, sizeof(int), cmp_rs);
+  for (int i = 0; i < m && i < c; ++i) sel[idx[i]] = 1;
+}
+/* kept_mass_norm_quality (projected.py:191-211), grouping ((G*u)*(2K+u))/(K*K) - dG, / Kn^2 */
+static inline float rs_knorm(float G, float K, float dG, float u) {
+  float Kn = K + u;
+  Kn = Kn < 1e-6f ? 1e-6f : Kn;
+  const float a = G * u;
+  const float b = 2.0f * K + u;
+  return (a * b / (K * K) - dG) / (Kn * Kn);
+}
+
+/* g, Mg, ||g||^2_M, K and J for a drop set (projected.py:859-868 / 903-918) */
+static float rs_objective(const float* Pb, const uint8_t* drop, const float* Vb, const float* M32, const float* vq,
+                          float tm, int n_cand, int big, float* g, float* Mg, float* gn_out, float* K_out,
+                          float* sumpd_out) {
+  float sp = 0.0f, mv[64];
+  for (int d = 0; d < 64; ++d) mv[d] = 0.0f;
+  for (int k = 0; k < n_cand; ++k) {
+    const float pd = drop[k] ? Pb[k] : 0.0f;
+    sp = sp + pd;
+    for (int d = 0; d < 64; ++d) mv[d] = fmaf(pd, Vb[(long long)k * 64 + d], mv[d]);
+  }
+  sp = rs_bf(sp, big);
+  for (int d = 0; d < 64; ++d) g[d] = sp * vq[d] - rs_bf(mv[d], big);
+  for (int i = 0; i < 64; ++i) {
+    float a = 0.0f;
+    for (int j = 0; j < 64; ++j) a = fmaf(M32[i * 64 + j], g[j], a);
+    Mg[i] = a;
+  }
+  float gn = 0.0f;
+  for (int d = 0; d < 64; ++d) gn = gn + g[d] * Mg[d];
+  float K = tm - sp;
+  K = K < 1e-6f ? 1e-6f : K;
+  *gn_out = gn;
+  *K_out = K;
+  *sumpd_out = sp;
+  return gn / (K * K);
+}
+
+int oracle_restore_swap(const float* A, const float* V, const float* M, const int* nts, int H, int q_blk, int kb_p,
+                        int n_cand, int n_iters, double restore_frac, double decay, int flags, uint8_t* keep,
+                        float* obj_out, float* s_out) {
+  const int big = (flags & RS_BF16) != 0, track = (flags & RS_TRACK_BEST) != 0;
+  const int renorm = (flags & RS_NO_RENORM) == 0;
+  const int maxim = (flags & RS_MAXIMIZE) != 0, inv = (flags & RS_INVERT_CUT) != 0;
+  float* Vb = (float*)malloc(sizeof(float) * (size_t)kb_p * 64);
+  float* Mb = (float*)malloc(sizeof(float) * 64 * 64);
+  float* termk = (float*)malloc(sizeof(float) * (size_t)kb_p);
+  float* Pb = (float*)malloc(sizeof(float) * (size_t)kb_p);
+  float* s = (float*)malloc(sizeof(float) * (size_t)n_cand);
+  float* scut = (float*)malloc(sizeof(float) * (size_t)n_cand);
+  float* ssq = (float*)malloc(sizeof(float) * (size_t)n_cand);
+  float* rq = (float*)malloc(sizeof(float) * (size_t)n_cand);
+  float* cq = (float*)malloc(sizeof(float) * (size_t)n_cand);
+  uint8_t* drop = (uint8_t*)malloc((size_t)n_cand);
+  uint8_t* best = (uint8_t*)malloc((size_t)n_cand);
+  uint8_t* sel = (uint8_t*)malloc((size_t)n_cand);
+  uint8_t* sel2 = (uint8_t*)malloc((size_t)n_cand);
+  uint8_t* valid = (uint8_t*)malloc((size_t)n_cand);
+  uint32_t* keys = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)n_cand);
+  int* idx = (int*)malloc(sizeof(int) * (size_t)n_cand);
+  for (int h = 0; h < H; ++h) {
+    const float* M32 = M + (long long)h * 4096;
+    for (int i = 0; i < 4096; ++i) Mb[i] = rs_bf(M32[i], big);
+    for (long long i = 0; i < (long long)kb_p * 64; ++i) Vb[i] = rs_bf(V[(long long)h * kb_p * 64 + i], big);
+    /* term_k of quadratic_deviation: Mvk = M v_k (big), term_k = sum_i big(Mvk_i * v_ki) (big) */
+    for (int k = 0; k < n_cand; ++k) {
+      float tk = 0.0f;
+      for (int i = 0; i < 64; ++i) {
+        float a = 0.0f;
+        for (int j = 0; j < 64; ++j) a = fmaf(Mb[i * 64 + j], Vb[(long long)k * 64 + j], a);
+        tk = tk + rs_bf(rs_bf(a, big) * Vb[(long long)k * 64 + i], big);
+      }
+      termk[k] = rs_bf(tk, big);
+    }
+    for (int q = 0; q < q_blk; ++q) {
+      const long long row = (long long)h * q_blk + q;
+      const float* Arow = A + row * kb_p;
+      for (int k = 0; k < kb_p; ++k) Pb[k] = rs_bf(Arow[k], big);
+      /* dense_reference: v_bar_query = P @ v_bar (big), total_mass = sum P (big) */
+      float vq[64], tm = 0.0f;
+      for (int d = 0; d < 64; ++d) vq[d] = 0.0f;
+      for (int k = 0; k < kb_p; ++k) {
+        tm = tm + Pb[k];
+        for (int d = 0; d < 64; ++d) vq[d] = fmaf(Pb[k], Vb[(long long)k * 64 + d], vq[d]);
+      }
+      tm = rs_bf(tm, big);
+      for (int d = 0; d < 64; ++d) vq[d] = rs_bf(vq[d], big);
+      /* quadratic_deviation's query side: Mvq (big), term_q (big) */
+      float Mvq[64], tq = 0.0f;
+      for (int i = 0; i < 64; ++i) {
+        float a = 0.0f;
+        for (int j = 0; j < 64; ++j) a = fmaf(Mb[i * 64 + j], vq[j], a);
+        Mvq[i] = rs_bf(a, big);
+      }
+      for (int i = 0; i < 64; ++i) tq = tq + rs_bf(Mvq[i] * vq[i], big);
+      tq = rs_bf(tq, big);
+      /* s = P * sqrt(max(term_q - 2 cross + term_k, 0)); s_cut = s / max(1 - P, 1e-4); s^2 */
+      for (int k = 0; k < n_cand; ++k) {
+        float cr = 0.0f;
+        for (int i = 0; i < 64; ++i) cr = fmaf(Mvq[i], Vb[(long long)k * 64 + i], cr);
+        cr = rs_bf(cr, big);
+        float qd = rs_bf(rs_bf(tq - rs_bf(2.0f * cr, big), big) + termk[k], big);
+        qd = qd < 0.0f ? 0.0f : qd;
+        const float sq = rs_bf(sqrtf(qd), big);
+        s[k] = rs_bf(Pb[k] * sq, big);
+        float om = rs_bf(1.0f - Pb[k], big);
+        om = rs_bf(om < 1e-4f ? 1e-4f : om, big);
+        scut[k] = renorm ? rs_bf(s[k] / om, big) : s[k];
+        ssq[k] = rs_bf(s[k] * s[k], big);
+        if (s_out) s_out[row * n_cand + k] = s[k];
+      }
+      /* initial one-shot cut: keep the top min(nts, n_cand) by s_cut (lowest under invert_cut) */
+      int nkeep = nts[row];
+      nkeep = nkeep < 0 ? 0 : (nkeep > n_cand ? n_cand : nkeep);
+      for (int k = 0; k < n_cand; ++k) {
+        valid[k] = 1;
+        rq[k] = inv ? -scut[k] : scut[k];
+      }
+      rs_top_m(rq, valid, n_cand, nkeep, sel, keys, idx);
+      for (int k = 0; k < n_cand; ++k) drop[k] = !sel[k];
+      float g[64], Mg[64], gn, K, sp;
+      float best_obj = 0.0f;
+      if (track) {
+        best_obj = rs_objective(Pb, drop, Vb, M32, vq, tm, n_cand, big, g, Mg, &gn, &K, &sp);
+        memcpy(best, drop, (size_t)n_cand);
+      }
+      double remaining = restore_frac;
+      for (int it = 0; it < n_iters; ++it) {
+        const double frac = remaining * decay;
+        remaining -= frac;
+        const int pic0 = (int)rintf((float)frac * (float)nts[row]);
+        const float J = rs_objective(Pb, drop, Vb, M32, vq, tm, n_cand, big, g, Mg, &gn, &K, &sp);
+        if (track) {
+          const int better = maxim ? J > best_obj : J < best_obj;
+          if (better) {
+            best_obj = J;
+            memcpy(best, drop, (size_t)n_cand);
+          }
+        }
+        float tqr = 0.0f, Mgb[64];
+        for (int d = 0; d < 64; ++d) tqr = tqr + vq[d] * Mg[d];
+        const float tqb = rs_bf(tqr, big);
+        for (int d = 0; d < 64; ++d) Mgb[d] = rs_bf(Mg[d], big);
+        int n_drop = 0, n_kept = 0;
+        float rmax = -INFINITY;
+        for (int k = 0; k < n_cand; ++k) {
+          float tk = 0.0f;
+          for (int d = 0; d < 64; ++d) tk = fmaf(Vb[(long long)k * 64 + d], Mgb[d], tk);
+          tk = rs_bf(tk, big);
+          const float raw = rs_bf(Pb[k] * rs_bf(tk - tqb, big), big);
+          float r = rs_knorm(gn, K, 2.0f * raw + ssq[k], Pb[k]);
+          float c = rs_knorm(gn, K, ssq[k] - 2.0f * raw, -Pb[k]);
+          if (maxim) {
+            r = -r;
+            c = -c;
+          }
+          rq[k] = drop[k] ? r : -INFINITY;
+          cq[k] = drop[k] ? -INFINITY : c;
+          if (drop[k]) {
+            ++n_drop;
+            rmax = rq[k] > rmax ? rq[k] : rmax;
+          } else {
+            ++n_kept;
+          }
+        }
+        const int beneficial = rmax > 0.0f;
+        int pic = pic0;
+        if (beneficial && pic < 1) pic = 1;
+        int cnt = pic < n_drop ? pic : n_drop;
+        cnt = cnt < n_kept ? cnt : n_kept;
+        if (!beneficial) cnt = 0;
+        for (int k = 0; k < n_cand; ++k) valid[k] = drop[k];
+        rs_top_m(rq, valid, n_cand, cnt, sel, keys, idx);
+        for (int k = 0; k < n_cand; ++k) valid[k] = !drop[k];
+        rs_top_m(cq, valid, n_cand, cnt, sel2, keys, idx);
+        for (int k = 0; k < n_cand; ++k) drop[k] = (uint8_t)((drop[k] && !sel[k]) || sel2[k]);
+      }
+      float fin = 0.0f;
+      if (track || obj_out) fin = rs_objective(Pb, drop, Vb, M32, vq, tm, n_cand, big, g, Mg, &gn, &K, &sp);
+      if (track) {
+        const int better = maxim ? fin > best_obj : fin < best_obj;
+        if (!better) {
+          memcpy(drop, best, (size_t)n_cand);
+          fin = best_obj;
+        }
+      }
+      if (obj_out) obj_out[row] = fin;
+      for (int k = 0; k < n_cand; ++k) keep[row * n_cand + k] = (uint8_t)!drop[k];
+    }
+  }
+  free(Vb); free(Mb); free(termk); free(Pb); free(s); free(scut); free(ssq); free(rq); free(cq);
+  free(drop); free(best); free(sel); free(sel2); free(valid); free(keys); free(idx);
+  return 0;
+}

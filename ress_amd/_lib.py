@@ -27,6 +27,7 @@ _SIGS = {
     "ress_sparse_attn_fwd": "pppppppippiiiiifpilllps",
     "ress_sparse_attn_fwd_bf16": "plllpppp" + "iiiiif" + "pi" + "lll" + "ps",
     "ress_qattn_block_sparse_fwd": "pppipipppppiiiilllllliiifipls",
+    "ress_restore_swap": "pppp" + "iiiiii" + "dd" + "i" + "ppp" + "pl" + "s",
 }
 _CT = {
     "p": ctypes.c_void_p,
@@ -54,6 +55,8 @@ def lib():
         L.ress_abi_version.restype = ctypes.c_int
         L.ress_qattn_workspace_size.restype = ctypes.c_longlong
         L.ress_qattn_workspace_size.argtypes = [ctypes.c_int] * 3
+        L.ress_restore_swap_workspace_size.restype = ctypes.c_longlong
+        L.ress_restore_swap_workspace_size.argtypes = [ctypes.c_int] * 3
         for name, sig in _SIGS.items():
             fn = getattr(L, name)
             fn.restype = ctypes.c_int
@@ -87,4 +90,5 @@ def last_error():
 
 
 def exported_symbols():
-    return list(_SIGS) + ["ress_last_error", "ress_abi_version", "ress_qattn_workspace_size"]
+    return list(_SIGS) + ["ress_last_error", "ress_abi_version", "ress_qattn_workspace_size",
+                          "ress_restore_swap_workspace_size"]

@@ -99,7 +99,9 @@ def _rank_key(block_criterion, attn_cond, attn_full, v_bar_full, counts, grid, M
                 raise AssertionError(f"block_criterion={block_criterion!r} requires bake_and_attach_M(model) first")
         else:
             M = torch.eye(hd, device=attn_full.device, dtype=torch.float32).expand(grid.H, hd, hd)
-        return _projected.restore_swap_rank_by(
+        # the keep set as a 1/0 key: top-counts of it is the set the reference's rank_by
+        # (where(drop, s, s + max|s| + 1)) yields through build_block_mask
+        return _projected.restore_swap_keep(
             attn_full, v_bar_full, M, counts, n_cand=grid.n_cand, n_iters=spec.n_iters, track_best=spec.track_best,
             big_dtype=spec.big_dtype, restore_frac=spec.restore_frac, decay=spec.decay, maximize=spec.maximize,
             invert_cut=spec.invert_cut)

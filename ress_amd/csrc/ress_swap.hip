@@ -1,0 +1,425 @@
+// ReSS restore-swap block ranking for gfx950.
+//
+// Replaces restore_swap_rank_by (reference src/ress/scoring/projected.py:395-1058) with
+// the round body of scoring/fused_round.py (kept-mass-normalised objective
+// J = ||g||^2_M / K^2, drift compensate, geometric schedule, >=1 floor on beneficial
+// rows, track-best) and fused_topm's exact top-m (ties to the lowest index). Every
+// (batch*head, query-block) row is independent, so one wave owns one row for the whole
+// algorithm -- initial cut, n_iters rounds, track-best -- with no grid-wide sync.
+//
+// Numerics. With `big` (the recipe's _bf16) every value the reference keeps in bf16 is
+// rounded at the reference's points (quadratic_deviation projected.py:259-288,
+// dense_reference :313-356, the round :903-947, fused_round.py:176-226). Dot products
+// and sums are sequential fp32 chains in index order (fmaf for products, plain adds for
+// sums of rounded terms): lane-parallel over the independent outputs, never split.
+//
+// Work: per row, O(kb_p * 64) for the dense reference, O(n_cand * 64) per round for the
+// masked sums and term_k; selections are 32-step MSB-first threshold searches over
+// order keys with wave ballots.
+#include "common.h"
+
+#define RS_BF16 1
+#define RS_TRACK_BEST 2
+#define RS_MAXIMIZE 4
+#define RS_INVERT_CUT 8
+#define RS_NO_RENORM 16
+#define RS_MAX_KBP 2048  // candidates per row handled (32 per lane)
+
+__device__ __forceinline__ float rs_bf(float x, bool big) {
+  if (!big) return x;
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return __uint_as_float(((u >> 16) | 0x40u) << 16);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return __uint_as_float((u >> 16) << 16);
+}
+// fused_topm's order key: non-negatives get the sign bit set, negatives are complemented
+__device__ __forceinline__ uint32_t rs_key(float x) {
+  const uint32_t u = __float_as_uint(x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+// kept_mass_norm_quality (projected.py:191-211), grouping ((G*u)*(2K+u))/(K*K) - dG, / Kn^2
+__device__ __forceinline__ float rs_knorm(float G, float K, float dG, float u) {
+  float Kn = K + u;
+  Kn = Kn < 1e-6f ? 1e-6f : Kn;
+  const float a = G * u;
+  const float b = 2.0f * K + u;
+  return (a * b / (K * K) - dG) / (Kn * Kn);
+}
+
+// Exact top-m of key[i] (lane element i <-> candidate lane + 64 i) among `valid` bits,
+// ties to the lowest candidate index; returns the selection as per-lane bits.
+template <int NPL>
+__device__ __forceinline__ uint32_t rs_top_m(const uint32_t (&key)[NPL], uint32_t valid, int m, int lane) {
+  if (m <= 0) return 0u;
+  uint32_t thr = 0u;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t cand = thr | (1u << b);
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) c += __popcll(__ballot(((valid >> i) & 1u) && key[i] >= cand));
+    if (c >= m) thr = cand;
+  }
+  int n_gt = 0;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) n_gt += __popcll(__ballot(((valid >> i) & 1u) && key[i] > thr));
+  const int take_eq = m - n_gt;  // ties at thr taken in index order
+  uint32_t sel = 0u;
+  int before = 0;  // tied entries with a smaller index in earlier lane elements
+  const unsigned long long lower = lane ? (~0ull >> (64 - lane)) : 0ull;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const bool v = (valid >> i) & 1u;
+    const bool eq = v && key[i] == thr;
+    const unsigned long long be = __ballot(eq);
+    const int rank = before + __popcll(be & lower);
+    if ((v && key[i] > thr) || (eq && rank < take_eq)) sel |= 1u << i;
+    before += __popcll(be);
+  }
+  return sel;
+}
+
+// Per-head preparation: Vr = big(V) [kb_p][64] and its transpose VrT [64][kb_p], and the
+// key side of quadratic_deviation, termk[k] = big(sum_i big(big(Mb v_k)_i * v_ki)).
+__global__ __launch_bounds__(64) void k_rs_head(const float* __restrict__ V, const float* __restrict__ M, int H,
+                                                int kb_p, int n_cand, int big, float* __restrict__ Vr,
+                                                float* __restrict__ VrT, float* __restrict__ termk) {
+  __shared__ float MbT[64 * 64];  // MbT[j*64 + i] = big(M[i][j])
+  __shared__ float vk[64];
+  const int k = blockIdx.x, bh = blockIdx.y, lane = threadIdx.x;
+  const float* Mh = M + (long long)(bh % H) * 4096;
+  for (int e = lane; e < 4096; e += 64) MbT[(e & 63) * 64 + (e >> 6)] = rs_bf(Mh[e], big);
+  const float x = rs_bf(V[((long long)bh * kb_p + k) * 64 + lane], big);
+  Vr[((long long)bh * kb_p + k) * 64 + lane] = x;
+  VrT[((long long)bh * 64 + lane) * kb_p + k] = x;
+  vk[lane] = x;
+  __syncthreads();
+  if (k >= n_cand) return;
+  float a = 0.0f;  // (Mb v_k)_lane, sequential over j
+  for (int j = 0; j < 64; ++j) a = fmaf(MbT[j * 64 + lane], vk[j], a);
+  __syncthreads();
+  vk[lane] = rs_bf(rs_bf(a, big) * x, big);  // the rounded product for dim lane
+  __syncthreads();
+  if (lane == 0) {
+    float t = 0.0f;
+    for (int i = 0; i < 64; ++i) t = t + vk[i];
+    termk[(long long)bh * n_cand + k] = rs_bf(t, big);
+  }
+}
+
+struct RsArgs {
+  const float* A;  // [BH][q_blk][kb_p]
+  const float* M;  // [H][64][64]
+  const int* nts;  // [BH][q_blk]
+  const float* Vr;
+  const float* VrT;
+  const float* termk;
+  float* rank_key;  // [BH][q_blk][n_cand]: 1 = kept, 0 = dropped
+  float* obj;       // [BH][q_blk] or null: J of the returned set
+  float* s_out;     // [BH][q_blk][n_cand] or null: s = P*sqrt(d^T M d)
+  int H, q_blk, kb_p, n_cand, n_iters, flags;
+  double restore_frac, decay;  // geometric schedule (projected.py:775-790)
+};
+
+// The rows of one head: 4 waves, each its own row.
+template <int NPL>
+__global__ __launch_bounds__(256) void k_restore_swap(RsArgs a) {
+  extern __shared__ float sh[];
+  float* M32T = sh;                 // [64][64] M^T (fp32)
+  float* MbT = sh + 4096;           // [64][64] big(M)^T
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float* wsh = sh + 8192 + w * (a.kb_p + 5 * 64);
+  float* Pw = wsh;                  // [kb_p] big(P) of the row, then P*drop
+  float* vqs = wsh + a.kb_p;        // [64]
+  float* t0 = vqs + 64;             // [64] scratch vectors
+  float* t1 = t0 + 64;
+  float* t2 = t1 + 64;
+  float* t3 = t2 + 64;
+  const int bh = blockIdx.y;
+  const bool big = a.flags & RS_BF16, track = a.flags & RS_TRACK_BEST;
+  const bool maxim = a.flags & RS_MAXIMIZE, inv = a.flags & RS_INVERT_CUT;
+  const bool renorm = !(a.flags & RS_NO_RENORM);
+  const float* Mh = a.M + (long long)(bh % a.H) * 4096;
+  for (int e = threadIdx.x; e < 4096; e += 256) {
+    const float m = Mh[e];
+    M32T[(e & 63) * 64 + (e >> 6)] = m;
+    MbT[(e & 63) * 64 + (e >> 6)] = rs_bf(m, big);
+  }
+  __syncthreads();
+  const float* Vr = a.Vr + (long long)bh * a.kb_p * 64;
+  const float* VrT = a.VrT + (long long)bh * 64 * a.kb_p;
+  const float* tkey = a.termk + (long long)bh * a.n_cand;
+  const int n_cand = a.n_cand, kb_p = a.kb_p;
+  const int q = blockIdx.x * 4 + w;
+  if (q >= a.q_blk) return;  // no block-level sync after this point
+  const long long row = (long long)bh * a.q_blk + q;
+
+  // ---- row inputs and the dense reference ---------------------------------------
+  const float* Arow = a.A + row * kb_p;
+  for (int k = lane; k < kb_p; k += 64) Pw[k] = rs_bf(Arow[k], big);
+  float Pb[NPL], ssq[NPL];
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int k = lane + 64 * i;
+    Pb[i] = k < n_cand ? rs_bf(Arow[k], big) : 0.0f;
+  }
+  uint32_t cand_bits = 0u;  // lane elements that are candidates
+#pragma unroll
+  for (int i = 0; i < NPL; ++i)
+    if (lane + 64 * i < n_cand) cand_bits |= 1u << i;
+  __builtin_amdgcn_wave_barrier();
+  float vq, tm = 0.0f;  // v_bar_query[lane], total mass (same in every lane)
+  {
+    float acc = 0.0f;
+    for (int k = 0; k < kb_p; ++k) {
+      const float p = Pw[k];
+      tm = tm + p;
+      acc = fmaf(p, Vr[(long long)k * 64 + lane], acc);
+    }
+    vq = rs_bf(acc, big);
+    tm = rs_bf(tm, big);
+  }
+  vqs[lane] = vq;
+  __builtin_amdgcn_wave_barrier();
+  // quadratic_deviation's query side: Mvq = big(Mb vq), term_q = big(sum big(Mvq*vq))
+  float mvq;
+  {
+    float acc = 0.0f;
+    for (int j = 0; j < 64; ++j) acc = fmaf(MbT[j * 64 + lane], vqs[j], acc);
+    mvq = rs_bf(acc, big);
+  }
+  t0[lane] = mvq;
+  t1[lane] = rs_bf(mvq * vq, big);
+  __builtin_amdgcn_wave_barrier();
+  float tq = 0.0f;
+  for (int i = 0; i < 64; ++i) tq = tq + t1[i];
+  tq = rs_bf(tq, big);
+  // s, s_cut, s^2 per candidate
+  uint32_t key[NPL];
+  {
+    float cr[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) cr[i] = 0.0f;
+    for (int d = 0; d < 64; ++d) {
+      const float m = t0[d];
+      const float* col = VrT + (long long)d * kb_p;
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) {
+        const int k = lane + 64 * i;
+        if (k < n_cand) cr[i] = fmaf(m, col[k], cr[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const int k = lane + 64 * i;
+      float sc = 0.0f;
+      ssq[i] = 0.0f;
+      if (k < n_cand) {
+        const float c2 = rs_bf(2.0f * rs_bf(cr[i], big), big);
+        float qd = rs_bf(rs_bf(tq - c2, big) + tkey[k], big);
+        qd = qd < 0.0f ? 0.0f : qd;
+        const float sq = rs_bf(sqrtf(qd), big);
+        const float s = rs_bf(Pb[i] * sq, big);
+        float om = rs_bf(1.0f - Pb[i], big);
+        om = rs_bf(om < 1e-4f ? 1e-4f : om, big);
+        sc = renorm ? rs_bf(s / om, big) : s;
+        ssq[i] = rs_bf(s * s, big);
+        if (a.s_out) a.s_out[row * n_cand + k] = s;
+      }
+      key[i] = rs_key(inv ? -sc : sc);
+    }
+  }
+  int nts = a.nts[row];
+  const int nkeep = nts < 0 ? 0 : (nts > n_cand ? n_cand : nts);
+  uint32_t drop = cand_bits & ~rs_top_m<NPL>(key, cand_bits, nkeep, lane);
+
+  // J, and g / Mg / ||g||^2_M / K of a drop set (projected.py:859-868, 903-918)
+  float gn = 0.0f, Kk = 1.0f;
+  auto objective = [&](uint32_t dr) -> float {
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const int k = lane + 64 * i;
+      if (k < n_cand) Pw[k] = ((dr >> i) & 1u) ? Pb[i] : 0.0f;
+    }
+    __builtin_amdgcn_wave_barrier();
+    float acc = 0.0f, sp = 0.0f;
+    for (int k = 0; k < n_cand; ++k) {
+      const float p = Pw[k];
+      sp = sp + p;
+      acc = fmaf(p, Vr[(long long)k * 64 + lane], acc);
+    }
+    sp = rs_bf(sp, big);
+    const float g = sp * vq - rs_bf(acc, big);
+    __builtin_amdgcn_wave_barrier();
+    t1[lane] = g;
+    __builtin_amdgcn_wave_barrier();
+    float mg = 0.0f;
+    for (int j = 0; j < 64; ++j) mg = fmaf(M32T[j * 64 + lane], t1[j], mg);
+    t2[lane] = g * mg;    // products of ||g||^2_M
+    t3[lane] = mg;
+    __builtin_amdgcn_wave_barrier();
+    float n2 = 0.0f;
+    for (int d = 0; d < 64; ++d) n2 = n2 + t2[d];
+    float K = tm - sp;
+    K = K < 1e-6f ? 1e-6f : K;
+    gn = n2;
+    Kk = K;
+    return n2 / (K * K);
+  };
+
+  uint32_t best = drop;
+  float best_obj = track ? objective(drop) : 0.0f;
+  double remaining = a.restore_frac;  // the reference forms the round fractions in double
+  for (int it = 0; it < a.n_iters; ++it) {
+    const double frac = remaining * a.decay;
+    remaining -= frac;
+    const int pic0 = (int)rintf((float)frac * (float)nts);
+    const float J = objective(drop);  // leaves Mg in t3
+    if (track && (maxim ? J > best_obj : J < best_obj)) {
+      best_obj = J;
+      best = drop;
+    }
+    // term_q of the round, big(Mg)
+    __builtin_amdgcn_wave_barrier();
+    t2[lane] = vq * t3[lane];
+    t0[lane] = rs_bf(t3[lane], big);
+    __builtin_amdgcn_wave_barrier();
+    float tqr = 0.0f;
+    for (int d = 0; d < 64; ++d) tqr = tqr + t2[d];
+    const float tqb = rs_bf(tqr, big);
+    float tk[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) tk[i] = 0.0f;
+    for (int d = 0; d < 64; ++d) {
+      const float m = t0[d];
+      const float* col = VrT + (long long)d * kb_p;
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) {
+        const int k = lane + 64 * i;
+        if (k < n_cand) tk[i] = fmaf(col[k], m, tk[i]);
+      }
+    }
+    uint32_t rkey[NPL], ckey[NPL];
+    float rmax = -__builtin_huge_valf();
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const float raw = rs_bf(Pb[i] * rs_bf(rs_bf(tk[i], big) - tqb, big), big);
+      float r = rs_knorm(gn, Kk, 2.0f * raw + ssq[i], Pb[i]);
+      float c = rs_knorm(gn, Kk, ssq[i] - 2.0f * raw, -Pb[i]);
+      if (maxim) {
+        r = -r;
+        c = -c;
+      }
+      if ((drop >> i) & 1u) rmax = fmaxf(rmax, r);
+      rkey[i] = rs_key(r);
+      ckey[i] = rs_key(c);
+    }
+    // wave max of rmax: beneficial iff some drop candidate has quality > 0
+    const bool beneficial = __ballot(rmax > 0.0f) != 0ull;
+    int n_drop = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) n_drop += __popcll(__ballot((drop >> i) & 1u));
+    int n_kept = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) n_kept += __popcll(__ballot(((cand_bits & ~drop) >> i) & 1u));
+    int pic = pic0;
+    if (beneficial && pic < 1) pic = 1;
+    int cnt = pic < n_drop ? pic : n_drop;
+    cnt = cnt < n_kept ? cnt : n_kept;
+    if (!beneficial) cnt = 0;
+    const uint32_t restore = rs_top_m<NPL>(rkey, drop, cnt, lane);
+    const uint32_t comp = rs_top_m<NPL>(ckey, cand_bits & ~drop, cnt, lane);
+    drop = (drop & ~restore) | comp;
+  }
+  float fin = 0.0f;
+  if (track || a.obj) fin = objective(drop);
+  if (track && !(maxim ? fin > best_obj : fin < best_obj)) {
+    drop = best;
+    fin = best_obj;
+  }
+  if (a.obj && lane == 0) a.obj[row] = fin;
+  float* out = a.rank_key + row * n_cand;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int k = lane + 64 * i;
+    if (k < n_cand) out[k] = ((drop >> i) & 1u) ? 0.0f : 1.0f;
+  }
+}
+
+// ============================================================================
+// C ABI
+// ============================================================================
+template <int NPL>
+static int launch_rs(dim3 grid, dim3 block, size_t lds, hipStream_t stream, const RsArgs& a) {
+  // rows of up to 2048 blocks need more than the default 64 KiB of dynamic LDS
+  RESS_REQUIRE(hipFuncSetAttribute((const void*)k_restore_swap<NPL>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)lds) == hipSuccess,
+               "ress_restore_swap: cannot reserve %zu bytes of LDS", lds);
+  hipLaunchKernelGGL(k_restore_swap<NPL>, grid, block, lds, stream, a);
+  RESS_LAUNCHED("k_restore_swap");
+  return 0;
+}
+
+RESS_API long long ress_restore_swap_workspace_size(int BH, int kb_p, int n_cand) {
+  return (long long)BH * kb_p * 64 * 4 * 2 + (long long)BH * n_cand * 4;
+}
+
+// restore_swap_rank_by (src/ress/scoring/projected.py:395-1058) for every (batch*head,
+// query-block) row: A [BH][q_blk][kb_p] the pooled map over the patch key blocks
+// (attn_full), V [BH][kb_p][64] the block means (v_bar_full), M [H][64][64] (head h =
+// bh % H; identity for the _nowo recipes), nts [BH][q_blk] the kept budgets (after the
+// min-2 floor). Writes rank_key [BH][q_blk][n_cand] = 1 for kept candidates, 0 for
+// dropped: top-nts of it is the restore-swap keep set, which is what build_block_mask
+// selects from the reference's rank_by (where(drop, s, s + max|s| + 1)). obj [BH][q_blk]
+// (optional) receives J = ||g||^2_M / K^2 of the returned set, s_out [BH][q_blk][n_cand]
+// (optional) the scores s = P*sqrt(d^T M d) that rank_by is built from. flags: 1 bf16
+// k-wide tensors (_bf16), 2 track_best, 4 maximize (_antiswap), 8 invert_cut (_anti),
+// 16 renormalize off (the cut ranks s instead of s/(1-P)).
+// Round i moves round(float(f_i) * nts) blocks (at least 1 on rows with a beneficial
+// candidate), f_i = restore_frac * decay * (1 - decay)^i formed in double as the
+// reference does. workspace: ress_restore_swap_workspace_size bytes.
+RESS_API int ress_restore_swap(const void* A, const void* V, const void* M, const void* nts, int BH, int H, int q_blk,
+                               int kb_p, int n_cand, int n_iters, double restore_frac, double decay, int flags,
+                               void* rank_key, void* obj, void* s_out, void* workspace, long long workspace_bytes,
+                               hipStream_t stream) {
+  RESS_REQUIRE(BH > 0 && H > 0 && BH % H == 0 && q_blk >= 0 && kb_p > 0 && n_cand > 0 && n_cand <= kb_p,
+               "ress_restore_swap: bad geometry BH=%d H=%d q_blk=%d kb_p=%d n_cand=%d", BH, H, q_blk, kb_p, n_cand);
+  RESS_REQUIRE(n_cand <= RS_MAX_KBP && kb_p <= RS_MAX_KBP,
+               "ress_restore_swap: rows of more than %d key blocks are not supported (kb_p=%d)", RS_MAX_KBP, kb_p);
+  RESS_REQUIRE(n_iters >= 0 && n_iters <= 16, "ress_restore_swap: n_iters must be in [0, 16]");
+  RESS_REQUIRE(A && V && M && nts && rank_key && workspace, "ress_restore_swap: null pointer");
+  RESS_REQUIRE(workspace_bytes >= ress_restore_swap_workspace_size(BH, kb_p, n_cand),
+               "ress_restore_swap: workspace of %lld bytes required", ress_restore_swap_workspace_size(BH, kb_p, n_cand));
+  if (q_blk == 0) return 0;
+  float* Vr = (float*)workspace;
+  float* VrT = Vr + (long long)BH * kb_p * 64;
+  float* termk = VrT + (long long)BH * kb_p * 64;
+  const int big = (flags & RS_BF16) ? 1 : 0;
+  hipLaunchKernelGGL(k_rs_head, dim3(kb_p, BH), dim3(64), 0, stream, (const float*)V, (const float*)M, H, kb_p, n_cand,
+                     big, Vr, VrT, termk);
+  RESS_LAUNCHED("k_rs_head");
+  RsArgs a;
+  a.A = (const float*)A;
+  a.M = (const float*)M;
+  a.nts = (const int*)nts;
+  a.Vr = Vr;
+  a.VrT = VrT;
+  a.termk = termk;
+  a.rank_key = (float*)rank_key;
+  a.obj = (float*)obj;
+  a.s_out = (float*)s_out;
+  a.H = H;
+  a.q_blk = q_blk;
+  a.kb_p = kb_p;
+  a.n_cand = n_cand;
+  a.n_iters = n_iters;
+  a.flags = flags;
+  a.restore_frac = restore_frac;
+  a.decay = decay;
+  const size_t lds = sizeof(float) * (8192 + 4 * (size_t)(kb_p + 5 * 64));
+  const dim3 grid(cdiv(q_blk, 4), BH), block(256);
+  const int npl = cdiv(n_cand, 64);
+  if (npl <= 4) return launch_rs<4>(grid, block, lds, stream, a);
+  if (npl <= 8) return launch_rs<8>(grid, block, lds, stream, a);
+  if (npl <= 16) return launch_rs<16>(grid, block, lds, stream, a);
+  return launch_rs<32>(grid, block, lds, stream, a);
+}

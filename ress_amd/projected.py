@@ -7,6 +7,7 @@ s_ij = P_ij * sqrt(d^T M_h d), d = v_bar_query_i - v_bar_j.
 
 import torch
 
+from ress_amd import _lib
 from ress_amd.wiring import global_blocks
 
 KEPT_MASS_EPS = 1e-6
@@ -70,8 +71,64 @@ def kept_mass_norm_quality(G, K, delta_G, u, eps=KEPT_MASS_EPS):
     return (G.unsqueeze(-1) * u * (2.0 * K_ + u) / K_.pow(2) - delta_G) / K_new.pow(2)
 
 
+_RS_BF16, _RS_TRACK_BEST, _RS_MAXIMIZE, _RS_INVERT_CUT, _RS_NO_RENORM = 1, 2, 4, 8, 16
+
+
+def _restore_swap(attn_pooled, v_bar, M, num_to_select, restore_frac, n_iters, track_best, big_dtype, decay,
+                  renormalize, n_cand, maximize, invert_cut, want_s):
+    """Run the restore-swap kernel (ress_swap.hip). Returns (keep_key, s) with keep_key
+    (..., nh, q_blk, n_cand) fp32 = 1 kept / 0 dropped, and s the drift scores (or None)."""
+    if big_dtype not in (None, torch.float32, torch.bfloat16):
+        raise NotImplementedError(f"big_dtype {big_dtype} (fp32 and bf16 are implemented)")
+    *lead, nh, q_blk, kb_p = attn_pooled.shape
+    if v_bar.shape[-2:] != (kb_p, 64) or M.shape != (nh, 64, 64):
+        raise ValueError("v_bar must be (..., nh, k_blk, 64) and M (nh, 64, 64)")
+    if n_cand is None:
+        n_cand = kb_p
+    dev = attn_pooled.device
+    A = attn_pooled.float().contiguous()
+    V = v_bar.float().contiguous()
+    Mf = M.float().contiguous()
+    nts = num_to_select.to(torch.int32).expand(*lead, nh, q_blk).contiguous()
+    BH = A.numel() // (q_blk * kb_p) if q_blk else nh
+    keep = torch.empty(*lead, nh, q_blk, n_cand, dtype=torch.float32, device=dev)
+    s = torch.empty_like(keep) if want_s else None
+    flags = ((_RS_BF16 if big_dtype == torch.bfloat16 else 0) | (_RS_TRACK_BEST if track_best else 0)
+             | (_RS_MAXIMIZE if maximize else 0) | (_RS_INVERT_CUT if invert_cut else 0)
+             | (0 if (True if renormalize is None else renormalize) else _RS_NO_RENORM))
+    ws_bytes = _lib.lib().ress_restore_swap_workspace_size(BH, kb_p, n_cand)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    _lib.call("ress_restore_swap", _lib.ptr(A), _lib.ptr(V), _lib.ptr(Mf), _lib.ptr(nts), BH, nh, q_blk, kb_p, n_cand,
+              int(n_iters), float(restore_frac), float(decay), flags, _lib.ptr(keep), None, _lib.ptr(s), _lib.ptr(ws),
+              ws_bytes, _lib.stream_handle(dev))
+    return keep, s
+
+
+def restore_swap_keep(attn_pooled, v_bar, M, num_to_select, restore_frac=0.5, n_iters=1, track_best=False,
+                      big_dtype=None, decay=0.5, renormalize=None, n_cand=None, maximize=False, invert_cut=False):
+    """The restore-swap keep set as a rank key (1 = kept, 0 = dropped): the top
+    num_to_select of it is exactly the set restore_swap_rank_by's rank_by selects."""
+    keep, _ = _restore_swap(attn_pooled, v_bar, M, num_to_select, restore_frac, n_iters, track_best, big_dtype, decay,
+                            renormalize, n_cand, maximize, invert_cut, want_s=False)
+    return keep
+
+
 def restore_swap_rank_by(attn_pooled, v_bar, M, num_to_select, restore_frac=0.5, n_iters=1, dtype=torch.float32,
                          track_best=False, big_dtype=None, decay=0.5, renormalize=None, n_cand=None,
                          maximize=False, invert_cut=False):
-    """ReSS restore-swap ranking (reference projected.py:395-1058)."""
-    raise NotImplementedError("restore-swap ranking is not implemented yet")
+    """ReSS restore-swap ranking (reference projected.py:395-1058), on the GPU kernel.
+
+    attn_pooled (..., nh, q_blk, k_blk) the pooled map over the kernel's patch key blocks,
+    v_bar (..., nh, k_blk, 64), M (nh, 64, 64), num_to_select (..., nh, q_blk). Initial
+    cut by s/(1-P) (s with renormalize=False), then n_iters restore/compensate rounds on
+    J = ||g||^2_M / K^2 with the geometric schedule restore_frac * decay * (1-decay)^i,
+    track_best keeping each row's best state. big_dtype=torch.bfloat16 rounds the
+    k-wide tensors as the reference's _bf16 recipes do. Returns rank_by (..., nh, q_blk,
+    n_cand) = where(drop, s, s + max|s| + 1), in big_dtype (fp32 if None)."""
+    if dtype != torch.float32:
+        raise NotImplementedError("the accumulation dtype is fp32")
+    keep, s = _restore_swap(attn_pooled, v_bar, M, num_to_select, restore_frac, n_iters, track_best, big_dtype,
+                            decay, renormalize, n_cand, maximize, invert_cut, want_s=True)
+    s = s.to(big_dtype or torch.float32)
+    offset = (s.abs().amax() + 1.0) if s.numel() else torch.ones((), dtype=s.dtype, device=s.device)
+    return torch.where(keep > 0.5, s + offset, s)
