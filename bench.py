@@ -122,6 +122,11 @@ def main():
         bud = budget.UniformBudget()
     budget_fn = lambda a: bud.num_to_select(0, a, sr, cdf, 1.0)  # noqa: E731
     out = torch.empty(1, 16, grid.Tk, 64, dtype=torch.float32, device=dev)
+    criterion, M = "probability", None
+    if cfg["mode"] == "ress":  # restore-swap ranking with M_h from a seeded W_O
+        criterion = f"restore_swap_iter{cfg['n_iters']}_bf16_trackbest"
+        W_O = synth.make_w_o().to(dev)
+        M = torch.stack([W_O[:, h * 64:(h + 1) * 64].T @ W_O[:, h * 64:(h + 1) * 64] for h in range(16)])
 
     # attention-kernel events: recorded on the stream the kernel is launched on
     ev = []
@@ -136,15 +141,30 @@ def main():
         return r
 
     import ress_amd.attention as attn_mod
+    from ress_amd import projected
     attn_mod.kernels.sparse_attention = timed_attention
+    rs_ev = []
+    orig_rs = projected.restore_swap_keep
+
+    def timed_restore_swap(*a, **kw):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        r = orig_rs(*a, **kw)
+        e.record()
+        rs_ev.append((s, e))
+        return r
+
+    projected.restore_swap_keep = timed_restore_swap
 
     def step():
-        return sparse_global_attention(q, k, v, grid, budget_fn=budget_fn, out=out, qk_mode=args.qk_mode)
+        return sparse_global_attention(q, k, v, grid, budget_fn=budget_fn, out=out, qk_mode=args.qk_mode,
+                                       block_criterion=criterion, M=M)
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     ev.clear()
+    rs_ev.clear()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
@@ -154,11 +174,13 @@ def main():
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
     attn_ms = sum(s.elapsed_time(e) for s, e in ev) / len(ev)
+    rs_ms = sum(s.elapsed_time(e) for s, e in rs_ev) / len(rs_ev) if rs_ev else None
     attn_mod.kernels.sparse_attention = orig_attn
+    projected.restore_swap_keep = orig_rs
 
     # work actually done (same map every step)
     res = sparse_global_attention(q, k, v, grid, budget_fn=budget_fn, out=out, keep_intermediates=True,
-                                  qk_mode=args.qk_mode)
+                                  qk_mode=args.qk_mode, block_criterion=criterion, M=M)
     torch.cuda.synchronize()
     lut, nvalid = res.lut.cpu().numpy(), res.nvalid.cpu().numpy()
     flops_kept = retained_flops(nvalid, lut, grid)
@@ -200,10 +222,12 @@ def main():
                    "frames": frames, "tokens": N, "heads": 16, "head_dim": 64, "sparse_ratio": sr,
                    "cdf_threshold": cdf, "realized_sparsity": round(sparsity, 4), "qk_mode": args.qk_mode},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": round(peak, 1), "unit": "TFLOP/s",
-                     "frac": round(achieved / peak, 4), "traffic": measured_traffic(f"k_sparse_attn_{args.qk_mode}"),
+                     "frac": round(achieved / peak, 4),
+                     "traffic": measured_traffic(f"k_sparse_attn_{args.qk_mode}") if args.config == 1 else None,
                      "frac_of_int8_peak": round(achieved / PEAK_INT8_TOPS, 4),
                      "kernel": "k_sparse_attn", "kernel_ms": round(attn_ms, 4),
                      "retained_flop_per_launch": flops_kept},
+        "restore_swap_ms": None if rs_ms is None else round(rs_ms, 4),
         "prep": {"ms": round(prep_ms, 4), "algorithmic_bytes": prep_bytes,
                  "achieved_GBs": round(prep_bytes / (prep_ms * 1e-3) / 1e9, 1), "peak_GBs": PEAK_HBM_GBS},
     }

@@ -120,14 +120,25 @@ struct RsArgs {
   double restore_frac, decay;  // geometric schedule (projected.py:775-790)
 };
 
-// The rows of one head: 4 waves, each its own row.
-template <int NPL>
-__global__ __launch_bounds__(256) void k_restore_swap(RsArgs a) {
+// V of the head in LDS (VLDS, bf16 mode with kb_p <= RS_LDS_KBP): bf16 pairs, word w of
+// row k at k*32 + (w ^ (k & 31)), so that both access patterns -- lanes over the 64
+// dims of one key block, and lanes over consecutive key blocks at one dim -- hit 32
+// distinct banks. Otherwise V is read from the L2-resident copies Vr / VrT.
+#define RS_LDS_KBP 1024
+__device__ __forceinline__ float rs_vlds(const uint32_t* vw, int k, int d) {
+  const uint32_t word = vw[k * 32 + ((d >> 1) ^ (k & 31))];
+  return __uint_as_float((d & 1) ? (word & 0xffff0000u) : (word << 16));
+}
+
+// The rows of one head: WAVES waves, each its own row at a time.
+template <int NPL, bool VLDS, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_per_wg) {
   extern __shared__ float sh[];
   float* M32T = sh;                 // [64][64] M^T (fp32)
   float* MbT = sh + 4096;           // [64][64] big(M)^T
+  uint32_t* vw = reinterpret_cast<uint32_t*>(sh + 8192);  // VLDS: [kb_p][32] bf16 pairs
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  float* wsh = sh + 8192 + w * (a.kb_p + 5 * 64);
+  float* wsh = sh + 8192 + (VLDS ? a.kb_p * 32 : 0) + w * (a.kb_p + 5 * 64);
   float* Pw = wsh;                  // [kb_p] big(P) of the row, then P*drop
   float* vqs = wsh + a.kb_p;        // [64]
   float* t0 = vqs + 64;             // [64] scratch vectors
@@ -139,18 +150,35 @@ __global__ __launch_bounds__(256) void k_restore_swap(RsArgs a) {
   const bool maxim = a.flags & RS_MAXIMIZE, inv = a.flags & RS_INVERT_CUT;
   const bool renorm = !(a.flags & RS_NO_RENORM);
   const float* Mh = a.M + (long long)(bh % a.H) * 4096;
-  for (int e = threadIdx.x; e < 4096; e += 256) {
+  for (int e = threadIdx.x; e < 4096; e += 64 * WAVES) {
     const float m = Mh[e];
     M32T[(e & 63) * 64 + (e >> 6)] = m;
     MbT[(e & 63) * 64 + (e >> 6)] = rs_bf(m, big);
   }
-  __syncthreads();
   const float* Vr = a.Vr + (long long)bh * a.kb_p * 64;
   const float* VrT = a.VrT + (long long)bh * 64 * a.kb_p;
+  if constexpr (VLDS) {
+    for (int e = threadIdx.x; e < a.kb_p * 32; e += 64 * WAVES) {
+      const int k = e >> 5, wd = e & 31;
+      const uint32_t lo = __float_as_uint(Vr[(long long)k * 64 + 2 * wd]) >> 16;
+      const uint32_t hi = __float_as_uint(Vr[(long long)k * 64 + 2 * wd + 1]) & 0xffff0000u;
+      vw[k * 32 + (wd ^ (k & 31))] = hi | lo;  // Vr holds bf16-exact values in this mode
+    }
+  }
+  __syncthreads();
+  // V[k][d] for lanes over d (vrow) and for lanes over k (vcol)
+  auto vrow = [&](int k, int d) -> float {
+    if constexpr (VLDS) return rs_vlds(vw, k, d);
+    else return Vr[(long long)k * 64 + d];
+  };
+  auto vcol = [&](int d, int k) -> float {
+    if constexpr (VLDS) return rs_vlds(vw, k, d);
+    else return VrT[(long long)d * a.kb_p + k];
+  };
   const float* tkey = a.termk + (long long)bh * a.n_cand;
   const int n_cand = a.n_cand, kb_p = a.kb_p;
-  const int q = blockIdx.x * 4 + w;
-  if (q >= a.q_blk) return;  // no block-level sync after this point
+  const int q_end = min(a.q_blk, (blockIdx.x + 1) * rows_per_wg);
+  for (int q = blockIdx.x * rows_per_wg + w; q < q_end; q += WAVES) {
   const long long row = (long long)bh * a.q_blk + q;
 
   // ---- row inputs and the dense reference ---------------------------------------
@@ -170,10 +198,11 @@ __global__ __launch_bounds__(256) void k_restore_swap(RsArgs a) {
   float vq, tm = 0.0f;  // v_bar_query[lane], total mass (same in every lane)
   {
     float acc = 0.0f;
+#pragma unroll 16
     for (int k = 0; k < kb_p; ++k) {
       const float p = Pw[k];
       tm = tm + p;
-      acc = fmaf(p, Vr[(long long)k * 64 + lane], acc);
+      acc = fmaf(p, vrow(k, lane), acc);
     }
     vq = rs_bf(acc, big);
     tm = rs_bf(tm, big);
@@ -184,6 +213,7 @@ __global__ __launch_bounds__(256) void k_restore_swap(RsArgs a) {
   float mvq;
   {
     float acc = 0.0f;
+#pragma unroll 16
     for (int j = 0; j < 64; ++j) acc = fmaf(MbT[j * 64 + lane], vqs[j], acc);
     mvq = rs_bf(acc, big);
   }
@@ -191,6 +221,7 @@ __global__ __launch_bounds__(256) void k_restore_swap(RsArgs a) {
   t1[lane] = rs_bf(mvq * vq, big);
   __builtin_amdgcn_wave_barrier();
   float tq = 0.0f;
+#pragma unroll 16
   for (int i = 0; i < 64; ++i) tq = tq + t1[i];
   tq = rs_bf(tq, big);
   // s, s_cut, s^2 per candidate
@@ -201,11 +232,10 @@ __global__ __launch_bounds__(256) void k_restore_swap(RsArgs a) {
     for (int i = 0; i < NPL; ++i) cr[i] = 0.0f;
     for (int d = 0; d < 64; ++d) {
       const float m = t0[d];
-      const float* col = VrT + (long long)d * kb_p;
 #pragma unroll
       for (int i = 0; i < NPL; ++i) {
         const int k = lane + 64 * i;
-        if (k < n_cand) cr[i] = fmaf(m, col[k], cr[i]);
+        if (k < n_cand) cr[i] = fmaf(m, vcol(d, k), cr[i]);
       }
     }
 #pragma unroll
@@ -242,10 +272,11 @@ __global__ __launch_bounds__(256) void k_restore_swap(RsArgs a) {
     }
     __builtin_amdgcn_wave_barrier();
     float acc = 0.0f, sp = 0.0f;
+#pragma unroll 16
     for (int k = 0; k < n_cand; ++k) {
       const float p = Pw[k];
       sp = sp + p;
-      acc = fmaf(p, Vr[(long long)k * 64 + lane], acc);
+      acc = fmaf(p, vrow(k, lane), acc);
     }
     sp = rs_bf(sp, big);
     const float g = sp * vq - rs_bf(acc, big);
@@ -253,11 +284,13 @@ __global__ __launch_bounds__(256) void k_restore_swap(RsArgs a) {
     t1[lane] = g;
     __builtin_amdgcn_wave_barrier();
     float mg = 0.0f;
+#pragma unroll 16
     for (int j = 0; j < 64; ++j) mg = fmaf(M32T[j * 64 + lane], t1[j], mg);
     t2[lane] = g * mg;    // products of ||g||^2_M
     t3[lane] = mg;
     __builtin_amdgcn_wave_barrier();
     float n2 = 0.0f;
+#pragma unroll 16
     for (int d = 0; d < 64; ++d) n2 = n2 + t2[d];
     float K = tm - sp;
     K = K < 1e-6f ? 1e-6f : K;
@@ -284,6 +317,7 @@ __global__ __launch_bounds__(256) void k_restore_swap(RsArgs a) {
     t0[lane] = rs_bf(t3[lane], big);
     __builtin_amdgcn_wave_barrier();
     float tqr = 0.0f;
+#pragma unroll 16
     for (int d = 0; d < 64; ++d) tqr = tqr + t2[d];
     const float tqb = rs_bf(tqr, big);
     float tk[NPL];
@@ -291,11 +325,10 @@ __global__ __launch_bounds__(256) void k_restore_swap(RsArgs a) {
     for (int i = 0; i < NPL; ++i) tk[i] = 0.0f;
     for (int d = 0; d < 64; ++d) {
       const float m = t0[d];
-      const float* col = VrT + (long long)d * kb_p;
 #pragma unroll
       for (int i = 0; i < NPL; ++i) {
         const int k = lane + 64 * i;
-        if (k < n_cand) tk[i] = fmaf(col[k], m, tk[i]);
+        if (k < n_cand) tk[i] = fmaf(vcol(d, k), m, tk[i]);
       }
     }
     uint32_t rkey[NPL], ckey[NPL];
@@ -343,20 +376,41 @@ __global__ __launch_bounds__(256) void k_restore_swap(RsArgs a) {
     const int k = lane + 64 * i;
     if (k < n_cand) out[k] = ((drop >> i) & 1u) ? 0.0f : 1.0f;
   }
+  }  // rows of this wave
 }
 
 // ============================================================================
 // C ABI
 // ============================================================================
-template <int NPL>
-static int launch_rs(dim3 grid, dim3 block, size_t lds, hipStream_t stream, const RsArgs& a) {
-  // rows of up to 2048 blocks need more than the default 64 KiB of dynamic LDS
-  RESS_REQUIRE(hipFuncSetAttribute((const void*)k_restore_swap<NPL>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   (int)lds) == hipSuccess,
+template <int NPL, bool VLDS, int WAVES>
+static int launch_rs(int BH, size_t lds, hipStream_t stream, const RsArgs& a) {
+  // the LDS-resident V needs more than the default 64 KiB of dynamic LDS
+  RESS_REQUIRE(hipFuncSetAttribute((const void*)k_restore_swap<NPL, VLDS, WAVES>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess,
                "ress_restore_swap: cannot reserve %zu bytes of LDS", lds);
-  hipLaunchKernelGGL(k_restore_swap<NPL>, grid, block, lds, stream, a);
+  // one head's rows split over enough workgroups to give every CU about one
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                              hipSuccess || cus <= 0)
+    cus = 256;
+  const int per_head = max(1, min(cdiv(a.q_blk, WAVES), cdiv(cus, BH)));
+  const int rows_per_wg = cdiv(a.q_blk, per_head);
+  hipLaunchKernelGGL((k_restore_swap<NPL, VLDS, WAVES>), dim3(cdiv(a.q_blk, rows_per_wg), BH), dim3(64 * WAVES),
+                     lds, stream, a, rows_per_wg);
   RESS_LAUNCHED("k_restore_swap");
   return 0;
+}
+
+template <int NPL>
+static int launch_rs_npl(int BH, int kb_p, bool big, hipStream_t stream, const RsArgs& a) {
+  if constexpr (NPL * 64 <= RS_LDS_KBP) {  // rows that fit take the LDS-resident V
+    if (big && kb_p <= RS_LDS_KBP) {
+      const size_t lds = sizeof(float) * (8192 + 32 * (size_t)kb_p + 8 * (size_t)(kb_p + 5 * 64));
+      return launch_rs<NPL, true, 8>(BH, lds, stream, a);
+    }
+  }
+  const size_t lds = sizeof(float) * (8192 + 4 * (size_t)(kb_p + 5 * 64));
+  return launch_rs<NPL, false, 4>(BH, lds, stream, a);
 }
 
 RESS_API long long ress_restore_swap_workspace_size(int BH, int kb_p, int n_cand) {
@@ -415,11 +469,9 @@ RESS_API int ress_restore_swap(const void* A, const void* V, const void* M, cons
   a.flags = flags;
   a.restore_frac = restore_frac;
   a.decay = decay;
-  const size_t lds = sizeof(float) * (8192 + 4 * (size_t)(kb_p + 5 * 64));
-  const dim3 grid(cdiv(q_blk, 4), BH), block(256);
   const int npl = cdiv(n_cand, 64);
-  if (npl <= 4) return launch_rs<4>(grid, block, lds, stream, a);
-  if (npl <= 8) return launch_rs<8>(grid, block, lds, stream, a);
-  if (npl <= 16) return launch_rs<16>(grid, block, lds, stream, a);
-  return launch_rs<32>(grid, block, lds, stream, a);
+  if (npl <= 4) return launch_rs_npl<4>(BH, kb_p, big, stream, a);
+  if (npl <= 8) return launch_rs_npl<8>(BH, kb_p, big, stream, a);
+  if (npl <= 16) return launch_rs_npl<16>(BH, kb_p, big, stream, a);
+  return launch_rs_npl<32>(BH, kb_p, big, stream, a);
 }
