@@ -14,8 +14,8 @@
 // sums of rounded terms): lane-parallel over the independent outputs, never split.
 //
 // Work: per row, O(kb_p * 64) for the dense reference, O(n_cand * 64) per round for the
-// masked sums and term_k; selections are 32-step MSB-first threshold searches over
-// order keys with wave ballots.
+// masked sums and term_k; selections are 4-digit radix selects over the order keys with
+// a per-wave LDS histogram.
 #include "common.h"
 
 #define RS_BF16 1
@@ -46,63 +46,43 @@ __device__ __forceinline__ float rs_knorm(float G, float K, float dG, float u) {
   return (a * b / (K * K) - dG) / (Kn * Kn);
 }
 
-// Exact top-m of key[i] (lane element i <-> candidate lane + 64 i) among `valid` bits,
-// ties to the lowest candidate index; returns the selection as per-lane bits.
-template <int NPL>
-__device__ __forceinline__ uint32_t rs_top_m(const uint32_t (&key)[NPL], uint32_t valid, int m, int lane) {
-  if (m <= 0) return 0u;
-  uint32_t thr = 0u;
-  for (int b = 31; b >= 0; --b) {
-    const uint32_t cand = thr | (1u << b);
-    int c = 0;
-#pragma unroll
-    for (int i = 0; i < NPL; ++i) c += __popcll(__ballot(((valid >> i) & 1u) && key[i] >= cand));
-    if (c >= m) thr = cand;
-  }
-  int n_gt = 0;
-#pragma unroll
-  for (int i = 0; i < NPL; ++i) n_gt += __popcll(__ballot(((valid >> i) & 1u) && key[i] > thr));
-  const int take_eq = m - n_gt;  // ties at thr taken in index order
-  uint32_t sel = 0u;
-  int before = 0;  // tied entries with a smaller index in earlier lane elements
-  const unsigned long long lower = lane ? (~0ull >> (64 - lane)) : 0ull;
-#pragma unroll
-  for (int i = 0; i < NPL; ++i) {
-    const bool v = (valid >> i) & 1u;
-    const bool eq = v && key[i] == thr;
-    const unsigned long long be = __ballot(eq);
-    const int rank = before + __popcll(be & lower);
-    if ((v && key[i] > thr) || (eq && rank < take_eq)) sel |= 1u << i;
-    before += __popcll(be);
-  }
-  return sel;
-}
-
-// Per-head preparation: Vr = big(V) [kb_p][64] and its transpose VrT [64][kb_p], and the
-// key side of quadratic_deviation, termk[k] = big(sum_i big(big(Mb v_k)_i * v_ki)).
-__global__ __launch_bounds__(64) void k_rs_head(const float* __restrict__ V, const float* __restrict__ M, int H,
-                                                int kb_p, int n_cand, int big, float* __restrict__ Vr,
-                                                float* __restrict__ VrT, float* __restrict__ termk) {
-  __shared__ float MbT[64 * 64];  // MbT[j*64 + i] = big(M[i][j])
-  __shared__ float vk[64];
-  const int k = blockIdx.x, bh = blockIdx.y, lane = threadIdx.x;
+// Per-head preparation, 64 key blocks per workgroup: Vr = big(V) [kb_p][64], its
+// transpose VrT [64][kb_p] (through an LDS tile, both stores coalesced), and the key side
+// of quadratic_deviation, termk[k] = big(sum_i big(big(Mb v_k)_i * v_ki)) with the
+// product and the sum sequential in index order.
+__global__ __launch_bounds__(256) void k_rs_head(const float* __restrict__ V, const float* __restrict__ M, int H,
+                                                 int kb_p, int n_cand, int big, float* __restrict__ Vr,
+                                                 float* __restrict__ VrT, float* __restrict__ termk) {
+  __shared__ float MbT[64 * 64];     // MbT[j*64 + i] = big(M[i][j])
+  __shared__ float tile[64][65];     // [key][dim], padded
+  __shared__ float prod[4][64];      // one key's rounded products per wave
+  const int k0 = blockIdx.x * 64, bh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const float* Mh = M + (long long)(bh % H) * 4096;
-  for (int e = lane; e < 4096; e += 64) MbT[(e & 63) * 64 + (e >> 6)] = rs_bf(Mh[e], big);
-  const float x = rs_bf(V[((long long)bh * kb_p + k) * 64 + lane], big);
-  Vr[((long long)bh * kb_p + k) * 64 + lane] = x;
-  VrT[((long long)bh * 64 + lane) * kb_p + k] = x;
-  vk[lane] = x;
+  for (int e = tid; e < 4096; e += 256) MbT[(e & 63) * 64 + (e >> 6)] = rs_bf(Mh[e], big);
+  for (int r = w; r < 64; r += 4) {  // rows of V: lane = dim
+    const int k = k0 + r;
+    float x = 0.0f;
+    if (k < kb_p) {
+      x = rs_bf(V[((long long)bh * kb_p + k) * 64 + lane], big);
+      Vr[((long long)bh * kb_p + k) * 64 + lane] = x;
+    }
+    tile[r][lane] = x;
+  }
   __syncthreads();
-  if (k >= n_cand) return;
-  float a = 0.0f;  // (Mb v_k)_lane, sequential over j
-  for (int j = 0; j < 64; ++j) a = fmaf(MbT[j * 64 + lane], vk[j], a);
-  __syncthreads();
-  vk[lane] = rs_bf(rs_bf(a, big) * x, big);  // the rounded product for dim lane
-  __syncthreads();
-  if (lane == 0) {
+  for (int d = w; d < 64; d += 4) {  // columns: lane = key
+    if (k0 + lane < kb_p) VrT[((long long)bh * 64 + d) * kb_p + k0 + lane] = tile[lane][d];
+  }
+  for (int r = w; r < 64; r += 4) {  // termk: wave per key, lane = output dim i
+    const int k = k0 + r;
+    if (k >= n_cand) break;
+    float acc = 0.0f;
+    for (int j = 0; j < 64; ++j) acc = fmaf(MbT[j * 64 + lane], tile[r][j], acc);
+    prod[w][lane] = rs_bf(rs_bf(acc, big) * tile[r][lane], big);
+    __builtin_amdgcn_wave_barrier();
     float t = 0.0f;
-    for (int i = 0; i < 64; ++i) t = t + vk[i];
-    termk[(long long)bh * n_cand + k] = rs_bf(t, big);
+    for (int i = 0; i < 64; ++i) t = t + prod[w][i];
+    if (lane == 0) termk[(long long)bh * n_cand + k] = rs_bf(t, big);
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -120,14 +100,73 @@ struct RsArgs {
   double restore_frac, decay;  // geometric schedule (projected.py:775-790)
 };
 
+// Exact top-m among `valid` lane elements by MSB-first radix select over the order keys
+// (four 8-bit digits, a 256-bin histogram in LDS per digit), then ties at the threshold
+// taken in candidate-index order. hist: 256 ints of this wave's LDS.
+template <int NPL>
+__device__ __forceinline__ uint32_t rs_top_m(const uint32_t (&key)[NPL], uint32_t valid, int m, int lane,
+                                             int* hist) {
+  if (m <= 0) return 0u;
+  int n_valid = 0;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) n_valid += __popcll(__ballot((valid >> i) & 1u));
+  if (n_valid <= m) return valid;
+  uint32_t prefix = 0u, pmask = 0u;
+  int need = m;  // still to take among the keys matching the fixed high digits
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    hist[lane] = hist[lane + 64] = hist[lane + 128] = hist[lane + 192] = 0;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < NPL; ++i)
+      if (((valid >> i) & 1u) && (key[i] & pmask) == prefix) atomicAdd(&hist[(key[i] >> shift) & 255u], 1);
+    __builtin_amdgcn_wave_barrier();
+    // lane l owns bins 4l..4l+3; suffix counts S(t) = #{digit >= t}
+    const int h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2], h3 = hist[4 * lane + 3];
+    const int own = h0 + h1 + h2 + h3;
+    int suf = own;  // inclusive suffix over lanes >= l
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_down(suf, off);
+      if (lane + off < 64) suf += y;
+    }
+    const int above = suf - own;  // keys in bins of higher lanes
+    const int s3 = above + h3, s2 = s3 + h2, s1 = s2 + h1, s0 = s1 + h0;
+    // the digit t with S(t) >= need > S(t+1) is unique
+    int t = -1, gt = 0;
+    if (s3 >= need && above < need) t = 3, gt = above;
+    else if (s2 >= need && s3 < need) t = 2, gt = s3;
+    else if (s1 >= need && s2 < need) t = 1, gt = s2;
+    else if (s0 >= need && s1 < need) t = 0, gt = s1;
+    const unsigned long long hit = __ballot(t >= 0);
+    const int src = __ffsll((long long)hit) - 1;
+    const int digit = __shfl(4 * lane + t, src), n_gt = __shfl(gt, src);
+    need -= n_gt;
+    prefix |= (uint32_t)digit << shift;
+    pmask |= 255u << shift;
+    __builtin_amdgcn_wave_barrier();
+  }
+  const uint32_t thr = prefix;  // the m-th largest key; `need` of its ties are taken
+  uint32_t sel = 0u;
+  int before = 0;
+  const unsigned long long lower = lane ? (~0ull >> (64 - lane)) : 0ull;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const bool v = (valid >> i) & 1u;
+    const bool eq = v && key[i] == thr;
+    const unsigned long long be = __ballot(eq);
+    const int rank = before + __popcll(be & lower);
+    if ((v && key[i] > thr) || (eq && rank < need)) sel |= 1u << i;
+    before += __popcll(be);
+  }
+  return sel;
+}
+
 // V of the head in LDS (VLDS, bf16 mode with kb_p <= RS_LDS_KBP): bf16 pairs, word w of
 // row k at k*32 + (w ^ (k & 31)), so that both access patterns -- lanes over the 64
-// dims of one key block, and lanes over consecutive key blocks at one dim -- hit 32
-// distinct banks. Otherwise V is read from the L2-resident copies Vr / VrT.
+// dims of one key block, and lanes over consecutive key blocks at one dim pair -- hit
+// 32 distinct banks. Otherwise V is read from the L2-resident copies Vr / VrT.
 #define RS_LDS_KBP 1024
-__device__ __forceinline__ float rs_vlds(const uint32_t* vw, int k, int d) {
-  const uint32_t word = vw[k * 32 + ((d >> 1) ^ (k & 31))];
-  return __uint_as_float((d & 1) ? (word & 0xffff0000u) : (word << 16));
+__device__ __forceinline__ uint32_t rs_vword(const uint32_t* vw, int k, int pair) {
+  return vw[k * 32 + (pair ^ (k & 31))];
 }
 
 // The rows of one head: WAVES waves, each its own row at a time.
@@ -138,13 +177,15 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
   float* MbT = sh + 4096;           // [64][64] big(M)^T
   uint32_t* vw = reinterpret_cast<uint32_t*>(sh + 8192);  // VLDS: [kb_p][32] bf16 pairs
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  float* wsh = sh + 8192 + (VLDS ? a.kb_p * 32 : 0) + w * (a.kb_p + 5 * 64);
-  float* Pw = wsh;                  // [kb_p] big(P) of the row, then P*drop
-  float* vqs = wsh + a.kb_p;        // [64]
-  float* t0 = vqs + 64;             // [64] scratch vectors
-  float* t1 = t0 + 64;
+  const int kb4 = (a.kb_p + 3) & ~3;
+  float* wsh = sh + 8192 + (VLDS ? a.kb_p * 32 : 0) + w * (kb4 + 5 * 64);
+  float* Pw = wsh;                  // [kb_p] big(P) of the row, then P*drop (16-byte aligned)
+  float* vqs = wsh + kb4;           // [64]
+  float* t0 = vqs + 64;             // [64] scratch vectors; t0..t3 double as the
+  float* t1 = t0 + 64;              //      256-bin selection histogram
   float* t2 = t1 + 64;
   float* t3 = t2 + 64;
+  int* hist = reinterpret_cast<int*>(t0);
   const int bh = blockIdx.y;
   const bool big = a.flags & RS_BF16, track = a.flags & RS_TRACK_BEST;
   const bool maxim = a.flags & RS_MAXIMIZE, inv = a.flags & RS_INVERT_CUT;
@@ -166,216 +207,246 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
     }
   }
   __syncthreads();
-  // V[k][d] for lanes over d (vrow) and for lanes over k (vcol)
-  auto vrow = [&](int k, int d) -> float {
-    if constexpr (VLDS) return rs_vlds(vw, k, d);
-    else return Vr[(long long)k * 64 + d];
+  const int vsh = (lane & 1) ? 0 : 16;  // this lane's dim in the upper half of its pair word
+  // V[k][lane] (lanes over dims)
+  auto vrow = [&](int k) -> float {
+    if constexpr (VLDS) return __uint_as_float((rs_vword(vw, k, lane >> 1) << vsh) & 0xffff0000u);
+    else return Vr[(long long)k * 64 + lane];
   };
-  auto vcol = [&](int d, int k) -> float {
-    if constexpr (VLDS) return rs_vlds(vw, k, d);
-    else return VrT[(long long)d * a.kb_p + k];
+  // (V[k][2p], V[k][2p+1]) (lanes over key blocks)
+  auto vpair = [&](int p, int k, float& v0, float& v1) {
+    if constexpr (VLDS) {
+      const uint32_t word = rs_vword(vw, k, p);
+      v0 = __uint_as_float(word << 16);
+      v1 = __uint_as_float(word & 0xffff0000u);
+    } else {
+      v0 = VrT[(long long)(2 * p) * a.kb_p + k];
+      v1 = VrT[(long long)(2 * p + 1) * a.kb_p + k];
+    }
   };
   const float* tkey = a.termk + (long long)bh * a.n_cand;
   const int n_cand = a.n_cand, kb_p = a.kb_p;
-  const int q_end = min(a.q_blk, (blockIdx.x + 1) * rows_per_wg);
-  for (int q = blockIdx.x * rows_per_wg + w; q < q_end; q += WAVES) {
-  const long long row = (long long)bh * a.q_blk + q;
-
-  // ---- row inputs and the dense reference ---------------------------------------
-  const float* Arow = a.A + row * kb_p;
-  for (int k = lane; k < kb_p; k += 64) Pw[k] = rs_bf(Arow[k], big);
-  float Pb[NPL], ssq[NPL];
-#pragma unroll
-  for (int i = 0; i < NPL; ++i) {
-    const int k = lane + 64 * i;
-    Pb[i] = k < n_cand ? rs_bf(Arow[k], big) : 0.0f;
-  }
-  uint32_t cand_bits = 0u;  // lane elements that are candidates
+  const int nel = (n_cand + 63) >> 6;  // lane elements holding candidates (wave-uniform)
+  uint32_t cand_bits = 0u;             // lane elements that are candidates
 #pragma unroll
   for (int i = 0; i < NPL; ++i)
     if (lane + 64 * i < n_cand) cand_bits |= 1u << i;
-  __builtin_amdgcn_wave_barrier();
-  float vq, tm = 0.0f;  // v_bar_query[lane], total mass (same in every lane)
-  {
-    float acc = 0.0f;
-#pragma unroll 16
-    for (int k = 0; k < kb_p; ++k) {
-      const float p = Pw[k];
-      tm = tm + p;
-      acc = fmaf(p, vrow(k, lane), acc);
+  // sequential sum + dot over k < n of Pw[k] and V[k][lane] (4 P values per LDS read)
+  auto pv_chain = [&](int n, float& sum, float& dot) {
+    float sp = 0.0f, acc = 0.0f;
+    const int n4 = n & ~3;
+#pragma unroll 4
+    for (int k = 0; k < n4; k += 4) {
+      const float4 p4 = *reinterpret_cast<const float4*>(Pw + k);
+      sp = sp + p4.x;
+      acc = fmaf(p4.x, vrow(k), acc);
+      sp = sp + p4.y;
+      acc = fmaf(p4.y, vrow(k + 1), acc);
+      sp = sp + p4.z;
+      acc = fmaf(p4.z, vrow(k + 2), acc);
+      sp = sp + p4.w;
+      acc = fmaf(p4.w, vrow(k + 3), acc);
     }
-    vq = rs_bf(acc, big);
-    tm = rs_bf(tm, big);
-  }
-  vqs[lane] = vq;
-  __builtin_amdgcn_wave_barrier();
-  // quadratic_deviation's query side: Mvq = big(Mb vq), term_q = big(sum big(Mvq*vq))
-  float mvq;
-  {
-    float acc = 0.0f;
-#pragma unroll 16
-    for (int j = 0; j < 64; ++j) acc = fmaf(MbT[j * 64 + lane], vqs[j], acc);
-    mvq = rs_bf(acc, big);
-  }
-  t0[lane] = mvq;
-  t1[lane] = rs_bf(mvq * vq, big);
-  __builtin_amdgcn_wave_barrier();
-  float tq = 0.0f;
-#pragma unroll 16
-  for (int i = 0; i < 64; ++i) tq = tq + t1[i];
-  tq = rs_bf(tq, big);
-  // s, s_cut, s^2 per candidate
-  uint32_t key[NPL];
-  {
-    float cr[NPL];
-#pragma unroll
-    for (int i = 0; i < NPL; ++i) cr[i] = 0.0f;
-    for (int d = 0; d < 64; ++d) {
-      const float m = t0[d];
-#pragma unroll
-      for (int i = 0; i < NPL; ++i) {
-        const int k = lane + 64 * i;
-        if (k < n_cand) cr[i] = fmaf(m, vcol(d, k), cr[i]);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-      const int k = lane + 64 * i;
-      float sc = 0.0f;
-      ssq[i] = 0.0f;
-      if (k < n_cand) {
-        const float c2 = rs_bf(2.0f * rs_bf(cr[i], big), big);
-        float qd = rs_bf(rs_bf(tq - c2, big) + tkey[k], big);
-        qd = qd < 0.0f ? 0.0f : qd;
-        const float sq = rs_bf(sqrtf(qd), big);
-        const float s = rs_bf(Pb[i] * sq, big);
-        float om = rs_bf(1.0f - Pb[i], big);
-        om = rs_bf(om < 1e-4f ? 1e-4f : om, big);
-        sc = renorm ? rs_bf(s / om, big) : s;
-        ssq[i] = rs_bf(s * s, big);
-        if (a.s_out) a.s_out[row * n_cand + k] = s;
-      }
-      key[i] = rs_key(inv ? -sc : sc);
-    }
-  }
-  int nts = a.nts[row];
-  const int nkeep = nts < 0 ? 0 : (nts > n_cand ? n_cand : nts);
-  uint32_t drop = cand_bits & ~rs_top_m<NPL>(key, cand_bits, nkeep, lane);
-
-  // J, and g / Mg / ||g||^2_M / K of a drop set (projected.py:859-868, 903-918)
-  float gn = 0.0f, Kk = 1.0f;
-  auto objective = [&](uint32_t dr) -> float {
-#pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-      const int k = lane + 64 * i;
-      if (k < n_cand) Pw[k] = ((dr >> i) & 1u) ? Pb[i] : 0.0f;
-    }
-    __builtin_amdgcn_wave_barrier();
-    float acc = 0.0f, sp = 0.0f;
-#pragma unroll 16
-    for (int k = 0; k < n_cand; ++k) {
+    for (int k = n4; k < n; ++k) {
       const float p = Pw[k];
       sp = sp + p;
-      acc = fmaf(p, vrow(k, lane), acc);
+      acc = fmaf(p, vrow(k), acc);
     }
-    sp = rs_bf(sp, big);
-    const float g = sp * vq - rs_bf(acc, big);
-    __builtin_amdgcn_wave_barrier();
-    t1[lane] = g;
-    __builtin_amdgcn_wave_barrier();
-    float mg = 0.0f;
-#pragma unroll 16
-    for (int j = 0; j < 64; ++j) mg = fmaf(M32T[j * 64 + lane], t1[j], mg);
-    t2[lane] = g * mg;    // products of ||g||^2_M
-    t3[lane] = mg;
-    __builtin_amdgcn_wave_barrier();
-    float n2 = 0.0f;
-#pragma unroll 16
-    for (int d = 0; d < 64; ++d) n2 = n2 + t2[d];
-    float K = tm - sp;
-    K = K < 1e-6f ? 1e-6f : K;
-    gn = n2;
-    Kk = K;
-    return n2 / (K * K);
+    sum = sp;
+    dot = acc;
+  };
+  // out[i] = sequential dot over d of vec[d] (LDS, broadcast) and V[k_i][d]
+  auto vdot_cols = [&](const float* vec, float (&out)[NPL]) {
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) out[i] = 0.0f;
+    for (int p = 0; p < 32; ++p) {
+      const float m0 = vec[2 * p], m1 = vec[2 * p + 1];
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) {
+        if (i < nel) {
+          int k = lane + 64 * i;
+          k = k < n_cand ? k : n_cand - 1;
+          float v0, v1;
+          vpair(p, k, v0, v1);
+          out[i] = fmaf(m1, v1, fmaf(m0, v0, out[i]));
+        }
+      }
+    }
   };
 
-  uint32_t best = drop;
-  float best_obj = track ? objective(drop) : 0.0f;
-  double remaining = a.restore_frac;  // the reference forms the round fractions in double
-  for (int it = 0; it < a.n_iters; ++it) {
-    const double frac = remaining * a.decay;
-    remaining -= frac;
-    const int pic0 = (int)rintf((float)frac * (float)nts);
-    const float J = objective(drop);  // leaves Mg in t3
-    if (track && (maxim ? J > best_obj : J < best_obj)) {
-      best_obj = J;
-      best = drop;
-    }
-    // term_q of the round, big(Mg)
-    __builtin_amdgcn_wave_barrier();
-    t2[lane] = vq * t3[lane];
-    t0[lane] = rs_bf(t3[lane], big);
-    __builtin_amdgcn_wave_barrier();
-    float tqr = 0.0f;
-#pragma unroll 16
-    for (int d = 0; d < 64; ++d) tqr = tqr + t2[d];
-    const float tqb = rs_bf(tqr, big);
-    float tk[NPL];
+  const int q_end = min(a.q_blk, (blockIdx.x + 1) * rows_per_wg);
+  for (int q = blockIdx.x * rows_per_wg + w; q < q_end; q += WAVES) {
+    const long long row = (long long)bh * a.q_blk + q;
+
+    // ---- row inputs and the dense reference -------------------------------------
+    const float* Arow = a.A + row * kb_p;
+    for (int k = lane; k < kb_p; k += 64) Pw[k] = rs_bf(Arow[k], big);
+    float Pb[NPL], ssq[NPL];
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) tk[i] = 0.0f;
-    for (int d = 0; d < 64; ++d) {
-      const float m = t0[d];
+    for (int i = 0; i < NPL; ++i) {
+      const int k = lane + 64 * i;
+      Pb[i] = k < n_cand ? rs_bf(Arow[k], big) : 0.0f;
+    }
+    __builtin_amdgcn_wave_barrier();
+    float vq, tm;  // v_bar_query[lane] = big(P @ v_bar), total mass big(sum P) (all lanes)
+    {
+      float acc;
+      pv_chain(kb_p, tm, acc);
+      vq = rs_bf(acc, big);
+      tm = rs_bf(tm, big);
+    }
+    vqs[lane] = vq;
+    __builtin_amdgcn_wave_barrier();
+    // quadratic_deviation's query side: Mvq = big(Mb vq), term_q = big(sum big(Mvq*vq))
+    float mvq;
+    {
+      float acc = 0.0f;
+#pragma unroll 16
+      for (int j = 0; j < 64; ++j) acc = fmaf(MbT[j * 64 + lane], vqs[j], acc);
+      mvq = rs_bf(acc, big);
+    }
+    t0[lane] = mvq;
+    t1[lane] = rs_bf(mvq * vq, big);
+    __builtin_amdgcn_wave_barrier();
+    float tq = 0.0f;
+#pragma unroll 16
+    for (int i = 0; i < 64; ++i) tq = tq + t1[i];
+    tq = rs_bf(tq, big);
+    // s, s_cut, s^2 per candidate
+    uint32_t key[NPL];
+    {
+      float cr[NPL];
+      vdot_cols(t0, cr);  // cross = Mvq . v_k
 #pragma unroll
       for (int i = 0; i < NPL; ++i) {
         const int k = lane + 64 * i;
-        if (k < n_cand) tk[i] = fmaf(vcol(d, k), m, tk[i]);
+        float sc = 0.0f;
+        ssq[i] = 0.0f;
+        if (i < nel && k < n_cand) {
+          const float c2 = rs_bf(2.0f * rs_bf(cr[i], big), big);
+          float qd = rs_bf(rs_bf(tq - c2, big) + tkey[k], big);
+          qd = qd < 0.0f ? 0.0f : qd;
+          const float sq = rs_bf(sqrtf(qd), big);
+          const float s = rs_bf(Pb[i] * sq, big);
+          float om = rs_bf(1.0f - Pb[i], big);
+          om = rs_bf(om < 1e-4f ? 1e-4f : om, big);
+          sc = renorm ? rs_bf(s / om, big) : s;
+          ssq[i] = rs_bf(s * s, big);
+          if (a.s_out) a.s_out[row * n_cand + k] = s;
+        }
+        key[i] = rs_key(inv ? -sc : sc);
       }
     }
-    uint32_t rkey[NPL], ckey[NPL];
-    float rmax = -__builtin_huge_valf();
+    const int nts = a.nts[row];
+    const int nkeep = nts < 0 ? 0 : (nts > n_cand ? n_cand : nts);
+    __builtin_amdgcn_wave_barrier();
+    uint32_t drop = cand_bits & ~rs_top_m<NPL>(key, cand_bits, nkeep, lane, hist);
+
+    // J, and g / Mg (left in t3) / ||g||^2_M / K of a drop set (projected.py:859-868, 903-918)
+    float gn = 0.0f, Kk = 1.0f;
+    auto objective = [&](uint32_t dr) -> float {
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) {
+        const int k = lane + 64 * i;
+        if (i < nel && k < n_cand) Pw[k] = ((dr >> i) & 1u) ? Pb[i] : 0.0f;
+      }
+      __builtin_amdgcn_wave_barrier();
+      float sp, acc;
+      pv_chain(n_cand, sp, acc);
+      sp = rs_bf(sp, big);
+      const float g = sp * vq - rs_bf(acc, big);
+      t1[lane] = g;
+      __builtin_amdgcn_wave_barrier();
+      float mg = 0.0f;
+#pragma unroll 16
+      for (int j = 0; j < 64; ++j) mg = fmaf(M32T[j * 64 + lane], t1[j], mg);
+      t2[lane] = g * mg;  // products of ||g||^2_M
+      t3[lane] = mg;
+      __builtin_amdgcn_wave_barrier();
+      float n2 = 0.0f;
+#pragma unroll 16
+      for (int d = 0; d < 64; ++d) n2 = n2 + t2[d];
+      float K = tm - sp;
+      K = K < 1e-6f ? 1e-6f : K;
+      gn = n2;
+      Kk = K;
+      return n2 / (K * K);
+    };
+
+    uint32_t best = drop;
+    float best_obj = track ? objective(drop) : 0.0f;
+    double remaining = a.restore_frac;  // the reference forms the round fractions in double
+    for (int it = 0; it < a.n_iters; ++it) {
+      const double frac = remaining * a.decay;
+      remaining -= frac;
+      const int pic0 = (int)rintf((float)frac * (float)nts);
+      const float J = objective(drop);  // leaves Mg in t3
+      if (track && (maxim ? J > best_obj : J < best_obj)) {
+        best_obj = J;
+        best = drop;
+      }
+      // term_q of the round, big(Mg)
+      __builtin_amdgcn_wave_barrier();
+      t2[lane] = vq * t3[lane];
+      t0[lane] = rs_bf(t3[lane], big);
+      __builtin_amdgcn_wave_barrier();
+      float tqr = 0.0f;
+#pragma unroll 16
+      for (int d = 0; d < 64; ++d) tqr = tqr + t2[d];
+      const float tqb = rs_bf(tqr, big);
+      float tk[NPL];
+      vdot_cols(t0, tk);  // term_k = v_k . big(Mg)
+      uint32_t rkey[NPL], ckey[NPL];
+      float rmax = -__builtin_huge_valf();
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) {
+        rkey[i] = ckey[i] = 0u;
+        if (i < nel) {
+          const float raw = rs_bf(Pb[i] * rs_bf(rs_bf(tk[i], big) - tqb, big), big);
+          float r = rs_knorm(gn, Kk, 2.0f * raw + ssq[i], Pb[i]);
+          float c = rs_knorm(gn, Kk, ssq[i] - 2.0f * raw, -Pb[i]);
+          if (maxim) {
+            r = -r;
+            c = -c;
+          }
+          if ((drop >> i) & 1u) rmax = fmaxf(rmax, r);
+          rkey[i] = rs_key(r);
+          ckey[i] = rs_key(c);
+        }
+      }
+      // beneficial iff some drop candidate has quality > 0
+      const bool beneficial = __ballot(rmax > 0.0f) != 0ull;
+      int n_drop = 0, n_kept = 0;
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) {
+        n_drop += __popcll(__ballot((drop >> i) & 1u));
+        n_kept += __popcll(__ballot(((cand_bits & ~drop) >> i) & 1u));
+      }
+      int pic = pic0;
+      if (beneficial && pic < 1) pic = 1;
+      int cnt = pic < n_drop ? pic : n_drop;
+      cnt = cnt < n_kept ? cnt : n_kept;
+      if (!beneficial) cnt = 0;
+      __builtin_amdgcn_wave_barrier();
+      const uint32_t restore = rs_top_m<NPL>(rkey, drop, cnt, lane, hist);
+      const uint32_t comp = rs_top_m<NPL>(ckey, cand_bits & ~drop, cnt, lane, hist);
+      drop = (drop & ~restore) | comp;
+    }
+    float fin = 0.0f;
+    if (track || a.obj) fin = objective(drop);
+    if (track && !(maxim ? fin > best_obj : fin < best_obj)) {
+      drop = best;
+      fin = best_obj;
+    }
+    if (a.obj && lane == 0) a.obj[row] = fin;
+    float* out = a.rank_key + row * n_cand;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
-      const float raw = rs_bf(Pb[i] * rs_bf(rs_bf(tk[i], big) - tqb, big), big);
-      float r = rs_knorm(gn, Kk, 2.0f * raw + ssq[i], Pb[i]);
-      float c = rs_knorm(gn, Kk, ssq[i] - 2.0f * raw, -Pb[i]);
-      if (maxim) {
-        r = -r;
-        c = -c;
-      }
-      if ((drop >> i) & 1u) rmax = fmaxf(rmax, r);
-      rkey[i] = rs_key(r);
-      ckey[i] = rs_key(c);
+      const int k = lane + 64 * i;
+      if (k < n_cand) out[k] = ((drop >> i) & 1u) ? 0.0f : 1.0f;
     }
-    // wave max of rmax: beneficial iff some drop candidate has quality > 0
-    const bool beneficial = __ballot(rmax > 0.0f) != 0ull;
-    int n_drop = 0;
-#pragma unroll
-    for (int i = 0; i < NPL; ++i) n_drop += __popcll(__ballot((drop >> i) & 1u));
-    int n_kept = 0;
-#pragma unroll
-    for (int i = 0; i < NPL; ++i) n_kept += __popcll(__ballot(((cand_bits & ~drop) >> i) & 1u));
-    int pic = pic0;
-    if (beneficial && pic < 1) pic = 1;
-    int cnt = pic < n_drop ? pic : n_drop;
-    cnt = cnt < n_kept ? cnt : n_kept;
-    if (!beneficial) cnt = 0;
-    const uint32_t restore = rs_top_m<NPL>(rkey, drop, cnt, lane);
-    const uint32_t comp = rs_top_m<NPL>(ckey, cand_bits & ~drop, cnt, lane);
-    drop = (drop & ~restore) | comp;
-  }
-  float fin = 0.0f;
-  if (track || a.obj) fin = objective(drop);
-  if (track && !(maxim ? fin > best_obj : fin < best_obj)) {
-    drop = best;
-    fin = best_obj;
-  }
-  if (a.obj && lane == 0) a.obj[row] = fin;
-  float* out = a.rank_key + row * n_cand;
-#pragma unroll
-  for (int i = 0; i < NPL; ++i) {
-    const int k = lane + 64 * i;
-    if (k < n_cand) out[k] = ((drop >> i) & 1u) ? 0.0f : 1.0f;
-  }
+    __builtin_amdgcn_wave_barrier();
   }  // rows of this wave
 }
 
@@ -405,11 +476,11 @@ template <int NPL>
 static int launch_rs_npl(int BH, int kb_p, bool big, hipStream_t stream, const RsArgs& a) {
   if constexpr (NPL * 64 <= RS_LDS_KBP) {  // rows that fit take the LDS-resident V
     if (big && kb_p <= RS_LDS_KBP) {
-      const size_t lds = sizeof(float) * (8192 + 32 * (size_t)kb_p + 8 * (size_t)(kb_p + 5 * 64));
+      const size_t lds = sizeof(float) * (8192 + 32 * (size_t)kb_p + 8 * (size_t)(((kb_p + 3) & ~3) + 5 * 64));
       return launch_rs<NPL, true, 8>(BH, lds, stream, a);
     }
   }
-  const size_t lds = sizeof(float) * (8192 + 4 * (size_t)(kb_p + 5 * 64));
+  const size_t lds = sizeof(float) * (8192 + 4 * (size_t)(((kb_p + 3) & ~3) + 5 * 64));
   return launch_rs<NPL, false, 4>(BH, lds, stream, a);
 }
 
@@ -448,8 +519,8 @@ RESS_API int ress_restore_swap(const void* A, const void* V, const void* M, cons
   float* VrT = Vr + (long long)BH * kb_p * 64;
   float* termk = VrT + (long long)BH * kb_p * 64;
   const int big = (flags & RS_BF16) ? 1 : 0;
-  hipLaunchKernelGGL(k_rs_head, dim3(kb_p, BH), dim3(64), 0, stream, (const float*)V, (const float*)M, H, kb_p, n_cand,
-                     big, Vr, VrT, termk);
+  hipLaunchKernelGGL(k_rs_head, dim3(cdiv(kb_p, 64), BH), dim3(256), 0, stream, (const float*)V, (const float*)M, H,
+                     kb_p, n_cand, big, Vr, VrT, termk);
   RESS_LAUNCHED("k_rs_head");
   RsArgs a;
   a.A = (const float*)A;
