@@ -179,3 +179,26 @@ def restore_swap(A, V, M, nts, n_cand, n_iters=5, restore_frac=0.5, decay=0.5, b
     lib().oracle_restore_swap(_p(A), _p(V), _p(M), _p(nts), H, q_blk, kb_p, n_cand, n_iters,
                               ctypes.c_double(restore_frac), ctypes.c_double(decay), flags, _p(keep), _p(obj), _p(s))
     return (keep, obj, s) if want_s else (keep, obj)
+
+
+def meansim_map(q, k, km=None, simthreshd1=0.1, cdfthreshd=0.9, attention_sink=0, H=None):
+    """SpargeAttn-convention meansim block map (oracle_meansim_map). q (BH,Tq,64), k (BH,Tk,64)
+    bf16 (torch or uint16); km (BH,64) f32 or None; thresholds scalar or per head.
+    Returns a dict of map, q_i8, q_scale, k_i8, k_scale, pooled_q, pooled_k, sim_q, sim_k."""
+    qa, ka = _u16(q), _u16(k)
+    BH, Tq, _ = qa.shape
+    Tk = ka.shape[1]
+    H = H or BH
+    nq, nk = -(-Tq // 128), -(-Tk // 64)
+    th = np.ascontiguousarray(np.broadcast_to(np.asarray(simthreshd1, np.float32), (H,)))
+    cd = np.ascontiguousarray(np.broadcast_to(np.asarray(cdfthreshd, np.float32), (H,)))
+    kmv = None if km is None else np.ascontiguousarray(km, np.float32).reshape(BH, 64)
+    o = dict(map=np.zeros((BH, nq, nk), np.uint8), q_i8=np.zeros((BH, nq * 128, 64), np.int8),
+             q_scale=np.zeros((BH, nq), np.float32), k_i8=np.zeros((BH, nk * 64, 64), np.int8),
+             k_scale=np.zeros((BH, nk), np.float32), pooled_q=np.zeros((BH, nq, 64), np.float32),
+             pooled_k=np.zeros((BH, nk, 64), np.float32), sim_q=np.zeros((BH, nq), np.uint8),
+             sim_k=np.zeros((BH, nk), np.uint8))
+    lib().oracle_meansim_map(_p(qa), _p(ka), _p(kmv), BH, H, Tq, Tk, _p(th), _p(cd), int(attention_sink),
+                             *(_p(o[n]) for n in ("map", "q_i8", "q_scale", "k_i8", "k_scale", "pooled_q", "pooled_k",
+                                                  "sim_q", "sim_k")))
+    return o

@@ -636,3 +636,136 @@ int oracle_restore_swap(const float* A, const float* V, const float* M, const in
   free(drop); free(best); free(sel); free(sel2); free(valid); free(keys); free(idx);
   return 0;
 }
+
+/* ---- SpargeAttn-convention block map (meansim) ----------------------------------------
+ * get_block_map_meansim_fuse_quant as the reference patches it (external/patches/
+ * spargeattn.patch:54-66: attention_sink = a count of leading tokens, forcing its
+ * ceil(s/64) leading key blocks; Q quantised with sm_scale = 1, the scale of
+ * quant_per_block, :38-41). SpargeAttn itself is not in the reference; this is the
+ * build's restatement (parity unpinned against SpargeAttn):
+ *  per block (Q 128, K 64 tokens; K smoothed by km when given), x the fp32 values:
+ *    pooled  = mean_t x_t                                  (SUM8x order)
+ *    sim     = ||sum_t x_t/||x_t|| ||^2 / n^2, the mean pairwise cosine similarity
+ *              (self pairs included; a zero row contributes 0); similar = sim > simthreshd1[h]
+ *    codes   = the per-block INT8 quantiser (scale = amax/127)
+ *  per (head, q-block) row: scores = DOT64(pooled_q, pooled_k)/8 over the similar K
+ *  blocks (the others -inf), softmax (ress exp, SUM64 sum), keep the top-n by (p desc,
+ *  index asc) with n = #{prefix sums of the sorted p <= cdfthreshd[h]}, then force on
+ *  the non-similar K blocks, every block of a non-similar Q row, and the sinks.
+ * q, k: (BH, T, 64) bf16; km [BH][64] or NULL; simth, cdfth [H].
+ * Outputs: map [BH][nq][nk] uint8, q_i8 [BH][nq*128][64], q_scale [BH][nq],
+ * k_i8 [BH][nk*64][64], k_scale [BH][nk], pooled_q [BH][nq][64], pooled_k [BH][nk][64],
+ * sim_q [BH][nq], sim_k [BH][nk] uint8. */
+static inline float tree8(const float* p) { return ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])); }
+
+static void ms_block(const uint16_t* x, const float* km, int T, int b, int BS, float th, float* pooled, uint8_t* sim,
+                     int8_t* codes, float* scale_out) {
+  const int base = b * BS, cnt = T - base < BS ? T - base : BS;
+  float xs[128][64], xh[128][64];
+  float amax = 0.0f;
+  for (int t = 0; t < cnt; ++t) {
+    float part[8];
+    for (int d = 0; d < 64; ++d) {
+      float v = bf16f(x[(long long)(base + t) * 64 + d]);
+      if (km) v = v - km[d];
+      xs[t][d] = v;
+      const float av = fabsf(v);
+      amax = av > amax ? av : amax;
+    }
+    for (int g = 0; g < 8; ++g) {
+      float a = 0.0f;
+      for (int c = 0; c < 8; ++c) a = fmaf(xs[t][8 * g + c], xs[t][8 * g + c], a);
+      part[g] = a;
+    }
+    const float n2 = tree8(part);
+    const float inv = n2 > 0.0f ? 1.0f / sqrtf(n2) : 0.0f;
+    for (int d = 0; d < 64; ++d) xh[t][d] = xs[t][d] * inv;
+  }
+  float ssum[64];
+  for (int d = 0; d < 64; ++d) {
+    float pp[8] = {0, 0, 0, 0, 0, 0, 0, 0}, ph[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int t = 0; t < cnt; ++t) {
+      pp[t & 7] = pp[t & 7] + xs[t][d];
+      ph[t & 7] = ph[t & 7] + xh[t][d];
+    }
+    pooled[d] = tree8(pp) / (float)cnt;
+    ssum[d] = tree8(ph);
+  }
+  float part[8];
+  for (int g = 0; g < 8; ++g) {
+    float a = 0.0f;
+    for (int c = 0; c < 8; ++c) a = fmaf(ssum[8 * g + c], ssum[8 * g + c], a);
+    part[g] = a;
+  }
+  const float s = tree8(part) / ((float)cnt * (float)cnt);
+  *sim = s > th;
+  const float scale = amax / 127.0f;
+  *scale_out = scale;
+  for (int t = 0; t < BS; ++t)
+    for (int d = 0; d < 64; ++d) codes[t * 64 + d] = t < cnt ? quant(xs[t][d], scale) : 0;
+}
+
+static const float* g_ms_p;
+static int cmp_ms(const void* a, const void* b) {
+  const int i = *(const int*)a, j = *(const int*)b;
+  const uint32_t ki = order_key(g_ms_p[i]), kj = order_key(g_ms_p[j]);
+  if (ki != kj) return ki > kj ? -1 : 1;
+  return (i > j) - (i < j);
+}
+
+void oracle_meansim_map(const uint16_t* q, const uint16_t* k, const float* km, int BH, int H, int Tq, int Tk,
+                        const float* simth, const float* cdfth, int attention_sink, uint8_t* map, int8_t* q_i8,
+                        float* q_scale, int8_t* k_i8, float* k_scale, float* pooled_q, float* pooled_k, uint8_t* sim_q,
+                        uint8_t* sim_k) {
+  const int nq = cdiv(Tq, 128), nk = cdiv(Tk, 64);
+  float* sc = (float*)malloc(sizeof(float) * nk);
+  int* idx = (int*)malloc(sizeof(int) * nk);
+  const int n_sink = attention_sink > 0 ? cdiv(attention_sink, 64) : 0;
+  for (int bh = 0; bh < BH; ++bh) {
+    const int h = bh % H;
+    for (int b = 0; b < nq; ++b)
+      ms_block(q + (long long)bh * Tq * 64, NULL, Tq, b, 128, simth[h], pooled_q + ((long long)bh * nq + b) * 64,
+               sim_q + (long long)bh * nq + b, q_i8 + ((long long)bh * nq + b) * 128 * 64, q_scale + (long long)bh * nq + b);
+    for (int b = 0; b < nk; ++b)
+      ms_block(k + (long long)bh * Tk * 64, km ? km + (long long)bh * 64 : NULL, Tk, b, 64, simth[h],
+               pooled_k + ((long long)bh * nk + b) * 64, sim_k + (long long)bh * nk + b,
+               k_i8 + ((long long)bh * nk + b) * 64 * 64, k_scale + (long long)bh * nk + b);
+    for (int r = 0; r < nq; ++r) {
+      uint8_t* row = map + ((long long)bh * nq + r) * nk;
+      const float* pq = pooled_q + ((long long)bh * nq + r) * 64;
+      float mx = -INFINITY;
+      for (int c = 0; c < nk; ++c) {
+        if (!sim_k[(long long)bh * nk + c]) {
+          sc[c] = -INFINITY;
+          continue;
+        }
+        const float* pk = pooled_k + ((long long)bh * nk + c) * 64;
+        float a = 0.0f;
+        for (int d = 0; d < 64; ++d) a = fmaf(pq[d], pk[d], a);
+        sc[c] = a * 0.125f;
+        mx = sc[c] > mx ? sc[c] : mx;
+      }
+      memset(row, 0, nk);
+      if (mx > -INFINITY) {
+        for (int c = 0; c < nk; ++c) sc[c] = sc[c] == -INFINITY ? 0.0f : oracle_expf(sc[c] - mx);
+        const float sum = sum64(sc, nk);
+        for (int c = 0; c < nk; ++c) sc[c] = sc[c] / sum;
+        for (int c = 0; c < nk; ++c) idx[c] = c;
+        g_ms_p = sc;
+        qsort(idx, nk, sizeof(int), cmp_ms);
+        float cum = 0.0f;
+        int n = 0;
+        for (int i = 0; i < nk; ++i) {
+          cum = cum + sc[idx[i]];
+          if (cum <= cdfth[h]) n = i + 1;
+          else break;
+        }
+        for (int i = 0; i < n; ++i) row[idx[i]] = 1;
+      }
+      for (int c = 0; c < nk; ++c)
+        if (!sim_k[(long long)bh * nk + c] || !sim_q[(long long)bh * nq + r] || c < n_sink) row[c] = 1;
+    }
+  }
+  free(sc);
+  free(idx);
+}
