@@ -107,6 +107,23 @@ int ress_fill_block_map(void* map, const void* counts, const void* sorted_idx, l
  * map [rows][k] uint8 -> lut [rows][k] int32 (ascending), nvalid [rows]. */
 int ress_block_map_lut(const void* map, long long rows, int k, void* lut, void* nvalid, hipStream_t stream);
 
+/* ---- SpargeAttn meansim block map (meansim.hip) --------------------------- */
+
+/* Replaces get_block_map_meansim_fuse_quant (SpargeAttn spas_sage_attn/utils.py as
+ * patched by external/patches/spargeattn.patch:50-67; attention_sink = a count of
+ * leading tokens forcing its ceil(sink/64) leading key blocks, :63-65; Q quantised with
+ * sm_scale = 1, :38-41). q (B,H,Tq,64), k (B,H,Tk,64) bf16 with element strides, km
+ * [B*H][64] f32 or NULL, simthreshd1 / cdfthreshd [H] f32 (device). Outputs: map
+ * [B*H][nq][nk] uint8 (nq = ceil(Tq/128), nk = ceil(Tk/64) <= 4096), q_i8
+ * [B*H][nq*128][64], q_scale [B*H][nq], k_i8 [B*H][nk*64][64], k_scale [B*H][nk], and the
+ * intermediate pooled_q [B*H][nq][64], pooled_k [B*H][nk][64] f32, sim_q [B*H][nq],
+ * sim_k [B*H][nk] uint8 (1 = similar block). Non-causal only. */
+int ress_meansim_block_map(const void* q, const void* k, const void* km, int B, int H, int Tq, int Tk,
+                           long long sqB, long long sqH, long long sqT, long long skB, long long skH, long long skT,
+                           const void* simthreshd1, const void* cdfthreshd, int attention_sink, void* map, void* q_i8,
+                           void* q_scale, void* k_i8, void* k_scale, void* pooled_q, void* pooled_k, void* sim_q,
+                           void* sim_k, hipStream_t stream);
+
 /* ---- ReSS restore-swap (ress_swap.hip) ------------------------------------ */
 
 /* Replaces restore_swap_rank_by (src/ress/scoring/projected.py:395-1058) with its fused

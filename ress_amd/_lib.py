@@ -28,6 +28,7 @@ _SIGS = {
     "ress_sparse_attn_fwd_bf16": "plllpppp" + "iiiiif" + "pi" + "lll" + "ps",
     "ress_qattn_block_sparse_fwd": "pppipipppppiiiilllllliiifipls",
     "ress_restore_swap": "pppp" + "iiiiii" + "dd" + "i" + "ppp" + "pl" + "s",
+    "ress_meansim_block_map": "ppp" + "iiii" + "llllll" + "ppi" + "ppppppppp" + "s",
 }
 _CT = {
     "p": ctypes.c_void_p,

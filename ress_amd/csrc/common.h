@@ -121,6 +121,26 @@ __device__ __forceinline__ float ress_expf(float x) {
   return p * __int_as_float((ni + 127) << 23);
 }
 
+// ---- strided (B, H, T, D) operands ----------------------------------------
+struct Strides {  // element strides of a (B, H, T, D) tensor in any layout
+  long long b, h, t;
+  int H;
+};
+__device__ __forceinline__ long long bh_offset(int bh, const Strides& s) {
+  return (long long)(bh / s.H) * s.b + (long long)(bh % s.H) * s.h;
+}
+
+// ---- int8 packing ------------------------------------------------------------
+__device__ __forceinline__ uint2 pack_i8x8(const int c[8]) {
+  uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w0 |= ((uint32_t)(c[i] & 0xff)) << (8 * i);
+    w1 |= ((uint32_t)(c[4 + i] & 0xff)) << (8 * i);
+  }
+  return make_uint2(w0, w1);
+}
+
 // ---- order keys ------------------------------------------------------------
 // Order-preserving fp32 -> uint32 (unsigned compare == float compare; -0 == +0;
 // NaN above +inf).

@@ -13,16 +13,6 @@
 // token lane j = l>>3; a block of T tokens is read in T/8 coalesced 1 KiB rows.
 #include "common.h"
 
-__device__ __forceinline__ uint2 pack_i8x8(const int c[8]) {
-  uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    w0 |= ((uint32_t)(c[i] & 0xff)) << (8 * i);
-    w1 |= ((uint32_t)(c[4 + i] & 0xff)) << (8 * i);
-  }
-  return make_uint2(w0, w1);
-}
-
 // hi (and, if lo_dst is set, split lo) codes of 8 values -> two 8-byte stores
 __device__ __forceinline__ void store_codes(const float x[8], float scale, int8_t* hi_dst, int8_t* lo_dst) {
   int hi[8], lo[8];
@@ -34,14 +24,6 @@ __device__ __forceinline__ void store_codes(const float x[8], float scale, int8_
     for (int c = 0; c < 8; ++c) lo[c] = quant_i8_lo(x[c], scale, hi[c]);
     *reinterpret_cast<uint2*>(lo_dst) = pack_i8x8(lo);
   }
-}
-
-struct Strides {  // element strides of a (B, H, T, D) tensor in any layout
-  long long b, h, t;
-  int H;
-};
-__device__ __forceinline__ long long bh_offset(int bh, const Strides& s) {
-  return (long long)(bh / s.H) * s.b + (long long)(bh % s.H) * s.h;
 }
 
 // ----------------------------------------------------------------------------

@@ -5,6 +5,8 @@ implemented on libress_hip:
     block_map_lut_triton(map)                 spas_sage_attn.utils.block_map_lut_triton
     fill_block_map_triton(map, n, idx)        spas_sage_attn.utils.fill_block_map_triton
     hyperparameter_check(x, H, device)        spas_sage_attn.utils.hyperparameter_check
+    get_block_map_meansim_fuse_quant(q, k)    spas_sage_attn.utils.get_block_map_meansim_fuse_quant
+                                              (as patched, external/patches/spargeattn.patch:50-67)
     qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold(...)
                                               spas_sage_attn._qattn (the CUDA kernel)
 
@@ -154,6 +156,66 @@ def qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold(
               B, H, Tq, Tk, *v.stride()[:3], *o.stride()[:3], int(tensor_layout), int(is_causal), int(qk_quant_gran),
               float(sm_scale), int(return_pv_count), _lib.ptr(ws), ws_bytes, _lib.stream_handle(dev))
     return None
+
+
+def get_block_map_meansim_fuse_quant(q, k, km=None, is_causal=False, BLKQ=BLKQ, BLKK=BLKK, simthreshd1=0.1,
+                                     cdfthreshd=0.9, is_sparse=True, return_lut=False, attention_sink=0):
+    """SpargeAttn's fused block map, as the reference patches it (spargeattn.patch:50-67):
+    per-block mean pooling, mean intra-block cosine similarity and INT8 quantisation of
+    Q (128-token blocks) and K - km (64-token blocks), then per (head, q-block) row the
+    softmax of the pooled scores over the similar K blocks, the smallest prefix of
+    the sorted probabilities whose cumulative sum stays <= cdfthreshd, and the forced
+    blocks: non-similar K blocks, every block of a non-similar Q row, and the
+    ceil(attention_sink/64) leading blocks (attention_sink counts tokens, :63-65).
+
+    q (B,H,Tq,64), k (B,H,Tk,64) (computed in bf16), km (B,H,1,64) / (B*H,64) or None,
+    simthreshd1 / cdfthreshd scalars or per-head. Returns (final_map bool (B,H,nq,nk),
+    q_int8, q_scale, k_int8, k_scale), or with return_lut (lut, valid_block_num, q_int8,
+    q_scale, k_int8, k_scale); the INT8 tensors are views of block-padded buffers, the
+    layout per_block_int8 returns. Only the non-causal sparse form is provided
+    (is_causal=True / is_sparse=False raise): the reference calls neither, and
+    SpargeAttn's causal block mask is not in the reference to be matched."""
+    if (BLKQ, BLKK) != (128, 64):
+        raise NotImplementedError("blocks are 128/64")
+    if is_causal or not is_sparse:
+        raise NotImplementedError("only the non-causal sparse block map is provided")
+    attention_sink = int(attention_sink)
+    if attention_sink < 0:
+        raise ValueError("attention_sink counts leading tokens (>= 0)")
+    B, H, Tq, C = q.shape
+    Tk = k.shape[-2]
+    if C != 64 or k.shape[:2] != (B, H) or k.shape[-1] != 64:
+        raise ValueError("q, k must be (B,H,T,64) with matching B, H")
+    dev = q.device
+    qb, kb = q.to(torch.bfloat16), k.to(torch.bfloat16)
+    if qb.stride(-1) != 1 or any(s % 8 for s in qb.stride()[:3]) or qb.data_ptr() % 16:
+        qb = qb.contiguous()
+    if kb.stride(-1) != 1 or any(s % 8 for s in kb.stride()[:3]) or kb.data_ptr() % 16:
+        kb = kb.contiguous()
+    kmf = None
+    if km is not None:
+        kmf = km.to(device=dev, dtype=torch.float32).reshape(B * H, 64).contiguous()
+    simth = hyperparameter_check(simthreshd1, H, dev).float().contiguous()
+    cdfth = hyperparameter_check(cdfthreshd, H, dev).float().contiguous()
+    nq, nk = _cdiv(Tq, 128), _cdiv(Tk, 64)
+    final_map = torch.empty(B, H, nq, nk, dtype=torch.uint8, device=dev)
+    q_buf = torch.empty(B, H, nq * 128, 64, dtype=torch.int8, device=dev)
+    k_buf = torch.empty(B, H, nk * 64, 64, dtype=torch.int8, device=dev)
+    q_scale = torch.empty(B, H, nq, device=dev)
+    k_scale = torch.empty(B, H, nk, device=dev)
+    pooled_q = torch.empty(B * H, nq, 64, device=dev)
+    pooled_k = torch.empty(B * H, nk, 64, device=dev)
+    sim_q = torch.empty(B * H, nq, dtype=torch.uint8, device=dev)
+    sim_k = torch.empty(B * H, nk, dtype=torch.uint8, device=dev)
+    _lib.call("ress_meansim_block_map", _lib.ptr(qb), _lib.ptr(kb), _lib.ptr(kmf), B, H, Tq, Tk, *qb.stride()[:3],
+              *kb.stride()[:3], _lib.ptr(simth), _lib.ptr(cdfth), attention_sink, _lib.ptr(final_map),
+              _lib.ptr(q_buf), _lib.ptr(q_scale), _lib.ptr(k_buf), _lib.ptr(k_scale), _lib.ptr(pooled_q),
+              _lib.ptr(pooled_k), _lib.ptr(sim_q), _lib.ptr(sim_k), _lib.stream_handle(dev))
+    q_int8, k_int8 = q_buf[:, :, :Tq], k_buf[:, :, :Tk]
+    if not return_lut:
+        return final_map.bool(), q_int8, q_scale, k_int8, k_scale
+    lut, valid_block_num = block_map_lut_triton(final_map)
+    return lut, valid_block_num, q_int8, q_scale, k_int8, k_scale
 
 
 def sm_scale_default(head_dim=64):
