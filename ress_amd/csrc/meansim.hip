@@ -25,15 +25,16 @@
 // k_ms_stats: one 256-thread workgroup per (block, batch*head). Thread (token lane
 // tid>>3, dim group tid&7) loads 8 bf16 per token pass (BS/32 passes), keeps them in
 // registers for the codes, and stages fp32 copies in LDS for the per-dim column pass.
-// k_ms_map: one 256-thread workgroup per (q-block, batch*head); scores, softmax and
-// the ranks (by counting, against LDS-resident probabilities) are parallel, the CDF
-// prefix is one lane's sequential chain.
+// k_ms_map_wave (nk <= 1024): one wave per (q-block, batch*head) row; the order is a
+// bitonic sort of 64-bit (probability desc, index asc) keys held in registers, and the
+// CDF prefix is a wave-uniform sequential chain over the sorted lanes (readlane).
+// k_ms_map (nk > 1024): one 256-thread workgroup per row, the same sort in LDS.
 #include "common.h"
 
 namespace {
 
 constexpr int MS_LD = 68;          // LDS row stride (floats) of the staged block: 16-byte rows, offset banks
-constexpr int MS_MAX_NK = 4096;    // key blocks per row the map kernel holds in LDS (2 x 16 KiB)
+constexpr int MS_MAX_NK = 4096;    // key blocks per row the map kernel sorts in LDS (32 KiB keys + 16 KiB p)
 
 template <int BS>
 __global__ __launch_bounds__(256) void k_ms_stats(const uint16_t* __restrict__ x, Strides sx, int T,
@@ -145,11 +146,14 @@ __global__ __launch_bounds__(256) void k_ms_stats(const uint16_t* __restrict__ x
 
 __global__ __launch_bounds__(256) void k_ms_map(const float* __restrict__ pooled_q, const float* __restrict__ pooled_k,
                                                 const uint8_t* __restrict__ sim_q, const uint8_t* __restrict__ sim_k,
-                                                int H, int nq, int nk, const float* __restrict__ cdfth, int n_sink,
-                                                uint8_t* __restrict__ map) {
-  extern __shared__ __align__(16) float ms_dyn[];
-  float* p = ms_dyn;                 // [nk] scores -> exp -> probabilities
-  float* sorted = ms_dyn + nk;       // [nk] probabilities in selection order
+                                                int H, int nq, int nk, int np2, const float* __restrict__ cdfth,
+                                                int n_sink, uint8_t* __restrict__ map) {
+  extern __shared__ __align__(16) unsigned char ms_dyn[];
+  // keys [np2] u64: (~bits(p) << 32) | c, ascending = (p desc, c asc); padding sorts last.
+  // p [nk] f32: scores -> exp -> probabilities; then reused as the keep flags (bytes).
+  unsigned long long* keys = reinterpret_cast<unsigned long long*>(ms_dyn);
+  float* p = reinterpret_cast<float*>(ms_dyn + (size_t)np2 * 8);
+  uint8_t* flag = reinterpret_cast<uint8_t*>(p);
   __shared__ __align__(16) float pq[64];
   __shared__ float red[4];
   __shared__ int n_sel;
@@ -188,57 +192,288 @@ __global__ __launch_bounds__(256) void k_ms_map(const float* __restrict__ pooled
   if (lane == 0) red[w] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  int n = 0;
-  if (mx > -__builtin_huge_valf()) {
-    for (int c = tid; c < nk; c += 256) p[c] = sk[c] ? ress_expf(p[c] - mx) : 0.0f;
-    __syncthreads();
-    if (w == 0) {
-      float a = 0.0f;
-      for (int i = lane; i < nk; i += 64) a = a + p[i];
-      a = sum64_tree(a);
-      if (lane == 0) red[0] = a;
-    }
-    __syncthreads();
-    const float tot = red[0];
-    for (int c = tid; c < nk; c += 256) p[c] = p[c] / tot;
-    __syncthreads();
-    // rank = #{c' : p[c'] > p[c] or (p[c'] == p[c] and c' < c)}; every p is >= +0, so
-    // its bit pattern orders like the value
-    for (int c = tid; c < nk; c += 256) {
-      const uint32_t key = __float_as_uint(p[c]);
-      int rank = 0;
-      for (int i = 0; i < nk; ++i) {
-        const uint32_t ki = __float_as_uint(p[i]);
-        rank += (ki > key) | ((ki == key) & (i < c));
-      }
-      sorted[rank] = p[c];
-    }
-    __syncthreads();
-    if (tid == 0) {
-      const float th = cdfth[bh % H];
-      float cum = 0.0f;
-      int i = 0;
-      for (; i < nk; ++i) {
-        cum = cum + sorted[i];
-        if (!(cum <= th)) break;
-      }
-      n_sel = i;
-    }
-    __syncthreads();
-    n = n_sel;
+  if (!(mx > -__builtin_huge_valf())) {  // no similar key block: every block is forced on
+    for (int c = tid; c < nk; c += 256) row[c] = 1;
+    return;
   }
-  for (int c = tid; c < nk; c += 256) {
-    bool keep = !sk[c] || c < n_sink;
-    if (!keep && n > 0) {
-      const uint32_t key = __float_as_uint(p[c]);
-      int rank = 0;
-      for (int i = 0; i < nk && rank < n; ++i) {
-        const uint32_t ki = __float_as_uint(p[i]);
-        rank += (ki > key) | ((ki == key) & (i < c));
+  for (int c = tid; c < nk; c += 256) p[c] = sk[c] ? ress_expf(p[c] - mx) : 0.0f;
+  __syncthreads();
+  if (w == 0) {
+    float a = 0.0f;
+    for (int i = lane; i < nk; i += 64) a = a + p[i];
+    a = sum64_tree(a);
+    if (lane == 0) red[0] = a;
+  }
+  __syncthreads();
+  const float tot = red[0];
+  // every p is >= +0, so its bit pattern orders like the value
+  for (int c = tid; c < np2; c += 256)
+    keys[c] = c < nk ? ((unsigned long long)(~__float_as_uint(p[c] / tot)) << 32) | (unsigned)c : ~0ull;
+  __syncthreads();
+
+  // bitonic sort, ascending
+  for (int k = 2; k <= np2; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int t = tid; t < (np2 >> 1); t += 256) {
+        const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1)), l = i + j;
+        const unsigned long long a = keys[i], b = keys[l];
+        if ((a > b) == ((i & k) == 0)) {
+          keys[i] = b;
+          keys[l] = a;
+        }
       }
-      keep = rank < n;
+      __syncthreads();
     }
-    row[c] = keep ? 1 : 0;
+  }
+
+  // flags: forced blocks (non-similar, sinks); the selected prefix is added below
+  for (int c = tid; c < nk; c += 256) flag[c] = (!sk[c] || c < n_sink) ? 1 : 0;
+  __syncthreads();
+  if (tid == 0) {  // n = #{sequential prefix sums of the sorted p that are <= th}
+    const float th = cdfth[bh % H];
+    float cum = 0.0f;
+    int i = 0;
+    for (; i + 8 <= nk; i += 8) {
+      float v[8];
+#pragma unroll
+      for (int m = 0; m < 8; ++m) v[m] = __uint_as_float(~(unsigned)(keys[i + m] >> 32));
+      int stop = -1;
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        if (stop < 0) {
+          cum = cum + v[m];
+          if (!(cum <= th)) stop = m;
+        }
+      }
+      if (stop >= 0) {
+        i += stop;
+        goto done;
+      }
+    }
+    for (; i < nk; ++i) {
+      cum = cum + __uint_as_float(~(unsigned)(keys[i] >> 32));
+      if (!(cum <= th)) break;
+    }
+  done:
+    n_sel = i;
+  }
+  __syncthreads();
+  const int n = n_sel;
+  for (int i = tid; i < n; i += 256) flag[(unsigned)keys[i]] = 1;
+  __syncthreads();
+  for (int c = tid; c < nk; c += 256) row[c] = flag[c];
+}
+
+// One wave per (head, q-block) row, E = 64-key-block columns per lane (nk <= 64E), four
+// rows of one head per workgroup.
+//  scores  pooled K goes through LDS in coalesced 64-block tiles that the four rows
+//          share; lane l keeps the scores of columns c = 64e + l (also the SUM64 order).
+//  sort    only the probabilities are sorted (equal values are interchangeable in the
+//          prefix sums): a bitonic network over 32-bit keys in registers, partners 64
+//          positions or more apart in the same lane, closer ones one shuffle away.
+//  prefix  the sequential CDF chain of each row runs in one lane of wave 0 over the
+//          sorted values in LDS (the four rows' chains side by side), and every wave
+//          then counts its row's prefix sums <= th in parallel.
+//  select  with v the n-th largest probability: every column with p > v, and of those
+//          with p == v the lowest-indexed ones up to n (a ballot prefix count).
+template <int E>
+__global__ __launch_bounds__(256) void k_ms_map_wave(const float* __restrict__ pooled_q,
+                                                     const float* __restrict__ pooled_k,
+                                                     const uint8_t* __restrict__ sim_q,
+                                                     const uint8_t* __restrict__ sim_k, int H, int nq, int nk,
+                                                     const float* __restrict__ cdfth, int n_sink,
+                                                     uint8_t* __restrict__ map) {
+  constexpr int NP = 64 * E, LDK = 65, LDS_ROW = NP + 4;  // LDK / LDS_ROW: padded strides
+  __shared__ float pk_l[64 * LDK];
+  __shared__ __align__(16) float pq_l[4][64];
+  __shared__ __align__(16) float sv_l[4][LDS_ROW];
+  __shared__ int go_l[4];
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int bh = blockIdx.y, r = blockIdx.x * 4 + w;
+  const long long row_id = (long long)bh * nq + r;
+  const bool in_range = r < nq;
+  const bool active = in_range && sim_q[row_id];
+  if (in_range) pq_l[w][lane] = pooled_q[row_id * 64 + lane];
+  const float* pkh = pooled_k + (long long)bh * nk * 64;
+  const uint8_t* sk = sim_k + (long long)bh * nk;
+
+  // tiles of 64 key blocks: tile e+1 is loaded into registers while tile e is computed
+  float s[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) s[e] = 0.0f;
+  const int tiles = cdiv(nk, 64);
+  float4 nxt[4];
+  auto load_tile = [&](int t) {
+    const int cols = min(64, nk - 64 * t);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int f4 = tid + 256 * i, col = f4 >> 4;
+      nxt[i] = col < cols ? reinterpret_cast<const float4*>(pkh + (long long)(64 * t + col) * 64)[f4 & 15]
+                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  };
+  load_tile(0);
+#pragma unroll 1
+  for (int e = 0; e < tiles; ++e) {
+    __syncthreads();  // previous tile consumed (and pq_l written, first time)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int f4 = tid + 256 * i;
+      float* dst = pk_l + (f4 >> 4) * LDK + (f4 & 15) * 4;
+      dst[0] = nxt[i].x;
+      dst[1] = nxt[i].y;
+      dst[2] = nxt[i].z;
+      dst[3] = nxt[i].w;
+    }
+    __syncthreads();
+    if (e + 1 < tiles) load_tile(e + 1);
+    if (active && 64 * e + lane < nk) {
+      const float4* qv = reinterpret_cast<const float4*>(pq_l[w]);
+      const float* kc = pk_l + lane * LDK;
+      float a = 0.0f;
+#pragma unroll
+      for (int d4 = 0; d4 < 16; ++d4) {
+        const float4 qq = qv[d4];
+        a = fmaf(qq.x, kc[4 * d4 + 0], a);
+        a = fmaf(qq.y, kc[4 * d4 + 1], a);
+        a = fmaf(qq.z, kc[4 * d4 + 2], a);
+        a = fmaf(qq.w, kc[4 * d4 + 3], a);
+      }
+#pragma unroll
+      for (int e2 = 0; e2 < E; ++e2)
+        if (e2 == e) s[e2] = a;
+    }
+  }
+
+  bool simc[E];
+  float mx = -__builtin_huge_valf();
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int c = 64 * e + lane;
+    simc[e] = c < nk && sk[c];
+    s[e] = s[e] * 0.125f;
+    if (simc[e]) mx = fmaxf(mx, s[e]);
+  }
+  mx = wave_max(mx);
+  // the CDF path runs for a similar row with at least one similar key block; otherwise
+  // every block of the row is on
+  const bool go = active && mx > -__builtin_huge_valf();
+  uint32_t pb[E];  // bits of p at the lane's own columns (p >= +0: bits order like values)
+#pragma unroll
+  for (int e = 0; e < E; ++e) pb[e] = 0;
+  if (go) {
+    float part = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      s[e] = simc[e] ? ress_expf(s[e] - mx) : 0.0f;
+      if (64 * e + lane < nk) part = part + s[e];
+    }
+    const float tot = sum64_tree(part);
+    uint32_t u[E];  // ascending sort keys ~bits(p): descending p; padding (~0) last
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      pb[e] = __float_as_uint(s[e] / tot);
+      u[e] = 64 * e + lane < nk ? ~pb[e] : ~0u;
+    }
+#pragma unroll
+    for (int k = 2; k <= NP; k <<= 1) {
+#pragma unroll
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        if (j >= 64) {
+          const int ej = j >> 6;
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            if (e & ej) continue;
+            const uint32_t a = u[e], b = u[e | ej];
+            const bool asc = ((64 * e) & k) == 0;
+            u[e] = asc ? min(a, b) : max(a, b);
+            u[e | ej] = asc ? max(a, b) : min(a, b);
+          }
+        } else {
+          const bool lower = (lane & j) == 0;
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            const bool asc = k >= 64 ? ((64 * e) & k) == 0 : (lane & k) == 0;
+            const uint32_t a = u[e];
+            const uint32_t b = (uint32_t)__shfl_xor((int)a, j, 64);
+            u[e] = (lower == asc) ? min(a, b) : max(a, b);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) sv_l[w][64 * e + lane] = __uint_as_float(~u[e]);
+    if (lane == 0) go_l[w] = 1;
+    // s[] now holds the sorted values (position 64e + lane): the chain overwrites sv_l
+#pragma unroll
+    for (int e = 0; e < E; ++e) s[e] = __uint_as_float(~u[e]);
+  } else if (lane == 0) {
+    go_l[w] = 0;
+  }
+  __syncthreads();
+  if (w == 0 && lane < 4 && go_l[lane]) {  // the four rows' sequential chains, side by side
+    float* v = sv_l[lane];
+    float cum = 0.0f;
+    int i = 0;
+    for (; i + 16 <= nk; i += 16) {  // 16 values per LDS round trip
+      float4 x[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) x[g] = reinterpret_cast<const float4*>(v + i)[g];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        x[g].x = cum + x[g].x;
+        x[g].y = x[g].x + x[g].y;
+        x[g].z = x[g].y + x[g].z;
+        x[g].w = x[g].z + x[g].w;
+        cum = x[g].w;
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g) reinterpret_cast<float4*>(v + i)[g] = x[g];
+    }
+    for (; i < nk; ++i) {
+      cum = cum + v[i];
+      v[i] = cum;
+    }
+  }
+  __syncthreads();
+  if (!in_range) return;
+  uint8_t* row = map + row_id * nk;
+  if (!go) {
+    for (int c = lane; c < nk; c += 64) row[c] = 1;
+    return;
+  }
+  const float th = cdfth[bh % H];
+  int cnt = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = 64 * e + lane;
+    cnt += (i < nk && sv_l[w][i] <= th) ? 1 : 0;
+  }
+  const int n = wave_sum_i(cnt);  // the sums only grow: the count is the prefix length
+  uint32_t vbits = 0;
+  int n_gt = 0;
+  if (n > 0) {  // v = the n-th largest p (sorted position n-1; s[] holds the sorted values)
+    const int pos = n - 1, slot = pos >> 6;
+    float sel = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) sel = e == slot ? s[e] : sel;
+    vbits = __float_as_uint(__shfl(sel, pos & 63, 64));
+    int gt = 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) gt += (64 * e + lane < nk && pb[e] > vbits) ? 1 : 0;
+    n_gt = wave_sum_i(gt);
+  }
+  int eq_before = 0;  // equal-to-v columns at lower indices, accumulated over slots
+  const unsigned long long lt_mask = (1ull << lane) - 1ull;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int c = 64 * e + lane;
+    const bool eq = n > 0 && c < nk && pb[e] == vbits;
+    const unsigned long long m = __ballot(eq);
+    const int rank_eq = eq_before + __popcll(m & lt_mask);
+    eq_before += __popcll(m);
+    const bool sel = n > 0 && c < nk && (pb[e] > vbits || (eq && rank_eq < n - n_gt));
+    if (c < nk) row[c] = (sel || !sk[c] || c < n_sink) ? 1 : 0;
   }
 }
 
@@ -275,9 +510,28 @@ RESS_API int ress_meansim_block_map(const void* q, const void* k, const void* km
                      (float*)pooled_k, (uint8_t*)sim_k);
   RESS_LAUNCHED("k_ms_stats<64>");
   const int n_sink = attention_sink > 0 ? cdiv(attention_sink, 64) : 0;
-  hipLaunchKernelGGL(k_ms_map, dim3(nq, BH), dim3(256), (size_t)2 * nk * sizeof(float), stream,
-                     (const float*)pooled_q, (const float*)pooled_k, (const uint8_t*)sim_q, (const uint8_t*)sim_k, H,
-                     nq, nk, (const float*)cdfthreshd, n_sink, (uint8_t*)map);
+  const dim3 wgrid(cdiv(nq, 4), BH);
+  const float* pq = (const float*)pooled_q;
+  const float* pk = (const float*)pooled_k;
+  const uint8_t *sq8 = (const uint8_t*)sim_q, *sk8 = (const uint8_t*)sim_k;
+  const float* cd = (const float*)cdfthreshd;
+  uint8_t* m8 = (uint8_t*)map;
+  if (nk <= 64) {
+    hipLaunchKernelGGL(k_ms_map_wave<1>, wgrid, dim3(256), 0, stream, pq, pk, sq8, sk8, H, nq, nk, cd, n_sink, m8);
+  } else if (nk <= 128) {
+    hipLaunchKernelGGL(k_ms_map_wave<2>, wgrid, dim3(256), 0, stream, pq, pk, sq8, sk8, H, nq, nk, cd, n_sink, m8);
+  } else if (nk <= 256) {
+    hipLaunchKernelGGL(k_ms_map_wave<4>, wgrid, dim3(256), 0, stream, pq, pk, sq8, sk8, H, nq, nk, cd, n_sink, m8);
+  } else if (nk <= 512) {
+    hipLaunchKernelGGL(k_ms_map_wave<8>, wgrid, dim3(256), 0, stream, pq, pk, sq8, sk8, H, nq, nk, cd, n_sink, m8);
+  } else if (nk <= 1024) {
+    hipLaunchKernelGGL(k_ms_map_wave<16>, wgrid, dim3(256), 0, stream, pq, pk, sq8, sk8, H, nq, nk, cd, n_sink, m8);
+  } else {
+    int np2 = 2;
+    while (np2 < nk) np2 <<= 1;
+    hipLaunchKernelGGL(k_ms_map, dim3(nq, BH), dim3(256), (size_t)np2 * 8 + (size_t)nk * 4, stream, pq, pk, sq8, sk8,
+                       H, nq, nk, np2, cd, n_sink, m8);
+  }
   RESS_LAUNCHED("k_ms_map");
   return 0;
 }

@@ -66,8 +66,11 @@ def _check(q, k, km, simth, cdfth, sink, dev, qdev=None, kdev=None):
     return fm, want
 
 
+# key-block counts 4, 3, 24 (one column per lane), 65, 188, 625 (2, 4, 16 per lane) and
+# 1026 (the workgroup-per-row kernel beyond 1024)
 @pytest.mark.parametrize("B,H,Tq,Tk,sink", [(1, 2, 300, 250, 0), (2, 3, 128, 130, 1), (1, 4, 1000, 1500, 150),
-                                            (1, 2, 513, 4097, 128)])
+                                            (1, 2, 513, 4097, 128), (1, 2, 700, 12000, 64), (1, 1, 1030, 40000, 0),
+                                            (1, 1, 300, 65636, 0)])
 def test_meansim_bit_exact(dev, B, H, Tq, Tk, sink):
     q, k = _qk(B * 1000 + Tq + Tk, B, H, Tq, Tk, dup=True, zeros=True)
     km = k.float().mean(2, keepdim=True)
