@@ -11,7 +11,7 @@ import torch
 import oracle
 from oracle import reference as ref
 from pipeline_oracle import oracle_layer, row_sample
-from ress_amd import budget, kernels, synth
+from ress_amd import _lib, budget, kernels, synth
 from ress_amd.attention import sparse_global_attention
 from ress_amd.kernels import LayerGrid
 
@@ -101,6 +101,24 @@ def test_pooled_scores_bit_exact(layer, dev):
     ofull, ocond = oracle.pooled_scores(o["pooled_q"], o["pooled_k"], g.n_cand)
     assert _bits_equal(_np(full).reshape(ofull.shape), ofull)
     assert _bits_equal(_np(cond).reshape(ocond.shape), ocond)
+
+
+@pytest.mark.parametrize("q_blk,kb_p", [(5, 1), (7, 70), (3, 687), (2, 2048), (3, 2049)])
+def test_pooled_scores_row_lengths(q_blk, kb_p, dev):
+    """Rows of one tile, a ragged tile, the configs[2] length, the tiled kernel's limit and
+    the direct kernel beyond it; q_blk not a multiple of the four rows per workgroup."""
+    rng = np.random.default_rng(kb_p)
+    pq = (rng.normal(size=(2, q_blk, 64)) * 2).astype(np.float32)
+    pk = (rng.normal(size=(2, kb_p, 64)) * 2).astype(np.float32)
+    n_cand = max(kb_p - 3, 0)
+    full = torch.empty(2, q_blk, kb_p, device=dev)
+    cond = torch.empty(2, q_blk, max(n_cand, 1), device=dev)
+    tq, tk = torch.from_numpy(pq).to(dev), torch.from_numpy(pk).to(dev)
+    _lib.call("ress_pooled_scores", _lib.ptr(tq), _lib.ptr(tk), 2, q_blk, kb_p, n_cand, 0.125, _lib.ptr(full),
+              _lib.ptr(cond), _lib.stream_handle(dev))
+    ofull, ocond = oracle.pooled_scores(pq, pk, n_cand)
+    assert _bits_equal(_np(full), ofull)
+    assert _bits_equal(_np(cond)[:, :, :n_cand], ocond)
 
 
 @pytest.mark.parametrize("sr,cdf", [(0.5, 0.9), (None, 0.9), (0.7, None), (0.2, 0.5)])
