@@ -10,10 +10,12 @@ special-query rows dense, output in storage order.
     python bench.py [--steps K] [--warmup W] [--config 1] [--no-cpu-baseline]
 
 Prints one JSON line. value = effective TFLOP/s = 4 N^2 H D / t (dense-equivalent);
-ms_per_step = ms per layer. roofline = the attention kernel's retained-block FLOPs over
+ms_per_step = ms per layer (ms_per_step_median: the median of the per-step HIP-event
+times). roofline = the attention kernel's retained-block FLOPs over
 its own HIP-event-timed duration against the dense MFMA peak of its arithmetic (QK^T
 half at the bf16 or INT8 rate, PV half at the bf16 rate); frac_of_int8_peak prices the
-same FLOPs against the INT8 peak.
+same FLOPs against the INT8 peak, frac_of_measured_peak against the rates measured on
+this GPU (measured_peaks: MFMA microbenchmark, 1 GiB copy).
 """
 
 import argparse
@@ -36,6 +38,47 @@ def mfma_peak(qk_mode):
     QK^T at the bf16 or INT8 rate, harmonic combination of the two halves."""
     qk = PEAK_BF16_TFLOPS if qk_mode == "bf16" else PEAK_INT8_TOPS
     return 1.0 / (0.5 / qk + 0.5 / PEAK_BF16_TFLOPS)
+
+
+def measured_peaks(dev):
+    """This GPU's measured dense MFMA rates (bf16, int8) from the libress_peak.so
+    microbenchmark (four independent accumulator chains per wave, two workgroups of four
+    waves per CU) and its HBM copy bandwidth (1 GiB device-to-device copy, read + write)."""
+    import ctypes
+
+    import torch
+
+    from ress_amd.build import PEAK_LIB
+    L = ctypes.CDLL(PEAK_LIB)
+    L.ress_peak_mfma.restype = ctypes.c_int
+    L.ress_peak_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    wgs = 2 * cus
+    out = torch.empty(wgs * 256, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    res = {"cus": cus}
+    for kind, name, per_mfma in ((0, "bf16_tflops", 32768), (1, "int8_tops", 65536)):
+        iters = 20000
+        if L.ress_peak_mfma(kind, 64, wgs, out.data_ptr(), stream) != 0:
+            raise RuntimeError("ress_peak_mfma failed")
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        L.ress_peak_mfma(kind, iters, wgs, out.data_ptr(), stream)
+        e.record()
+        torch.cuda.synchronize()
+        res[name] = round(wgs * 4 * iters * 4 * per_mfma / (s.elapsed_time(e) * 1e-3) / 1e12, 1)
+    src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(5):
+        dst.copy_(src)
+    e.record()
+    torch.cuda.synchronize()
+    res["hbm_copy_GBs"] = round(5 * 2 * src.numel() * 4 / (s.elapsed_time(e) * 1e-3) / 1e9, 1)
+    del src, dst
+    return res
 
 
 def parse():
@@ -203,14 +246,16 @@ def main():
     torch.cuda.synchronize()
     ev.clear()
     rs_ev.clear()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
-    start.record()
-    for _ in range(args.steps):
+    marks[0].record()
+    for i in range(args.steps):
         res = step()
-    end.record()
+        marks[i + 1].record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
+    ms = marks[0].elapsed_time(marks[-1]) / args.steps
+    step_ms = sorted(marks[i].elapsed_time(marks[i + 1]) for i in range(args.steps))
+    ms_median = step_ms[len(step_ms) // 2]
     attn_ms = sum(s.elapsed_time(e) for s, e in ev) / len(ev)
     rs_ms = sum(s.elapsed_time(e) for s, e in rs_ev) / len(rs_ev) if rs_ev else None
     attn_mod.kernels.sparse_attention = orig_attn
@@ -242,6 +287,9 @@ def main():
     prep_bytes = elems * {"bf16": 10, "i8x2": 14, "i8": 12}[args.qk_mode]
     peak = mfma_peak(args.qk_mode)
     ms_meansim, ms_bytes = time_meansim(q, k, reps)
+    peaks = measured_peaks(dev)
+    qk_meas = peaks["bf16_tflops"] if args.qk_mode == "bf16" else peaks["int8_tops"]
+    peak_meas = 1.0 / (0.5 / qk_meas + 0.5 / peaks["bf16_tflops"])
 
     result = {
         "metric": "ms/global-attn layer + effective TFLOPS, N=21984 H16 D64 @70% sparse, 1 GPU",
@@ -251,6 +299,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        "ms_per_step_median": round(ms_median, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -264,14 +313,16 @@ def main():
                      "frac": round(achieved / peak, 4),
                      "traffic": measured_traffic(f"k_sparse_attn_{args.qk_mode}") if args.config == 1 else None,
                      "frac_of_int8_peak": round(achieved / PEAK_INT8_TOPS, 4),
+                     "measured_peak": round(peak_meas, 1), "frac_of_measured_peak": round(achieved / peak_meas, 4),
                      "kernel": "k_sparse_attn", "kernel_ms": round(attn_ms, 4),
                      "retained_flop_per_launch": flops_kept},
         "restore_swap_ms": None if rs_ms is None else round(rs_ms, 4),
+        "measured_peaks": peaks,
         "prep": {"ms": round(prep_ms, 4), "algorithmic_bytes": prep_bytes,
                  "achieved_GBs": round(prep_bytes / (prep_ms * 1e-3) / 1e9, 1), "peak_GBs": PEAK_HBM_GBS},
         "meansim_scoring": {"ms": round(ms_meansim, 4), "algorithmic_bytes": ms_bytes,
                             "achieved_GBs": round(ms_bytes / (ms_meansim * 1e-3) / 1e9, 1),
-                            "peak_GBs": PEAK_HBM_GBS,
+                            "peak_GBs": PEAK_HBM_GBS, "measured_copy_GBs": peaks["hbm_copy_GBs"],
                             "what": "SpargeAttn get_block_map_meansim_fuse_quant over the full sequence "
                                     "(K smoothed by its mean, sinks = first frame)"},
     }
@@ -296,8 +347,10 @@ def main():
         cb = time_block_masked_sdpa(q.cpu(), k.cpu(), v.cpu(), frames, P, S, lut, nvalid, budget_s=args.cpu_budget_s)
         result["cpu_baseline"] = {
             "value": round(cb["ms_per_layer"], 1), "unit": "ms/layer", "cores": cb["threads"], "kind": "port",
-            "sample": f"fp32 block-masked SDPA (PyTorch CPU) on {cb['rows_timed']} of {cb['rows_total']} "
-                      f"(head, q-block) rows, {cb['elapsed_s']:.1f}s, extrapolated by kept-block count"}
+            "cpu": cb["cpu_model"],
+            "sample": f"fp32 block-masked SDPA (PyTorch CPU) on a fixed sample of {cb['rows_timed']} of "
+                      f"{cb['rows_total']} (head, q-block) rows: median of {cb['runs']} timed runs after a "
+                      f"warm-up ({cb['elapsed_s']:.1f}s in all), extrapolated by kept-block count"}
     print(json.dumps(result))
 
 

@@ -19,8 +19,9 @@ from oracle.reference import split_tokens
 
 
 def time_block_masked_sdpa(q, k, v, frames, P, S, lut, nvalid, budget_s=15.0, max_rows=None, seed=0):
-    """Times fp32 block-masked SDPA over a random sample of kernel rows until about
-    `budget_s` seconds of CPU work, then extrapolates to all rows.
+    """Times fp32 block-masked SDPA over a fixed random sample of kernel rows (about a
+    quarter of `budget_s` per pass: one warm-up pass that picks the sample, then three
+    timed passes, median taken), then extrapolates to all rows.
 
     lut/nvalid: numpy [BH][q_blk_total][kb_tot] / [BH][q_blk_total]. Returns a dict with
     the extrapolated ms per layer, the sample size and the threads used."""
@@ -50,19 +51,37 @@ def time_block_masked_sdpa(q, k, v, frames, P, S, lut, nvalid, budget_s=15.0, ma
             qq = qs[b, h, r0:min(r0 + 128, T_s)]
         return F.scaled_dot_product_attention(qq[None], key[b, h, idx][None], val[b, h, idx][None])
 
-    run(*all_rows[order[0]])  # warm-up
-    done, work_done = 0, 0
-    total_work = float(nvalid.sum())
+    # warm-up pass, which also fixes the sample: rows in a seeded random order until
+    # about a quarter of the budget is spent; the sample is then timed three more times
     t0 = time.perf_counter()
+    sample = []
     for i in order:
-        bh, qb = all_rows[i]
-        run(bh, qb)
-        done += 1
-        work_done += float(nvalid[bh, qb])
-        if time.perf_counter() - t0 > budget_s or (max_rows and done >= max_rows):
+        run(*all_rows[i])
+        sample.append(all_rows[i])
+        if time.perf_counter() - t0 > budget_s / 4 or (max_rows and len(sample) >= max_rows):
             break
+    runs = []
+    for _ in range(3):
+        t1 = time.perf_counter()
+        for bh, qb in sample:
+            run(bh, qb)
+        runs.append(time.perf_counter() - t1)
     elapsed = time.perf_counter() - t0
+    work_done = float(sum(nvalid[bh, qb] for bh, qb in sample))
+    total_work = float(nvalid.sum())
     # extrapolate by kept-block work (rows differ in length)
-    ms_layer = elapsed * 1e3 * total_work / work_done
-    return {"ms_per_layer": ms_layer, "rows_timed": done, "rows_total": len(all_rows), "threads": threads,
-            "elapsed_s": elapsed}
+    ms_layer = sorted(runs)[1] * 1e3 * total_work / work_done
+    return {"ms_per_layer": ms_layer, "rows_timed": len(sample), "rows_total": len(all_rows), "threads": threads,
+            "elapsed_s": elapsed, "runs": len(runs), "cpu_model": _cpu_model()}
+
+
+def _cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), for the report."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"

@@ -3,7 +3,8 @@
     python -m ress_amd.build            # or ress_amd.build.build_library()
 
 Objects go to ress_amd/_build/, the library to ress_amd/libress_hip.so (in-tree, so it
-travels with the source tree to the GPU host). Always recompiles.
+travels with the source tree to the GPU host). bench.py's measured-peak kernels
+(csrc_bench/peak.hip) build into ress_amd/libress_peak.so. Always recompiles.
 """
 
 import concurrent.futures
@@ -13,6 +14,9 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
+# bench support (measured MFMA peak), a library of its own: libress_peak.so
+BENCH_SRC = os.path.join(HERE, "csrc_bench", "peak.hip")
+PEAK_LIB = os.path.join(HERE, "libress_peak.so")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libress_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -65,6 +69,13 @@ def build_library(verbose=False):
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources")
+    cmd = [HIPCC, *FLAGS, "-shared", "-o", PEAK_LIB + ".tmp", BENCH_SRC]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {BENCH_SRC}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(PEAK_LIB + ".tmp", PEAK_LIB)
+    if verbose:
+        print(f"built {PEAK_LIB}")
     return LIB
 
 

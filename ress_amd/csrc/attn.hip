@@ -360,28 +360,19 @@ __device__ __forceinline__ void attn_block_i8(const uint4* __restrict__ stage, i
   }
 }
 
-// bf16 mode: one 64-key block, with its LDS traffic issued ahead of use. All eight K
-// operand reads and tile 0's four V reads go out first (LDS returns in order, so each
-// MFMA waits only for its own operand), both tiles' S^T MFMAs follow, then one
-// running-max update per block with lazy rescale, and P = exp2(S*c - m) with PV per
-// tile (tile 1's V reads issued under tile 0's PV).
-template <bool MASK>
-__device__ __forceinline__ void attn_block_bf16(const uint4* __restrict__ stage, int kch, int nk, float c,
-                                                const int (&ks0)[4], const int (&ks1)[4], const uint4 (&qv)[4], int g,
-                                                int qi, float& m_run, float& l_run, v16f& o0, v16f& o1) {
-  const uint4* sv = stage + kch;
-  uint4 k0[4], k1[4], v0[4];
+// bf16 mode, software-pipelined over blocks: the S^T MFMAs of block i+1 (qk_block_bf16)
+// are issued before the softmax and PV of block i (sv_block_bf16), so the matrix cores
+// work on the next block's scores while the VALU computes this block's probabilities.
+
+// S^T of one 64-key block: tile 0 (keys 0..31) into a0, tile 1 into a1. All eight K
+// operand reads go out before the first MFMA (LDS returns in order).
+__device__ __forceinline__ void qk_block_bf16(const uint4* __restrict__ stage, const int (&ks0)[4], const int (&ks1)[4],
+                                              const uint4 (&qv)[4], v16f& a0, v16f& a1) {
+  uint4 k0[4], k1[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) k0[j] = stage[ks0[j]];
 #pragma unroll
   for (int j = 0; j < 4; ++j) k1[j] = stage[ks1[j]];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    v0[2 * h] = sv[v_slot(qi, 2 * h + g)];
-    v0[2 * h + 1] = sv[v_slot(32 + qi, 2 * h + g)];
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  v16f a0, a1;
 #pragma unroll
   for (int r = 0; r < 16; ++r) a0[r] = a1[r] = 0.0f;
 #pragma unroll
@@ -392,6 +383,22 @@ __device__ __forceinline__ void attn_block_bf16(const uint4* __restrict__ stage,
   for (int j = 0; j < 4; ++j)
     a1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, k1[j]), __builtin_bit_cast(v8bf, qv[j]), a1,
                                                  0, 0, 0);
+}
+
+// Online softmax and O^T += V^T P^T for one 64-key block whose scores are (a0, a1):
+// one running-max update per block with lazy rescale, P = exp2(S*c - m) per tile.
+// Register r of a tile is key 32t + 8(r/4) + 4g + r%4.
+template <bool MASK>
+__device__ __forceinline__ void sv_block_bf16(const uint4* __restrict__ stage, int kch, int nk, float c, const v16f& a0,
+                                              const v16f& a1, int g, int qi, float& m_run, float& l_run, v16f& o0,
+                                              v16f& o1) {
+  const uint4* sv = stage + kch;
+  uint4 v0[4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    v0[2 * h] = sv[v_slot(qi, 2 * h + g)];
+    v0[2 * h + 1] = sv[v_slot(32 + qi, 2 * h + g)];
+  }
   float s0[16], s1[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -430,7 +437,6 @@ __device__ __forceinline__ void attn_block_bf16(const uint4* __restrict__ stage,
     }
   }
   const float nm = -m_run;
-  // P tile t, row sum, O^T += V^T P^T; register r is key 32t + 8(r/4) + 4g + r%4
   auto pv = [&](const float (&sc)[16], const uint4 (&vv)[4]) {
     float p[16];
 #pragma unroll
@@ -472,7 +478,7 @@ template <int QK, bool V_F16, int OUT>
 __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __restrict__ lut_all,
                                                 const int* __restrict__ nvalid, const float* __restrict__ k_scale,
                                                 uint4* __restrict__ s0, uint4* __restrict__ s1,
-                                                uint4* __restrict__ s2, int bh, int qb) {
+                                                uint4* __restrict__ s2, uint4* __restrict__ s3, int bh, int qb) {
   constexpr int KCH = StageShape<QK>::KCH;
   constexpr int DMA = StageShape<QK>::DMA;
   const long long row = (long long)bh * a.q_blk_total + qb;
@@ -550,12 +556,69 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
   v16f o0, o1;
 #pragma unroll
   for (int r = 0; r < 16; ++r) o0[r] = o1[r] = 0.0f;
+  // Only the sequence's last key block can be partial; LUTs are ascending, so if it is
+  // kept it is the last entry. Full blocks run unmasked, the partial one is peeled off.
+  const bool tail_partial = nv > 0 && (a.Tk & 63) != 0 && lut[nv - 1] == a.kb_tot - 1;
+
+  if constexpr (QK == QK_BF16) {
+    // Four stages: block i lives in stage i % 4 and is fetched three steps ahead. Step i
+    // issues the DMA of block i+3 into the stage block i-1 used, the S^T MFMAs of block
+    // i+1 (resident since the end of step i-1), then the softmax and PV of block i, and
+    // waits for block i+2. The stages are distinct LDS objects and the loop is unrolled
+    // by four, so the compiler can see that no DMA writes a stage being read.
+    if (nv > 0) stage_load(s0, lut[0]);
+    if (nv > 1) stage_load(s1, lut[1]);
+    if (nv > 2) {
+      stage_load(s2, lut[2]);
+      wait_lds_dma_but<DMA>();
+    } else {
+      wait_lds_dma();
+    }
+    __syncthreads();
+    v16f a0, a1;
+    if (nv > 0) qk_block_bf16(s0, ks0, ks1, qv, a0, a1);
+    int kb3 = nv > 3 ? lut[3] : 0;
+    int kb4 = nv > 4 ? lut[4] : 0;
+    auto step = [&](const uint4* cur, const uint4* nxt, uint4* ahead, int it) {
+      const bool fetch = it + 3 < nv;
+      if (fetch) stage_load(ahead, kb3);
+      v16f n0, n1;
+      qk_block_bf16(nxt, ks0, ks1, qv, n0, n1);
+      sv_block_bf16<false>(cur, KCH, 64, qs, a0, a1, g, qi, m_run, l_run, o0, o1);
+      // the LUT read is issued after the block's LDS reads, so their waits do not include it
+      __builtin_amdgcn_sched_barrier(0);
+      const int kb5 = it + 5 < nv ? lut[it + 5] : 0;
+      kb3 = kb4;
+      kb4 = kb5;
+      a0 = n0;
+      a1 = n1;
+      if (fetch) wait_lds_dma_but<DMA>();
+      else wait_lds_dma();
+      stage_barrier();
+    };
+    int it = 0;
+    for (; it + 4 < nv; it += 4) {
+      step(s0, s1, s3, it);
+      step(s1, s2, s0, it + 1);
+      step(s2, s3, s1, it + 2);
+      step(s3, s0, s2, it + 3);
+    }
+    if (it + 1 < nv) step(s0, s1, s3, it++);
+    if (it + 1 < nv) step(s1, s2, s0, it++);
+    if (it + 1 < nv) step(s2, s3, s1, it++);
+    if (nv > 0) {  // the last block (it == nv - 1), in stage it % 4
+      const int st = it & 3;
+      const uint4* cur = st == 0 ? s0 : (st == 1 ? s1 : (st == 2 ? s2 : s3));
+      if (tail_partial)
+        sv_block_bf16<true>(cur, KCH, a.Tk - lut[nv - 1] * 64, qs, a0, a1, g, qi, m_run, l_run, o0, o1);
+      else
+        sv_block_bf16<false>(cur, KCH, 64, qs, a0, a1, g, qi, m_run, l_run, o0, o1);
+      __syncthreads();  // the next row's prologue overwrites the stages
+    }
+  } else {
   auto block = [&](const uint4* cur, int nk, float cb, auto mask_tag) {
     constexpr bool M = decltype(mask_tag)::value;
-    if constexpr (QK == QK_BF16)
-      attn_block_bf16<M>(cur, KCH, nk, cb, ks0, ks1, qv, g, qi, m_run, l_run, o0, o1);
-    else
-      attn_block_i8<QK, V_F16, M>(cur, KCH, nk, cb, ks0, ks1, qv, g, qi, m_run, l_run, o0, o1);
+    attn_block_i8<QK, V_F16, M>(cur, KCH, nk, cb, ks0, ks1, qv, g, qi, m_run, l_run, o0, o1);
   };
 
   // Three stages: block i lives in stage i % 3 and is fetched two steps ahead, so each
@@ -576,10 +639,6 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
   int kb1 = nv > 1 ? lut[1] : 0;
   int kb2 = nv > 2 ? lut[2] : 0;
   float c = nv > 0 ? block_scale(kb) : 0.0f;
-  // Only the sequence's last key block can be partial; LUTs are ascending, so if it is
-  // kept it is the last entry. Full blocks run the unmasked loop, the partial one is
-  // peeled off after it.
-  const bool tail_partial = nv > 0 && (a.Tk & 63) != 0 && lut[nv - 1] == a.kb_tot - 1;
   const int nv_full = nv - (tail_partial ? 1 : 0);
 
   // One kept block: start the DMA of block it+2 into `ahead`, consume `cur`, then wait
@@ -617,6 +676,7 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
     const int nk = a.Tk - kb * 64;
     block(cur, nk, c, std::true_type{});
     __syncthreads();  // the next row's prologue overwrites this stage
+  }
   }
 
   // ---- epilogue ------------------------------------------------------------
@@ -658,6 +718,7 @@ __global__ __launch_bounds__(256, Occupancy<QK>::value) void k_sparse_attn(AttnA
   __shared__ __attribute__((aligned(16))) uint4 stage0[STAGE];
   __shared__ __attribute__((aligned(16))) uint4 stage1[STAGE];
   __shared__ __attribute__((aligned(16))) uint4 stage2[STAGE];
+  __shared__ __attribute__((aligned(16))) uint4 stage3[QK == QK_BF16 ? STAGE : 1];  // bf16: four stages
   __shared__ int s_item;
 
   // ---- persistent loop over this XCD's range of rows ------------------------
@@ -671,7 +732,7 @@ __global__ __launch_bounds__(256, Occupancy<QK>::value) void k_sparse_attn(AttnA
     if (item >= item_end) break;
     int bh, qb;
     item_to_row(item, a.q_blk_p, a.q_blk_total, bh, qb);
-    sparse_attn_row<QK, V_F16, OUT>(a, lut, nvalid, k_scale, stage0, stage1, stage2, bh, qb);
+    sparse_attn_row<QK, V_F16, OUT>(a, lut, nvalid, k_scale, stage0, stage1, stage2, stage3, bh, qb);
   }
 }
 
