@@ -183,7 +183,10 @@ def main():
     cfg = synth.CONFIGS[args.config]
     dev = torch.device("cuda:0")
     t0 = time.time()
-    q, k, v, meta = synth.make_layer_qkv(cfg["frames"], corr=cfg["corr"])
+    q, k, v, meta = synth.make_layer_qkv(
+        cfg["frames"], corr=cfg["corr"],
+        progress=(lambda m: print(f"[bench] generating inputs: {m}", file=sys.stderr, flush=True))
+        if cfg["frames"] > 32 else None)
     q, k, v = q.to(dev), k.to(dev), v.to(dev)
     if args.calib_copy_mib:
         src = torch.empty(args.calib_copy_mib << 18, dtype=torch.float32, device=dev).fill_(1.0)

@@ -114,7 +114,7 @@ int ress_block_map_lut(const void* map, long long rows, int k, void* lut, void* 
  * leading tokens forcing its ceil(sink/64) leading key blocks, :63-65; Q quantised with
  * sm_scale = 1, :38-41). q (B,H,Tq,64), k (B,H,Tk,64) bf16 with element strides, km
  * [B*H][64] f32 or NULL, simthreshd1 / cdfthreshd [H] f32 (device). Outputs: map
- * [B*H][nq][nk] uint8 (nq = ceil(Tq/128), nk = ceil(Tk/64) <= 4096), q_i8
+ * [B*H][nq][nk] uint8 (nq = ceil(Tq/128), nk = ceil(Tk/64) <= 6144), q_i8
  * [B*H][nq*128][64], q_scale [B*H][nq], k_i8 [B*H][nk*64][64], k_scale [B*H][nk], and the
  * intermediate pooled_q [B*H][nq][64], pooled_k [B*H][nk][64] f32, sim_q [B*H][nq],
  * sim_k [B*H][nk] uint8 (1 = similar block). Non-causal only. */

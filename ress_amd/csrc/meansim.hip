@@ -25,16 +25,20 @@
 // k_ms_stats: one 256-thread workgroup per (block, batch*head). Thread (token lane
 // tid>>3, dim group tid&7) loads 8 bf16 per token pass (BS/32 passes), keeps them in
 // registers for the codes, and stages fp32 copies in LDS for the per-dim column pass.
-// k_ms_map_wave (nk <= 1024): one wave per (q-block, batch*head) row; the order is a
-// bitonic sort of 64-bit (probability desc, index asc) keys held in registers, and the
-// CDF prefix is a wave-uniform sequential chain over the sorted lanes (readlane).
-// k_ms_map (nk > 1024): one 256-thread workgroup per row, the same sort in LDS.
+// k_ms_map_wave (nk <= 1024): one wave per (q-block, batch*head) row, four rows per
+// workgroup; details at the kernel.
+// k_ms_map (nk > 1024): one 256-thread workgroup per row: the same value sort in LDS,
+// one lane's CDF chain, and the tie rank by a workgroup scan.
 #include "common.h"
 
 namespace {
 
 constexpr int MS_LD = 68;          // LDS row stride (floats) of the staged block: 16-byte rows, offset banks
-constexpr int MS_MAX_NK = 4096;    // key blocks per row the map kernel sorts in LDS (32 KiB keys + 16 KiB p)
+constexpr int MS_MAX_NK = 6144;
+// bytes of k_ms_map's key / score-tile region: np2 keys or one 64 x 65-float tile
+__host__ __device__ constexpr size_t ms_map_key_bytes(int np2) {
+  return (size_t)np2 * 4 > 64 * 65 * 4 ? (size_t)np2 * 4 : 64 * 65 * 4;
+}    // key blocks per row the map kernel sorts in LDS (<= 32 KiB keys + 24 KiB p)
 
 template <int BS>
 __global__ __launch_bounds__(256) void k_ms_stats(const uint16_t* __restrict__ x, Strides sx, int T,
@@ -144,18 +148,22 @@ __global__ __launch_bounds__(256) void k_ms_stats(const uint16_t* __restrict__ x
   }
 }
 
+template <int NP2>
 __global__ __launch_bounds__(256) void k_ms_map(const float* __restrict__ pooled_q, const float* __restrict__ pooled_k,
                                                 const uint8_t* __restrict__ sim_q, const uint8_t* __restrict__ sim_k,
-                                                int H, int nq, int nk, int np2, const float* __restrict__ cdfth,
-                                                int n_sink, uint8_t* __restrict__ map) {
+                                                int H, int nq, int nk, const float* __restrict__ cdfth, int n_sink,
+                                                uint8_t* __restrict__ map) {
+  constexpr int np2 = NP2, PAIRS = NP2 / 512;  // compare-exchanges per thread per stage
   extern __shared__ __align__(16) unsigned char ms_dyn[];
-  // keys [np2] u64: (~bits(p) << 32) | c, ascending = (p desc, c asc); padding sorts last.
-  // p [nk] f32: scores -> exp -> probabilities; then reused as the keep flags (bytes).
-  unsigned long long* keys = reinterpret_cast<unsigned long long*>(ms_dyn);
-  float* p = reinterpret_cast<float*>(ms_dyn + (size_t)np2 * 8);
-  uint8_t* flag = reinterpret_cast<uint8_t*>(p);
+  // u [np2]: ascending sort keys ~bits(p) (descending p; padding ~0 sorts last); before
+  // the sort the same space holds the 64 x 65-float pooled-K tiles of the score pass.
+  // p [nk]: scores -> exponentials -> probabilities, in column order.
+  uint32_t* u = reinterpret_cast<uint32_t*>(ms_dyn);
+  float* tile = reinterpret_cast<float*>(ms_dyn);
+  float* p = reinterpret_cast<float*>(ms_dyn + ms_map_key_bytes(np2));
   __shared__ __align__(16) float pq[64];
   __shared__ float red[4];
+  __shared__ int ired[4];
   __shared__ int n_sel;
   const int r = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   uint8_t* row = map + ((long long)bh * nq + r) * nk;
@@ -168,25 +176,48 @@ __global__ __launch_bounds__(256) void k_ms_map(const float* __restrict__ pooled
   if (tid < 64) pq[tid] = pooled_q[((long long)bh * nq + r) * 64 + tid];
   __syncthreads();
 
+  // scores: 64-block tiles of pooled K loaded coalesced into LDS (row stride 65), one
+  // column per thread of wave 0; tile t+1 is loaded into registers while tile t is used
   float mx = -__builtin_huge_valf();
-  for (int c = tid; c < nk; c += 256) {
-    float s = -__builtin_huge_valf();
-    if (sk[c]) {
-      const float4* kv = reinterpret_cast<const float4*>(pooled_k + ((long long)bh * nk + c) * 64);
-      const float4* qv = reinterpret_cast<const float4*>(pq);
-      float a = 0.0f;
+  const float* pkh = pooled_k + (long long)bh * nk * 64;
+  float4 nxt[4];
+  auto load_tile = [&](int c0) {
+    const int cols = min(64, nk - c0);
 #pragma unroll
-      for (int d4 = 0; d4 < 16; ++d4) {
-        const float4 kk = kv[d4], qq = qv[d4];
-        a = fmaf(qq.x, kk.x, a);
-        a = fmaf(qq.y, kk.y, a);
-        a = fmaf(qq.z, kk.z, a);
-        a = fmaf(qq.w, kk.w, a);
-      }
-      s = a * 0.125f;
-      mx = fmaxf(mx, s);
+    for (int i = 0; i < 4; ++i) {
+      const int f4 = tid + 256 * i, col = f4 >> 4;
+      nxt[i] = col < cols ? reinterpret_cast<const float4*>(pkh + (long long)(c0 + col) * 64)[f4 & 15]
+                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    p[c] = s;
+  };
+  load_tile(0);
+  for (int c0 = 0; c0 < nk; c0 += 64) {
+    const int cols = min(64, nk - c0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int f4 = tid + 256 * i;
+      float* dst = tile + (f4 >> 4) * 65 + (f4 & 15) * 4;
+      dst[0] = nxt[i].x;
+      dst[1] = nxt[i].y;
+      dst[2] = nxt[i].z;
+      dst[3] = nxt[i].w;
+    }
+    __syncthreads();
+    if (c0 + 64 < nk) load_tile(c0 + 64);
+    if (tid < cols) {
+      const int c = c0 + tid;
+      float s = -__builtin_huge_valf();
+      if (sk[c]) {
+        const float* kc = tile + tid * 65;
+        float a = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 64; ++d) a = fmaf(pq[d], kc[d], a);
+        s = a * 0.125f;
+        mx = fmaxf(mx, s);
+      }
+      p[c] = s;
+    }
+    __syncthreads();
   }
   mx = wave_max(mx);
   if (lane == 0) red[w] = mx;
@@ -206,62 +237,92 @@ __global__ __launch_bounds__(256) void k_ms_map(const float* __restrict__ pooled
   }
   __syncthreads();
   const float tot = red[0];
-  // every p is >= +0, so its bit pattern orders like the value
-  for (int c = tid; c < np2; c += 256)
-    keys[c] = c < nk ? ((unsigned long long)(~__float_as_uint(p[c] / tot)) << 32) | (unsigned)c : ~0ull;
+  for (int c = tid; c < nk; c += 256) p[c] = p[c] / tot;
   __syncthreads();
-
-  // bitonic sort, ascending
-  for (int k = 2; k <= np2; k <<= 1) {
+  // every p is >= +0, so its bit pattern orders like the value; only the values are
+  // sorted (equal values are interchangeable in the prefix sums)
+  for (int c = tid; c < np2; c += 256) u[c] = c < nk ? ~__float_as_uint(p[c]) : ~0u;
+  __syncthreads();
+  for (int k = 2; k <= np2; k <<= 1) {  // bitonic sort, ascending
     for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int t = tid; t < (np2 >> 1); t += 256) {
-        const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1)), l = i + j;
-        const unsigned long long a = keys[i], b = keys[l];
-        if ((a > b) == ((i & k) == 0)) {
-          keys[i] = b;
-          keys[l] = a;
-        }
+      // all of a thread's reads go out before its writes (one LDS round trip per stage)
+      uint32_t x[PAIRS], y[PAIRS];
+#pragma unroll
+      for (int q = 0; q < PAIRS; ++q) {
+        const int t = tid + 256 * q, i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
+        x[q] = u[i];
+        y[q] = u[i + j];
+      }
+#pragma unroll
+      for (int q = 0; q < PAIRS; ++q) {
+        const int t = tid + 256 * q, i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
+        const bool asc = (i & k) == 0;
+        u[i] = asc ? min(x[q], y[q]) : max(x[q], y[q]);
+        u[i + j] = asc ? max(x[q], y[q]) : min(x[q], y[q]);
       }
       __syncthreads();
     }
   }
-
-  // flags: forced blocks (non-similar, sinks); the selected prefix is added below
-  for (int c = tid; c < nk; c += 256) flag[c] = (!sk[c] || c < n_sink) ? 1 : 0;
-  __syncthreads();
   if (tid == 0) {  // n = #{sequential prefix sums of the sorted p that are <= th}
     const float th = cdfth[bh % H];
     float cum = 0.0f;
-    int i = 0;
-    for (; i + 8 <= nk; i += 8) {
-      float v[8];
+    int n = 0;
+    for (int i = 0; i < nk; i += 16) {  // 16 keys per LDS round trip; the sums only grow
+      uint4 x[4];
 #pragma unroll
-      for (int m = 0; m < 8; ++m) v[m] = __uint_as_float(~(unsigned)(keys[i + m] >> 32));
-      int stop = -1;
+      for (int g = 0; g < 4; ++g) x[g] = reinterpret_cast<const uint4*>(u + i)[g];  // i + 16 <= np2
+      const uint32_t* xv = reinterpret_cast<const uint32_t*>(x);
 #pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        if (stop < 0) {
-          cum = cum + v[m];
-          if (!(cum <= th)) stop = m;
-        }
+      for (int m = 0; m < 16; ++m) {
+        cum = cum + __uint_as_float(~xv[m]);
+        n += (i + m < nk && cum <= th) ? 1 : 0;
       }
-      if (stop >= 0) {
-        i += stop;
-        goto done;
-      }
-    }
-    for (; i < nk; ++i) {
-      cum = cum + __uint_as_float(~(unsigned)(keys[i] >> 32));
       if (!(cum <= th)) break;
     }
-  done:
-    n_sel = i;
+    n_sel = n;
   }
   __syncthreads();
   const int n = n_sel;
-  for (int i = tid; i < n; i += 256) flag[(unsigned)keys[i]] = 1;
+  const uint32_t vbits = n > 0 ? ~u[n - 1] : 0u;  // the n-th largest p
+  // contiguous column chunks: p > v is kept; of the p == v columns, the lowest-indexed
+  // n - #{p > v} (an exclusive scan of the per-chunk counts gives each one's rank)
+  const int chunk = cdiv(nk, 256), c0 = min(nk, tid * chunk), c1 = min(nk, c0 + chunk);
+  int gt = 0, eq = 0;
+  for (int c = c0; c < c1; ++c) {
+    const uint32_t b = __float_as_uint(p[c]);
+    gt += b > vbits ? 1 : 0;
+    eq += b == vbits ? 1 : 0;
+  }
+  int incl = eq;  // inclusive scan of eq over the workgroup, in thread order
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += y;
+  }
+  const int gsum = wave_sum_i(gt);
+  if (lane == 63) ired[w] = incl;
+  if (lane == 0) red[w] = __int_as_float(gsum);
   __syncthreads();
-  for (int c = tid; c < nk; c += 256) row[c] = flag[c];
+  int before = 0, n_gt = 0;
+  for (int i = 0; i < 4; ++i) {
+    if (i < w) before += ired[i];
+    n_gt += __float_as_int(red[i]);
+  }
+  int rank_eq = before + incl - eq;
+  const int take_eq = n - n_gt;
+  for (int c = c0; c < c1; ++c) {
+    const uint32_t b = __float_as_uint(p[c]);
+    bool sel = false;
+    if (n > 0) {
+      if (b > vbits) {
+        sel = true;
+      } else if (b == vbits) {
+        sel = rank_eq < take_eq;
+        ++rank_eq;
+      }
+    }
+    row[c] = (sel || !sk[c] || c < n_sink) ? 1 : 0;
+  }
 }
 
 // One wave per (head, q-block) row, E = 64-key-block columns per lane (nk <= 64E), four
@@ -527,10 +588,16 @@ RESS_API int ress_meansim_block_map(const void* q, const void* k, const void* km
   } else if (nk <= 1024) {
     hipLaunchKernelGGL(k_ms_map_wave<16>, wgrid, dim3(256), 0, stream, pq, pk, sq8, sk8, H, nq, nk, cd, n_sink, m8);
   } else {
-    int np2 = 2;
-    while (np2 < nk) np2 <<= 1;
-    hipLaunchKernelGGL(k_ms_map, dim3(nq, BH), dim3(256), (size_t)np2 * 8 + (size_t)nk * 4, stream, pq, pk, sq8, sk8,
-                       H, nq, nk, np2, cd, n_sink, m8);
+    const size_t lds4 = (size_t)nk * 4;
+    if (nk <= 2048)
+      hipLaunchKernelGGL(k_ms_map<2048>, dim3(nq, BH), dim3(256), ms_map_key_bytes(2048) + lds4, stream, pq, pk, sq8,
+                         sk8, H, nq, nk, cd, n_sink, m8);
+    else if (nk <= 4096)
+      hipLaunchKernelGGL(k_ms_map<4096>, dim3(nq, BH), dim3(256), ms_map_key_bytes(4096) + lds4, stream, pq, pk, sq8,
+                         sk8, H, nq, nk, cd, n_sink, m8);
+    else
+      hipLaunchKernelGGL(k_ms_map<8192>, dim3(nq, BH), dim3(256), ms_map_key_bytes(8192) + lds4, stream, pq, pk, sq8,
+                         sk8, H, nq, nk, cd, n_sink, m8);
   }
   RESS_LAUNCHED("k_ms_map");
   return 0;

@@ -104,9 +104,9 @@ def _project(z, W):
 
 
 def make_layer_qkv(frames, H=16, D=64, B=1, rank=16, seed=0, corr="shared", rho=0.6, ar=0.98, noise=0.1,
-                   blur=8, hilbert=True, device="cpu"):
+                   blur=8, hilbert=True, device="cpu", progress=None):
     """(q, k, v): bf16 (B, H, frames*1374, D) in VGGT storage order, plus the meta dict
-    {frames, P, S}."""
+    {frames, P, S}. `progress`, if given, is called with a short string per head."""
     rng = np.random.default_rng(seed)
     G, S = GRID, N_SPECIAL
     fields = np.empty((frames, G, G, rank))
@@ -134,6 +134,8 @@ def make_layer_qkv(frames, H=16, D=64, B=1, rank=16, seed=0, corr="shared", rho=
         out.append(np.empty((B, H, frames * P, D), dtype=np.float32))
     for b in range(B):
         for h in range(H):
+            if progress:
+                progress(f"head {b * H + h + 1}/{B * H}")
             Wq = rng.standard_normal((rank, D)) / math.sqrt(rank)
             Wk = Wq + 0.5 * rng.standard_normal((rank, D)) / math.sqrt(rank)
             Wv = rng.standard_normal((rank, D)) / math.sqrt(rank)

@@ -82,6 +82,12 @@ def test_meansim_bit_exact(dev, B, H, Tq, Tk, sink):
     assert 0 < fm.float().mean().item() < 1
 
 
+def test_meansim_longest_rows(dev):
+    """4100 key blocks (the workgroup kernel's value sort over 8192 slots, scan tie-break)."""
+    q, k = _qk(12, 1, 1, 1030, 4100 * 64, dup=True, zeros=True)
+    _check(q, k, k.float().mean(2, keepdim=True), 0.2, 0.95, 1374, dev)
+
+
 def test_meansim_no_km_scalar_thresholds(dev):
     q, k = _qk(7, 1, 3, 700, 900)
     _check(q, k, None, 0.1, 0.9, 0, dev)
