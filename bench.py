@@ -166,12 +166,91 @@ def time_meansim(q, k, reps):
     return s.elapsed_time(e) / reps, nbytes
 
 
+def run_aggregator(args):
+    """a VGGT-1B-style aggregator (random init; 24 frame/global ViT-L
+    block pairs, dim 1024, 16 heads) on 64 synthetic 518x518 frames (N = 87,936 tokens),
+    ReSS (restore_swap_iter5_bf16_trackbest, HeSS budgets from synthetic per-layer tables)
+    on all 24 global layers at sparse_ratio 0.8. A step is one forward; the global-attention
+    share is the HIP-event time inside the 24 patched global-attention forwards (QKV
+    projection to W_O included) over the step. The dense comparison is the same model
+    (same seed) with plain SDPA global attention."""
+    import torch
+
+    import ress_amd as ress
+    from ress_amd import synth
+    from ress_amd.aggregator import build_vggt_aggregator, synthetic_frames
+    from ress_amd.wiring import global_blocks
+
+    dev = torch.device("cuda:0")
+    S, depth = 64, 24
+    cam, pc = synth.make_hess_tables()
+    model = build_vggt_aggregator(depth, 1024, 16, device=dev, tables=(pc, cam))
+    images = synthetic_frames(S, size=518, device=dev)
+    ress.apply_ress(model, 0.8, n_iters=5)
+    spans = []
+    for block in global_blocks(model):
+        fwd = block.attn.forward
+
+        def timed(*a, _fwd=fwd, **kw):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            out = _fwd(*a, **kw)
+            e.record()
+            spans.append((s, e))
+            return out
+
+        block.attn.forward = timed
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            model(images)
+        torch.cuda.synchronize()
+        spans.clear()
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+        marks[0].record()
+        for i in range(args.steps):
+            model(images)
+            marks[i + 1].record()
+        torch.cuda.synchronize()
+    ms = marks[0].elapsed_time(marks[-1]) / args.steps
+    step_ms = sorted(marks[i].elapsed_time(marks[i + 1]) for i in range(args.steps))
+    glob_ms = sum(s.elapsed_time(e) for s, e in spans) / args.steps
+    result = {
+        "metric": "ms per end-to-end aggregator forward (24 global layers under ReSS) + global-attention share",
+        "value": round(ms, 2), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 2), "ms_per_step_median": round(step_ms[len(step_ms) // 2], 2),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (64 frames 518x518: uniform [0,1] pixels + a shared low-frequency pattern); random weights",
+        "config": {"workload": "BASELINE configs[3]: VGGT-1B-style aggregator, ReSS on all 24 global layers",
+                   "frames": S, "tokens": S * 1374, "layers": depth, "dim": 1024, "heads": 16, "sparse_ratio": 0.8,
+                   "criterion": "restore_swap_iter5_bf16_trackbest"},
+        "global_attention_ms": round(glob_ms, 2), "global_attention_share": round(glob_ms / ms, 4),
+    }
+    if not args.no_dense:
+        del model
+        torch.cuda.empty_cache()
+        plain = build_vggt_aggregator(depth, 1024, 16, device=dev, wire=False)
+        with torch.no_grad():
+            plain(images)
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            plain(images)
+            e.record()
+            torch.cuda.synchronize()
+        result["dense_sdpa_forward_ms"] = round(s.elapsed_time(e), 2)
+        result["speedup_vs_dense"] = round(s.elapsed_time(e) / ms, 3)
+    print(json.dumps(result))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only "
                                    "(see DESIGN.md)", "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.config == 3:
+        run_aggregator(args)
+        return
     import numpy as np
     import torch
     import torch.nn.functional as F

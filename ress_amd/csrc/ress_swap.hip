@@ -234,9 +234,31 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
   // sequential sum + dot over k < n of Pw[k] and V[k][lane] (4 P values per LDS read)
   auto pv_chain = [&](int n, float& sum, float& dot) {
     float sp = 0.0f, acc = 0.0f;
+    int k0 = 0;
+    if constexpr (!VLDS) {
+      // V from L2: sixteen rows' loads go out before their chain steps
+      const int n16 = n & ~15;
+      for (; k0 < n16; k0 += 16) {
+        float vv[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) vv[j] = vrow(k0 + j);
+#pragma unroll
+        for (int j = 0; j < 16; j += 4) {
+          const float4 p4 = *reinterpret_cast<const float4*>(Pw + k0 + j);
+          sp = sp + p4.x;
+          acc = fmaf(p4.x, vv[j], acc);
+          sp = sp + p4.y;
+          acc = fmaf(p4.y, vv[j + 1], acc);
+          sp = sp + p4.z;
+          acc = fmaf(p4.z, vv[j + 2], acc);
+          sp = sp + p4.w;
+          acc = fmaf(p4.w, vv[j + 3], acc);
+        }
+      }
+    }
     const int n4 = n & ~3;
 #pragma unroll 4
-    for (int k = 0; k < n4; k += 4) {
+    for (int k = k0; k < n4; k += 4) {
       const float4 p4 = *reinterpret_cast<const float4*>(Pw + k);
       sp = sp + p4.x;
       acc = fmaf(p4.x, vrow(k), acc);
@@ -397,22 +419,23 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
       const float tqb = rs_bf(tqr, big);
       float tk[NPL];
       vdot_cols(t0, tk);  // term_k = v_k . big(Mg)
-      uint32_t rkey[NPL], ckey[NPL];
+      // restore quality of the dropped (higher is better), then the compensation quality
+      // of the kept, one key array at a time
+      auto quality = [&](int i, bool restore_side) -> float {
+        const float raw = rs_bf(Pb[i] * rs_bf(rs_bf(tk[i], big) - tqb, big), big);
+        const float q = restore_side ? rs_knorm(gn, Kk, 2.0f * raw + ssq[i], Pb[i])
+                                     : rs_knorm(gn, Kk, ssq[i] - 2.0f * raw, -Pb[i]);
+        return maxim ? -q : q;
+      };
+      uint32_t qkey[NPL];
       float rmax = -__builtin_huge_valf();
 #pragma unroll
       for (int i = 0; i < NPL; ++i) {
-        rkey[i] = ckey[i] = 0u;
+        qkey[i] = 0u;
         if (i < nel) {
-          const float raw = rs_bf(Pb[i] * rs_bf(rs_bf(tk[i], big) - tqb, big), big);
-          float r = rs_knorm(gn, Kk, 2.0f * raw + ssq[i], Pb[i]);
-          float c = rs_knorm(gn, Kk, ssq[i] - 2.0f * raw, -Pb[i]);
-          if (maxim) {
-            r = -r;
-            c = -c;
-          }
+          const float r = quality(i, true);
           if ((drop >> i) & 1u) rmax = fmaxf(rmax, r);
-          rkey[i] = rs_key(r);
-          ckey[i] = rs_key(c);
+          qkey[i] = rs_key(r);
         }
       }
       // beneficial iff some drop candidate has quality > 0
@@ -429,8 +452,11 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
       cnt = cnt < n_kept ? cnt : n_kept;
       if (!beneficial) cnt = 0;
       __builtin_amdgcn_wave_barrier();
-      const uint32_t restore = rs_top_m<NPL>(rkey, drop, cnt, lane, hist);
-      const uint32_t comp = rs_top_m<NPL>(ckey, cand_bits & ~drop, cnt, lane, hist);
+      const uint32_t restore = rs_top_m<NPL>(qkey, drop, cnt, lane, hist);
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) qkey[i] = i < nel ? rs_key(quality(i, false)) : 0u;
+      __builtin_amdgcn_wave_barrier();
+      const uint32_t comp = rs_top_m<NPL>(qkey, cand_bits & ~drop, cnt, lane, hist);
       drop = (drop & ~restore) | comp;
     }
     float fin = 0.0f;

@@ -1,0 +1,101 @@
+"""The public API on a whole model (reference src/ress/api.py:95-144 through the patched
+global-attention forward, wiring.py:76-106): a small VGGT-style aggregator with random
+weights, its global blocks wired to the block-sparse forward.
+
+* apply_dense and apply_sparse_vggt at sparse_ratio 0 (every block kept, so the HIP
+  sparse kernels compute full attention) reproduce the unwired model's plain-SDPA
+  forward within bf16 tolerance;
+* apply_sparse_vggt / apply_hess / apply_ress at a real sparse ratio run on every
+  global layer, keep about the requested fraction of blocks, and stay close to dense;
+* switching modes back to dense restores the dense output exactly (modes do not leak)."""
+
+import pytest
+import torch
+
+import ress_amd as ress
+import ress_amd.wiring as wiring
+from ress_amd import synth
+from ress_amd.aggregator import build_vggt_aggregator, synthetic_frames
+
+pytestmark = pytest.mark.gpu
+
+DEPTH, DIM, HEADS, FRAMES, SIZE = 2, 256, 4, 8, 196   # 8 frames x (14*14 + 5) = 1608 tokens
+
+
+def _cos(a, b):
+    return torch.nn.functional.cosine_similarity(a.float().flatten(), b.float().flatten(), dim=0).item()
+
+
+@pytest.fixture(scope="module")
+def models(dev):
+    tables = synth.make_hess_tables(n_layers=DEPTH, n_heads=HEADS)
+    wired = build_vggt_aggregator(DEPTH, DIM, HEADS, device=dev, tables=(tables[1], tables[0]))
+    plain = build_vggt_aggregator(DEPTH, DIM, HEADS, device=dev, wire=False)
+    images = synthetic_frames(FRAMES, size=SIZE, device=dev)
+    with torch.no_grad():
+        want = plain(images)
+    torch.cuda.synchronize()
+    return wired, images, want
+
+
+def test_dense_and_all_blocks_match_plain_sdpa(models):
+    model, images, want = models
+    with torch.no_grad():
+        ress.apply_dense(model)
+        got_dense = model(images)
+        ress.apply_sparse_vggt(model, 0.0)
+        got_sparse = model(images)
+    torch.cuda.synchronize()
+    for got in (got_dense, got_sparse):
+        assert torch.isfinite(got).all()
+        assert _cos(got, want) >= 0.999
+        assert (got.float() - want.float()).abs().max().item() <= 5e-2 * want.float().abs().max().item()
+
+
+@pytest.mark.parametrize("mode", ["sparse_vggt", "hess", "ress"])
+def test_sparse_modes_run_every_layer(models, mode):
+    model, images, want = models
+    sr = 0.5
+    seen = []  # each global layer's realised sparsity, through the forward's aux store
+    with torch.no_grad():
+        if mode == "sparse_vggt":
+            ress.apply_sparse_vggt(model, sr)
+        elif mode == "hess":
+            ress.apply_hess(model, sr)
+        else:
+            ress.apply_ress(model, sr, n_iters=5)
+        orig = wiring.ress_attention_forward
+
+        def spy(*a, **kw):
+            store = {}
+            kw["aux_store"] = store
+            kw["aux_full"] = False
+            out = orig(*a, **kw)
+            seen.append(store["value"].sparsity)
+            return out
+
+        wiring.ress_attention_forward = spy
+        try:
+            got = model(images)
+        finally:
+            wiring.ress_attention_forward = orig
+    torch.cuda.synchronize()
+    assert len(seen) == DEPTH
+    assert torch.isfinite(got).all()
+    # about half of the candidate blocks dropped (sinks and dense special rows keep some)
+    for s in seen:
+        assert 0.2 <= s <= 0.6, seen
+    assert _cos(got, want) >= 0.95
+
+
+def test_modes_do_not_leak(models):
+    model, images, _ = models
+    with torch.no_grad():
+        ress.apply_dense(model)
+        a = model(images)
+        ress.apply_ress(model, 0.7)
+        model(images)
+        ress.apply_dense(model)
+        b = model(images)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
