@@ -108,17 +108,58 @@ def _rank_key(block_criterion, attn_cond, attn_full, v_bar_full, counts, grid, M
     raise ValueError(block_criterion)
 
 
+def same_frame_block_mask(q_blk, k_blk, N, H, W, device):
+    """(q_blk, k_blk) bool: True where query block q (128 patch tokens) and key block k
+    (64 patch tokens) touch a common frame of the frame-major N*(H*W) patch sequence, as
+    interval overlap of the frames each block spans (a block can straddle a frame
+    boundary) -- reference attention.py:112-144."""
+    HW = H * W
+    T = N * HW
+    q0 = torch.arange(q_blk, device=device) * KS_Q
+    q1 = (q0 + KS_Q - 1).clamp(max=T - 1)
+    k0 = torch.arange(k_blk, device=device) * KS_K
+    k1 = (k0 + KS_K - 1).clamp(max=T - 1)
+    qf0, qf1, kf0, kf1 = q0 // HW, q1 // HW, k0 // HW, k1 // HW
+    return ~((qf1[:, None] < kf0[None, :]) | (kf1[None, :] < qf0[:, None]))
+
+
+def protect_own_frame_swap(final_map, attn_pooled, grid):
+    """Budget-neutral own-frame protection (reference attention.py:583-618): per (head,
+    query-block) row, every own-frame candidate block that is not kept replaces a kept
+    block of another frame, one for one -- the lowest-attn_pooled swappable blocks go out,
+    the highest-attn_pooled missing ones come in, n_swap = min(#missing, #swappable) of
+    each -- so the kept count per row is unchanged. final_map (B,H,q_blk_p,kb_tot) bool or
+    uint8, attn_pooled (B,H,q_blk_p,n_cand). Ties of attn_pooled go to the lower block
+    index (the reference's CUDA argsort leaves them unspecified). Returns a bool map."""
+    n = grid.n_cand
+    fm = final_map.bool()
+    same = same_frame_block_mask(grid.q_blk_p, n, grid.frames, grid.P - grid.S, 1, fm.device)
+    same = same.expand_as(fm[..., :n])
+    kept = fm[..., :n]
+    missing = same & ~kept
+    swappable = kept & ~same
+    n_swap = torch.minimum(missing.sum(-1), swappable.sum(-1)).unsqueeze(-1)
+    out_pri = attn_pooled.float().masked_fill(~swappable, float("inf"))
+    rank_out = torch.argsort(torch.argsort(out_pri, dim=-1, stable=True), dim=-1, stable=True)
+    in_pri = attn_pooled.float().masked_fill(~missing, float("-inf"))
+    rank_in = torch.argsort(torch.argsort(in_pri, dim=-1, descending=True, stable=True), dim=-1, stable=True)
+    new_kept = (kept & ~(rank_out < n_swap)) | (rank_in < n_swap)
+    return torch.cat([new_kept, fm[..., n:]], dim=-1)
+
+
 def sparse_global_attention(q, k, v, grid, *, num_to_select=None, budget_fn=None, perhead_budget_fn=None,
                             joint_select_fn=None, block_criterion="probability", M=None, out=None,
-                            out_dtype=torch.float32, keep_intermediates=False, qk_mode=None):
+                            out_dtype=torch.float32, keep_intermediates=False, qk_mode=None,
+                            protect_own_frame=False):
     """One layer's block-sparse global attention on the GPU.
 
     q, k, v: bf16 (B, H, frames*P, 64) in storage order (per frame S special then P-S
     patch tokens). Patch queries attend to the selected key blocks plus the trailing
     special blocks; special queries attend densely (reference attention.py:404-412,
     446-491, 510-581, 625). qk_mode: the QK^T operands, "bf16" (default), "i8x2" or
-    "i8" (see kernels.Blocks); the block map does not depend on it. Returns a
-    LayerResult whose `out` is (B, H, frames*P, 64) in storage order."""
+    "i8" (see kernels.Blocks); the block map does not depend on it. protect_own_frame:
+    the budget-neutral own-frame swap on the selected map (protect_own_frame_swap).
+    Returns a LayerResult whose `out` is (B, H, frames*P, 64) in storage order."""
     blocks = kernels.prepare_blocks(q, k, v, grid, mode=qk_mode or DEFAULT_QK_MODE)
     attn_full, attn_cond = kernels.pooled_scores(blocks)
     v_bar_full = blocks.pooled_v.view(grid.B, grid.H, grid.kb_p, 64)
@@ -144,6 +185,9 @@ def sparse_global_attention(q, k, v, grid, *, num_to_select=None, budget_fn=None
                          counts.clamp(min=min(MIN_NUM_TO_SELECT, grid.n_cand)) if block_criterion != "probability"
                          else counts, grid, M, 64)
         final_map, lut, nvalid = kernels.select_blocks(rank, counts, grid, min(MIN_NUM_TO_SELECT, grid.n_cand))
+    if protect_own_frame and grid.q_blk_p:  # after either selection path, as the reference does
+        final_map = protect_own_frame_swap(final_map, attn_full[..., :grid.n_cand], grid)
+        lut, nvalid = kernels.lut_from_map(final_map, grid)
     o = kernels.sparse_attention(blocks, lut, nvalid, out=out, out_dtype=out_dtype)
     res = LayerResult(out=o, final_map=final_map)
     if keep_intermediates:
@@ -174,8 +218,6 @@ def ress_attention_forward(self, x, pos, num_to_select=None, budget_fn=None, per
     same arguments and return value: (B, N*P, dim) after the W_O projection."""
     if pool_mode != "avg":
         raise NotImplementedError("only avg pooling (the reference default) is implemented")
-    if protect_own_frame:
-        raise NotImplementedError("protect_own_frame is not implemented")
     q, k, v, shp = compute_qkv(self, x, pos, num_special_tokens=num_special_tokens, num_heads=num_heads,
                                shape=shape)
     B, N, P, hd, nh, S = shp["B"], shp["N"], shp["P"], shp["head_dim"], shp["num_heads"], shp["S"]
@@ -191,7 +233,7 @@ def ress_attention_forward(self, x, pos, num_to_select=None, budget_fn=None, per
         res = sparse_global_attention(
             qb, kbf, vbf, grid, num_to_select=num_to_select, budget_fn=budget_fn, perhead_budget_fn=perhead_budget_fn,
             joint_select_fn=joint_select_fn, block_criterion=block_criterion, M=getattr(self, "M", None),
-            keep_intermediates=aux_store is not None and aux_full)
+            keep_intermediates=aux_store is not None and aux_full, protect_own_frame=protect_own_frame)
         x_out = res.out
         sparsity = res.sparsity() if aux_store is not None else None
     if aux_store is not None:

@@ -263,6 +263,36 @@ def test_layer_pipeline_matches_oracle(cfg, mode, dev):
     print(f"[{cfg} {mode}] attention max-abs {w:.3e} min-cos {c:.6f}")
 
 
+def test_layer_protect_own_frame(dev):
+    """protect_own_frame inside the layer: the swapped map is the oracle map after the
+    budget-neutral own-frame swap, the LUT is rebuilt from it, per-row kept counts are
+    unchanged, and the attention follows the new LUT."""
+    from ress_amd.attention import protect_own_frame_swap
+    frames, sr = 4, 0.8
+    q, k, v, meta = synth.make_layer_qkv(frames)
+    P, S = meta["P"], meta["S"]
+    g = LayerGrid(1, 16, frames, P, S)
+    bud = budget.UniformBudget()
+    res = sparse_global_attention(q.to(dev), k.to(dev), v.to(dev), g,
+                                  budget_fn=lambda a: bud.num_to_select(0, a, sr, None, 1.0), keep_intermediates=True,
+                                  protect_own_frame=True)
+    torch.cuda.synchronize()
+    o = oracle_layer(q, k, v, frames, P, S, sparse_ratio=sr, cdf_threshold=None)
+    want = protect_own_frame_swap(torch.from_numpy(o["map"]).reshape(1, 16, g.q_blk_p, g.kb_tot),
+                                  torch.from_numpy(o["attn_full"]).reshape(1, 16, g.q_blk_p, -1)[..., :g.n_cand], g)
+    got = _np(res.final_map).astype(bool)
+    assert np.array_equal(got, want.numpy())
+    assert np.array_equal(got.sum(-1).reshape(-1), o["map"].reshape(-1, g.kb_tot).sum(-1))
+    lut, nv = _np(res.lut), _np(res.nvalid)
+    gm = got.reshape(16, g.q_blk_p, g.kb_tot)
+    for bh in range(16):
+        for r in range(g.q_blk_p):
+            cols = np.flatnonzero(gm[bh, r])
+            assert nv[bh, r] == cols.size and np.array_equal(lut[bh, r, :cols.size], cols)
+    rows = row_sample(nv, 8)
+    _check_attention(res.out, q, k, v, frames, P, S, lut, nv, rows)
+
+
 @pytest.mark.parametrize("mode", ["bf16", "i8x2"])
 @pytest.mark.parametrize("B,H,frames", [(2, 16, 3), (1, 5, 2), (1, 1, 1)])
 def test_attention_writes_every_row(B, H, frames, mode, dev):
