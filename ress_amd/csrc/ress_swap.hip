@@ -46,13 +46,12 @@ __device__ __forceinline__ float rs_knorm(float G, float K, float dG, float u) {
   return (a * b / (K * K) - dG) / (Kn * Kn);
 }
 
-// Per-head preparation, 64 key blocks per workgroup: Vr = big(V) [kb_p][64], its
-// transpose VrT [64][kb_p] (through an LDS tile, both stores coalesced), and the key side
-// of quadratic_deviation, termk[k] = big(sum_i big(big(Mb v_k)_i * v_ki)) with the
-// product and the sum sequential in index order.
+// Per-head preparation, 64 key blocks per workgroup: Vr = big(V) [kb_p][64] and the key
+// side of quadratic_deviation, termk[k] = big(sum_i big(big(Mb v_k)_i * v_ki)) with the
+// product and the sum sequential in index order (the block goes through an LDS tile).
 __global__ __launch_bounds__(256) void k_rs_head(const float* __restrict__ V, const float* __restrict__ M, int H,
                                                  int kb_p, int n_cand, int big, float* __restrict__ Vr,
-                                                 float* __restrict__ VrT, float* __restrict__ termk) {
+                                                 float* __restrict__ termk) {
   __shared__ float MbT[64 * 64];     // MbT[j*64 + i] = big(M[i][j])
   __shared__ float tile[64][65];     // [key][dim], padded
   __shared__ float prod[4][64];      // one key's rounded products per wave
@@ -69,9 +68,6 @@ __global__ __launch_bounds__(256) void k_rs_head(const float* __restrict__ V, co
     tile[r][lane] = x;
   }
   __syncthreads();
-  for (int d = w; d < 64; d += 4) {  // columns: lane = key
-    if (k0 + lane < kb_p) VrT[((long long)bh * 64 + d) * kb_p + k0 + lane] = tile[lane][d];
-  }
   for (int r = w; r < 64; r += 4) {  // termk: wave per key, lane = output dim i
     const int k = k0 + r;
     if (k >= n_cand) break;
@@ -91,7 +87,6 @@ struct RsArgs {
   const float* M;  // [H][64][64]
   const int* nts;  // [BH][q_blk]
   const float* Vr;
-  const float* VrT;
   const float* termk;
   float* rank_key;  // [BH][q_blk][n_cand]: 1 = kept, 0 = dropped
   float* obj;       // [BH][q_blk] or null: J of the returned set
@@ -160,25 +155,55 @@ __device__ __forceinline__ uint32_t rs_top_m(const uint32_t (&key)[NPL], uint32_
   return sel;
 }
 
-// V of the head in LDS (VLDS, bf16 mode with kb_p <= RS_LDS_KBP): bf16 pairs, word w of
-// row k at k*32 + (w ^ (k & 31)), so that both access patterns -- lanes over the 64
-// dims of one key block, and lanes over consecutive key blocks at one dim pair -- hit
-// 32 distinct banks. Otherwise V is read from the L2-resident copies Vr / VrT.
+// V of the head in LDS (VLDS, bf16 mode when it fits): bf16 pairs, word w of row k at
+// k*32 + (w ^ (k & 31)), so that both access patterns -- lanes over the 64 dims of one
+// key block, and lanes over consecutive key blocks at one dim pair -- hit 32 distinct
+// banks. Otherwise V is streamed from Vr (below).
 #define RS_LDS_KBP 1024
 __device__ __forceinline__ uint32_t rs_vword(const uint32_t* vw, int k, int pair) {
   return vw[k * 32 + (pair ^ (k & 31))];
 }
 
+// Streamed V (STREAM = !VLDS: rows whose V does not fit in LDS, or fp32 V): the workgroup's
+// waves run their rows in lockstep -- every row makes the same sequence of P.V chains and
+// per-candidate products, and only those synchronise -- and V goes through LDS in tiles
+// of 64 key blocks x 64 dims (fp32, 16 KiB), two buffers filled by LDS-DMA one tile
+// ahead, so each tile is fetched from L2 once for all of the workgroup's rows. In a tile,
+// 16-byte chunk c of row r sits at chunk position c ^ (r & 15): lanes over the dims of one
+// row and lanes over rows reading one chunk (ds_read_b128) are both conflict-free.
+__device__ __forceinline__ void rs_gl_lds16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)src,
+                                   (void __attribute__((address_space(3)))*)lds_base, 16, 0, 0);
+}
+template <int N>
+__device__ __forceinline__ void rs_wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// workgroup barrier that does not wait for the DMA in flight (__syncthreads would):
+// this wave's LDS accesses complete, then s_barrier; the empty asm keeps memory
+// accesses from moving across it
+__device__ __forceinline__ void rs_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // The rows of one head: WAVES waves, each its own row at a time.
 template <int NPL, bool VLDS, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_per_wg) {
+  constexpr bool STREAM = !VLDS;
   extern __shared__ float sh[];
   float* M32T = sh;                 // [64][64] M^T (fp32)
   float* MbT = sh + 4096;           // [64][64] big(M)^T
   uint32_t* vw = reinterpret_cast<uint32_t*>(sh + 8192);  // VLDS: [kb_p][32] bf16 pairs
+  // STREAM: the two V tile buffers (distinct objects, so the compiler can see that a
+  // DMA into one never aliases reads of the other)
+  __shared__ __align__(16) float4 tb0[STREAM ? 1024 : 1];
+  __shared__ __align__(16) float4 tb1[STREAM ? 1024 : 1];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int kb4 = (a.kb_p + 3) & ~3;
-  float* wsh = sh + 8192 + (VLDS ? a.kb_p * 32 : 0) + w * (kb4 + 5 * 64);
+  constexpr int OUTL = STREAM ? NPL * 64 : 0;  // STREAM: per-wave slots of the candidate products
+  float* wsh = sh + 8192 + (VLDS ? a.kb_p * 32 : 0) + w * (kb4 + 5 * 64 + OUTL);
   float* Pw = wsh;                  // [kb_p] big(P) of the row, then P*drop (16-byte aligned)
   float* vqs = wsh + kb4;           // [64]
   float* t0 = vqs + 64;             // [64] scratch vectors; t0..t3 double as the
@@ -186,6 +211,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
   float* t2 = t1 + 64;
   float* t3 = t2 + 64;
   int* hist = reinterpret_cast<int*>(t0);
+  float* outl = t3 + 64;            // STREAM: [NPL][64] candidate products, slot-major
   const int bh = blockIdx.y;
   const bool big = a.flags & RS_BF16, track = a.flags & RS_TRACK_BEST;
   const bool maxim = a.flags & RS_MAXIMIZE, inv = a.flags & RS_INVERT_CUT;
@@ -197,7 +223,6 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
     MbT[(e & 63) * 64 + (e >> 6)] = rs_bf(m, big);
   }
   const float* Vr = a.Vr + (long long)bh * a.kb_p * 64;
-  const float* VrT = a.VrT + (long long)bh * 64 * a.kb_p;
   if constexpr (VLDS) {
     for (int e = threadIdx.x; e < a.kb_p * 32; e += 64 * WAVES) {
       const int k = e >> 5, wd = e & 31;
@@ -208,21 +233,42 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
   }
   __syncthreads();
   const int vsh = (lane & 1) ? 0 : 16;  // this lane's dim in the upper half of its pair word
-  // V[k][lane] (lanes over dims)
-  auto vrow = [&](int k) -> float {
-    if constexpr (VLDS) return __uint_as_float((rs_vword(vw, k, lane >> 1) << vsh) & 0xffff0000u);
-    else return Vr[(long long)k * 64 + lane];
-  };
-  // (V[k][2p], V[k][2p+1]) (lanes over key blocks)
+  // VLDS: V[k][lane] (lanes over dims)
+  auto vrow = [&](int k) -> float { return __uint_as_float((rs_vword(vw, k, lane >> 1) << vsh) & 0xffff0000u); };
+  // VLDS: (V[k][2p], V[k][2p+1]) (lanes over key blocks)
   auto vpair = [&](int p, int k, float& v0, float& v1) {
-    if constexpr (VLDS) {
-      const uint32_t word = rs_vword(vw, k, p);
-      v0 = __uint_as_float(word << 16);
-      v1 = __uint_as_float(word & 0xffff0000u);
-    } else {
-      v0 = VrT[(long long)(2 * p) * a.kb_p + k];
-      v1 = VrT[(long long)(2 * p + 1) * a.kb_p + k];
+    const uint32_t word = rs_vword(vw, k, p);
+    v0 = __uint_as_float(word << 16);
+    v1 = __uint_as_float(word & 0xffff0000u);
+  };
+  // STREAM: tile t = V rows 64t..64t+63 (rows past kb_p repeat the last one; their
+  // results are never used). Each wave DMAs four of the tile's sixteen 1 KiB slices.
+  auto tile_dma = [&](float4* buf, int t) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int j = 4 * w + jj, sl = 64 * j + lane, r = sl >> 4, c = (sl & 15) ^ (r & 15);
+      const int row = min(64 * t + r, a.kb_p - 1);
+      rs_gl_lds16(Vr + (long long)row * 64 + 4 * c, buf + 64 * j);
     }
+  };
+  // collective over T tiles: body(tile, t) runs once the tile is in LDS for every wave;
+  // tile t+1 is in flight meanwhile (two buffers, unrolled by two so that each DMA's
+  // target is a different object from the buffer being read)
+  auto stream_tiles = [&](int T, auto&& body) {
+    rs_barrier();  // every wave is done with the buffers of the previous collective
+    tile_dma(tb0, 0);
+    auto step = [&](const float4* cur, float4* other, int t) {
+      rs_wait_vmcnt<0>();  // this wave's slices of tile t
+      rs_barrier();        // ... and every other wave's; tile t-1 (in `other`) is done
+      if (t + 1 < T) tile_dma(other, t + 1);
+      body(cur, t);
+    };
+    int t = 0;
+    for (; t + 2 <= T; t += 2) {
+      step(tb0, tb1, t);
+      step(tb1, tb0, t + 1);
+    }
+    if (t < T) step(tb0, tb1, t);
   };
   const float* tkey = a.termk + (long long)bh * a.n_cand;
   const int n_cand = a.n_cand, kb_p = a.kb_p;
@@ -234,28 +280,41 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
   // sequential sum + dot over k < n of Pw[k] and V[k][lane] (4 P values per LDS read)
   auto pv_chain = [&](int n, float& sum, float& dot) {
     float sp = 0.0f, acc = 0.0f;
-    int k0 = 0;
-    if constexpr (!VLDS) {
-      // V from L2: sixteen rows' loads go out before their chain steps
-      const int n16 = n & ~15;
-      for (; k0 < n16; k0 += 16) {
-        float vv[16];
+    if constexpr (STREAM) {  // collective: every wave of the workgroup calls it with the same n
+      const int dhi = lane >> 2, dlo = lane & 3;
+      stream_tiles((n + 63) >> 6, [&](const float4* tile, int t) {
+        const float* tf = reinterpret_cast<const float*>(tile);
+        const int m = min(64, n - 64 * t);
+        const float* pc = Pw + 64 * t;
+        int kk = 0;
+        for (; kk + 16 <= m; kk += 16) {  // sixteen rows' LDS reads in flight per batch
+          float v[16];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) vv[j] = vrow(k0 + j);
+          for (int u = 0; u < 16; ++u) v[u] = tf[(kk + u) * 64 + ((dhi ^ u) << 2) + dlo];  // kk % 16 == 0
 #pragma unroll
-        for (int j = 0; j < 16; j += 4) {
-          const float4 p4 = *reinterpret_cast<const float4*>(Pw + k0 + j);
-          sp = sp + p4.x;
-          acc = fmaf(p4.x, vv[j], acc);
-          sp = sp + p4.y;
-          acc = fmaf(p4.y, vv[j + 1], acc);
-          sp = sp + p4.z;
-          acc = fmaf(p4.z, vv[j + 2], acc);
-          sp = sp + p4.w;
-          acc = fmaf(p4.w, vv[j + 3], acc);
+          for (int u = 0; u < 16; u += 4) {
+            const float4 p4 = *reinterpret_cast<const float4*>(pc + kk + u);
+            sp = sp + p4.x;
+            acc = fmaf(p4.x, v[u], acc);
+            sp = sp + p4.y;
+            acc = fmaf(p4.y, v[u + 1], acc);
+            sp = sp + p4.z;
+            acc = fmaf(p4.z, v[u + 2], acc);
+            sp = sp + p4.w;
+            acc = fmaf(p4.w, v[u + 3], acc);
+          }
         }
-      }
+        for (; kk < m; ++kk) {
+          const float p = pc[kk];
+          sp = sp + p;
+          acc = fmaf(p, tf[kk * 64 + ((dhi ^ (kk & 15)) << 2) + dlo], acc);
+        }
+      });
+      sum = sp;
+      dot = acc;
+      return;
     }
+    int k0 = 0;
     const int n4 = n & ~3;
 #pragma unroll 4
     for (int k = k0; k < n4; k += 4) {
@@ -281,6 +340,23 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
   auto vdot_cols = [&](const float* vec, float (&out)[NPL]) {
 #pragma unroll
     for (int i = 0; i < NPL; ++i) out[i] = 0.0f;
+    if constexpr (STREAM) {  // collective: tile i holds the candidates of lane slot i
+      stream_tiles(nel, [&](const float4* tile, int i) {
+        const float4* vk = tile + lane * 16;
+        float o = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {  // dims 4q..4q+3: steps p = 2q, 2q+1
+          const float4 v = vk[q ^ (lane & 15)];
+          o = fmaf(vec[4 * q + 1], v.y, fmaf(vec[4 * q], v.x, o));
+          o = fmaf(vec[4 * q + 3], v.w, fmaf(vec[4 * q + 2], v.z, o));
+        }
+        outl[i * 64 + lane] = o;
+      });
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int e = 0; e < NPL; ++e) out[e] = e < nel ? outl[e * 64 + lane] : 0.0f;
+      return;
+    }
     for (int p = 0; p < 32; ++p) {
       const float m0 = vec[2 * p], m1 = vec[2 * p + 1];
 #pragma unroll
@@ -296,9 +372,13 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
     }
   };
 
-  const int q_end = min(a.q_blk, (blockIdx.x + 1) * rows_per_wg);
-  for (int q = blockIdx.x * rows_per_wg + w; q < q_end; q += WAVES) {
-    const long long row = (long long)bh * a.q_blk + q;
+  const int q_begin = blockIdx.x * rows_per_wg, q_end = min(a.q_blk, (blockIdx.x + 1) * rows_per_wg);
+  // STREAM: every wave makes the same number of passes (a wave without a row of its own
+  // repeats the last one and writes nothing), so the collective calls line up
+  const int passes = STREAM ? (q_end - q_begin + WAVES - 1) / WAVES : 0x7fffffff;
+  for (int pass = 0, q = q_begin + w; STREAM ? pass < passes : q < q_end; ++pass, q += WAVES) {
+    const bool own = q < q_end;
+    const long long row = (long long)bh * a.q_blk + (own ? q : q_end - 1);
 
     // ---- row inputs and the dense reference -------------------------------------
     const float* Arow = a.A + row * kb_p;
@@ -354,7 +434,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
           om = rs_bf(om < 1e-4f ? 1e-4f : om, big);
           sc = renorm ? rs_bf(s / om, big) : s;
           ssq[i] = rs_bf(s * s, big);
-          if (a.s_out) a.s_out[row * n_cand + k] = s;
+          if (a.s_out && own) a.s_out[row * n_cand + k] = s;
         }
         key[i] = rs_key(inv ? -sc : sc);
       }
@@ -465,12 +545,12 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
       drop = best;
       fin = best_obj;
     }
-    if (a.obj && lane == 0) a.obj[row] = fin;
+    if (a.obj && lane == 0 && own) a.obj[row] = fin;
     float* out = a.rank_key + row * n_cand;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
       const int k = lane + 64 * i;
-      if (k < n_cand) out[k] = ((drop >> i) & 1u) ? 0.0f : 1.0f;
+      if (k < n_cand && own) out[k] = ((drop >> i) & 1u) ? 0.0f : 1.0f;
     }
     __builtin_amdgcn_wave_barrier();
   }  // rows of this wave
@@ -498,20 +578,22 @@ static int launch_rs(int BH, size_t lds, hipStream_t stream, const RsArgs& a) {
   return 0;
 }
 
+// V resident in LDS (bf16 pairs, eight rows at a time) when it fits next to the M
+// tables and the rows' scratch; otherwise streamed through one shared tile.
+#define RS_LDS_BYTES 163840
 template <int NPL>
 static int launch_rs_npl(int BH, int kb_p, bool big, hipStream_t stream, const RsArgs& a) {
-  if constexpr (NPL * 64 <= RS_LDS_KBP) {  // rows that fit take the LDS-resident V
-    if (big && kb_p <= RS_LDS_KBP) {
-      const size_t lds = sizeof(float) * (8192 + 32 * (size_t)kb_p + 8 * (size_t)(((kb_p + 3) & ~3) + 5 * 64));
-      return launch_rs<NPL, true, 8>(BH, lds, stream, a);
-    }
+  const size_t scratch = ((size_t)((kb_p + 3) & ~3) + 5 * 64);
+  if constexpr (NPL * 64 <= RS_LDS_KBP) {
+    const size_t lds = sizeof(float) * (8192 + 32 * (size_t)kb_p + 8 * scratch);
+    if (big && lds <= RS_LDS_BYTES) return launch_rs<NPL, true, 8>(BH, lds, stream, a);
   }
-  const size_t lds = sizeof(float) * (8192 + 4 * (size_t)(((kb_p + 3) & ~3) + 5 * 64));
+  const size_t lds = sizeof(float) * (8192 + 4 * (scratch + NPL * 64));  // + the two 16 KiB static tiles
   return launch_rs<NPL, false, 4>(BH, lds, stream, a);
 }
 
 RESS_API long long ress_restore_swap_workspace_size(int BH, int kb_p, int n_cand) {
-  return (long long)BH * kb_p * 64 * 4 * 2 + (long long)BH * n_cand * 4;
+  return (long long)BH * kb_p * 64 * 4 + (long long)BH * n_cand * 4;  // Vr, termk
 }
 
 // restore_swap_rank_by (src/ress/scoring/projected.py:395-1058) for every (batch*head,
@@ -542,18 +624,16 @@ RESS_API int ress_restore_swap(const void* A, const void* V, const void* M, cons
                "ress_restore_swap: workspace of %lld bytes required", ress_restore_swap_workspace_size(BH, kb_p, n_cand));
   if (q_blk == 0) return 0;
   float* Vr = (float*)workspace;
-  float* VrT = Vr + (long long)BH * kb_p * 64;
-  float* termk = VrT + (long long)BH * kb_p * 64;
+  float* termk = Vr + (long long)BH * kb_p * 64;
   const int big = (flags & RS_BF16) ? 1 : 0;
   hipLaunchKernelGGL(k_rs_head, dim3(cdiv(kb_p, 64), BH), dim3(256), 0, stream, (const float*)V, (const float*)M, H,
-                     kb_p, n_cand, big, Vr, VrT, termk);
+                     kb_p, n_cand, big, Vr, termk);
   RESS_LAUNCHED("k_rs_head");
   RsArgs a;
   a.A = (const float*)A;
   a.M = (const float*)M;
   a.nts = (const int*)nts;
   a.Vr = Vr;
-  a.VrT = VrT;
   a.termk = termk;
   a.rank_key = (float*)rank_key;
   a.obj = (float*)obj;
