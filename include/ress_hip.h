@@ -107,6 +107,17 @@ int ress_fill_block_map(void* map, const void* counts, const void* sorted_idx, l
  * map [rows][k] uint8 -> lut [rows][k] int32 (ascending), nvalid [rows]. */
 int ress_block_map_lut(const void* map, long long rows, int k, void* lut, void* nvalid, hipStream_t stream);
 
+/* ---- QKV preparation (qkv.hip) ------------------------------------------------ */
+
+/* Replaces compute_patch_qkv's q_norm / k_norm and RoPE (src/ress/models/qkv.py:60-68)
+ * for modules with LayerNorm(64) q/k norms and the rotate-half 2D RoPE (first 32 head
+ * dims by row, last 32 by column, base^(-2i/32)): qkv (B,T,3*nh*64) bf16 (the qkv
+ * Linear's output), LayerNorm weights/biases [64] bf16, pos (B,T,2) int64 or NULL (no
+ * rotation) -> q, k, v (B,nh,T,64) bf16. */
+int ress_qk_norm_rope(const void* qkv, int B, int T, int nh, const void* q_weight, const void* q_bias,
+                      const void* k_weight, const void* k_bias, float eps, const void* pos, float rope_base,
+                      void* q_out, void* k_out, void* v_out, hipStream_t stream);
+
 /* ---- SpargeAttn meansim block map (meansim.hip) --------------------------- */
 
 /* Replaces get_block_map_meansim_fuse_quant (SpargeAttn spas_sage_attn/utils.py as

@@ -29,6 +29,7 @@ _SIGS = {
     "ress_qattn_block_sparse_fwd": "pppipipppppiiiilllllliiifipls",
     "ress_restore_swap": "pppp" + "iiiiii" + "dd" + "i" + "ppp" + "pl" + "s",
     "ress_meansim_block_map": "ppp" + "iiii" + "llllll" + "ppi" + "ppppppppp" + "s",
+    "ress_qk_norm_rope": "piii" + "pppp" + "f" + "pf" + "ppp" + "s",
 }
 _CT = {
     "p": ctypes.c_void_p,

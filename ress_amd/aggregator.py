@@ -52,7 +52,8 @@ class RoPE2D(nn.Module):
 class Attention(nn.Module):
     """qkv Linear, per-head LayerNorm on q and k, 2D RoPE, SDPA, output projection: the
     module layout the block-sparse forward reads (qkv, q_norm, k_norm, rope, proj,
-    proj_drop, num_heads)."""
+    proj_drop, num_heads). On the GPU in bf16 the norms and the rotation run as one fused
+    kernel (ress_qk_norm_rope); `fused = False` keeps the torch modules."""
 
     def __init__(self, dim, num_heads, rope):
         super().__init__()
@@ -64,14 +65,19 @@ class Attention(nn.Module):
         self.rope = rope
         self.proj = nn.Linear(dim, dim, bias=True)
         self.proj_drop = nn.Identity()
+        self.fused = True  # q/k norm + RoPE through the fused kernel when on the GPU in bf16
 
     def forward(self, x, pos=None):
+        from ress_amd.qkv import _fusable, fused_qk_norm_rope
         B, T, C = x.shape
         nh = self.num_heads
-        q, k, v = self.qkv(x).reshape(B, T, 3, nh, C // nh).permute(2, 0, 3, 1, 4).unbind(0)
-        q, k = self.q_norm(q), self.k_norm(k)
-        if pos is not None:
-            q, k = self.rope(q, pos), self.rope(k, pos)
+        if self.fused and _fusable(self, x, C // nh):
+            q, k, v = fused_qk_norm_rope(self, self.qkv(x), pos, nh)
+        else:
+            q, k, v = self.qkv(x).reshape(B, T, 3, nh, C // nh).permute(2, 0, 3, 1, 4).unbind(0)
+            q, k = self.q_norm(q), self.k_norm(k)
+            if pos is not None:
+                q, k = self.rope(q, pos), self.rope(k, pos)
         o = F.scaled_dot_product_attention(q, k, v)
         return self.proj_drop(self.proj(o.transpose(1, 2).reshape(B, T, C)))
 

@@ -8,6 +8,8 @@ the attention kernel writes its output back in storage order.
 
 import torch
 
+from ress_amd import _lib
+
 
 def grid_shape(x, pos, num_special_tokens=5, num_heads=16, shape=None):
     """(B, N frames, P tokens/frame, H, W, S, hd) of one global-attention input
@@ -27,12 +29,47 @@ def grid_shape(x, pos, num_special_tokens=5, num_heads=16, shape=None):
     return {"B": B, "N": N, "P": P, "head_dim": dim // num_heads, "num_heads": num_heads, "H": H, "W": W, "S": S}
 
 
+def _fusable(self, x, hd):
+    """True when the module's q/k normalisation and rotary embedding are the ones the
+    fused kernel implements: bf16 on the GPU, LayerNorm(64) with affine weights, and this
+    package's RoPE2D (or no rotation)."""
+    from ress_amd.aggregator import RoPE2D
+    rope = getattr(self, "rope", None)
+    qn, kn = getattr(self, "q_norm", None), getattr(self, "k_norm", None)
+    return (x.is_cuda and x.dtype == torch.bfloat16 and hd == 64
+            and all(isinstance(n, torch.nn.LayerNorm) and n.normalized_shape == (64,) and n.weight is not None
+                    and n.bias is not None and n.weight.dtype == torch.bfloat16 for n in (qn, kn))
+            and (rope is None or isinstance(rope, RoPE2D)))
+
+
+def fused_qk_norm_rope(self, qkv_out, pos, nh):
+    """q_norm / k_norm and the 2D RoPE of a qkv Linear output (B, T, 3*nh*64) bf16 in one
+    kernel (ress_qk_norm_rope) -> q, k, v (B, nh, T, 64) bf16 contiguous."""
+    B, T, _ = qkv_out.shape
+    dev = qkv_out.device
+    src = qkv_out.contiguous()
+    q = torch.empty(B, nh, T, 64, dtype=torch.bfloat16, device=dev)
+    k, v = torch.empty_like(q), torch.empty_like(q)
+    rope = getattr(self, "rope", None)
+    p = None if rope is None or pos is None else pos.to(device=dev, dtype=torch.int64).reshape(B, T, 2).contiguous()
+    qn, kn = self.q_norm, self.k_norm
+    _lib.call("ress_qk_norm_rope", _lib.ptr(src), B, T, nh, _lib.ptr(qn.weight), _lib.ptr(qn.bias),
+              _lib.ptr(kn.weight), _lib.ptr(kn.bias), float(qn.eps), _lib.ptr(p),
+              float(rope.base) if rope is not None else 0.0, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v),
+              _lib.stream_handle(dev))
+    return q, k, v
+
+
 def compute_qkv(self, x, pos, num_special_tokens=5, num_heads=16, shape=None):
     """(q, k, v, shape): each (B, nh, N*P, hd) in storage order, after q_norm/k_norm and
-    RoPE -- reference qkv.py:60-68 without the split."""
+    RoPE -- reference qkv.py:60-68 without the split. Modules with LayerNorm q/k norms and
+    this package's RoPE2D take the fused kernel; others run the torch modules."""
     shp = grid_shape(x, pos, num_special_tokens, num_heads, shape)
     B, NP, _ = x.shape
     nh, hd = shp["num_heads"], shp["head_dim"]
+    if _fusable(self, x, hd) and self.q_norm.eps == self.k_norm.eps:
+        q, k, v = fused_qk_norm_rope(self, self.qkv(x), pos, nh)
+        return q, k, v, shp
     qkv = self.qkv(x).reshape(B, NP, 3, nh, hd).permute(2, 0, 3, 1, 4)
     q, k, v = qkv.unbind(0)
     q, k = self.q_norm(q), self.k_norm(k)

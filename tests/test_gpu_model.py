@@ -88,6 +88,34 @@ def test_sparse_modes_run_every_layer(models, mode):
     assert _cos(got, want) >= 0.95
 
 
+def test_fused_qk_norm_rope_matches_modules(dev):
+    """The fused q/k LayerNorm + 2D RoPE kernel against the torch modules it replaces:
+    v is copied exactly; q and k agree to bf16 rounding (the kernel's powf/cosf/sinf and
+    LayerNorm reduction order are its own)."""
+    from ress_amd.aggregator import Attention, RoPE2D
+    from ress_amd.qkv import fused_qk_norm_rope
+    torch.manual_seed(3)
+    attn = Attention(256, 4, RoPE2D()).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        for n in (attn.q_norm, attn.k_norm):
+            n.weight.uniform_(0.5, 1.5)
+            n.bias.uniform_(-0.2, 0.2)
+    B, T = 2, 300
+    x = torch.randn(B, T, 256, device=dev).to(torch.bfloat16)
+    pos = torch.randint(0, 38, (B, T, 2), device=dev)
+    with torch.no_grad():
+        qkv = attn.qkv(x)
+        q, k, v = fused_qk_norm_rope(attn, qkv, pos, 4)
+        rq, rk, rv = qkv.reshape(B, T, 3, 4, 64).permute(2, 0, 3, 1, 4).unbind(0)
+        rq, rk = attn.rope(attn.q_norm(rq), pos), attn.rope(attn.k_norm(rk), pos)
+    torch.cuda.synchronize()
+    assert torch.equal(v, rv.contiguous())
+    for got, want in ((q, rq), (k, rk)):
+        err = (got.float() - want.float()).abs()
+        assert err.max().item() <= 2 ** -6 * want.float().abs().max().item()
+        assert (err > 0).float().mean().item() < 0.02  # nearly all bit-identical
+
+
 def test_modes_do_not_leak(models):
     model, images, _ = models
     with torch.no_grad():
