@@ -139,20 +139,28 @@ __device__ __forceinline__ float pair_sum(float x) {
 }
 
 // ---- work schedule ---------------------------------------------------------
-// Rows are items in head-major order (per head: its dense special rows, then its
-// patch rows). The schedule cuts the item list into 8 contiguous ranges of equal
-// work (kept blocks + a fixed per-row cost), one per XCD, so each XCD walks few
-// heads (their K/V stay in its L2) and all XCDs finish together.
+// Rows are items: first the dense special rows of every head, then the patch rows
+// head-major. The schedule cuts the item list into 8 contiguous ranges of equal work
+// (kept blocks + a fixed per-row cost), one per XCD, so each XCD walks few heads (their
+// K/V stay in its L2) and all XCDs finish together. The dense rows (every key block,
+// several times a patch row) lead so they start at once: in head-major order the dense
+// row of a head in the middle of a range would start late and end long after the rest.
 //   sched[0..8]   range bounds (sched[j] .. sched[j+1]-1 belong to XCD j)
 //   sched[16..23] per-XCD next-item counters (atomically advanced by the kernel)
 #define RESS_SCHED_INTS 32
 #define RESS_ROW_COST 2
 
-__device__ __forceinline__ void item_to_row(int i, int q_blk_p, int q_blk_total, int& bh, int& qb) {
-  bh = i / q_blk_total;
-  const int r = i - bh * q_blk_total;
-  const int qs = q_blk_total - q_blk_p;
-  qb = r < qs ? q_blk_p + r : r - qs;
+__device__ __forceinline__ void item_to_row(int i, int BH, int q_blk_p, int q_blk_total, int& bh, int& qb) {
+  const int qs = q_blk_total - q_blk_p;  // special (dense) q-blocks per head
+  const int ns = BH * qs;
+  if (i < ns) {
+    bh = i / qs;
+    qb = q_blk_p + (i - bh * qs);
+  } else {
+    const int j = i - ns;
+    bh = j / q_blk_p;
+    qb = j - bh * q_blk_p;
+  }
 }
 
 __global__ __launch_bounds__(1024) void k_attn_schedule(const int* __restrict__ nvalid, int BH, int q_blk_p,
@@ -165,7 +173,7 @@ __global__ __launch_bounds__(1024) void k_attn_schedule(const int* __restrict__ 
   long long s = 0;
   for (int i = i0; i < i1; ++i) {
     int bh, qb;
-    item_to_row(i, q_blk_p, q_blk_total, bh, qb);
+    item_to_row(i, BH, q_blk_p, q_blk_total, bh, qb);
     s += nvalid[(long long)bh * q_blk_total + qb] + RESS_ROW_COST;
   }
   part[tid] = s;
@@ -182,7 +190,7 @@ __global__ __launch_bounds__(1024) void k_attn_schedule(const int* __restrict__ 
   long long prev = -1;            // exclusive prefix of item i-1
   if (i0 > 0 && i0 < n) {
     int bh, qb;
-    item_to_row(i0 - 1, q_blk_p, q_blk_total, bh, qb);
+    item_to_row(i0 - 1, BH, q_blk_p, q_blk_total, bh, qb);
     prev = run - (nvalid[(long long)bh * q_blk_total + qb] + RESS_ROW_COST);
   }
   for (int i = i0; i < i1; ++i) {
@@ -190,7 +198,7 @@ __global__ __launch_bounds__(1024) void k_attn_schedule(const int* __restrict__ 
     for (int j = 1; j < 8; ++j)
       if (run * 8 >= (long long)j * W && prev * 8 < (long long)j * W) sched[j] = i;
     int bh, qb;
-    item_to_row(i, q_blk_p, q_blk_total, bh, qb);
+    item_to_row(i, BH, q_blk_p, q_blk_total, bh, qb);
     prev = run;
     run += nvalid[(long long)bh * q_blk_total + qb] + RESS_ROW_COST;
   }
@@ -731,7 +739,7 @@ __global__ __launch_bounds__(256, Occupancy<QK>::value) void k_sparse_attn(AttnA
     __syncthreads();
     if (item >= item_end) break;
     int bh, qb;
-    item_to_row(item, a.q_blk_p, a.q_blk_total, bh, qb);
+    item_to_row(item, a.BH, a.q_blk_p, a.q_blk_total, bh, qb);
     sparse_attn_row<QK, V_F16, OUT>(a, lut, nvalid, k_scale, stage0, stage1, stage2, stage3, bh, qb);
   }
 }
