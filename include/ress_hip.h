@@ -158,7 +158,10 @@ int ress_restore_swap(const void* A, const void* V, const void* M, const void* n
  * ress_prep_qkv + ress_select_blocks; out (B,H,frames*P,64) in storage order,
  * out_dtype 0 f32 / 1 bf16 / 2 f16, element strides soB/soH/soT. q_lo/k_lo both NULL: the
  * reference's single-term per-block INT8 QK^T; both set: the two-term split product.
- * sched: 32 int32 of device workspace (the persistent kernel's row schedule). */
+ * sched: ress_attn_sched_bytes(B, H, frames*P) bytes of 16-byte aligned device workspace
+ * (the persistent kernel's row schedule and the parts of the rows it splits; rewritten by
+ * every call, so calls that overlap must not share it). */
+long long ress_attn_sched_bytes(int B, int H, int Tq);
 int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void* q_scale, const void* k_i8,
                          const void* k_lo, const void* k_scale, const void* v_pack, int v_f16, const void* lut,
                          const void* nvalid, int B, int H, int frames, int P, int S, float sm_scale, void* out,
@@ -168,7 +171,7 @@ int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void* q_scale
 /* The fused-path attention of ress_sparse_attn_fwd (same reference lines) with QK^T on
  * the bf16 inputs (fp32 accumulation) instead of INT8 codes: q is the layer's bf16
  * (B,H,frames*P,64) query tensor in storage order with element strides sqB/sqH/sqT,
- * k_pack and v_pack come from ress_prep_qkv. sched: 32 int32 of device workspace. */
+ * k_pack and v_pack come from ress_prep_qkv. sched: as for ress_sparse_attn_fwd. */
 int ress_sparse_attn_fwd_bf16(const void* q, long long sqB, long long sqH, long long sqT, const void* k_pack,
                               const void* v_pack, const void* lut, const void* nvalid, int B, int H, int frames,
                               int P, int S, float sm_scale, void* out, int out_dtype, long long soB, long long soH,
@@ -176,8 +179,9 @@ int ress_sparse_attn_fwd_bf16(const void* q, long long sqB, long long sqH, long 
 
 /* Replaces SpargeAttn qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold
  * (call src/ress/models/attention.py:238-241) with the same argument meaning; see
- * attn.hip for the supported flag values. */
-long long ress_qattn_workspace_size(int B, int H, int Tk);
+ * attn.hip for the supported flag values. workspace: ress_qattn_workspace_size(B,H,Tq,Tk)
+ * bytes (packed V, then the attention's sched workspace), 16-byte aligned. */
+long long ress_qattn_workspace_size(int B, int H, int Tq, int Tk);
 int ress_qattn_block_sparse_fwd(const void* q_i8, const void* k_i8, const void* v, int v_f16, void* o,
                                 int o_dtype, const void* lut, const void* valid_block_num,
                                 const float* pv_threshold_host, const void* q_scale, const void* k_scale,

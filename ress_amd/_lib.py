@@ -56,7 +56,9 @@ def lib():
         L.ress_last_error.restype = ctypes.c_char_p
         L.ress_abi_version.restype = ctypes.c_int
         L.ress_qattn_workspace_size.restype = ctypes.c_longlong
-        L.ress_qattn_workspace_size.argtypes = [ctypes.c_int] * 3
+        L.ress_qattn_workspace_size.argtypes = [ctypes.c_int] * 4
+        L.ress_attn_sched_bytes.restype = ctypes.c_longlong
+        L.ress_attn_sched_bytes.argtypes = [ctypes.c_int] * 3
         L.ress_restore_swap_workspace_size.restype = ctypes.c_longlong
         L.ress_restore_swap_workspace_size.argtypes = [ctypes.c_int] * 3
         for name, sig in _SIGS.items():
@@ -93,4 +95,4 @@ def last_error():
 
 def exported_symbols():
     return list(_SIGS) + ["ress_last_error", "ress_abi_version", "ress_qattn_workspace_size",
-                          "ress_restore_swap_workspace_size"]
+                          "ress_attn_sched_bytes", "ress_restore_swap_workspace_size"]

@@ -46,8 +46,10 @@ struct AttnArgs {
   int H, BH;
   int q_blk_p, q_blk_total, kb_tot, Tk;
   float sm_scale_log2e;
-  int* sched;  // RESS_SCHED_INTS ints of workspace written by k_attn_schedule
-  TokenMap m;  // query rows: patch blocks via patch_to_storage, the rest via special_to_storage
+  int* sched;   // the row schedule written by k_attn_schedule (header of the sched workspace)
+  float* part;  // key-range parts of the split rows (rest of the sched workspace)
+  int split_L;  // rows split at the end of each XCD's range
+  TokenMap m;   // query rows: patch blocks via patch_to_storage, the rest via special_to_storage
 };
 
 enum { OUT_F32 = 0, OUT_BF16 = 1, OUT_F16 = 2 };
@@ -149,6 +151,16 @@ __device__ __forceinline__ float pair_sum(float x) {
 //   sched[16..23] per-XCD next-item counters (atomically advanced by the kernel)
 #define RESS_SCHED_INTS 32
 #define RESS_ROW_COST 2
+// Tail split. Workgroups run out of rows one by one at the end of a range; the spread of
+// their end times is about one row's duration. The last RESS_SPLIT_ROWS rows of each
+// range (half the workgroups of an XCD; measured best) therefore run as RESS_SPLIT_PARTS parts over
+// consecutive slices of their kept blocks. A part leaves its unnormalised O, running max
+// and row sum in a slot of the workspace (RESS_PART_FLOATS floats, register order), and
+// k_attn_merge combines the parts of each split row and writes it.
+#define RESS_SPLIT_ROWS 32
+#define RESS_SPLIT_PARTS 3
+#define RESS_PART_FLOATS (256 * 32 + 2 * 256)
+#define RESS_SCHED_HDR_BYTES 256
 
 __device__ __forceinline__ void item_to_row(int i, int BH, int q_blk_p, int q_blk_total, int& bh, int& qb) {
   const int qs = q_blk_total - q_blk_p;  // special (dense) q-blocks per head
@@ -482,16 +494,54 @@ struct StageShape {
   static constexpr int DMA = QK == QK_I8 ? 3 : 4;  // LDS-DMA instructions per lane per stage
 };
 
+// Output of one finished row (query block qb of head bh): O / row sum, in the output
+// dtype at the row's storage positions. o0/o1 hold O^T in the PV MFMA's register order.
+template <int OUT>
+__device__ __forceinline__ void store_row(const AttnArgs& a, int bh, int qb, const v16f& o0, const v16f& o1,
+                                          float l_run) {
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, qi = l & 31;
+  const bool special = qb >= a.q_blk_p;
+  const int qbase = special ? (qb - a.q_blk_p) * 128 : qb * 128;
+  const int cnt_q = min(128, (special ? a.m.T_s : a.m.T_p) - qbase);
+  const int qrow = 32 * w + qi;
+  const float lt = pair_sum(l_run);
+  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  if (qrow >= cnt_q) return;
+  const int tok = special ? special_to_storage(qbase + qrow, a.m) : patch_to_storage(qbase + qrow, a.m);
+  const long long off = (long long)(bh / a.H) * a.soB + (long long)(bh % a.H) * a.soH + (long long)tok * a.soT;
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const v16f& o = n ? o1 : o0;
+#pragma unroll
+    for (int a4 = 0; a4 < 4; ++a4) {
+      const int d0 = 32 * n + 8 * a4 + 4 * g;
+      const float y0 = o[4 * a4 + 0] * inv, y1 = o[4 * a4 + 1] * inv;
+      const float y2 = o[4 * a4 + 2] * inv, y3 = o[4 * a4 + 3] * inv;
+      if constexpr (OUT == OUT_F32) {
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + off + d0) = make_float4(y0, y1, y2, y3);
+      } else {
+        constexpr bool F16 = OUT == OUT_F16;
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.out) + off + d0) =
+            make_uint2(pack2<F16>(y0, y1), pack2<F16>(y2, y3));
+      }
+    }
+  }
+}
+
+// One row (query block qb of head bh) over its kept blocks kb_lo..kb_hi-1 (LUT
+// positions). part_out null: the whole row, written to the output; otherwise one part of
+// a split row, left in part_out for k_attn_merge.
 template <int QK, bool V_F16, int OUT>
 __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __restrict__ lut_all,
-                                                const int* __restrict__ nvalid, const float* __restrict__ k_scale,
-                                                uint4* __restrict__ s0, uint4* __restrict__ s1,
-                                                uint4* __restrict__ s2, uint4* __restrict__ s3, int bh, int qb) {
+                                                const float* __restrict__ k_scale, uint4* __restrict__ s0,
+                                                uint4* __restrict__ s1, uint4* __restrict__ s2,
+                                                uint4* __restrict__ s3, int bh, int qb, int kb_lo, int kb_hi,
+                                                float* __restrict__ part_out) {
   constexpr int KCH = StageShape<QK>::KCH;
   constexpr int DMA = StageShape<QK>::DMA;
   const long long row = (long long)bh * a.q_blk_total + qb;
-  const int nv = nvalid[row];
-  const int* lut = lut_all + row * a.kb_tot;
+  const int nv = kb_hi - kb_lo;
+  const int* lut = lut_all + row * a.kb_tot + kb_lo;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, qi = l & 31;
   const bool special = qb >= a.q_blk_p;
   const int qbase = special ? (qb - a.q_blk_p) * 128 : qb * 128;
@@ -688,28 +738,18 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
   }
 
   // ---- epilogue ------------------------------------------------------------
-  const float lt = pair_sum(l_run);
-  const float inv = (nv > 0 && lt > 0.0f) ? 1.0f / lt : 0.0f;
-  if (qrow >= cnt_q) return;  // this row function only; the caller's loop continues
-  const int tok = special ? special_to_storage(qbase + qrow, a.m) : patch_to_storage(qbase + qrow, a.m);
-  const long long off = (long long)(bh / a.H) * a.soB + (long long)(bh % a.H) * a.soH + (long long)tok * a.soT;
+  if (part_out) {  // unnormalised O, running max and row sum of this part, in register order
+    float4* po = reinterpret_cast<float4*>(part_out);
 #pragma unroll
-  for (int n = 0; n < 2; ++n) {
-    const v16f& o = n ? o1 : o0;
-#pragma unroll
-    for (int a4 = 0; a4 < 4; ++a4) {
-      const int d0 = 32 * n + 8 * a4 + 4 * g;
-      const float y0 = o[4 * a4 + 0] * inv, y1 = o[4 * a4 + 1] * inv;
-      const float y2 = o[4 * a4 + 2] * inv, y3 = o[4 * a4 + 3] * inv;
-      if constexpr (OUT == OUT_F32) {
-        *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + off + d0) = make_float4(y0, y1, y2, y3);
-      } else {
-        constexpr bool F16 = OUT == OUT_F16;
-        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.out) + off + d0) =
-            make_uint2(pack2<F16>(y0, y1), pack2<F16>(y2, y3));
-      }
+    for (int q = 0; q < 4; ++q) {
+      po[q * 256 + tid] = make_float4(o0[4 * q], o0[4 * q + 1], o0[4 * q + 2], o0[4 * q + 3]);
+      po[(4 + q) * 256 + tid] = make_float4(o1[4 * q], o1[4 * q + 1], o1[4 * q + 2], o1[4 * q + 3]);
     }
+    part_out[8192 + tid] = m_run;
+    part_out[8448 + tid] = l_run;
+    return;
   }
+  store_row<OUT>(a, bh, qb, o0, o1, l_run);
 }
 
 // Resident workgroups per CU (= waves per SIMD).
@@ -730,18 +770,75 @@ __global__ __launch_bounds__(256, Occupancy<QK>::value) void k_sparse_attn(AttnA
   __shared__ int s_item;
 
   // ---- persistent loop over this XCD's range of rows ------------------------
+  // positions b0 .. full_end-1 are whole rows; the last Lx rows of the range follow as
+  // RESS_SPLIT_PARTS consecutive positions each (part s of row j at full_end + S*j + s)
   const int xcd = blockIdx.x & 7;
-  const int item_end = a.sched[xcd + 1];
+  const int b1 = a.sched[xcd + 1];
+  const int Lx = min(a.split_L, b1 - a.sched[xcd]);
+  const int full_end = b1 - Lx;
+  const int item_end = full_end + Lx * RESS_SPLIT_PARTS;
   for (;;) {
     if (threadIdx.x == 0) s_item = atomicAdd(&a.sched[16 + xcd], 1);
     __syncthreads();
-    const int item = __builtin_amdgcn_readfirstlane(s_item);
+    const int pos = __builtin_amdgcn_readfirstlane(s_item);
     __syncthreads();
-    if (item >= item_end) break;
+    if (pos >= item_end) break;
     int bh, qb;
-    item_to_row(item, a.BH, a.q_blk_p, a.q_blk_total, bh, qb);
-    sparse_attn_row<QK, V_F16, OUT>(a, lut, nvalid, k_scale, stage0, stage1, stage2, stage3, bh, qb);
+    if (pos < full_end) {
+      item_to_row(pos, a.BH, a.q_blk_p, a.q_blk_total, bh, qb);
+      const int nv = nvalid[(long long)bh * a.q_blk_total + qb];
+      sparse_attn_row<QK, V_F16, OUT>(a, lut, k_scale, stage0, stage1, stage2, stage3, bh, qb, 0, nv, nullptr);
+    } else {
+      const int j = (pos - full_end) / RESS_SPLIT_PARTS, part = pos - full_end - j * RESS_SPLIT_PARTS;
+      item_to_row(full_end + j, a.BH, a.q_blk_p, a.q_blk_total, bh, qb);
+      const int nv = nvalid[(long long)bh * a.q_blk_total + qb];
+      float* slot = a.part + ((long long)(xcd * a.split_L + j) * RESS_SPLIT_PARTS + part) * RESS_PART_FLOATS;
+      sparse_attn_row<QK, V_F16, OUT>(a, lut, k_scale, stage0, stage1, stage2, stage3, bh, qb,
+                                      nv * part / RESS_SPLIT_PARTS, nv * (part + 1) / RESS_SPLIT_PARTS, slot);
+    }
   }
+}
+
+// The split rows: combine the parts' (O, m, l) (m in log2 units; an empty part has
+// m = -inf, l = 0, O = 0) and write the row. One workgroup per slot (XCD range x, row j).
+template <int OUT>
+__global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
+  const int L = a.split_L, slot = blockIdx.x, x = slot / L, j = slot - x * L;
+  const int b1 = a.sched[x + 1];
+  const int Lx = min(L, b1 - a.sched[x]);
+  if (j >= Lx) return;
+  int bh, qb;
+  item_to_row(b1 - Lx + j, a.BH, a.q_blk_p, a.q_blk_total, bh, qb);
+  const int tid = threadIdx.x;
+  const float* base = a.part + (long long)slot * RESS_SPLIT_PARTS * RESS_PART_FLOATS;
+  float m = -__builtin_huge_valf();
+#pragma unroll
+  for (int s = 0; s < RESS_SPLIT_PARTS; ++s) m = fmaxf(m, base[s * RESS_PART_FLOATS + 8192 + tid]);
+  v16f o0, o1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) o0[r] = o1[r] = 0.0f;
+  float l_run = 0.0f;
+#pragma unroll
+  for (int s = 0; s < RESS_SPLIT_PARTS; ++s) {
+    const float* ps = base + s * RESS_PART_FLOATS;
+    const float ms = ps[8192 + tid];
+    const float f = ms == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(ms - m);
+    l_run = fmaf(f, ps[8448 + tid], l_run);
+    const float4* po = reinterpret_cast<const float4*>(ps);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 u = po[q * 256 + tid], v = po[(4 + q) * 256 + tid];
+      o0[4 * q] = fmaf(f, u.x, o0[4 * q]);
+      o0[4 * q + 1] = fmaf(f, u.y, o0[4 * q + 1]);
+      o0[4 * q + 2] = fmaf(f, u.z, o0[4 * q + 2]);
+      o0[4 * q + 3] = fmaf(f, u.w, o0[4 * q + 3]);
+      o1[4 * q] = fmaf(f, v.x, o1[4 * q]);
+      o1[4 * q + 1] = fmaf(f, v.y, o1[4 * q + 1]);
+      o1[4 * q + 2] = fmaf(f, v.z, o1[4 * q + 2]);
+      o1[4 * q + 3] = fmaf(f, v.w, o1[4 * q + 3]);
+    }
+  }
+  store_row<OUT>(a, bh, qb, o0, o1, l_run);
 }
 
 // Plain (B,H,Tk,64) 16-bit V -> packed [BH][kb][64 dims][64 permuted keys].
@@ -803,8 +900,24 @@ static int launch_attn(const AttnArgs& a, int out_dtype, hipStream_t stream) {
       break;
   }
   RESS_LAUNCHED("k_sparse_attn");
+  const dim3 mgrid(8 * a.split_L);
+  switch (out_dtype) {
+    case OUT_F32:
+      hipLaunchKernelGGL(k_attn_merge<OUT_F32>, mgrid, block, 0, stream, a);
+      break;
+    case OUT_BF16:
+      hipLaunchKernelGGL(k_attn_merge<OUT_BF16>, mgrid, block, 0, stream, a);
+      break;
+    default:
+      hipLaunchKernelGGL(k_attn_merge<OUT_F16>, mgrid, block, 0, stream, a);
+      break;
+  }
+  RESS_LAUNCHED("k_attn_merge");
   return 0;
 }
+
+// rows split at the end of each XCD's range for n rows in all (at most one range's worth)
+static int split_rows(long long n) { return (int)(n < RESS_SPLIT_ROWS ? n : RESS_SPLIT_ROWS); }
 
 static bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -813,7 +926,7 @@ static int attn_args(AttnArgs& a, const void* v_pack, const void* lut, const voi
                      int Tk, float sm_scale, void* out, int out_dtype, long long soB, long long soH, long long soT,
                      void* sched) {
   RESS_REQUIRE(v_pack && lut && nvalid && out && sched, "sparse attention: null pointer");
-  RESS_REQUIRE(al16(v_pack), "sparse attention: v_pack must be 16-byte aligned");
+  RESS_REQUIRE(al16(v_pack) && al16(sched), "sparse attention: v_pack and sched must be 16-byte aligned");
   RESS_REQUIRE(out_dtype >= 0 && out_dtype <= 2, "sparse attention: out_dtype must be 0 (f32), 1 (bf16) or 2 (f16)");
   const int align = out_dtype == OUT_F32 ? 16 : 8;
   RESS_REQUIRE(((uintptr_t)out % align) == 0 && soT % 4 == 0 && soH % 4 == 0 && soB % 4 == 0,
@@ -834,6 +947,8 @@ static int attn_args(AttnArgs& a, const void* v_pack, const void* lut, const voi
   a.Tk = Tk;
   a.sm_scale_log2e = sm_scale * 1.4426950408889634f;
   a.sched = (int*)sched;
+  a.split_L = split_rows((long long)a.BH * a.q_blk_total);
+  a.part = reinterpret_cast<float*>(reinterpret_cast<char*>(sched) + RESS_SCHED_HDR_BYTES);
   a.m = m;
   return 0;
 }
@@ -876,7 +991,7 @@ static TokenMap layer_map(int frames, int P, int S) {
 // combine_special_and_patch (src/ress/models/qkv.py:71-81) is fused in. With q_lo/k_lo
 // (split-INT8 residual codes from ress_prep_qkv) QK^T is evaluated as a two-term INT8
 // product; without them it is the single-term per-block INT8 product of the reference.
-// sched: RESS_SCHED_INTS (32) int32 of device workspace for the row schedule.
+// sched: ress_attn_sched_bytes(B, H, frames*P) bytes of 16-byte aligned device workspace.
 RESS_API int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void* q_scale, const void* k_i8,
                                   const void* k_lo, const void* k_scale, const void* v_pack, int v_f16, const void* lut,
                                   const void* nvalid, int B, int H, int frames, int P, int S, float sm_scale, void* out,
@@ -914,8 +1029,19 @@ RESS_API int ress_sparse_attn_fwd_bf16(const void* q, long long sqB, long long s
 
 static long long qattn_vpack_bytes(int B, int H, int Tk) { return (long long)B * H * cdiv(Tk, 64) * 4096 * 2; }
 
-RESS_API long long ress_qattn_workspace_size(int B, int H, int Tk) {
-  return qattn_vpack_bytes(B, H, Tk) + RESS_SCHED_INTS * 4;
+// Workspace of the attention entry points for B*H heads of Tq query rows: the row
+// schedule (header) and the parts of the rows split at the end of each XCD's range
+// (at most RESS_SPLIT_ROWS rows per range, RESS_SPLIT_PARTS parts of RESS_PART_FLOATS
+// floats each). The fused path's patch/special split can add one query block per head.
+RESS_API long long ress_attn_sched_bytes(int B, int H, int Tq) {
+  if (B <= 0 || H <= 0 || Tq < 0) return -1;
+  const long long n = (long long)B * H * (cdiv(Tq, 128) + 1);
+  return RESS_SCHED_HDR_BYTES + 8LL * split_rows(n) * RESS_SPLIT_PARTS * RESS_PART_FLOATS * 4;
+}
+
+RESS_API long long ress_qattn_workspace_size(int B, int H, int Tq, int Tk) {
+  if (B <= 0 || H <= 0 || Tq < 0 || Tk < 0) return -1;
+  return qattn_vpack_bytes(B, H, Tk) + ress_attn_sched_bytes(B, H, Tq);
 }
 
 // Mirror of SpargeAttn's qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold
@@ -926,7 +1052,7 @@ RESS_API long long ress_qattn_workspace_size(int B, int H, int Tk) {
 // q_scale [B*H][ceil(Tq/128)], k_scale [B*H][ceil(Tk/64)]; o (B,H,Tq,64) with strides.
 // Supported: tensor_layout 1 (HND), is_causal 0, qk_quant_gran 1 (per block),
 // return_pv_count 0, pv_threshold disabled (>= 1e9, the reference passes 1e10).
-// workspace: ress_qattn_workspace_size(B,H,Tk) bytes (packed V + the row schedule).
+// workspace: ress_qattn_workspace_size(B,H,Tq,Tk) bytes (packed V + the row schedule).
 RESS_API int ress_qattn_block_sparse_fwd(const void* q_i8, const void* k_i8, const void* v, int v_f16, void* o,
                                          int o_dtype, const void* lut, const void* valid_block_num,
                                          const float* pv_threshold_host, const void* q_scale, const void* k_scale,
@@ -945,8 +1071,9 @@ RESS_API int ress_qattn_block_sparse_fwd(const void* q_i8, const void* k_i8, con
                    "passes 1e10 = disabled)",
                    (double)pv_threshold_host[h]);
   RESS_REQUIRE(B > 0 && H > 0 && Tq > 0 && Tk > 0, "ress_qattn_block_sparse_fwd: bad geometry");
-  RESS_REQUIRE(v && workspace && workspace_bytes >= ress_qattn_workspace_size(B, H, Tk),
-               "ress_qattn_block_sparse_fwd: workspace of %lld bytes required", ress_qattn_workspace_size(B, H, Tk));
+  RESS_REQUIRE(v && workspace && workspace_bytes >= ress_qattn_workspace_size(B, H, Tq, Tk),
+               "ress_qattn_block_sparse_fwd: workspace of %lld bytes required",
+               ress_qattn_workspace_size(B, H, Tq, Tk));
   RESS_REQUIRE(((uintptr_t)v & 15u) == 0 && svT % 8 == 0 && svH % 8 == 0 && svB % 8 == 0,
                "ress_qattn_block_sparse_fwd: v must be 16-byte aligned with strides a multiple of 8");
   const int kb_tot = cdiv(Tk, 64);

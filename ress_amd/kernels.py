@@ -261,7 +261,7 @@ def sparse_attention(blocks, lut, nvalid, out=None, out_dtype=torch.float32):
     if out is None:
         out = torch.empty(g.B, g.H, g.Tk, HEAD_DIM, dtype=out_dtype, device=dev)
     code = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[out.dtype]
-    sched = torch.empty(32, dtype=torch.int32, device=dev)
+    sched = torch.empty(_lib.lib().ress_attn_sched_bytes(g.B, g.H, g.Tk), dtype=torch.uint8, device=dev)
     P = _lib.ptr
     sm = 1.0 / math.sqrt(HEAD_DIM)
     if blocks.mode == "bf16":

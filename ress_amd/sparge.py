@@ -144,7 +144,7 @@ def qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold(
     pv_host = torch.as_tensor(pv_threshold, dtype=torch.float32).detach().cpu().reshape(-1).contiguous()
     if pv_host.numel() != H:
         raise ValueError("pv_threshold must have one value per head")
-    ws_bytes = _lib.lib().ress_qattn_workspace_size(B, H, Tk)
+    ws_bytes = _lib.lib().ress_qattn_workspace_size(B, H, Tq, Tk)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     code = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[o.dtype]
     lut_c = lut.to(torch.int32).contiguous()

@@ -52,8 +52,20 @@ def test_binding_argument_counts_match_header(library):
 
 
 def test_abi_version_and_error_string(library):
-    assert library.ress_abi_version() == 1
+    assert library.ress_abi_version() == 2
     assert isinstance(library.ress_last_error(), bytes)
+
+
+def test_workspace_sizes(library):
+    # 256-byte schedule header + 8 XCD ranges x (split rows) x 3 parts x (O, m, l) of
+    # 256 threads x (32 + 2) floats; split rows = min(32, query blocks incl. one per head)
+    part = 3 * 256 * 34 * 4
+    assert library.ress_attn_sched_bytes(1, 16, 21984) == 256 + 8 * 32 * part
+    assert library.ress_attn_sched_bytes(2, 3, 0) == 256 + 8 * 6 * part
+    assert library.ress_attn_sched_bytes(0, 3, 10) == -1
+    # SpargeAttn mirror: packed V (64x64 bf16 per key block) + the attention's workspace
+    assert library.ress_qattn_workspace_size(1, 2, 300, 200) == 2 * 4 * 4096 * 2 + 256 + 8 * 8 * part
+    assert library.ress_qattn_workspace_size(1, 2, -1, 200) == -1
 
 
 def test_argument_validation_without_a_gpu(library):
