@@ -314,21 +314,37 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
       dot = acc;
       return;
     }
-    int k0 = 0;
-    const int n4 = n & ~3;
-#pragma unroll 4
-    for (int k = k0; k < n4; k += 4) {
-      const float4 p4 = *reinterpret_cast<const float4*>(Pw + k);
-      sp = sp + p4.x;
-      acc = fmaf(p4.x, vrow(k), acc);
-      sp = sp + p4.y;
-      acc = fmaf(p4.y, vrow(k + 1), acc);
-      sp = sp + p4.z;
-      acc = fmaf(p4.z, vrow(k + 2), acc);
-      sp = sp + p4.w;
-      acc = fmaf(p4.w, vrow(k + 3), acc);
+    // VLDS: sixteen rows per batch, all of the batch's LDS reads issued before its chain
+    // steps, so the chain waits on LDS once per batch
+    const int n16 = n & ~15;
+    uint32_t wa[16];
+    float4 pa[4];
+    auto load16 = [&](int k, uint32_t(&wv)[16], float4(&pv)[4]) {
+#pragma unroll
+      for (int u = 0; u < 16; ++u) wv[u] = rs_vword(vw, k + u, lane >> 1);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) pv[u] = *reinterpret_cast<const float4*>(Pw + k + 4 * u);
+    };
+    auto chain16 = [&](const uint32_t(&wv)[16], const float4(&pv)[4]) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        sp = sp + pv[u].x;
+        acc = fmaf(pv[u].x, __uint_as_float((wv[4 * u] << vsh) & 0xffff0000u), acc);
+        sp = sp + pv[u].y;
+        acc = fmaf(pv[u].y, __uint_as_float((wv[4 * u + 1] << vsh) & 0xffff0000u), acc);
+        sp = sp + pv[u].z;
+        acc = fmaf(pv[u].z, __uint_as_float((wv[4 * u + 2] << vsh) & 0xffff0000u), acc);
+        sp = sp + pv[u].w;
+        acc = fmaf(pv[u].w, __uint_as_float((wv[4 * u + 3] << vsh) & 0xffff0000u), acc);
+      }
+    };
+    int k = 0;
+    for (; k < n16; k += 16) {
+      load16(k, wa, pa);
+      __builtin_amdgcn_sched_barrier(0);
+      chain16(wa, pa);
     }
-    for (int k = n4; k < n; ++k) {
+    for (; k < n; ++k) {
       const float p = Pw[k];
       sp = sp + p;
       acc = fmaf(p, vrow(k), acc);
@@ -357,18 +373,33 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
       for (int e = 0; e < NPL; ++e) out[e] = e < nel ? outl[e * 64 + lane] : 0.0f;
       return;
     }
-    for (int p = 0; p < 32; ++p) {
-      const float m0 = vec[2 * p], m1 = vec[2 * p + 1];
+    // VLDS: the words of dim pair p+1 are read while pair p is accumulated (two register
+    // buffers), so the products wait on LDS once per pair at most
+    uint32_t wa[NPL], wb[NPL];
+    auto load_pair = [&](int p, uint32_t(&wv)[NPL]) {
 #pragma unroll
       for (int i = 0; i < NPL; ++i) {
         if (i < nel) {
           int k = lane + 64 * i;
           k = k < n_cand ? k : n_cand - 1;
-          float v0, v1;
-          vpair(p, k, v0, v1);
-          out[i] = fmaf(m1, v1, fmaf(m0, v0, out[i]));
+          wv[i] = rs_vword(vw, k, p);
         }
       }
+    };
+    auto use_pair = [&](int p, const uint32_t(&wv)[NPL]) {
+      const float m0 = vec[2 * p], m1 = vec[2 * p + 1];
+#pragma unroll
+      for (int i = 0; i < NPL; ++i)
+        if (i < nel) out[i] = fmaf(m1, __uint_as_float(wv[i] & 0xffff0000u), fmaf(m0, __uint_as_float(wv[i] << 16), out[i]));
+    };
+    load_pair(0, wa);
+    for (int p = 0; p < 32; p += 2) {
+      load_pair(p + 1, wb);
+      __builtin_amdgcn_sched_barrier(0);
+      use_pair(p, wa);
+      if (p + 2 < 32) load_pair(p + 2, wa);
+      __builtin_amdgcn_sched_barrier(0);
+      use_pair(p + 1, wb);
     }
   };
 
