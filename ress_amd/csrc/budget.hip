@@ -61,6 +61,9 @@ __global__ __launch_bounds__(64) void k_fill_int(int* __restrict__ out, long lon
 // [B][H][q_blk] int32 (out may alias baseline). scores_norm [H] fp32 (already
 // normalised, or null for the uniform budget). iters_out [B][q_blk] receives the
 // number of cap-redistribute iterations, or -1 if max_iters was reached.
+// HB >= H is a compile-time bound: the per-head loops unroll over HB with an h < H
+// guard, so the head arrays stay in registers and the sums keep their order h = 0..H-1.
+template <int HB>
 __global__ __launch_bounds__(64) void k_head_budget(const int* baseline, int B, int H, int q_blk,
                                                     const float* __restrict__ scores_norm, float one_minus_beta,
                                                     float beta, int max_val, int max_iters, int min_select,
@@ -78,40 +81,57 @@ __global__ __launch_bounds__(64) void k_head_budget(const int* baseline, int B, 
     if (iters_out) iters_out[col] = 0;
     return;
   }
-  float adj[RESS_MAX_HEADS], w[RESS_MAX_HEADS];
+  float adj[HB], w[HB];
+  int bv[HB];
   long long total = 0;
-  for (int h = 0; h < H; ++h) total += base[(long long)h * q_blk];
+#pragma unroll
+  for (int h = 0; h < HB; ++h) {
+    bv[h] = h < H ? base[(long long)h * q_blk] : 0;
+    total += bv[h];
+  }
   const float total_f = (float)total;
-  for (int h = 0; h < H; ++h) {
-    const float ideal = scores_norm[h] * total_f;
-    adj[h] = one_minus_beta * (float)base[(long long)h * q_blk] + beta * ideal;
+#pragma unroll
+  for (int h = 0; h < HB; ++h) {
+    const float ideal = h < H ? scores_norm[h] * total_f : 0.0f;
+    adj[h] = one_minus_beta * (float)bv[h] + beta * ideal;
   }
   const float maxv = (float)max_val;
   int it = 0;
   for (; it < max_iters; ++it) {
     float esum = 0.0f;
     bool finite = true;
-    for (int h = 0; h < H; ++h) {
-      const float d = adj[h] - maxv;
-      const float ex = d < 0.0f ? 0.0f : d;  // clamp(min=0), NaN kept
-      finite = finite && (ex - ex == 0.0f);
-      esum = esum + ex;
+#pragma unroll
+    for (int h = 0; h < HB; ++h) {
+      if (h < H) {
+        const float d = adj[h] - maxv;
+        const float ex = d < 0.0f ? 0.0f : d;  // clamp(min=0), NaN kept
+        finite = finite && (ex - ex == 0.0f);
+        esum = esum + ex;
+      }
     }
     if (!finite || !(esum > 0.0f)) break;
     float wsum = 0.0f;
-    for (int h = 0; h < H; ++h) {
-      adj[h] = adj[h] > maxv ? maxv : adj[h];
-      w[h] = adj[h] * (adj[h] < maxv ? 1.0f : 0.0f);
-      wsum = wsum + w[h];
+#pragma unroll
+    for (int h = 0; h < HB; ++h) {
+      if (h < H) {
+        adj[h] = adj[h] > maxv ? maxv : adj[h];
+        w[h] = adj[h] * (adj[h] < maxv ? 1.0f : 0.0f);
+        wsum = wsum + w[h];
+      }
     }
     const float den = wsum + 0x1.12e0bep-30f;  // + 1e-9
-    for (int h = 0; h < H; ++h) adj[h] = adj[h] + (w[h] / den) * esum;
+#pragma unroll
+    for (int h = 0; h < HB; ++h)
+      if (h < H) adj[h] = adj[h] + (w[h] / den) * esum;
   }
   if (iters_out) iters_out[col] = it < max_iters ? it : -1;
-  for (int h = 0; h < H; ++h) {
-    const float a = adj[h] > maxv ? maxv : adj[h];
-    int c = (int)floorf(a);
-    dst[(long long)h * q_blk] = c < min_select ? min_select : c;
+#pragma unroll
+  for (int h = 0; h < HB; ++h) {
+    if (h < H) {
+      const float a = adj[h] > maxv ? maxv : adj[h];
+      int c = (int)floorf(a);
+      dst[(long long)h * q_blk] = c < min_select ? min_select : c;
+    }
   }
 }
 
@@ -149,9 +169,15 @@ RESS_API int ress_head_budget(const void* baseline, int B, int H, int q_blk, con
   RESS_REQUIRE(baseline && out_counts, "ress_head_budget: null pointer");
   RESS_REQUIRE(max_iters > 0, "ress_head_budget: max_iters must be positive");
   const int cols = B * q_blk;
-  hipLaunchKernelGGL(k_head_budget, dim3((cols + 63) / 64), dim3(64), 0, stream, (const int*)baseline, B, H, q_blk,
-                     (const float*)scores_norm, (float)(1.0 - beta), (float)beta, max_val, max_iters, min_select,
-                     (int*)out_counts, (int*)iters_out);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((cols + 63) / 64), dim3(64), 0, stream, (const int*)baseline, B, H, q_blk,
+                       (const float*)scores_norm, (float)(1.0 - beta), (float)beta, max_val, max_iters, min_select,
+                       (int*)out_counts, (int*)iters_out);
+  };
+  if (H <= 8) go(k_head_budget<8>);
+  else if (H <= 16) go(k_head_budget<16>);
+  else if (H <= 32) go(k_head_budget<32>);
+  else go(k_head_budget<RESS_MAX_HEADS>);
   RESS_LAUNCHED("k_head_budget");
   return 0;
 }

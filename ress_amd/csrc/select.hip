@@ -9,8 +9,8 @@
 // Selection order is (value descending, index ascending): the kept set of a row is
 // the n largest keys, ties at the threshold going to the lowest column index, the
 // rule of the reference's top-m kernel (src/ress/scoring/fused_topm.py:74-79).
-// The n-th largest key is found exactly by an MSB-first binary search over the
-// order-preserving uint32 image of the fp32 key.
+// The n-th largest key is found exactly by an MSB-first radix select (four 8-bit
+// digits) over the order-preserving uint32 image of the fp32 key.
 #include "common.h"
 
 // Kept columns of one row -> LUT (ascending) + count, one wave. keep(c) is evaluated
@@ -42,6 +42,8 @@ __global__ __launch_bounds__(64) void k_select(const float* __restrict__ rank_ke
                                                int min_select, uint8_t* __restrict__ map, int* __restrict__ lut,
                                                int* __restrict__ nvalid) {
   extern __shared__ uint32_t key[];  // n_cand order keys, then reused for the kept flags
+  __shared__ int hist[256];
+  __shared__ int pick[2];
   const int qb = blockIdx.x, bh = blockIdx.y, lane = threadIdx.x;
   const long long lrow = (long long)bh * q_blk_total + qb;
   int* lrow_p = lut + lrow * kb_tot;
@@ -57,14 +59,49 @@ __global__ __launch_bounds__(64) void k_select(const float* __restrict__ rank_ke
   n = n < min_select ? min_select : n;  // clamp(min=min(2, n_cand)), attention.py:525
   n = n < 0 ? 0 : (n > n_cand ? n_cand : n);
   __syncthreads();
-  // largest thr with #(key >= thr) >= n
-  uint32_t thr = 0u;
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t cand = thr | (1u << bit);
-    int c = 0;
-    for (int i = lane; i < n_cand; i += 64) c += key[i] >= cand ? 1 : 0;
-    c = wave_sum_i(c);
-    if (c >= n) thr = cand;
+  // thr = the n-th largest key (n = 0: all ones, nothing above it). MSB-first radix
+  // select: among the keys matching the digits fixed so far, an 8-bit histogram of the
+  // next digit; the digit holding the rank-th largest (rank counted from the top) is
+  // fixed and the keys above it leave the count.
+  uint32_t thr = ~0u;
+  if (n > 0) {
+    uint32_t prefix = 0u, pmask = 0u;
+    int rank = n;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      hist[lane] = hist[lane + 64] = hist[lane + 128] = hist[lane + 192] = 0;
+      __syncthreads();
+      for (int i = lane; i < n_cand; i += 64) {
+        const uint32_t kv = key[i];
+        if ((kv & pmask) == prefix) atomicAdd(&hist[(kv >> shift) & 255u], 1);
+      }
+      __syncthreads();
+      // lane l owns bins 4l..4l+3; above = matching keys in bins > 4l+3
+      const int h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2], h3 = hist[4 * lane + 3];
+      const int own = h0 + h1 + h2 + h3;
+      int incl = own;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += y;
+      }
+      const int total = __shfl(incl, 63, 64);
+      int above = total - incl;
+      const int hv[4] = {h0, h1, h2, h3};
+#pragma unroll
+      for (int t = 3; t >= 0; --t) {
+        if (above < rank && above + hv[t] >= rank) {
+          pick[0] = 4 * lane + t;
+          pick[1] = rank - above;
+        }
+        above += hv[t];
+      }
+      __syncthreads();
+      prefix |= (uint32_t)pick[0] << shift;
+      pmask |= 255u << shift;
+      rank = pick[1];
+      __syncthreads();
+    }
+    thr = prefix;
   }
   int ngt = 0;
   for (int i = lane; i < n_cand; i += 64) ngt += key[i] > thr ? 1 : 0;
