@@ -27,18 +27,15 @@
 // registers for the codes, and stages fp32 copies in LDS for the per-dim column pass.
 // k_ms_map_wave (nk <= 1024): one wave per (q-block, batch*head) row, four rows per
 // workgroup; details at the kernel.
-// k_ms_map (nk > 1024): one 256-thread workgroup per row: the same value sort in LDS,
-// one lane's CDF chain, and the tie rank by a workgroup scan.
+// k_ms_map_long (nk > 1024): one 256-thread workgroup per row: the same value sort with
+// the keys in registers (cross-wave stages through LDS), one lane's CDF chain, and the
+// tie rank by a workgroup scan.
 #include "common.h"
 
 namespace {
 
 constexpr int MS_LD = 68;          // LDS row stride (floats) of the staged block: 16-byte rows, offset banks
-constexpr int MS_MAX_NK = 6144;
-// bytes of k_ms_map's key / score-tile region: np2 keys or one 64 x 65-float tile
-__host__ __device__ constexpr size_t ms_map_key_bytes(int np2) {
-  return (size_t)np2 * 4 > 64 * 65 * 4 ? (size_t)np2 * 4 : 64 * 65 * 4;
-}    // key blocks per row the map kernel sorts in LDS (<= 32 KiB keys + 24 KiB p)
+constexpr int MS_MAX_NK = 6144;    // key blocks per row of the map kernels (<= 32 KiB keys + 24 KiB p in LDS)
 
 template <int BS>
 __global__ __launch_bounds__(256) void k_ms_stats(const uint16_t* __restrict__ x, Strides sx, int T,
@@ -148,76 +145,72 @@ __global__ __launch_bounds__(256) void k_ms_stats(const uint16_t* __restrict__ x
   }
 }
 
-template <int NP2>
-__global__ __launch_bounds__(256) void k_ms_map(const float* __restrict__ pooled_q, const float* __restrict__ pooled_k,
-                                                const uint8_t* __restrict__ sim_q, const uint8_t* __restrict__ sim_k,
-                                                int H, int nq, int nk, const float* __restrict__ cdfth, int n_sink,
-                                                uint8_t* __restrict__ map) {
-  constexpr int np2 = NP2, PAIRS = NP2 / 512;  // compare-exchanges per thread per stage
+// One 256-thread workgroup per (head, q-block) row for nk > 1024, E keys per lane
+// (NP2 = 256E sort positions):
+//  scores  wave w scores columns c = 256i + 64w + lane, each lane reading its column's
+//          pooled K (64 floats) straight from L2 (DOT64 chain, pooled Q in registers).
+//  sort    lane (w, lane) holds sort positions i = 64Ew + 64e + lane in registers; a
+//          bitonic network over i: partners 64 positions or more apart and in the same
+//          wave are another register of the lane, closer ones one shuffle away, and only
+//          the 3 stages whose partner is in another wave go through LDS.
+//  prefix  the sequential CDF chain over the sorted values in one lane, as in k_ms_map_wave.
+//  select  contiguous column chunks per thread and a workgroup scan for the tie rank.
+template <int E>
+__global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ pooled_q,
+                                                     const float* __restrict__ pooled_k,
+                                                     const uint8_t* __restrict__ sim_q,
+                                                     const uint8_t* __restrict__ sim_k, int H, int nq, int nk,
+                                                     const float* __restrict__ cdfth, int n_sink,
+                                                     uint8_t* __restrict__ map) {
+  constexpr int NW = 64 * E, NP2 = 4 * NW;
   extern __shared__ __align__(16) unsigned char ms_dyn[];
-  // u [np2]: ascending sort keys ~bits(p) (descending p; padding ~0 sorts last); before
-  // the sort the same space holds the 64 x 65-float pooled-K tiles of the score pass.
-  // p [nk]: scores -> exponentials -> probabilities, in column order.
-  uint32_t* u = reinterpret_cast<uint32_t*>(ms_dyn);
-  float* tile = reinterpret_cast<float*>(ms_dyn);
-  float* p = reinterpret_cast<float*>(ms_dyn + ms_map_key_bytes(np2));
-  __shared__ __align__(16) float pq[64];
+  uint32_t* kx = reinterpret_cast<uint32_t*>(ms_dyn);      // [NP2] exchange, then the sorted keys
+  float* p = reinterpret_cast<float*>(ms_dyn + NP2 * 4);  // [nk] scores -> p, column order
   __shared__ float red[4];
   __shared__ int ired[4];
   __shared__ int n_sel;
   const int r = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   uint8_t* row = map + ((long long)bh * nq + r) * nk;
   const uint8_t* sk = sim_k + (long long)bh * nk;
-
   if (!sim_q[(long long)bh * nq + r]) {  // a non-similar query block attends to every key block
     for (int c = tid; c < nk; c += 256) row[c] = 1;
     return;
   }
-  if (tid < 64) pq[tid] = pooled_q[((long long)bh * nq + r) * 64 + tid];
-  __syncthreads();
-
-  // scores: 64-block tiles of pooled K loaded coalesced into LDS (row stride 65), one
-  // column per thread of wave 0; tile t+1 is loaded into registers while tile t is used
-  float mx = -__builtin_huge_valf();
+  float pq[64];
+  {
+    const float4* q4 = reinterpret_cast<const float4*>(pooled_q + ((long long)bh * nq + r) * 64);
+#pragma unroll
+    for (int d4 = 0; d4 < 16; ++d4) {
+      const float4 x = q4[d4];
+      pq[4 * d4] = x.x;
+      pq[4 * d4 + 1] = x.y;
+      pq[4 * d4 + 2] = x.z;
+      pq[4 * d4 + 3] = x.w;
+    }
+  }
   const float* pkh = pooled_k + (long long)bh * nk * 64;
-  float4 nxt[4];
-  auto load_tile = [&](int c0) {
-    const int cols = min(64, nk - c0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int f4 = tid + 256 * i, col = f4 >> 4;
-      nxt[i] = col < cols ? reinterpret_cast<const float4*>(pkh + (long long)(c0 + col) * 64)[f4 & 15]
-                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
-  };
-  load_tile(0);
-  for (int c0 = 0; c0 < nk; c0 += 64) {
-    const int cols = min(64, nk - c0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int f4 = tid + 256 * i;
-      float* dst = tile + (f4 >> 4) * 65 + (f4 & 15) * 4;
-      dst[0] = nxt[i].x;
-      dst[1] = nxt[i].y;
-      dst[2] = nxt[i].z;
-      dst[3] = nxt[i].w;
-    }
-    __syncthreads();
-    if (c0 + 64 < nk) load_tile(c0 + 64);
-    if (tid < cols) {
-      const int c = c0 + tid;
+  float mx = -__builtin_huge_valf();
+  for (int c = 64 * w + lane; c - lane < nk; c += 256) {
+    if (c < nk) {
       float s = -__builtin_huge_valf();
       if (sk[c]) {
-        const float* kc = tile + tid * 65;
+        const float4* kc = reinterpret_cast<const float4*>(pkh + (long long)c * 64);
+        float4 kv[16];
+#pragma unroll
+        for (int d4 = 0; d4 < 16; ++d4) kv[d4] = kc[d4];
         float a = 0.0f;
 #pragma unroll
-        for (int d = 0; d < 64; ++d) a = fmaf(pq[d], kc[d], a);
+        for (int d4 = 0; d4 < 16; ++d4) {
+          a = fmaf(pq[4 * d4], kv[d4].x, a);
+          a = fmaf(pq[4 * d4 + 1], kv[d4].y, a);
+          a = fmaf(pq[4 * d4 + 2], kv[d4].z, a);
+          a = fmaf(pq[4 * d4 + 3], kv[d4].w, a);
+        }
         s = a * 0.125f;
         mx = fmaxf(mx, s);
       }
       p[c] = s;
     }
-    __syncthreads();
   }
   mx = wave_max(mx);
   if (lane == 0) red[w] = mx;
@@ -240,29 +233,56 @@ __global__ __launch_bounds__(256) void k_ms_map(const float* __restrict__ pooled
   for (int c = tid; c < nk; c += 256) p[c] = p[c] / tot;
   __syncthreads();
   // every p is >= +0, so its bit pattern orders like the value; only the values are
-  // sorted (equal values are interchangeable in the prefix sums)
-  for (int c = tid; c < np2; c += 256) u[c] = c < nk ? ~__float_as_uint(p[c]) : ~0u;
-  __syncthreads();
-  for (int k = 2; k <= np2; k <<= 1) {  // bitonic sort, ascending
+  // sorted (equal values are interchangeable in the prefix sums). Ascending keys ~bits(p):
+  // descending p, padding (~0) last.
+  uint32_t u[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = NW * w + 64 * e + lane;
+    u[e] = i < nk ? ~__float_as_uint(p[i]) : ~0u;
+  }
+#pragma unroll
+  for (int k = 2; k <= NP2; k <<= 1) {
+#pragma unroll
     for (int j = k >> 1; j > 0; j >>= 1) {
-      // all of a thread's reads go out before its writes (one LDS round trip per stage)
-      uint32_t x[PAIRS], y[PAIRS];
+      if (j >= NW) {  // partner in another wave: exchange through LDS
 #pragma unroll
-      for (int q = 0; q < PAIRS; ++q) {
-        const int t = tid + 256 * q, i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
-        x[q] = u[i];
-        y[q] = u[i + j];
-      }
+        for (int e = 0; e < E; ++e) kx[NW * w + 64 * e + lane] = u[e];
+        __syncthreads();
 #pragma unroll
-      for (int q = 0; q < PAIRS; ++q) {
-        const int t = tid + 256 * q, i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
-        const bool asc = (i & k) == 0;
-        u[i] = asc ? min(x[q], y[q]) : max(x[q], y[q]);
-        u[i + j] = asc ? max(x[q], y[q]) : min(x[q], y[q]);
+        for (int e = 0; e < E; ++e) {
+          const int i = NW * w + 64 * e + lane;
+          const uint32_t b = kx[i ^ j];
+          const bool asc = (i & k) == 0, lower = (i & j) == 0;
+          u[e] = (lower == asc) ? min(u[e], b) : max(u[e], b);
+        }
+        __syncthreads();  // every wave has read before the next exchange overwrites
+      } else if (j >= 64) {  // partner in another register of this lane
+        const int ej = j >> 6;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          if (e & ej) continue;
+          const uint32_t a = u[e], b = u[e | ej];
+          const bool asc = ((NW * w + 64 * e) & k) == 0;
+          u[e] = asc ? min(a, b) : max(a, b);
+          u[e | ej] = asc ? max(a, b) : min(a, b);
+        }
+      } else {  // partner lane ^ j of this register
+        const bool lower = (lane & j) == 0;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const int i = NW * w + 64 * e + lane;
+          const bool asc = (i & k) == 0;
+          const uint32_t a = u[e];
+          const uint32_t b = (uint32_t)__shfl_xor((int)a, j, 64);
+          u[e] = (lower == asc) ? min(a, b) : max(a, b);
+        }
       }
-      __syncthreads();
     }
   }
+#pragma unroll
+  for (int e = 0; e < E; ++e) kx[NW * w + 64 * e + lane] = u[e];
+  __syncthreads();
   if (tid == 0) {  // n = #{sequential prefix sums of the sorted p that are <= th}
     const float th = cdfth[bh % H];
     float cum = 0.0f;
@@ -270,7 +290,7 @@ __global__ __launch_bounds__(256) void k_ms_map(const float* __restrict__ pooled
     for (int i = 0; i < nk; i += 16) {  // 16 keys per LDS round trip; the sums only grow
       uint4 x[4];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) x[g] = reinterpret_cast<const uint4*>(u + i)[g];  // i + 16 <= np2
+      for (int g = 0; g < 4; ++g) x[g] = reinterpret_cast<const uint4*>(kx + i)[g];  // i + 16 <= NP2
       const uint32_t* xv = reinterpret_cast<const uint32_t*>(x);
 #pragma unroll
       for (int m = 0; m < 16; ++m) {
@@ -283,7 +303,7 @@ __global__ __launch_bounds__(256) void k_ms_map(const float* __restrict__ pooled
   }
   __syncthreads();
   const int n = n_sel;
-  const uint32_t vbits = n > 0 ? ~u[n - 1] : 0u;  // the n-th largest p
+  const uint32_t vbits = n > 0 ? ~kx[n - 1] : 0u;  // the n-th largest p
   // contiguous column chunks: p > v is kept; of the p == v columns, the lowest-indexed
   // n - #{p > v} (an exclusive scan of the per-chunk counts gives each one's rank)
   const int chunk = cdiv(nk, 256), c0 = min(nk, tid * chunk), c1 = min(nk, c0 + chunk);
@@ -590,14 +610,14 @@ RESS_API int ress_meansim_block_map(const void* q, const void* k, const void* km
   } else {
     const size_t lds4 = (size_t)nk * 4;
     if (nk <= 2048)
-      hipLaunchKernelGGL(k_ms_map<2048>, dim3(nq, BH), dim3(256), ms_map_key_bytes(2048) + lds4, stream, pq, pk, sq8,
-                         sk8, H, nq, nk, cd, n_sink, m8);
+      hipLaunchKernelGGL(k_ms_map_long<8>, dim3(nq, BH), dim3(256), 2048 * 4 + lds4, stream, pq, pk, sq8, sk8, H, nq,
+                         nk, cd, n_sink, m8);
     else if (nk <= 4096)
-      hipLaunchKernelGGL(k_ms_map<4096>, dim3(nq, BH), dim3(256), ms_map_key_bytes(4096) + lds4, stream, pq, pk, sq8,
-                         sk8, H, nq, nk, cd, n_sink, m8);
+      hipLaunchKernelGGL(k_ms_map_long<16>, dim3(nq, BH), dim3(256), 4096 * 4 + lds4, stream, pq, pk, sq8, sk8, H, nq,
+                         nk, cd, n_sink, m8);
     else
-      hipLaunchKernelGGL(k_ms_map<8192>, dim3(nq, BH), dim3(256), ms_map_key_bytes(8192) + lds4, stream, pq, pk, sq8,
-                         sk8, H, nq, nk, cd, n_sink, m8);
+      hipLaunchKernelGGL(k_ms_map_long<32>, dim3(nq, BH), dim3(256), 8192 * 4 + lds4, stream, pq, pk, sq8, sk8, H, nq,
+                         nk, cd, n_sink, m8);
   }
   RESS_LAUNCHED("k_ms_map");
   return 0;
