@@ -36,6 +36,11 @@ namespace {
 
 constexpr int MS_LD = 68;          // LDS row stride (floats) of the staged block: 16-byte rows, offset banks
 constexpr int MS_MAX_NK = 6144;    // key blocks per row of the map kernels (<= 32 KiB keys + 24 KiB p in LDS)
+constexpr int MS_CH_LD = 17;       // k_ms_map_long score chunks: 64 columns x 16 dims, odd row stride
+// front LDS region of k_ms_map_long: the NP2 sort keys, or the four waves' score chunks
+__host__ __device__ constexpr size_t ms_long_front_bytes(int np2) {
+  return (size_t)np2 * 4 > 4 * 64 * MS_CH_LD * 4 ? (size_t)np2 * 4 : 4 * 64 * MS_CH_LD * 4;
+}
 
 template <int BS>
 __global__ __launch_bounds__(256) void k_ms_stats(const uint16_t* __restrict__ x, Strides sx, int T,
@@ -145,6 +150,74 @@ __global__ __launch_bounds__(256) void k_ms_stats(const uint16_t* __restrict__ x
   }
 }
 
+// Bitonic network of k_ms_map_long over sort positions i = 64E*w + 64e + lane (lane
+// (w, lane) holds u[e]), stages as compile-time (K, J) so every register index is static:
+// J >= 64E pairs positions of two waves (through LDS), 64 <= J < 64E two registers of a
+// lane, J < 64 two lanes (shuffle).
+// the value of lane ^ J (J < 64): DPP quad permutes for 1 and 2, a bit-mode ds_swizzle
+// (source lane ((l & 31) ^ J) within each 32-lane half) for 4..16, the half swap for 32
+template <int J>
+__device__ __forceinline__ uint32_t ms_xor_lane(uint32_t a, int lane) {
+  if constexpr (J == 1) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)a, 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
+  } else if constexpr (J == 2) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)a, 0x4E, 0xF, 0xF, false);  // quad_perm 2,3,0,1
+  } else if constexpr (J < 32) {
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)a, 0x1F | (J << 10));
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(a, a, false, false);  // {lo,lo}, {hi,hi}
+    return lane < 32 ? (uint32_t)r[1] : (uint32_t)r[0];
+  }
+}
+
+template <int E, int K, int J>
+__device__ __forceinline__ void ms_bstage(uint32_t (&u)[E], uint32_t* kx, int w, int lane) {
+  constexpr int NW = 64 * E;
+  if constexpr (J >= NW) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) kx[NW * w + 64 * e + lane] = u[e];
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int i = NW * w + 64 * e + lane;
+      const uint32_t b = kx[i ^ J];
+      const bool asc = (i & K) == 0, lower = (i & J) == 0;
+      u[e] = (lower == asc) ? min(u[e], b) : max(u[e], b);
+    }
+    __syncthreads();  // every wave has read before the next exchange overwrites
+  } else if constexpr (J >= 64) {
+    constexpr int EJ = J / 64;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      if (e & EJ) continue;
+      const uint32_t a = u[e], b = u[e | EJ];
+      const bool asc = ((NW * w + 64 * e) & K) == 0;
+      u[e] = asc ? min(a, b) : max(a, b);
+      u[e | EJ] = asc ? max(a, b) : min(a, b);
+    }
+  } else {
+    const bool lower = (lane & J) == 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int i = NW * w + 64 * e + lane;
+      const bool asc = (i & K) == 0;
+      const uint32_t a = u[e];
+      const uint32_t b = ms_xor_lane<J>(a, lane);
+      u[e] = (lower == asc) ? min(a, b) : max(a, b);
+    }
+  }
+}
+template <int E, int K, int J>
+__device__ __forceinline__ void ms_bmerge(uint32_t (&u)[E], uint32_t* kx, int w, int lane) {
+  ms_bstage<E, K, J>(u, kx, w, lane);
+  if constexpr (J > 1) ms_bmerge<E, K, J / 2>(u, kx, w, lane);
+}
+template <int E, int K>
+__device__ __forceinline__ void ms_bsort(uint32_t (&u)[E], uint32_t* kx, int w, int lane) {
+  ms_bmerge<E, K, K / 2>(u, kx, w, lane);
+  if constexpr (K < 256 * E) ms_bsort<E, K * 2>(u, kx, w, lane);
+}
+
 // One 256-thread workgroup per (head, q-block) row for nk > 1024, E keys per lane
 // (NP2 = 256E sort positions):
 //  scores  wave w scores columns c = 256i + 64w + lane, each lane reading its column's
@@ -164,8 +237,10 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
                                                      uint8_t* __restrict__ map) {
   constexpr int NW = 64 * E, NP2 = 4 * NW;
   extern __shared__ __align__(16) unsigned char ms_dyn[];
-  uint32_t* kx = reinterpret_cast<uint32_t*>(ms_dyn);      // [NP2] exchange, then the sorted keys
-  float* p = reinterpret_cast<float*>(ms_dyn + NP2 * 4);  // [nk] scores -> p, column order
+  // front region (ms_long_front_bytes): the waves' score chunks, later the sort exchange
+  uint32_t* kx = reinterpret_cast<uint32_t*>(ms_dyn);  // [NP2] exchange, then the sorted keys
+  float* scw = reinterpret_cast<float*>(ms_dyn) + (threadIdx.x >> 6) * (64 * MS_CH_LD);  // [64][MS_CH_LD]
+  float* p = reinterpret_cast<float*>(ms_dyn + ms_long_front_bytes(NP2));  // [nk] scores -> p, column order
   __shared__ float red[4];
   __shared__ int ired[4];
   __shared__ int n_sel;
@@ -190,22 +265,44 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
   }
   const float* pkh = pooled_k + (long long)bh * nk * 64;
   float mx = -__builtin_huge_valf();
-  for (int c = 64 * w + lane; c - lane < nk; c += 256) {
+  // wave w scores columns c0..c0+63 (c0 = 256i + 64w), lane = column: the columns' pooled
+  // K goes through the wave's LDS chunk 16 dims at a time (coalesced loads, the next
+  // chunk in flight while one is used), and the DOT64 chain runs over d = 0..63 in order
+  for (int c0 = 64 * w; c0 < nk; c0 += 256) {
+    const int c = c0 + lane;
+    const bool live = c < nk && sk[c];
+    float4 ld[4];
+    auto load_chunk = [&](int q) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int f = 64 * t + lane, col = c0 + (f >> 2);
+        ld[t] = col < nk ? *reinterpret_cast<const float4*>(pkh + (long long)col * 64 + 16 * q + 4 * (f & 3))
+                         : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+    };
+    load_chunk(0);
+    float a = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int f = 64 * t + lane;
+        float* dst = scw + (f >> 2) * MS_CH_LD + 4 * (f & 3);
+        dst[0] = ld[t].x;
+        dst[1] = ld[t].y;
+        dst[2] = ld[t].z;
+        dst[3] = ld[t].w;
+      }
+      __builtin_amdgcn_wave_barrier();
+      if (q + 1 < 4) load_chunk(q + 1);
+      const float* kc = scw + lane * MS_CH_LD;
+#pragma unroll
+      for (int d = 0; d < 16; ++d) a = fmaf(pq[16 * q + d], kc[d], a);
+      __builtin_amdgcn_wave_barrier();  // every lane has read the chunk before it is overwritten
+    }
     if (c < nk) {
       float s = -__builtin_huge_valf();
-      if (sk[c]) {
-        const float4* kc = reinterpret_cast<const float4*>(pkh + (long long)c * 64);
-        float4 kv[16];
-#pragma unroll
-        for (int d4 = 0; d4 < 16; ++d4) kv[d4] = kc[d4];
-        float a = 0.0f;
-#pragma unroll
-        for (int d4 = 0; d4 < 16; ++d4) {
-          a = fmaf(pq[4 * d4], kv[d4].x, a);
-          a = fmaf(pq[4 * d4 + 1], kv[d4].y, a);
-          a = fmaf(pq[4 * d4 + 2], kv[d4].z, a);
-          a = fmaf(pq[4 * d4 + 3], kv[d4].w, a);
-        }
+      if (live) {
         s = a * 0.125f;
         mx = fmaxf(mx, s);
       }
@@ -241,63 +338,41 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
     const int i = NW * w + 64 * e + lane;
     u[e] = i < nk ? ~__float_as_uint(p[i]) : ~0u;
   }
-#pragma unroll
-  for (int k = 2; k <= NP2; k <<= 1) {
-#pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      if (j >= NW) {  // partner in another wave: exchange through LDS
-#pragma unroll
-        for (int e = 0; e < E; ++e) kx[NW * w + 64 * e + lane] = u[e];
-        __syncthreads();
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-          const int i = NW * w + 64 * e + lane;
-          const uint32_t b = kx[i ^ j];
-          const bool asc = (i & k) == 0, lower = (i & j) == 0;
-          u[e] = (lower == asc) ? min(u[e], b) : max(u[e], b);
-        }
-        __syncthreads();  // every wave has read before the next exchange overwrites
-      } else if (j >= 64) {  // partner in another register of this lane
-        const int ej = j >> 6;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-          if (e & ej) continue;
-          const uint32_t a = u[e], b = u[e | ej];
-          const bool asc = ((NW * w + 64 * e) & k) == 0;
-          u[e] = asc ? min(a, b) : max(a, b);
-          u[e | ej] = asc ? max(a, b) : min(a, b);
-        }
-      } else {  // partner lane ^ j of this register
-        const bool lower = (lane & j) == 0;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-          const int i = NW * w + 64 * e + lane;
-          const bool asc = (i & k) == 0;
-          const uint32_t a = u[e];
-          const uint32_t b = (uint32_t)__shfl_xor((int)a, j, 64);
-          u[e] = (lower == asc) ? min(a, b) : max(a, b);
-        }
-      }
-    }
-  }
+  ms_bsort<E, 2>(u, kx, w, lane);
 #pragma unroll
   for (int e = 0; e < E; ++e) kx[NW * w + 64 * e + lane] = u[e];
   __syncthreads();
   if (tid == 0) {  // n = #{sequential prefix sums of the sorted p that are <= th}
+    // p >= 0, so the sums only grow: n is the position of the first sum above th (nk if
+    // none). One add per key; the batch that crosses th is searched once; the next 16
+    // keys are read while a batch is summed. Keys past nk are p = 0 (padding).
     const float th = cdfth[bh % H];
     float cum = 0.0f;
-    int n = 0;
-    for (int i = 0; i < nk; i += 16) {  // 16 keys per LDS round trip; the sums only grow
-      uint4 x[4];
+    int n = nk;
+    uint4 x[4], y[4];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) x[g] = reinterpret_cast<const uint4*>(kx + i)[g];  // i + 16 <= NP2
+    for (int g = 0; g < 4; ++g) x[g] = reinterpret_cast<const uint4*>(kx)[g];  // 16 <= NP2
+    for (int i = 0; i < nk; i += 16) {
+      if (i + 16 < nk) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) y[g] = reinterpret_cast<const uint4*>(kx + i + 16)[g];  // i + 32 <= NP2
+      }
       const uint32_t* xv = reinterpret_cast<const uint32_t*>(x);
+      float cv[16];
 #pragma unroll
       for (int m = 0; m < 16; ++m) {
         cum = cum + __uint_as_float(~xv[m]);
-        n += (i + m < nk && cum <= th) ? 1 : 0;
+        cv[m] = cum;
       }
-      if (!(cum <= th)) break;
+      if (!(cum <= th)) {
+        int first = 15;
+#pragma unroll
+        for (int m = 14; m >= 0; --m) first = cv[m] <= th ? first : m;
+        n = min(nk, i + first);
+        break;
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g) x[g] = y[g];
     }
     n_sel = n;
   }
@@ -610,13 +685,13 @@ RESS_API int ress_meansim_block_map(const void* q, const void* k, const void* km
   } else {
     const size_t lds4 = (size_t)nk * 4;
     if (nk <= 2048)
-      hipLaunchKernelGGL(k_ms_map_long<8>, dim3(nq, BH), dim3(256), 2048 * 4 + lds4, stream, pq, pk, sq8, sk8, H, nq,
+      hipLaunchKernelGGL(k_ms_map_long<8>, dim3(nq, BH), dim3(256), ms_long_front_bytes(2048) + lds4, stream, pq, pk, sq8, sk8, H, nq,
                          nk, cd, n_sink, m8);
     else if (nk <= 4096)
-      hipLaunchKernelGGL(k_ms_map_long<16>, dim3(nq, BH), dim3(256), 4096 * 4 + lds4, stream, pq, pk, sq8, sk8, H, nq,
+      hipLaunchKernelGGL(k_ms_map_long<16>, dim3(nq, BH), dim3(256), ms_long_front_bytes(4096) + lds4, stream, pq, pk, sq8, sk8, H, nq,
                          nk, cd, n_sink, m8);
     else
-      hipLaunchKernelGGL(k_ms_map_long<32>, dim3(nq, BH), dim3(256), 8192 * 4 + lds4, stream, pq, pk, sq8, sk8, H, nq,
+      hipLaunchKernelGGL(k_ms_map_long<32>, dim3(nq, BH), dim3(256), ms_long_front_bytes(8192) + lds4, stream, pq, pk, sq8, sk8, H, nq,
                          nk, cd, n_sink, m8);
   }
   RESS_LAUNCHED("k_ms_map");
