@@ -340,29 +340,40 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
   }
   ms_bsort<E, 2>(u, kx, w, lane);
 #pragma unroll
-  for (int e = 0; e < E; ++e) kx[NW * w + 64 * e + lane] = u[e];
+  for (int e = 0; e < E; ++e) kx[NW * w + 64 * e + lane] = ~u[e];  // the sorted p (descending), as bits
   __syncthreads();
   if (tid == 0) {  // n = #{sequential prefix sums of the sorted p that are <= th}
     // p >= 0, so the sums only grow: n is the position of the first sum above th (nk if
     // none). One add per key; the batch that crosses th is searched once; the next 16
     // keys are read while a batch is summed. Keys past nk are p = 0 (padding).
     const float th = cdfth[bh % H];
+    const float4* v4 = reinterpret_cast<const float4*>(kx);
     float cum = 0.0f;
     int n = nk;
-    uint4 x[4], y[4];
+    // 16 values a batch, the next two batches' reads in flight (v4[4b .. 4b+3] is batch b;
+    // batches up to NP2/16 exist, NP2 >= 2048)
+    float4 x[4], y[4], z[4];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) x[g] = reinterpret_cast<const uint4*>(kx)[g];  // 16 <= NP2
+    for (int g = 0; g < 4; ++g) {
+      x[g] = v4[g];
+      y[g] = v4[4 + g];
+    }
     for (int i = 0; i < nk; i += 16) {
-      if (i + 16 < nk) {
+      if (i + 32 < nk) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) y[g] = reinterpret_cast<const uint4*>(kx + i + 16)[g];  // i + 32 <= NP2
+        for (int g = 0; g < 4; ++g) z[g] = v4[(i + 32) / 4 + g];  // i + 48 <= NP2
       }
-      const uint32_t* xv = reinterpret_cast<const uint32_t*>(x);
       float cv[16];
 #pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        cum = cum + __uint_as_float(~xv[m]);
-        cv[m] = cum;
+      for (int g = 0; g < 4; ++g) {
+        cum = cum + x[g].x;
+        cv[4 * g] = cum;
+        cum = cum + x[g].y;
+        cv[4 * g + 1] = cum;
+        cum = cum + x[g].z;
+        cv[4 * g + 2] = cum;
+        cum = cum + x[g].w;
+        cv[4 * g + 3] = cum;
       }
       if (!(cum <= th)) {
         int first = 15;
@@ -372,13 +383,16 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
         break;
       }
 #pragma unroll
-      for (int g = 0; g < 4; ++g) x[g] = y[g];
+      for (int g = 0; g < 4; ++g) {
+        x[g] = y[g];
+        y[g] = z[g];
+      }
     }
     n_sel = n;
   }
   __syncthreads();
   const int n = n_sel;
-  const uint32_t vbits = n > 0 ? ~kx[n - 1] : 0u;  // the n-th largest p
+  const uint32_t vbits = n > 0 ? kx[n - 1] : 0u;  // the n-th largest p
   // contiguous column chunks: p > v is kept; of the p == v columns, the lowest-indexed
   // n - #{p > v} (an exclusive scan of the per-chunk counts gives each one's rank)
   const int chunk = cdiv(nk, 256), c0 = min(nk, tid * chunk), c1 = min(nk, c0 + chunk);
