@@ -15,7 +15,9 @@ times). roofline = the attention kernel's retained-block FLOPs over
 its own HIP-event-timed duration against the dense MFMA peak of its arithmetic (QK^T
 half at the bf16 or INT8 rate, PV half at the bf16 rate); frac_of_int8_peak prices the
 same FLOPs against the INT8 peak, frac_of_measured_peak against the rates measured on
-this GPU (measured_peaks: MFMA microbenchmark, 1 GiB copy).
+this GPU (measured_peaks: MFMA microbenchmark, 1 GiB copy). traffic (HBM bytes per
+launch) and mfma_busy_pct_pmc (matrix-core busy cycles over active SIMD cycles) are read
+from the committed rocprofv3 PMC summaries in profiles/ (configs[1] only).
 """
 
 import argparse
@@ -97,21 +99,33 @@ def parse():
     return ap.parse_args()
 
 
+def _profile_value(name, key):
+    """The number on the `key:` line of profiles/<name>, or None."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith(key + ":"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        return None
+    return None
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel`, from the committed PMC summary (profiles/), or None.
 
     The summary holds FETCH_SIZE and WRITE_SIZE per dispatch, each divided by what the
     same counter read for a plain copy of known size; its 'traffic_bytes_per_launch'
     line is the sum."""
-    path = os.path.join(ROOT, "profiles", f"{kernel}_config1_pmc_traffic.txt")
-    try:
-        with open(path) as f:
-            for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return float(line.split(":", 1)[1])
-    except OSError:
-        return None
-    return None
+    return _profile_value(f"{kernel}_config1_pmc_traffic.txt", "traffic_bytes_per_launch")
+
+
+def measured_mfma_busy(kernel):
+    """Percent of SIMD cycles the matrix cores were busy during `kernel` (rocprofv3's
+    MfmaUtil: SQ_VALU_MFMA_BUSY_CYCLES over the active cycles of every SIMD), from the
+    committed PMC summary, or None."""
+    return _profile_value(f"{kernel}_config1_pmc_mfma.txt", "mfma_busy_pct_per_launch")
 
 
 def retained_flops(nvalid, lut, grid):
@@ -394,6 +408,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": round(peak, 1), "unit": "TFLOP/s",
                      "frac": round(achieved / peak, 4),
                      "traffic": measured_traffic(f"k_sparse_attn_{args.qk_mode}") if args.config == 1 else None,
+                     "mfma_busy_pct_pmc": measured_mfma_busy(f"k_sparse_attn_{args.qk_mode}") if args.config == 1 else None,
                      "frac_of_int8_peak": round(achieved / PEAK_INT8_TOPS, 4),
                      "measured_peak": round(peak_meas, 1), "frac_of_measured_peak": round(achieved / peak_meas, 4),
                      "kernel": "k_sparse_attn", "kernel_ms": round(attn_ms, 4),
