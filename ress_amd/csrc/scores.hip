@@ -12,12 +12,13 @@
 // wave per row; pooled K goes through LDS in coalesced 64-block tiles that the four rows
 // share (tile t+1 is loaded into registers while tile t is used), and lane l owns the
 // columns kb = 64t + l, which is also the SUM64 partial order. k_pooled_scores: one wave
-// per row reading pooled K directly, for longer rows.
+// per row for longer rows, pooled K staged through a small LDS chunk per 64 columns.
 #include "common.h"
 
 namespace {
 constexpr int PS_TILED_MAX = 2048;
 constexpr int PS_LDK = 65;  // tile row stride (floats): conflict-free column reads
+constexpr int PS_CH_LD = 17;  // k_pooled_scores chunk row stride (floats)
 
 __global__ __launch_bounds__(256) void k_pooled_scores_tiled(const float* __restrict__ pooled_q,
                                                              const float* __restrict__ pooled_k, int q_blk,
@@ -109,25 +110,52 @@ __global__ __launch_bounds__(64) void k_pooled_scores(const float* __restrict__ 
                                                       float* __restrict__ attn_cond) {
   extern __shared__ float e[];  // kb_p floats
   __shared__ float pq[64];
+  __shared__ float chunk[64 * PS_CH_LD];  // 64 columns x 16 dims of pooled K
   const int qb = blockIdx.x, bh = blockIdx.y, lane = threadIdx.x;
   pq[lane] = pooled_q[((long long)bh * q_blk + qb) * 64 + lane];
   __syncthreads();
-  const float4* pk = reinterpret_cast<const float4*>(pooled_k + (long long)bh * kb_p * 64);
+  const float* pkh = pooled_k + (long long)bh * kb_p * 64;
 
+  // 64 columns per step (lane = column): their pooled K goes through LDS 16 dims at a
+  // time with coalesced loads (the next chunk in flight while one is used); the DOT64
+  // chain runs over d = 0..63 in order
   float lmax = -__builtin_huge_valf();
-  for (int kb = lane; kb < kb_p; kb += 64) {
+  for (int c0 = 0; c0 < kb_p; c0 += 64) {
+    float4 ld[4];
+    auto load_chunk = [&](int q) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int f = 64 * t + lane, col = c0 + (f >> 2);
+        ld[t] = col < kb_p ? *reinterpret_cast<const float4*>(pkh + (long long)col * 64 + 16 * q + 4 * (f & 3))
+                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+    };
+    load_chunk(0);
     float acc = 0.0f;
 #pragma unroll
-    for (int d4 = 0; d4 < 16; ++d4) {
-      const float4 b = pk[kb * 16 + d4];
-      acc = fmaf(pq[4 * d4 + 0], b.x, acc);
-      acc = fmaf(pq[4 * d4 + 1], b.y, acc);
-      acc = fmaf(pq[4 * d4 + 2], b.z, acc);
-      acc = fmaf(pq[4 * d4 + 3], b.w, acc);
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int f = 64 * t + lane;
+        float* dst = chunk + (f >> 2) * PS_CH_LD + 4 * (f & 3);
+        dst[0] = ld[t].x;
+        dst[1] = ld[t].y;
+        dst[2] = ld[t].z;
+        dst[3] = ld[t].w;
+      }
+      __builtin_amdgcn_wave_barrier();
+      if (q + 1 < 4) load_chunk(q + 1);
+      const float* kc = chunk + lane * PS_CH_LD;
+#pragma unroll
+      for (int d = 0; d < 16; ++d) acc = fmaf(pq[16 * q + d], kc[d], acc);
+      __builtin_amdgcn_wave_barrier();  // every lane has read the chunk before it is overwritten
     }
-    const float s = acc * scale;
-    e[kb] = s;
-    lmax = fmaxf(lmax, s);
+    const int kb = c0 + lane;
+    if (kb < kb_p) {
+      const float s = acc * scale;
+      e[kb] = s;
+      lmax = fmaxf(lmax, s);
+    }
   }
   const float m = wave_max(lmax);
   float part = 0.0f;
