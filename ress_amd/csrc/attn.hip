@@ -542,7 +542,9 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
   const long long row = (long long)bh * a.q_blk_total + qb;
   const int nv = kb_hi - kb_lo;
   const int* lut = lut_all + row * a.kb_tot + kb_lo;
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, qi = l & 31;
+  // the wave index is wave-uniform: held in an SGPR, the LDS-DMA destinations (m0) are
+  // scalar arithmetic
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, g = l >> 5, qi = l & 31;
   const bool special = qb >= a.q_blk_p;
   const int qbase = special ? (qb - a.q_blk_p) * 128 : qb * 128;
   const int cnt_q = min(128, (special ? a.m.T_s : a.m.T_p) - qbase);
@@ -583,27 +585,39 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
   // Stage loads are LDS-DMA: lane l of wave w fills 16-byte slots 64w+l (INT8 K hi, K lo)
   // or 128w+l, 128w+64+l (bf16 K, V), so it fetches the global chunk that the swizzle
   // places there (the XOR swizzles are their own inverse).
-  const int kslot = 64 * w + l;
-  const int ksrc = 16 * (4 * (kslot >> 2) + ((kslot & 3) ^ ((((kslot >> 2) >> 1) ^ ((kslot >> 2) >> 3)) & 3)));
-  const int vslot0 = 128 * w + l, vslot1 = vslot0 + 64;
-  const int vsrc0 = 16 * (8 * (vslot0 >> 3) + ((vslot0 & 7) ^ (((vslot0 >> 3) ^ (vslot0 >> 6)) & 7)));
-  const int vsrc1 = 16 * (8 * (vslot1 >> 3) + ((vslot1 & 7) ^ (((vslot1 >> 3) ^ (vslot1 >> 6)) & 7)));
+  // Byte offsets are unsigned 32-bit, so each DMA address is a uniform 64-bit block base
+  // plus a zero-extended lane offset (the SGPR-base form of the load, no 64-bit VALU add).
+  const unsigned kslot = 64 * w + l;
+  const unsigned ksrc = 16 * (4 * (kslot >> 2) + ((kslot & 3) ^ ((((kslot >> 2) >> 1) ^ ((kslot >> 2) >> 3)) & 3)));
+  const unsigned vslot0 = 128 * w + l, vslot1 = vslot0 + 64;
+  const unsigned vsrc0 = 16 * (8 * (vslot0 >> 3) + ((vslot0 & 7) ^ (((vslot0 >> 3) ^ (vslot0 >> 6)) & 7)));
+  const unsigned vsrc1 = 16 * (8 * (vslot1 >> 3) + ((vslot1 & 7) ^ (((vslot1 >> 3) ^ (vslot1 >> 6)) & 7)));
   const char* kblk0 = QK == QK_BF16 ? reinterpret_cast<const char*>(a.k_pack) + (long long)bh * a.kb_tot * 8192
                                     : reinterpret_cast<const char*>(a.k_i8) + (long long)bh * a.kb_tot * 4096;
   const char* klblk0 =
       QK == QK_I8X2 ? reinterpret_cast<const char*>(a.k_lo) + (long long)bh * a.kb_tot * 4096 : nullptr;
   const char* vblk0 = reinterpret_cast<const char*>(a.v_pack) + (long long)bh * a.kb_tot * 8192;
+  // The block bases pass through an empty asm so that they stay uniform SGPR values:
+  // otherwise the compiler hoists base + lane offset out of the loop as a 64-bit VGPR and
+  // adds the block offset with a VALU op per load.
+  auto uniform_base = [](const char* p) {
+    asm("" : "+s"(p));
+    return p;
+  };
   auto stage_load = [&](uint4* stage, int kb) {
     char* base = reinterpret_cast<char*>(stage);
+    const char* vb = uniform_base(vblk0 + (long long)kb * 8192);
     if constexpr (QK == QK_BF16) {
-      gl_lds16(kblk0 + (long long)kb * 8192 + vsrc0, base + 2048 * w);
-      gl_lds16(kblk0 + (long long)kb * 8192 + vsrc1, base + 2048 * w + 1024);
+      const char* kbp = uniform_base(kblk0 + (long long)kb * 8192);
+      gl_lds16(kbp + vsrc0, base + 2048 * w);
+      gl_lds16(kbp + vsrc1, base + 2048 * w + 1024);
     } else {
-      gl_lds16(kblk0 + (long long)kb * 4096 + ksrc, base + 1024 * w);
-      if constexpr (QK == QK_I8X2) gl_lds16(klblk0 + (long long)kb * 4096 + ksrc, base + 4096 + 1024 * w);
+      gl_lds16(uniform_base(kblk0 + (long long)kb * 4096) + ksrc, base + 1024 * w);
+      if constexpr (QK == QK_I8X2)
+        gl_lds16(uniform_base(klblk0 + (long long)kb * 4096) + ksrc, base + 4096 + 1024 * w);
     }
-    gl_lds16(vblk0 + (long long)kb * 8192 + vsrc0, base + 16 * KCH + 2048 * w);
-    gl_lds16(vblk0 + (long long)kb * 8192 + vsrc1, base + 16 * KCH + 2048 * w + 1024);
+    gl_lds16(vb + vsrc0, base + 16 * KCH + 2048 * w);
+    gl_lds16(vb + vsrc1, base + 16 * KCH + 2048 * w + 1024);
   };
   // LDS sources of this lane's K operands, per tile
   int ks0[4], ks1[4];
@@ -639,13 +653,13 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
     int kb4 = nv > 4 ? lut[4] : 0;
     auto step = [&](const uint4* cur, const uint4* nxt, uint4* ahead, int it) {
       const bool fetch = it + 3 < nv;
+      // the LUT entry of block it+5 is read first: its latency overlaps this step's first
+      // LDS operand reads instead of delaying the step-end barrier
+      const int kb5 = it + 5 < nv ? lut[it + 5] : 0;
       if (fetch) stage_load(ahead, kb3);
       v16f n0, n1;
       qk_block_bf16(nxt, ks0, ks1, qv, n0, n1);
       sv_block_bf16<false>(cur, KCH, 64, qs, a0, a1, g, qi, m_run, l_run, o0, o1);
-      // the LUT read is issued after the block's LDS reads, so their waits do not include it
-      __builtin_amdgcn_sched_barrier(0);
-      const int kb5 = it + 5 < nv ? lut[it + 5] : 0;
       kb3 = kb4;
       kb4 = kb5;
       a0 = n0;
