@@ -156,13 +156,15 @@ __device__ __forceinline__ uint32_t rs_top_m(const uint32_t (&key)[NPL], uint32_
 }
 
 // V of the head in LDS (VLDS, bf16 mode when it fits): bf16 pairs, word w of row k at
-// k*32 + (w ^ (k & 31)), so that both access patterns -- lanes over the 64 dims of one
-// key block, and lanes over consecutive key blocks at one dim pair -- hit 32 distinct
-// banks. Otherwise V is streamed from Vr (below).
+// k*33 + w (one pad word per row). Lanes over the 64 dims of one key block read 32
+// consecutive words, lanes over 32 consecutive key blocks at one dim pair hit 32 distinct
+// banks, and a batch of consecutive rows is one lane base plus immediate offsets (no
+// per-row address arithmetic). Otherwise V is streamed from Vr (below).
 #define RS_LDS_KBP 1024
-__device__ __forceinline__ uint32_t rs_vword(const uint32_t* vw, int k, int pair) {
-  return vw[k * 32 + (pair ^ (k & 31))];
-}
+#define RS_VROW 33
+// LDS words of the resident V, rounded up so that the per-wave scratch after it stays
+// 16-byte aligned
+__host__ __device__ __forceinline__ int rs_vw_words(int kb_p) { return (kb_p * RS_VROW + 3) & ~3; }
 
 // Streamed V (STREAM = !VLDS: rows whose V does not fit in LDS, or fp32 V): the workgroup's
 // waves run their rows in lockstep -- every row makes the same sequence of P.V chains and
@@ -195,7 +197,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
   extern __shared__ float sh[];
   float* M32T = sh;                 // [64][64] M^T (fp32)
   float* MbT = sh + 4096;           // [64][64] big(M)^T
-  uint32_t* vw = reinterpret_cast<uint32_t*>(sh + 8192);  // VLDS: [kb_p][32] bf16 pairs
+  uint32_t* vw = reinterpret_cast<uint32_t*>(sh + 8192);  // VLDS: [kb_p][RS_VROW] bf16 pairs
   // STREAM: the two V tile buffers (distinct objects, so the compiler can see that a
   // DMA into one never aliases reads of the other)
   __shared__ __align__(16) float4 tb0[STREAM ? 1024 : 1];
@@ -203,7 +205,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int kb4 = (a.kb_p + 3) & ~3;
   constexpr int OUTL = STREAM ? NPL * 64 : 0;  // STREAM: per-wave slots of the candidate products
-  float* wsh = sh + 8192 + (VLDS ? a.kb_p * 32 : 0) + w * (kb4 + 5 * 64 + OUTL);
+  float* wsh = sh + 8192 + (VLDS ? rs_vw_words(a.kb_p) : 0) + w * (kb4 + 5 * 64 + OUTL);
   float* Pw = wsh;                  // [kb_p] big(P) of the row, then P*drop (16-byte aligned)
   float* vqs = wsh + kb4;           // [64]
   float* t0 = vqs + 64;             // [64] scratch vectors; t0..t3 double as the
@@ -228,19 +230,16 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
       const int k = e >> 5, wd = e & 31;
       const uint32_t lo = __float_as_uint(Vr[(long long)k * 64 + 2 * wd]) >> 16;
       const uint32_t hi = __float_as_uint(Vr[(long long)k * 64 + 2 * wd + 1]) & 0xffff0000u;
-      vw[k * 32 + (wd ^ (k & 31))] = hi | lo;  // Vr holds bf16-exact values in this mode
+      vw[k * RS_VROW + wd] = hi | lo;  // Vr holds bf16-exact values in this mode
     }
   }
   __syncthreads();
-  const int vsh = (lane & 1) ? 0 : 16;  // this lane's dim in the upper half of its pair word
+  // VLDS: this lane's dim of a pair word as fp32 in one byte permute: the word's low half
+  // (even dim) or high half (odd dim) moved to the upper 16 bits, zeros below
+  const uint32_t vsel = (lane & 1) ? 0x03020c0cu : 0x01000c0cu;
+  auto vdim = [&](uint32_t word) -> float { return __uint_as_float(__builtin_amdgcn_perm(0u, word, vsel)); };
   // VLDS: V[k][lane] (lanes over dims)
-  auto vrow = [&](int k) -> float { return __uint_as_float((rs_vword(vw, k, lane >> 1) << vsh) & 0xffff0000u); };
-  // VLDS: (V[k][2p], V[k][2p+1]) (lanes over key blocks)
-  auto vpair = [&](int p, int k, float& v0, float& v1) {
-    const uint32_t word = rs_vword(vw, k, p);
-    v0 = __uint_as_float(word << 16);
-    v1 = __uint_as_float(word & 0xffff0000u);
-  };
+  auto vrow = [&](int k) -> float { return vdim(vw[k * RS_VROW + (lane >> 1)]); };
   // STREAM: tile t = V rows 64t..64t+63 (rows past kb_p repeat the last one; their
   // results are never used). Each wave DMAs four of the tile's sixteen 1 KiB slices.
   auto tile_dma = [&](float4* buf, int t) {
@@ -320,8 +319,9 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
     uint32_t wa[16];
     float4 pa[4];
     auto load16 = [&](int k, uint32_t(&wv)[16], float4(&pv)[4]) {
+      const uint32_t* vb = vw + k * RS_VROW + (lane >> 1);
 #pragma unroll
-      for (int u = 0; u < 16; ++u) wv[u] = rs_vword(vw, k + u, lane >> 1);
+      for (int u = 0; u < 16; ++u) wv[u] = vb[u * RS_VROW];
 #pragma unroll
       for (int u = 0; u < 4; ++u) pv[u] = *reinterpret_cast<const float4*>(Pw + k + 4 * u);
     };
@@ -329,13 +329,13 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         sp = sp + pv[u].x;
-        acc = fmaf(pv[u].x, __uint_as_float((wv[4 * u] << vsh) & 0xffff0000u), acc);
+        acc = fmaf(pv[u].x, vdim(wv[4 * u]), acc);
         sp = sp + pv[u].y;
-        acc = fmaf(pv[u].y, __uint_as_float((wv[4 * u + 1] << vsh) & 0xffff0000u), acc);
+        acc = fmaf(pv[u].y, vdim(wv[4 * u + 1]), acc);
         sp = sp + pv[u].z;
-        acc = fmaf(pv[u].z, __uint_as_float((wv[4 * u + 2] << vsh) & 0xffff0000u), acc);
+        acc = fmaf(pv[u].z, vdim(wv[4 * u + 2]), acc);
         sp = sp + pv[u].w;
-        acc = fmaf(pv[u].w, __uint_as_float((wv[4 * u + 3] << vsh) & 0xffff0000u), acc);
+        acc = fmaf(pv[u].w, vdim(wv[4 * u + 3]), acc);
       }
     };
     int k = 0;
@@ -373,33 +373,49 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
       for (int e = 0; e < NPL; ++e) out[e] = e < nel ? outl[e * 64 + lane] : 0.0f;
       return;
     }
-    // VLDS: the words of dim pair p+1 are read while pair p is accumulated (two register
-    // buffers), so the products wait on LDS once per pair at most
-    uint32_t wa[NPL], wb[NPL];
-    auto load_pair = [&](int p, uint32_t(&wv)[NPL]) {
+    // VLDS: NS = nel rounded up to a multiple of 4 slots is a compile-time count (one
+    // instance per value), so no slot carries a runtime guard. Slots below NS - 4 hold
+    // candidates lane + 64i < n_cand and read one lane base plus immediate offsets; the
+    // last four read rows clamped to n_cand - 1 (the products of slots >= nel are never
+    // used). The words of dim pair p+1 are read while pair p is accumulated (two register
+    // buffers), so the products wait on LDS once per pair at most.
+    auto products = [&](auto ns_tag) {
+      constexpr int NS = decltype(ns_tag)::value;
+      const uint32_t* vl = vw + lane * RS_VROW;
+      const uint32_t* vlast[4];
 #pragma unroll
-      for (int i = 0; i < NPL; ++i) {
-        if (i < nel) {
-          int k = lane + 64 * i;
-          k = k < n_cand ? k : n_cand - 1;
-          wv[i] = rs_vword(vw, k, p);
-        }
+      for (int j = 0; j < 4; ++j) vlast[j] = vw + min(lane + 64 * (NS - 4 + j), n_cand - 1) * RS_VROW;
+      uint32_t wa[NS], wb[NS];
+      auto load_pair = [&](int p, uint32_t(&wv)[NS]) {
+#pragma unroll
+        for (int i = 0; i < NS - 4; ++i) wv[i] = vl[64 * RS_VROW * i + p];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wv[NS - 4 + j] = vlast[j][p];
+      };
+      auto use_pair = [&](int p, const uint32_t(&wv)[NS]) {
+        const float m0 = vec[2 * p], m1 = vec[2 * p + 1];
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+          out[i] = fmaf(m1, __uint_as_float(wv[i] & 0xffff0000u), fmaf(m0, __uint_as_float(wv[i] << 16), out[i]));
+      };
+      load_pair(0, wa);
+      for (int p = 0; p < 32; p += 2) {
+        load_pair(p + 1, wb);
+        __builtin_amdgcn_sched_barrier(0);
+        use_pair(p, wa);
+        if (p + 2 < 32) load_pair(p + 2, wa);
+        __builtin_amdgcn_sched_barrier(0);
+        use_pair(p + 1, wb);
       }
     };
-    auto use_pair = [&](int p, const uint32_t(&wv)[NPL]) {
-      const float m0 = vec[2 * p], m1 = vec[2 * p + 1];
-#pragma unroll
-      for (int i = 0; i < NPL; ++i)
-        if (i < nel) out[i] = fmaf(m1, __uint_as_float(wv[i] & 0xffff0000u), fmaf(m0, __uint_as_float(wv[i] << 16), out[i]));
-    };
-    load_pair(0, wa);
-    for (int p = 0; p < 32; p += 2) {
-      load_pair(p + 1, wb);
-      __builtin_amdgcn_sched_barrier(0);
-      use_pair(p, wa);
-      if (p + 2 < 32) load_pair(p + 2, wa);
-      __builtin_amdgcn_sched_barrier(0);
-      use_pair(p + 1, wb);
+    const int ng = (nel + 3) >> 2;  // wave-uniform
+    if (ng <= 1) products(std::integral_constant<int, 4>{});
+    if constexpr (NPL >= 8) {
+      if (ng == 2) products(std::integral_constant<int, 8>{});
+    }
+    if constexpr (NPL >= 16) {
+      if (ng == 3) products(std::integral_constant<int, 12>{});
+      if (ng == 4) products(std::integral_constant<int, 16>{});
     }
   };
 
@@ -616,7 +632,7 @@ template <int NPL>
 static int launch_rs_npl(int BH, int kb_p, bool big, hipStream_t stream, const RsArgs& a) {
   const size_t scratch = ((size_t)((kb_p + 3) & ~3) + 5 * 64);
   if constexpr (NPL * 64 <= RS_LDS_KBP) {
-    const size_t lds = sizeof(float) * (8192 + 32 * (size_t)kb_p + 8 * scratch);
+    const size_t lds = sizeof(float) * (8192 + (size_t)rs_vw_words(kb_p) + 8 * scratch);
     if (big && lds <= RS_LDS_BYTES) return launch_rs<NPL, true, 8>(BH, lds, stream, a);
   }
   const size_t lds = sizeof(float) * (8192 + 4 * (scratch + NPL * 64));  // + the two 16 KiB static tiles

@@ -48,7 +48,7 @@ def _gpu_restore_swap(A, V, M, nts, n_cand, n_iters, restore_frac, decay, flags,
     return key.cpu().numpy(), s.cpu().numpy(), obj.cpu().numpy()
 
 
-SHAPES = [(2, 7, 40, 39), (3, 9, 130, 129), (2, 5, 685, 684), (1, 3, 900, 899), (1, 3, 1100, 1100), (1, 2, 1369, 1368)]
+SHAPES = [(2, 7, 40, 39), (3, 9, 130, 129), (2, 5, 400, 399), (2, 5, 685, 684), (1, 3, 900, 899), (1, 3, 1100, 1100), (1, 2, 1369, 1368)]
 MODES = {
     "ress_recipe": (5, 0.5, 0.5, 1 | 2),
     "fp32": (5, 0.5, 0.5, 2),
