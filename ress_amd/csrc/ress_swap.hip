@@ -281,15 +281,19 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
     float sp = 0.0f, acc = 0.0f;
     if constexpr (STREAM) {  // collective: every wave of the workgroup calls it with the same n
       const int dhi = lane >> 2, dlo = lane & 3;
+      // this lane's word of row u of a 16-row group (the tile swizzle): computed once, so
+      // a batch's reads are these offsets plus an immediate (tile, batch)
+      int roff[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) roff[u] = u * 64 + ((dhi ^ u) << 2) + dlo;
       stream_tiles((n + 63) >> 6, [&](const float4* tile, int t) {
         const float* tf = reinterpret_cast<const float*>(tile);
         const int m = min(64, n - 64 * t);
         const float* pc = Pw + 64 * t;
-        int kk = 0;
-        for (; kk + 16 <= m; kk += 16) {  // sixteen rows' LDS reads in flight per batch
+        auto batch = [&](int kk) {  // rows kk..kk+15 (kk % 16 == 0), all sixteen reads in flight
           float v[16];
 #pragma unroll
-          for (int u = 0; u < 16; ++u) v[u] = tf[(kk + u) * 64 + ((dhi ^ u) << 2) + dlo];  // kk % 16 == 0
+          for (int u = 0; u < 16; ++u) v[u] = tf[kk * 64 + roff[u]];
 #pragma unroll
           for (int u = 0; u < 16; u += 4) {
             const float4 p4 = *reinterpret_cast<const float4*>(pc + kk + u);
@@ -302,6 +306,16 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
             sp = sp + p4.w;
             acc = fmaf(p4.w, v[u + 3], acc);
           }
+        };
+        int kk = 0;
+        if (m == 64) {  // full tile: batch offsets are compile-time
+          batch(0);
+          batch(16);
+          batch(32);
+          batch(48);
+          kk = 64;
+        } else {
+          for (; kk + 16 <= m; kk += 16) batch(kk);
         }
         for (; kk < m; ++kk) {
           const float p = pc[kk];
@@ -357,14 +371,22 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
 #pragma unroll
     for (int i = 0; i < NPL; ++i) out[i] = 0.0f;
     if constexpr (STREAM) {  // collective: tile i holds the candidates of lane slot i
+      // vec (the same for every tile) in registers, and all sixteen of a tile's reads
+      // issued before its chain: one wave per SIMD leaves nothing else to cover LDS
+      // latency between the chain's steps
+      float4 vc[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) vc[q] = *reinterpret_cast<const float4*>(vec + 4 * q);
       stream_tiles(nel, [&](const float4* tile, int i) {
         const float4* vk = tile + lane * 16;
+        float4 v[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) v[q] = vk[q ^ (lane & 15)];
         float o = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {  // dims 4q..4q+3: steps p = 2q, 2q+1
-          const float4 v = vk[q ^ (lane & 15)];
-          o = fmaf(vec[4 * q + 1], v.y, fmaf(vec[4 * q], v.x, o));
-          o = fmaf(vec[4 * q + 3], v.w, fmaf(vec[4 * q + 2], v.z, o));
+        for (int q = 0; q < 16; ++q) {  // dims 4q..4q+3 in order
+          o = fmaf(vc[q].y, v[q].y, fmaf(vc[q].x, v[q].x, o));
+          o = fmaf(vc[q].w, v[q].w, fmaf(vc[q].z, v[q].z, o));
         }
         outl[i * 64 + lane] = o;
       });
