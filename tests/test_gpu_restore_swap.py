@@ -48,7 +48,10 @@ def _gpu_restore_swap(A, V, M, nts, n_cand, n_iters, restore_frac, decay, flags,
     return key.cpu().numpy(), s.cpu().numpy(), obj.cpu().numpy()
 
 
-SHAPES = [(2, 7, 40, 39), (3, 9, 130, 129), (2, 5, 400, 399), (2, 5, 685, 684), (1, 3, 900, 899), (1, 3, 1100, 1100), (1, 2, 1369, 1368)]
+# row lengths: every lane-width variant, LDS-resident V (bf16 up to ~730 blocks), and streamed
+# V through four tile buffers (up to ~1700 blocks) or two (1800)
+SHAPES = [(2, 7, 40, 39), (3, 9, 130, 129), (2, 5, 400, 399), (2, 5, 685, 684), (1, 3, 900, 899),
+          (1, 3, 1100, 1100), (1, 2, 1369, 1368), (1, 2, 1800, 1799)]
 MODES = {
     "ress_recipe": (5, 0.5, 0.5, 1 | 2),
     "fp32": (5, 0.5, 0.5, 2),
