@@ -8,10 +8,14 @@
 // 32 with the column, rotate-half pairs (j, j+16) at frequencies base^(-2i/32)), with the
 // same rounding points as the torch modules: LayerNorm output rounded to the activation
 // dtype (bf16), the rotation in fp32 (x*cos + rot(x)*sin, no contraction), rounded again.
+// cos/sin are the hardware functions (not the library's), so a small fraction of q/k
+// values differ from the modules' by one bf16 rounding.
 //
-// One workgroup per token, nh*16 threads: thread t owns dims 4(t%16)..+3 of head t/16 for
-// q, k and v. LayerNorm statistics reduce over the head's 16 threads (xor 1..8); the
-// rotation partner dims j +- 16 sit 4 threads away (xor 4).
+// One workgroup per QKN_TOKENS consecutive tokens, nh*16 threads: thread t owns dims
+// 4(t%16)..+3 of head t/16 for q, k and v. Its four rotation frequencies are computed once
+// for all of the workgroup's tokens, and q and k share each token's cos/sin. LayerNorm
+// statistics reduce over the head's 16 threads (xor 1..8); the rotation partner dims
+// j +- 16 sit 4 threads away (xor 4).
 #include "common.h"
 
 namespace {
@@ -43,21 +47,19 @@ __device__ __forceinline__ float4 head_norm(float4 x, const uint16_t* w, const u
                      round_bf16(c.z * rstd * gw.z + gb.z), round_bf16(c.w * rstd * gw.w + gb.w));
 }
 
-// rotate-half RoPE of dims d0..d0+3 within a 32-dim half at position p
-__device__ __forceinline__ float4 rope4(float4 y, int d0, float p, float base) {
+#define QKN_TOKENS 16
+
+// rotate-half RoPE of dims d0..d0+3 within a 32-dim half, given cos/sin of their angles
+__device__ __forceinline__ float4 rope4(float4 y, int d0, const float (&cs)[4], const float (&sn)[4]) {
   const float4 o = make_float4(__shfl_xor(y.x, 4, 64), __shfl_xor(y.y, 4, 64), __shfl_xor(y.z, 4, 64),
                                __shfl_xor(y.w, 4, 64));  // dims d0 +- 16
-  const int j = d0 & 31, i0 = j & 15;
-  const bool lo = j < 16;
+  const bool lo = (d0 & 31) < 16;
   float r[4];
   const float yy[4] = {y.x, y.y, y.z, y.w}, oo[4] = {o.x, o.y, o.z, o.w};
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const float inv = 1.0f / powf(base, (float)(2 * (i0 + u)) / 32.0f);
-    const float ang = p * inv;
-    const float cs = cosf(ang), sn = sinf(ang);
     const float rot = lo ? -oo[u] : oo[u];
-    const float a = yy[u] * cs, bb = rot * sn;
+    const float a = yy[u] * cs[u], bb = rot * sn[u];
     r[u] = round_bf16(a + bb);
   }
   return make_float4(r[0], r[1], r[2], r[3]);
@@ -69,21 +71,39 @@ __global__ __launch_bounds__(1024) void k_qk_norm_rope(const uint16_t* __restric
                                                        float eps, const long long* __restrict__ pos, float base,
                                                        uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_out,
                                                        uint16_t* __restrict__ v_out) {
-  const int tok = blockIdx.x, b = blockIdx.y, t = threadIdx.x, h = t >> 4, d0 = (t & 15) * 4;
+  const int b = blockIdx.y, t = threadIdx.x, h = t >> 4, d0 = (t & 15) * 4;
   const int C = nh * 64;
-  const uint16_t* src = qkv + ((long long)b * T + tok) * 3 * C + h * 64 + d0;
-  const float4 q = ld_bf16x4(src), k = ld_bf16x4(src + C);
-  const uint2 v = *reinterpret_cast<const uint2*>(src + 2 * C);
-  const long long o = (((long long)b * nh + h) * T + tok) * 64 + d0;
-  *reinterpret_cast<uint2*>(v_out + o) = v;
-  float4 qn = head_norm(q, qw, qb, d0, eps), kn = head_norm(k, kw, kb, d0, eps);
-  if (pos) {
-    const float p = (float)pos[((long long)b * T + tok) * 2 + (d0 >> 5)];
-    qn = rope4(qn, d0, p, base);
-    kn = rope4(kn, d0, p, base);
+  // frequencies base^(-2i/32) of this thread's dims (i = (d0 % 32) % 16 + u)
+  float inv[4];
+  const int i0 = (d0 & 31) & 15;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) inv[u] = 1.0f / powf(base, (float)(2 * (i0 + u)) / 32.0f);
+  const int tok1 = min(T, (int)(blockIdx.x + 1) * QKN_TOKENS);
+  for (int tok = blockIdx.x * QKN_TOKENS; tok < tok1; ++tok) {
+    const uint16_t* src = qkv + ((long long)b * T + tok) * 3 * C + h * 64 + d0;
+    const float4 q = ld_bf16x4(src), k = ld_bf16x4(src + C);
+    const uint2 v = *reinterpret_cast<const uint2*>(src + 2 * C);
+    const long long o = (((long long)b * nh + h) * T + tok) * 64 + d0;
+    *reinterpret_cast<uint2*>(v_out + o) = v;
+    float4 qn = head_norm(q, qw, qb, d0, eps), kn = head_norm(k, kw, kb, d0, eps);
+    if (pos) {
+      const float p = (float)pos[((long long)b * T + tok) * 2 + (d0 >> 5)];
+      float cs[4], sn[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float ang = p * inv[u];
+        // the hardware sine/cosine: angles here are at most a few tens of radians, where
+        // their absolute error (~1e-6) moves about one output in a thousand by one bf16
+        // rounding against the library's cosf/sinf, at a fraction of the cost
+        cs[u] = __cosf(ang);
+        sn[u] = __sinf(ang);
+      }
+      qn = rope4(qn, d0, cs, sn);
+      kn = rope4(kn, d0, cs, sn);
+    }
+    st_bf16x4(q_out + o, qn.x, qn.y, qn.z, qn.w);
+    st_bf16x4(k_out + o, kn.x, kn.y, kn.z, kn.w);
   }
-  st_bf16x4(q_out + o, qn.x, qn.y, qn.z, qn.w);
-  st_bf16x4(k_out + o, kn.x, kn.y, kn.z, kn.w);
 }
 
 }  // namespace
@@ -102,7 +122,7 @@ RESS_API int ress_qk_norm_rope(const void* qkv, int B, int T, int nh, const void
                    ((uintptr_t)k_weight & 7u) == 0 && ((uintptr_t)k_bias & 7u) == 0,
                "ress_qk_norm_rope: buffers must be 8-byte aligned");
   if (T == 0) return 0;
-  hipLaunchKernelGGL(k_qk_norm_rope, dim3(T, B), dim3(nh * 16), 0, stream, (const uint16_t*)qkv, T, nh,
+  hipLaunchKernelGGL(k_qk_norm_rope, dim3(cdiv(T, QKN_TOKENS), B), dim3(nh * 16), 0, stream, (const uint16_t*)qkv, T, nh,
                      (const uint16_t*)q_weight, (const uint16_t*)q_bias, (const uint16_t*)k_weight,
                      (const uint16_t*)k_bias, eps, (const long long*)pos, rope_base, (uint16_t*)q_out,
                      (uint16_t*)k_out, (uint16_t*)v_out);

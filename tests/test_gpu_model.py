@@ -90,8 +90,8 @@ def test_sparse_modes_run_every_layer(models, mode):
 
 def test_fused_qk_norm_rope_matches_modules(dev):
     """The fused q/k LayerNorm + 2D RoPE kernel against the torch modules it replaces:
-    v is copied exactly; q and k agree to bf16 rounding (the kernel's powf/cosf/sinf and
-    LayerNorm reduction order are its own)."""
+    v is copied exactly; q and k agree to bf16 rounding (the kernel's hardware cos/sin and
+    its LayerNorm reduction order are its own)."""
     from ress_amd.aggregator import Attention, RoPE2D
     from ress_amd.qkv import fused_qk_norm_rope
     torch.manual_seed(3)
