@@ -11,14 +11,13 @@
 // k_pooled_scores_tiled (kb_p <= 2048): four q-block rows of one head per workgroup, one
 // wave per row; pooled K goes through LDS in coalesced 64-block tiles that the four rows
 // share (tile t+1 is loaded into registers while tile t is used), and lane l owns the
-// columns kb = 64t + l, which is also the SUM64 partial order. k_pooled_scores: one wave
-// per row for longer rows, pooled K staged through a small LDS chunk per 64 columns.
+// columns kb = 64t + l, which is also the SUM64 partial order. k_pooled_scores_rows for
+// longer rows (below).
 #include "common.h"
 
 namespace {
 constexpr int PS_TILED_MAX = 2048;
 constexpr int PS_LDK = 65;  // tile row stride (floats): conflict-free column reads
-constexpr int PS_CH_LD = 17;  // k_pooled_scores chunk row stride (floats)
 
 __global__ __launch_bounds__(256) void k_pooled_scores_tiled(const float* __restrict__ pooled_q,
                                                              const float* __restrict__ pooled_k, int q_blk,
@@ -104,78 +103,108 @@ __global__ __launch_bounds__(256) void k_pooled_scores_tiled(const float* __rest
 }
 }  // namespace
 
-__global__ __launch_bounds__(64) void k_pooled_scores(const float* __restrict__ pooled_q,
-                                                      const float* __restrict__ pooled_k, int q_blk, int kb_p,
-                                                      int n_cand, float scale, float* __restrict__ attn_full,
-                                                      float* __restrict__ attn_cond) {
-  extern __shared__ float e[];  // kb_p floats
-  __shared__ float pq[64];
-  __shared__ float chunk[64 * PS_CH_LD];  // 64 columns x 16 dims of pooled K
-  const int qb = blockIdx.x, bh = blockIdx.y, lane = threadIdx.x;
-  pq[lane] = pooled_q[((long long)bh * q_blk + qb) * 64 + lane];
-  __syncthreads();
+// Rows longer than PS_TILED_MAX: PS_RW rows per wave (two measured fastest: more rows per
+// wave do not pay at configs[4]'s shape), four waves, so a workgroup covers
+// 4*PS_RW consecutive q-block rows of one head. Pooled K goes through LDS in the same
+// coalesced 64-column tiles as the tiled kernel, shared by all of the workgroup's rows,
+// and lane l computes column 64t + l for each of its wave's rows: PS_RW independent DOT64
+// chains per lane. The raw scores are written to attn_full; the softmax passes then read
+// back, lane by lane, the columns the same lane wrote (SUM64 order), recomputing the
+// exponentials in the last pass rather than storing them.
+constexpr int PS_RW = 2;
+__global__ __launch_bounds__(256) void k_pooled_scores_rows(const float* __restrict__ pooled_q,
+                                                            const float* __restrict__ pooled_k, int q_blk, int kb_p,
+                                                            int n_cand, float scale, float* __restrict__ attn_full,
+                                                            float* __restrict__ attn_cond) {
+  __shared__ float pk_l[64 * PS_LDK];
+  __shared__ __align__(16) float pq_l[4 * PS_RW][64];
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int bh = blockIdx.y, qb_wg = blockIdx.x * 4 * PS_RW, qb0 = qb_wg + w * PS_RW;
+  for (int i = tid; i < 4 * PS_RW * 64; i += 256) {
+    const int qb = qb_wg + (i >> 6);
+    pq_l[i >> 6][i & 63] = qb < q_blk ? pooled_q[((long long)bh * q_blk + qb) * 64 + (i & 63)] : 0.0f;
+  }
+  const int nrow = max(0, min(PS_RW, q_blk - qb0));  // this wave's valid rows (wave-uniform)
   const float* pkh = pooled_k + (long long)bh * kb_p * 64;
-
-  // 64 columns per step (lane = column): their pooled K goes through LDS 16 dims at a
-  // time with coalesced loads (the next chunk in flight while one is used); the DOT64
-  // chain runs over d = 0..63 in order
-  float lmax = -__builtin_huge_valf();
-  for (int c0 = 0; c0 < kb_p; c0 += 64) {
-    float4 ld[4];
-    auto load_chunk = [&](int q) {
+  float* full0 = attn_full + ((long long)bh * q_blk + qb0) * kb_p;
+  const int tiles = cdiv(kb_p, 64);
+  float4 nxt[4];
+  auto load_tile = [&](int t) {
+    const int cols = min(64, kb_p - 64 * t);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int f = 64 * t + lane, col = c0 + (f >> 2);
-        ld[t] = col < kb_p ? *reinterpret_cast<const float4*>(pkh + (long long)col * 64 + 16 * q + 4 * (f & 3))
-                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      }
-    };
-    load_chunk(0);
-    float acc = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int f = 64 * t + lane;
-        float* dst = chunk + (f >> 2) * PS_CH_LD + 4 * (f & 3);
-        dst[0] = ld[t].x;
-        dst[1] = ld[t].y;
-        dst[2] = ld[t].z;
-        dst[3] = ld[t].w;
-      }
-      __builtin_amdgcn_wave_barrier();
-      if (q + 1 < 4) load_chunk(q + 1);
-      const float* kc = chunk + lane * PS_CH_LD;
-#pragma unroll
-      for (int d = 0; d < 16; ++d) acc = fmaf(pq[16 * q + d], kc[d], acc);
-      __builtin_amdgcn_wave_barrier();  // every lane has read the chunk before it is overwritten
+    for (int i = 0; i < 4; ++i) {
+      const int f4 = tid + 256 * i, col = f4 >> 4;
+      nxt[i] = col < cols ? reinterpret_cast<const float4*>(pkh + (long long)(64 * t + col) * 64)[f4 & 15]
+                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    const int kb = c0 + lane;
-    if (kb < kb_p) {
-      const float s = acc * scale;
-      e[kb] = s;
-      lmax = fmaxf(lmax, s);
+  };
+  load_tile(0);
+  float lmax[PS_RW];
+#pragma unroll
+  for (int r = 0; r < PS_RW; ++r) lmax[r] = -__builtin_huge_valf();
+#pragma unroll 1
+  for (int t = 0; t < tiles; ++t) {
+    __syncthreads();  // previous tile consumed (and pq_l written, first time)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int f4 = tid + 256 * i;
+      float* dst = pk_l + (f4 >> 4) * PS_LDK + (f4 & 15) * 4;
+      dst[0] = nxt[i].x;
+      dst[1] = nxt[i].y;
+      dst[2] = nxt[i].z;
+      dst[3] = nxt[i].w;
+    }
+    __syncthreads();
+    if (t + 1 < tiles) load_tile(t + 1);
+    const int kb = 64 * t + lane;
+    if (nrow > 0 && kb < kb_p) {
+      const float* kc = pk_l + lane * PS_LDK;
+      float acc[PS_RW];
+#pragma unroll
+      for (int r = 0; r < PS_RW; ++r) acc[r] = 0.0f;
+#pragma unroll 4  // fully unrolled, the compiler issues every Q and K read up front (300 VGPRs)
+      for (int d4 = 0; d4 < 16; ++d4) {
+        const float k0 = kc[4 * d4], k1 = kc[4 * d4 + 1], k2 = kc[4 * d4 + 2], k3 = kc[4 * d4 + 3];
+#pragma unroll
+        for (int r = 0; r < PS_RW; ++r) {
+          const float4 qq = reinterpret_cast<const float4*>(pq_l[w * PS_RW + r])[d4];
+          acc[r] = fmaf(qq.x, k0, acc[r]);
+          acc[r] = fmaf(qq.y, k1, acc[r]);
+          acc[r] = fmaf(qq.z, k2, acc[r]);
+          acc[r] = fmaf(qq.w, k3, acc[r]);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < PS_RW; ++r)
+        if (r < nrow) {
+          const float sc = acc[r] * scale;
+          full0[(long long)r * kb_p + kb] = sc;
+          lmax[r] = fmaxf(lmax[r], sc);
+        }
     }
   }
-  const float m = wave_max(lmax);
-  float part = 0.0f;
-  for (int kb = lane; kb < kb_p; kb += 64) {
-    const float x = ress_expf(e[kb] - m);
-    e[kb] = x;
-    part = part + x;
+  // softmax of each row, by this wave alone (each lane reads back only the columns it wrote)
+  for (int r = 0; r < nrow; ++r) {
+    float* full = full0 + (long long)r * kb_p;
+    const float m = wave_max(lmax[r]);
+    float part = 0.0f;
+    for (int kb = lane; kb < kb_p; kb += 64) part = part + ress_expf(full[kb] - m);
+    const float total = sum64_tree(part);
+    float cpart = 0.0f;
+    float* cond = attn_cond + ((long long)bh * q_blk + qb0 + r) * n_cand;
+    for (int kb = lane; kb < kb_p; kb += 64) {
+      const float x = ress_expf(full[kb] - m);
+      const float p = x / total;
+      full[kb] = p;
+      if (kb < n_cand) {
+        cpart = cpart + p;
+        cond[kb] = x;  // exponential for now; divided below once rs is known
+      }
+    }
+    float rs = sum64_tree(cpart);
+    rs = fmaxf(rs, 0x1.0c6f7ap-20f);  // clamp(min=1e-6)
+    for (int kb = lane; kb < n_cand; kb += 64) cond[kb] = (cond[kb] / total) / rs;
   }
-  const float total = sum64_tree(part);
-  float* full = attn_full + ((long long)bh * q_blk + qb) * kb_p;
-  float cpart = 0.0f;
-  for (int kb = lane; kb < kb_p; kb += 64) {
-    const float p = e[kb] / total;
-    full[kb] = p;
-    if (kb < n_cand) cpart = cpart + p;
-  }
-  float rs = sum64_tree(cpart);
-  rs = fmaxf(rs, 0x1.0c6f7ap-20f);  // clamp(min=1e-6)
-  float* cond = attn_cond + ((long long)bh * q_blk + qb) * n_cand;
-  for (int kb = lane; kb < n_cand; kb += 64) cond[kb] = (e[kb] / total) / rs;
 }
 
 // attn_full / attn_cond from pooled Q [BH][q_blk][64] and pooled K [BH][kb_p][64].
@@ -185,7 +214,6 @@ RESS_API int ress_pooled_scores(const void* pooled_q, const void* pooled_k, int 
                                 float scale, void* attn_full, void* attn_cond, hipStream_t stream) {
   RESS_REQUIRE(BH > 0 && q_blk > 0 && kb_p > 0 && n_cand >= 0 && n_cand <= kb_p,
                "ress_pooled_scores: bad geometry BH=%d q_blk=%d kb_p=%d n_cand=%d", BH, q_blk, kb_p, n_cand);
-  RESS_REQUIRE(kb_p <= 16384, "ress_pooled_scores: kb_p=%d exceeds the LDS row limit 16384", kb_p);
   RESS_REQUIRE(pooled_q && pooled_k && attn_full && attn_cond, "ress_pooled_scores: null pointer");
   RESS_REQUIRE(((uintptr_t)pooled_k & 15u) == 0, "ress_pooled_scores: pooled_k must be 16-byte aligned");
   if (kb_p <= PS_TILED_MAX) {
@@ -193,7 +221,7 @@ RESS_API int ress_pooled_scores(const void* pooled_q, const void* pooled_k, int 
                        (const float*)pooled_q, (const float*)pooled_k, q_blk, kb_p, n_cand, scale, (float*)attn_full,
                        (float*)attn_cond);
   } else {
-    hipLaunchKernelGGL(k_pooled_scores, dim3(q_blk, BH), dim3(64), kb_p * sizeof(float), stream,
+    hipLaunchKernelGGL(k_pooled_scores_rows, dim3(cdiv(q_blk, 4 * PS_RW), BH), dim3(256), 0, stream,
                        (const float*)pooled_q, (const float*)pooled_k, q_blk, kb_p, n_cand, scale, (float*)attn_full,
                        (float*)attn_cond);
   }

@@ -103,7 +103,7 @@ def test_pooled_scores_bit_exact(layer, dev):
     assert _bits_equal(_np(cond).reshape(ocond.shape), ocond)
 
 
-@pytest.mark.parametrize("q_blk,kb_p", [(5, 1), (7, 70), (3, 687), (2, 2048), (3, 2049)])
+@pytest.mark.parametrize("q_blk,kb_p", [(5, 1), (7, 70), (3, 687), (2, 2048), (3, 2049), (17, 4300)])
 def test_pooled_scores_row_lengths(q_blk, kb_p, dev):
     """Rows of one tile, a ragged tile, the configs[2] length, the tiled kernel's limit and
     the direct kernel beyond it; q_blk not a multiple of the four rows per workgroup."""
