@@ -92,11 +92,17 @@ __global__ __launch_bounds__(1024) void k_qk_norm_rope(const uint16_t* __restric
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const float ang = p * inv[u];
-        // the hardware sine/cosine: angles here are at most a few tens of radians, where
-        // their absolute error (~1e-6) moves about one output in a thousand by one bf16
-        // rounding against the library's cosf/sinf, at a fraction of the cost
-        cs[u] = __cosf(ang);
-        sn[u] = __sinf(ang);
+        // the hardware sine/cosine for patch-grid positions (|angle| <= |p| <= 256 rad): their
+        // absolute error (~1e-6 at a few tens of radians) moves about one output in a thousand
+        // by one bf16 rounding against the library's cosf/sinf, at a fraction of the cost;
+        // larger positions take the library functions
+        if (fabsf(p) <= 256.0f) {
+          cs[u] = __cosf(ang);
+          sn[u] = __sinf(ang);
+        } else {
+          cs[u] = cosf(ang);
+          sn[u] = sinf(ang);
+        }
       }
       qn = rope4(qn, d0, cs, sn);
       kn = rope4(kn, d0, cs, sn);

@@ -88,10 +88,12 @@ def test_sparse_modes_run_every_layer(models, mode):
     assert _cos(got, want) >= 0.95
 
 
-def test_fused_qk_norm_rope_matches_modules(dev):
+@pytest.mark.parametrize("max_pos", [38, 5000], ids=["grid", "large_positions"])
+def test_fused_qk_norm_rope_matches_modules(max_pos, dev):
     """The fused q/k LayerNorm + 2D RoPE kernel against the torch modules it replaces:
-    v is copied exactly; q and k agree to bf16 rounding (the kernel's hardware cos/sin and
-    its LayerNorm reduction order are its own)."""
+    v is copied exactly; q and k agree to bf16 rounding (the kernel's hardware cos/sin for
+    patch-grid positions, the library functions beyond 256, and its LayerNorm reduction
+    order are its own)."""
     from ress_amd.aggregator import Attention, RoPE2D
     from ress_amd.qkv import fused_qk_norm_rope
     torch.manual_seed(3)
@@ -102,7 +104,7 @@ def test_fused_qk_norm_rope_matches_modules(dev):
             n.bias.uniform_(-0.2, 0.2)
     B, T = 2, 300
     x = torch.randn(B, T, 256, device=dev).to(torch.bfloat16)
-    pos = torch.randint(0, 38, (B, T, 2), device=dev)
+    pos = torch.randint(0, max_pos, (B, T, 2), device=dev)
     with torch.no_grad():
         qkv = attn.qkv(x)
         q, k, v = fused_qk_norm_rope(attn, qkv, pos, 4)
