@@ -113,7 +113,9 @@ int ress_block_map_lut(const void* map, long long rows, int k, void* lut, void* 
  * for modules with LayerNorm(64) q/k norms and the rotate-half 2D RoPE (first 32 head
  * dims by row, last 32 by column, base^(-2i/32)): qkv (B,T,3*nh*64) bf16 (the qkv
  * Linear's output), LayerNorm weights/biases [64] bf16, pos (B,T,2) int64 or NULL (no
- * rotation) -> q, k, v (B,nh,T,64) bf16. */
+ * rotation) -> q, k, v (B,nh,T,64) bf16. v is copied exactly; q and k match the torch
+ * modules to one bf16 rounding (hardware sine/cosine for |pos| <= 256, the library
+ * functions beyond). */
 int ress_qk_norm_rope(const void* qkv, int B, int T, int nh, const void* q_weight, const void* q_bias,
                       const void* k_weight, const void* k_bias, float eps, const void* pos, float rope_base,
                       void* q_out, void* k_out, void* v_out, hipStream_t stream);
