@@ -16,6 +16,8 @@
 // Work: per row, O(kb_p * 64) for the dense reference, O(n_cand * 64) per round for the
 // masked sums and term_k; selections are 4-digit radix selects over the order keys with
 // a per-wave LDS histogram.
+#include <type_traits>
+
 #include "common.h"
 
 #define RS_BF16 1

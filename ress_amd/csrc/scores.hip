@@ -8,31 +8,37 @@
 // and SUM64 denominators; outputs
 //   attn_full [BH][q_blk][kb_p]   softmax over all kb_p pooled key blocks
 //   attn_cond [BH][q_blk][n_cand] the first n_cand renormalised to sum 1
-// k_pooled_scores_tiled (kb_p <= 2048): four q-block rows of one head per workgroup, one
-// wave per row; pooled K goes through LDS in coalesced 64-block tiles that the four rows
-// share (tile t+1 is loaded into registers while tile t is used), and lane l owns the
-// columns kb = 64t + l, which is also the SUM64 partial order. k_pooled_scores_rows for
-// longer rows (below).
+// k_pooled_scores_tiled (kb_p <= 1024): 4*PS_TW q-block rows of one head per workgroup,
+// PS_TW per wave (independent DOT64 chains per lane; two when that still leaves 512
+// workgroups, else one), scores in LDS; pooled K goes through LDS in coalesced 64-block
+// tiles that the rows share (tile t+1 is loaded into registers while tile t is used), and
+// lane l owns the columns kb = 64t + l, which is also the SUM64 partial order.
+// k_pooled_scores_rows for longer rows (below).
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
-constexpr int PS_TILED_MAX = 2048;
+constexpr int PS_TILED_MAX = 1024;
 constexpr int PS_LDK = 65;  // tile row stride (floats): conflict-free column reads
 
+template <int PS_TW>  // rows per wave
 __global__ __launch_bounds__(256) void k_pooled_scores_tiled(const float* __restrict__ pooled_q,
                                                              const float* __restrict__ pooled_k, int q_blk,
                                                              int kb_p, int n_cand, float scale,
                                                              float* __restrict__ attn_full,
                                                              float* __restrict__ attn_cond) {
-  extern __shared__ float ps_dyn[];  // [4][kb_p] scores, then exponentials, per wave
+  extern __shared__ float ps_dyn[];  // [4*PS_TW][kb_p] scores, then exponentials, per row
   __shared__ float pk_l[64 * PS_LDK];
-  __shared__ __align__(16) float pq_l[4][64];
+  __shared__ __align__(16) float pq_l[4 * PS_TW][64];
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int bh = blockIdx.y, qb = blockIdx.x * 4 + w;
-  const bool in_range = qb < q_blk;
-  const long long row = (long long)bh * q_blk + qb;
-  float* e = ps_dyn + w * kb_p;
-  if (in_range) pq_l[w][lane] = pooled_q[row * 64 + lane];
+  const int bh = blockIdx.y, qb_wg = blockIdx.x * 4 * PS_TW, qb0 = qb_wg + w * PS_TW;
+  for (int i = tid; i < 4 * PS_TW * 64; i += 256) {
+    const int qb = qb_wg + (i >> 6);
+    pq_l[i >> 6][i & 63] = qb < q_blk ? pooled_q[((long long)bh * q_blk + qb) * 64 + (i & 63)] : 0.0f;
+  }
+  const int nrow = max(0, min(PS_TW, q_blk - qb0));  // this wave's valid rows (wave-uniform)
+  float* e0 = ps_dyn + w * PS_TW * kb_p;
   const float* pkh = pooled_k + (long long)bh * kb_p * 64;
   const int tiles = cdiv(kb_p, 64);
   float4 nxt[4];
@@ -46,7 +52,9 @@ __global__ __launch_bounds__(256) void k_pooled_scores_tiled(const float* __rest
     }
   };
   load_tile(0);
-  float lmax = -__builtin_huge_valf();
+  float lmax[PS_TW];
+#pragma unroll
+  for (int r = 0; r < PS_TW; ++r) lmax[r] = -__builtin_huge_valf();
 #pragma unroll 1
   for (int t = 0; t < tiles; ++t) {
     __syncthreads();  // previous tile consumed (and pq_l written, first time)
@@ -62,44 +70,55 @@ __global__ __launch_bounds__(256) void k_pooled_scores_tiled(const float* __rest
     __syncthreads();
     if (t + 1 < tiles) load_tile(t + 1);
     const int kb = 64 * t + lane;
-    if (in_range && kb < kb_p) {
-      const float4* qv = reinterpret_cast<const float4*>(pq_l[w]);
+    if (nrow > 0 && kb < kb_p) {
       const float* kc = pk_l + lane * PS_LDK;
-      float acc = 0.0f;
+      float acc[PS_TW];
 #pragma unroll
+      for (int r = 0; r < PS_TW; ++r) acc[r] = 0.0f;
+#pragma unroll 4
       for (int d4 = 0; d4 < 16; ++d4) {
-        const float4 qq = qv[d4];
-        acc = fmaf(qq.x, kc[4 * d4 + 0], acc);
-        acc = fmaf(qq.y, kc[4 * d4 + 1], acc);
-        acc = fmaf(qq.z, kc[4 * d4 + 2], acc);
-        acc = fmaf(qq.w, kc[4 * d4 + 3], acc);
+        const float k0 = kc[4 * d4], k1 = kc[4 * d4 + 1], k2 = kc[4 * d4 + 2], k3 = kc[4 * d4 + 3];
+#pragma unroll
+        for (int r = 0; r < PS_TW; ++r) {
+          const float4 qq = reinterpret_cast<const float4*>(pq_l[w * PS_TW + r])[d4];
+          acc[r] = fmaf(qq.x, k0, acc[r]);
+          acc[r] = fmaf(qq.y, k1, acc[r]);
+          acc[r] = fmaf(qq.z, k2, acc[r]);
+          acc[r] = fmaf(qq.w, k3, acc[r]);
+        }
       }
-      const float s = acc * scale;
-      e[kb] = s;
-      lmax = fmaxf(lmax, s);
+#pragma unroll
+      for (int r = 0; r < PS_TW; ++r) {
+        const float sc = acc[r] * scale;
+        e0[r * kb_p + kb] = sc;
+        lmax[r] = fmaxf(lmax[r], sc);
+      }
     }
   }
-  if (!in_range) return;
   // from here each lane reads back only its own columns: no further synchronisation
-  const float m = wave_max(lmax);
-  float part = 0.0f;
-  for (int kb = lane; kb < kb_p; kb += 64) {
-    const float x = ress_expf(e[kb] - m);
-    e[kb] = x;
-    part = part + x;
+  for (int r = 0; r < nrow; ++r) {
+    float* e = e0 + r * kb_p;
+    const long long row = (long long)bh * q_blk + qb0 + r;
+    const float m = wave_max(lmax[r]);
+    float part = 0.0f;
+    for (int kb = lane; kb < kb_p; kb += 64) {
+      const float x = ress_expf(e[kb] - m);
+      e[kb] = x;
+      part = part + x;
+    }
+    const float total = sum64_tree(part);
+    float* full = attn_full + row * kb_p;
+    float cpart = 0.0f;
+    for (int kb = lane; kb < kb_p; kb += 64) {
+      const float p = e[kb] / total;
+      full[kb] = p;
+      if (kb < n_cand) cpart = cpart + p;
+    }
+    float rs = sum64_tree(cpart);
+    rs = fmaxf(rs, 0x1.0c6f7ap-20f);  // clamp(min=1e-6)
+    float* cond = attn_cond + row * n_cand;
+    for (int kb = lane; kb < n_cand; kb += 64) cond[kb] = (e[kb] / total) / rs;
   }
-  const float total = sum64_tree(part);
-  float* full = attn_full + row * kb_p;
-  float cpart = 0.0f;
-  for (int kb = lane; kb < kb_p; kb += 64) {
-    const float p = e[kb] / total;
-    full[kb] = p;
-    if (kb < n_cand) cpart = cpart + p;
-  }
-  float rs = sum64_tree(cpart);
-  rs = fmaxf(rs, 0x1.0c6f7ap-20f);  // clamp(min=1e-6)
-  float* cond = attn_cond + row * n_cand;
-  for (int kb = lane; kb < n_cand; kb += 64) cond[kb] = (e[kb] / total) / rs;
 }
 }  // namespace
 
@@ -217,9 +236,14 @@ RESS_API int ress_pooled_scores(const void* pooled_q, const void* pooled_k, int 
   RESS_REQUIRE(pooled_q && pooled_k && attn_full && attn_cond, "ress_pooled_scores: null pointer");
   RESS_REQUIRE(((uintptr_t)pooled_k & 15u) == 0, "ress_pooled_scores: pooled_k must be 16-byte aligned");
   if (kb_p <= PS_TILED_MAX) {
-    hipLaunchKernelGGL(k_pooled_scores_tiled, dim3(cdiv(q_blk, 4), BH), dim3(256), 4 * kb_p * sizeof(float), stream,
-                       (const float*)pooled_q, (const float*)pooled_k, q_blk, kb_p, n_cand, scale, (float*)attn_full,
-                       (float*)attn_cond);
+    auto go = [&](auto tw) {
+      constexpr int TW = decltype(tw)::value;
+      hipLaunchKernelGGL(k_pooled_scores_tiled<TW>, dim3(cdiv(q_blk, 4 * TW), BH), dim3(256),
+                         4 * TW * kb_p * sizeof(float), stream, (const float*)pooled_q, (const float*)pooled_k, q_blk,
+                         kb_p, n_cand, scale, (float*)attn_full, (float*)attn_cond);
+    };
+    if ((long long)cdiv(q_blk, 8) * BH >= 512) go(std::integral_constant<int, 2>{});
+    else go(std::integral_constant<int, 1>{});
   } else {
     hipLaunchKernelGGL(k_pooled_scores_rows, dim3(cdiv(q_blk, 4 * PS_RW), BH), dim3(256), 0, stream,
                        (const float*)pooled_q, (const float*)pooled_k, q_blk, kb_p, n_cand, scale, (float*)attn_full,

@@ -103,10 +103,10 @@ def test_pooled_scores_bit_exact(layer, dev):
     assert _bits_equal(_np(cond).reshape(ocond.shape), ocond)
 
 
-@pytest.mark.parametrize("q_blk,kb_p", [(5, 1), (7, 70), (3, 687), (2, 2048), (3, 2049), (17, 4300)])
+@pytest.mark.parametrize("q_blk,kb_p", [(5, 1), (7, 70), (3, 687), (9, 1024), (3, 1025), (2, 2048), (17, 4300)])
 def test_pooled_scores_row_lengths(q_blk, kb_p, dev):
-    """Rows of one tile, a ragged tile, the configs[2] length, the tiled kernel's limit and
-    the direct kernel beyond it; q_blk not a multiple of the four rows per workgroup."""
+    """Rows of one tile, a ragged tile, the configs[2] length, the tiled kernel's limit (1024)
+    and the row kernel beyond it; q_blk not a multiple of the rows per workgroup."""
     rng = np.random.default_rng(kb_p)
     pq = (rng.normal(size=(2, q_blk, 64)) * 2).astype(np.float32)
     pk = (rng.normal(size=(2, kb_p, 64)) * 2).astype(np.float32)
@@ -119,6 +119,24 @@ def test_pooled_scores_row_lengths(q_blk, kb_p, dev):
     ofull, ocond = oracle.pooled_scores(pq, pk, n_cand)
     assert _bits_equal(_np(full), ofull)
     assert _bits_equal(_np(cond)[:, :, :n_cand], ocond)
+
+
+def test_pooled_scores_two_rows_per_wave(dev):
+    """Enough rows for the tiled kernel's two-rows-per-wave instance (>= 512 workgroups),
+    q_blk not a multiple of its eight rows per workgroup."""
+    BH, q_blk, kb_p = 16, 257, 333
+    rng = np.random.default_rng(7)
+    pq = (rng.normal(size=(BH, q_blk, 64)) * 2).astype(np.float32)
+    pk = (rng.normal(size=(BH, kb_p, 64)) * 2).astype(np.float32)
+    n_cand = kb_p - 1
+    full = torch.empty(BH, q_blk, kb_p, device=dev)
+    cond = torch.empty(BH, q_blk, n_cand, device=dev)
+    tq, tk = torch.from_numpy(pq).to(dev), torch.from_numpy(pk).to(dev)
+    _lib.call("ress_pooled_scores", _lib.ptr(tq), _lib.ptr(tk), BH, q_blk, kb_p, n_cand, 0.125, _lib.ptr(full),
+              _lib.ptr(cond), _lib.stream_handle(dev))
+    ofull, ocond = oracle.pooled_scores(pq, pk, n_cand)
+    assert _bits_equal(_np(full), ofull)
+    assert _bits_equal(_np(cond), ocond)
 
 
 @pytest.mark.parametrize("sr,cdf", [(0.5, 0.9), (None, 0.9), (0.7, None), (0.2, 0.5)])
