@@ -174,7 +174,9 @@ def test_head_budget_non_convergence_is_reported(dev):
     assert np.array_equal(_np(out), want)
 
 
-@pytest.mark.parametrize("n_cand,kb_tot,sink_lead", [(342, 344, 0), (85, 86, 0), (64, 64, 5), (1, 3, 0), (700, 710, 22)])
+# rows below 1024 candidates run on one wave, longer rows on four (a cross-wave tie order)
+@pytest.mark.parametrize("n_cand,kb_tot,sink_lead", [(342, 344, 0), (85, 86, 0), (64, 64, 5), (1, 3, 0), (700, 710, 22),
+                                                     (1500, 1503, 3), (4293, 4294, 22)])
 def test_select_bit_exact_with_ties(n_cand, kb_tot, sink_lead, dev):
     rng = np.random.default_rng(n_cand)
     BH, q_sel, q_tot = 4, 11, 12
