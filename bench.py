@@ -17,7 +17,7 @@ half at the bf16 or INT8 rate, PV half at the bf16 rate); frac_of_int8_peak pric
 same FLOPs against the INT8 peak, frac_of_measured_peak against the rates measured on
 this GPU (measured_peaks: MFMA microbenchmark, 1 GiB copy). traffic (HBM bytes per
 launch) and mfma_busy_pct_pmc (matrix-core busy cycles over active SIMD cycles) are read
-from the committed rocprofv3 PMC summaries in profiles/ (configs[1] only).
+from the committed rocprofv3 PMC summaries in profiles/ (the default 16-frame layer only).
 """
 
 import argparse
@@ -259,8 +259,8 @@ def run_aggregator(args):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only "
-                                   "(see DESIGN.md)", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding (by heads, one "
+                                   "all-gather of the HeSS counts) is not built", "n_gpus": args.gpus}))
         sys.exit(2)
     if args.config == 3:
         run_aggregator(args)

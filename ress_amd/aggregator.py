@@ -1,5 +1,5 @@
 """A VGGT-1B-style aggregator with random weights, for end-to-end runs of the
-block-sparse global attention.
+block-sparse global attention (64 frames of 518x518, ReSS on every global layer).
 
 Structure of the aggregator the reference wires (VGGT, `model.aggregator.global_blocks`,
 reference src/ress/models/wiring.py:33-40; the attention module shape read by

@@ -123,7 +123,7 @@ __global__ __launch_bounds__(256) void k_pooled_scores_tiled(const float* __rest
 }  // namespace
 
 // Rows longer than PS_TILED_MAX: PS_RW rows per wave (two measured fastest: more rows per
-// wave do not pay at configs[4]'s shape), four waves, so a workgroup covers
+// wave do not pay on 4294-block rows), four waves, so a workgroup covers
 // 4*PS_RW consecutive q-block rows of one head. Pooled K goes through LDS in the same
 // coalesced 64-column tiles as the tiled kernel, shared by all of the workgroup's rows,
 // and lane l computes column 64t + l for each of its wave's rows: PS_RW independent DOT64

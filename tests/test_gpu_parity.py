@@ -43,7 +43,7 @@ def _rand_layer(frames, P, S, H, seed):
 
 
 SHAPES = [
-    ("vggt_f4", None),            # BASELINE configs[0] geometry, synthetic field
+    ("vggt_f4", None),            # 4 frames of VGGT token geometry, synthetic field
     ("ragged", (3, 203, 5, 2)),   # partial q/k blocks, straddling special block
     ("plain", (1, 320, 0, 3)),    # no special tokens
     ("tiny", (2, 40, 5, 1)),      # fewer tokens than one q block
@@ -105,7 +105,7 @@ def test_pooled_scores_bit_exact(layer, dev):
 
 @pytest.mark.parametrize("q_blk,kb_p", [(5, 1), (7, 70), (3, 687), (9, 1024), (3, 1025), (2, 2048), (17, 4300)])
 def test_pooled_scores_row_lengths(q_blk, kb_p, dev):
-    """Rows of one tile, a ragged tile, the configs[2] length, the tiled kernel's limit (1024)
+    """Rows of one tile, a ragged tile, a 32-frame row (687 blocks), the tiled kernel's limit (1024)
     and the row kernel beyond it; q_blk not a multiple of the rows per workgroup."""
     rng = np.random.default_rng(kb_p)
     pq = (rng.normal(size=(2, q_blk, 64)) * 2).astype(np.float32)
