@@ -177,8 +177,8 @@ __device__ __forceinline__ void item_to_row(int i, int BH, int q_blk_p, int q_bl
 
 __global__ __launch_bounds__(1024) void k_attn_schedule(const int* __restrict__ nvalid, int BH, int q_blk_p,
                                                         int q_blk_total, int* __restrict__ sched) {
-  __shared__ long long part[1024];
-  const int tid = threadIdx.x;
+  __shared__ long long wtot[16];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int n = BH * q_blk_total;
   const int per = (n + 1023) / 1024;
   const int i0 = min(n, tid * per), i1 = min(n, i0 + per);
@@ -188,17 +188,25 @@ __global__ __launch_bounds__(1024) void k_attn_schedule(const int* __restrict__ 
     item_to_row(i, BH, q_blk_p, q_blk_total, bh, qb);
     s += nvalid[(long long)bh * q_blk_total + qb] + RESS_ROW_COST;
   }
-  part[tid] = s;
   if (tid < 9) sched[tid] = tid == 0 ? 0 : n;
-  __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {  // inclusive scan
-    const long long v = tid >= off ? part[tid - off] : 0;
-    __syncthreads();
-    part[tid] += v;
-    __syncthreads();
+  // inclusive scan of the threads' sums: lane shuffles within each wave, then the 16 wave
+  // totals through LDS (one barrier)
+  long long incl = s;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const long long y = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += y;
   }
-  const long long W = part[1023];
-  long long run = part[tid] - s;  // exclusive prefix of this thread's first item
+  if (lane == 63) wtot[wv] = incl;
+  __syncthreads();
+  long long W = 0;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const long long t = wtot[k];
+    incl += k < wv ? t : 0;
+    W += t;
+  }
+  long long run = incl - s;  // exclusive prefix of this thread's first item
   long long prev = -1;            // exclusive prefix of item i-1
   if (i0 > 0 && i0 < n) {
     int bh, qb;
