@@ -443,6 +443,50 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
     }
   };
 
+  // sequential fmaf over j = 0..63 of this lane's column col[64 j] and the broadcast vec[j]
+  // (vec 16-byte aligned); each batch's LDS reads are issued before its chain steps
+  auto dot64 = [&](const float* col, const float* vec) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 64; j += 8) {
+      float c[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) c[u] = col[(j + u) * 64];
+      const float4 va = *reinterpret_cast<const float4*>(vec + j);
+      const float4 vb = *reinterpret_cast<const float4*>(vec + j + 4);
+      __builtin_amdgcn_sched_barrier(0);
+      acc = fmaf(c[0], va.x, acc);
+      acc = fmaf(c[1], va.y, acc);
+      acc = fmaf(c[2], va.z, acc);
+      acc = fmaf(c[3], va.w, acc);
+      acc = fmaf(c[4], vb.x, acc);
+      acc = fmaf(c[5], vb.y, acc);
+      acc = fmaf(c[6], vb.z, acc);
+      acc = fmaf(c[7], vb.w, acc);
+    }
+    return acc;
+  };
+  // sequential sum of the 64 broadcast values vec[0..63] (16-byte aligned), sixteen reads
+  // in flight per batch
+  auto sum64 = [&](const float* vec) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 64; i += 16) {
+      float4 v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = *reinterpret_cast<const float4*>(vec + i + 4 * q);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc = acc + v[q].x;
+        acc = acc + v[q].y;
+        acc = acc + v[q].z;
+        acc = acc + v[q].w;
+      }
+    }
+    return acc;
+  };
+
   const int q_begin = blockIdx.x * rows_per_wg, q_end = min(a.q_blk, (blockIdx.x + 1) * rows_per_wg);
   // STREAM: every wave makes the same number of passes (a wave without a row of its own
   // repeats the last one and writes nothing), so the collective calls line up
@@ -473,18 +517,12 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
     // quadratic_deviation's query side: Mvq = big(Mb vq), term_q = big(sum big(Mvq*vq))
     float mvq;
     {
-      float acc = 0.0f;
-#pragma unroll 16
-      for (int j = 0; j < 64; ++j) acc = fmaf(MbT[j * 64 + lane], vqs[j], acc);
-      mvq = rs_bf(acc, big);
+      mvq = rs_bf(dot64(MbT + lane, vqs), big);
     }
     t0[lane] = mvq;
     t1[lane] = rs_bf(mvq * vq, big);
     __builtin_amdgcn_wave_barrier();
-    float tq = 0.0f;
-#pragma unroll 16
-    for (int i = 0; i < 64; ++i) tq = tq + t1[i];
-    tq = rs_bf(tq, big);
+    const float tq = rs_bf(sum64(t1), big);
     // s, s_cut, s^2 per candidate
     uint32_t key[NPL];
     {
@@ -531,15 +569,11 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
       const float g = sp * vq - rs_bf(acc, big);
       t1[lane] = g;
       __builtin_amdgcn_wave_barrier();
-      float mg = 0.0f;
-#pragma unroll 16
-      for (int j = 0; j < 64; ++j) mg = fmaf(M32T[j * 64 + lane], t1[j], mg);
+      const float mg = dot64(M32T + lane, t1);
       t2[lane] = g * mg;  // products of ||g||^2_M
       t3[lane] = mg;
       __builtin_amdgcn_wave_barrier();
-      float n2 = 0.0f;
-#pragma unroll 16
-      for (int d = 0; d < 64; ++d) n2 = n2 + t2[d];
+      const float n2 = sum64(t2);
       float K = tm - sp;
       K = K < 1e-6f ? 1e-6f : K;
       gn = n2;
@@ -564,10 +598,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
       t2[lane] = vq * t3[lane];
       t0[lane] = rs_bf(t3[lane], big);
       __builtin_amdgcn_wave_barrier();
-      float tqr = 0.0f;
-#pragma unroll 16
-      for (int d = 0; d < 64; ++d) tqr = tqr + t2[d];
-      const float tqb = rs_bf(tqr, big);
+      const float tqb = rs_bf(sum64(t2), big);
       float tk[NPL];
       vdot_cols(t0, tk);  // term_k = v_k . big(Mg)
       // restore quality of the dropped (higher is better), then the compensation quality
