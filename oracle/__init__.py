@@ -181,6 +181,28 @@ def restore_swap(A, V, M, nts, n_cand, n_iters=5, restore_frac=0.5, decay=0.5, b
     return (keep, obj, s) if want_s else (keep, obj)
 
 
+def rs_probe(A, V, M, drop, n_cand, big_bf16=False, renormalize=True):
+    """What oracle_restore_swap ranks by, for a given drop set (oracle_rs_probe): returns
+    (s, scut (H,q_blk,n_cand), J (H,q_blk), rq, cq (H,q_blk,n_cand)): the drift scores, the
+    initial cut's key, the objective ||g||^2_M / K^2 of the drop set, and the round's
+    restore / drop marginals of every candidate (minimisation sign, unmasked).
+    drop (H,q_blk,n_cand) bool, True = dropped."""
+    A = np.ascontiguousarray(A, np.float32)
+    V = np.ascontiguousarray(V, np.float32)
+    M = np.ascontiguousarray(M, np.float32)
+    d = np.ascontiguousarray(drop, np.uint8)
+    H, q_blk, kb_p = A.shape
+    s = np.zeros((H, q_blk, n_cand), np.float32)
+    scut = np.zeros((H, q_blk, n_cand), np.float32)
+    J = np.zeros((H, q_blk), np.float32)
+    rq = np.zeros((H, q_blk, n_cand), np.float32)
+    cq = np.zeros((H, q_blk, n_cand), np.float32)
+    flags = (RS_BF16 if big_bf16 else 0) | (0 if renormalize else RS_NO_RENORM)
+    lib().oracle_rs_probe(_p(A), _p(V), _p(M), _p(d), H, q_blk, kb_p, n_cand, flags, _p(s), _p(scut), _p(J), _p(rq),
+                          _p(cq))
+    return s, scut, J, rq, cq
+
+
 def meansim_map(q, k, km=None, simthreshd1=0.1, cdfthreshd=0.9, attention_sink=0, H=None):
     """SpargeAttn-convention meansim block map (oracle_meansim_map). q (BH,Tq,64), k (BH,Tk,64)
     bf16 (torch or uint16); km (BH,64) f32 or None; thresholds scalar or per head.

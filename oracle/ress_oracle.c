@@ -480,6 +480,85 @@ static float rs_objective(const float* Pb, const uint8_t* drop, const float* Vb,
   return gn / (K * K);
 }
 
+/* Per-head preparation: bf16-rounded M and V (when big) and the key side of
+ * quadratic_deviation, term_k = big(sum_i big(big(M v_k)_i * v_ki)) (projected.py:282-284). */
+static void rs_head_setup(const float* M32, const float* Vh, int kb_p, int n_cand, int big, float* Mb, float* Vb,
+                          float* termk) {
+  for (int i = 0; i < 4096; ++i) Mb[i] = rs_bf(M32[i], big);
+  for (long long i = 0; i < (long long)kb_p * 64; ++i) Vb[i] = rs_bf(Vh[i], big);
+  for (int k = 0; k < n_cand; ++k) {
+    float tk = 0.0f;
+    for (int i = 0; i < 64; ++i) {
+      float a = 0.0f;
+      for (int j = 0; j < 64; ++j) a = fmaf(Mb[i * 64 + j], Vb[(long long)k * 64 + j], a);
+      tk = tk + rs_bf(rs_bf(a, big) * Vb[(long long)k * 64 + i], big);
+    }
+    termk[k] = rs_bf(tk, big);
+  }
+}
+
+/* Per-row scores: dense_reference (projected.py:313-356: v_bar_query = P @ v_bar, total mass),
+ * quadratic_deviation's query side and cross term (:259-288), s = P*sqrt(quad), the cut key
+ * s/(1-P).clamp(1e-4) (or s when renorm is off) and s^2 (:780-783). */
+static void rs_row_setup(const float* Arow, const float* Mb, const float* Vb, const float* termk, int kb_p, int n_cand,
+                         int big, int renorm, float* Pb, float* vq, float* tm_out, float* s, float* scut, float* ssq) {
+  for (int k = 0; k < kb_p; ++k) Pb[k] = rs_bf(Arow[k], big);
+  float tm = 0.0f;
+  for (int d = 0; d < 64; ++d) vq[d] = 0.0f;
+  for (int k = 0; k < kb_p; ++k) {
+    tm = tm + Pb[k];
+    for (int d = 0; d < 64; ++d) vq[d] = fmaf(Pb[k], Vb[(long long)k * 64 + d], vq[d]);
+  }
+  *tm_out = rs_bf(tm, big);
+  for (int d = 0; d < 64; ++d) vq[d] = rs_bf(vq[d], big);
+  float Mvq[64], tq = 0.0f;
+  for (int i = 0; i < 64; ++i) {
+    float a = 0.0f;
+    for (int j = 0; j < 64; ++j) a = fmaf(Mb[i * 64 + j], vq[j], a);
+    Mvq[i] = rs_bf(a, big);
+  }
+  for (int i = 0; i < 64; ++i) tq = tq + rs_bf(Mvq[i] * vq[i], big);
+  tq = rs_bf(tq, big);
+  for (int k = 0; k < n_cand; ++k) {
+    float cr = 0.0f;
+    for (int i = 0; i < 64; ++i) cr = fmaf(Mvq[i], Vb[(long long)k * 64 + i], cr);
+    cr = rs_bf(cr, big);
+    float qd = rs_bf(rs_bf(tq - rs_bf(2.0f * cr, big), big) + termk[k], big);
+    qd = qd < 0.0f ? 0.0f : qd;
+    const float sq = rs_bf(sqrtf(qd), big);
+    s[k] = rs_bf(Pb[k] * sq, big);
+    float om = rs_bf(1.0f - Pb[k], big);
+    om = rs_bf(om < 1e-4f ? 1e-4f : om, big);
+    scut[k] = renorm ? rs_bf(s[k] / om, big) : s[k];
+    ssq[k] = rs_bf(s[k] * s[k], big);
+  }
+}
+
+/* One round's marginals for the current drop set (projected.py:903-947, fused_round.py
+ * :170-226): J = ||g||^2_M / K^2, and per candidate k the knorm quality of restoring it
+ * (dG = 2 raw + s^2, u = +P_k) and of dropping it (dG = s^2 - 2 raw, u = -P_k), with
+ * raw = big(P_k * big(v_k.Mg - v_bar_query.Mg)). rq/cq are written for every candidate
+ * (not masked by the drop set, not sign-flipped); returns J. */
+static float rs_round_qualities(const float* Pb, const uint8_t* drop, const float* Vb, const float* M32,
+                                const float* vq, float tm, const float* ssq, int n_cand, int big, float* rq,
+                                float* cq) {
+  float g[64], Mg[64], gn, K, sp;
+  const float J = rs_objective(Pb, drop, Vb, M32, vq, tm, n_cand, big, g, Mg, &gn, &K, &sp);
+  float tqr = 0.0f, Mgb[64];
+  for (int d = 0; d < 64; ++d) tqr = tqr + vq[d] * Mg[d];
+  const float tqb = rs_bf(tqr, big);
+  for (int d = 0; d < 64; ++d) Mgb[d] = rs_bf(Mg[d], big);
+  for (int k = 0; k < n_cand; ++k) {
+    float tk = 0.0f;
+    for (int d = 0; d < 64; ++d) tk = fmaf(Vb[(long long)k * 64 + d], Mgb[d], tk);
+    tk = rs_bf(tk, big);
+    const float raw = rs_bf(Pb[k] * rs_bf(tk - tqb, big), big);
+    rq[k] = rs_knorm(gn, K, 2.0f * raw + ssq[k], Pb[k]);
+    cq[k] = rs_knorm(gn, K, ssq[k] - 2.0f * raw, -Pb[k]);
+  }
+  return J;
+}
+
 int oracle_restore_swap(const float* A, const float* V, const float* M, const int* nts, int H, int q_blk, int kb_p,
                         int n_cand, int n_iters, double restore_frac, double decay, int flags, uint8_t* keep,
                         float* obj_out, float* s_out) {
@@ -504,55 +583,13 @@ int oracle_restore_swap(const float* A, const float* V, const float* M, const in
   int* idx = (int*)malloc(sizeof(int) * (size_t)n_cand);
   for (int h = 0; h < H; ++h) {
     const float* M32 = M + (long long)h * 4096;
-    for (int i = 0; i < 4096; ++i) Mb[i] = rs_bf(M32[i], big);
-    for (long long i = 0; i < (long long)kb_p * 64; ++i) Vb[i] = rs_bf(V[(long long)h * kb_p * 64 + i], big);
-    /* term_k of quadratic_deviation: Mvk = M v_k (big), term_k = sum_i big(Mvk_i * v_ki) (big) */
-    for (int k = 0; k < n_cand; ++k) {
-      float tk = 0.0f;
-      for (int i = 0; i < 64; ++i) {
-        float a = 0.0f;
-        for (int j = 0; j < 64; ++j) a = fmaf(Mb[i * 64 + j], Vb[(long long)k * 64 + j], a);
-        tk = tk + rs_bf(rs_bf(a, big) * Vb[(long long)k * 64 + i], big);
-      }
-      termk[k] = rs_bf(tk, big);
-    }
+    rs_head_setup(M32, V + (long long)h * kb_p * 64, kb_p, n_cand, big, Mb, Vb, termk);
     for (int q = 0; q < q_blk; ++q) {
       const long long row = (long long)h * q_blk + q;
-      const float* Arow = A + row * kb_p;
-      for (int k = 0; k < kb_p; ++k) Pb[k] = rs_bf(Arow[k], big);
-      /* dense_reference: v_bar_query = P @ v_bar (big), total_mass = sum P (big) */
-      float vq[64], tm = 0.0f;
-      for (int d = 0; d < 64; ++d) vq[d] = 0.0f;
-      for (int k = 0; k < kb_p; ++k) {
-        tm = tm + Pb[k];
-        for (int d = 0; d < 64; ++d) vq[d] = fmaf(Pb[k], Vb[(long long)k * 64 + d], vq[d]);
-      }
-      tm = rs_bf(tm, big);
-      for (int d = 0; d < 64; ++d) vq[d] = rs_bf(vq[d], big);
-      /* quadratic_deviation's query side: Mvq (big), term_q (big) */
-      float Mvq[64], tq = 0.0f;
-      for (int i = 0; i < 64; ++i) {
-        float a = 0.0f;
-        for (int j = 0; j < 64; ++j) a = fmaf(Mb[i * 64 + j], vq[j], a);
-        Mvq[i] = rs_bf(a, big);
-      }
-      for (int i = 0; i < 64; ++i) tq = tq + rs_bf(Mvq[i] * vq[i], big);
-      tq = rs_bf(tq, big);
-      /* s = P * sqrt(max(term_q - 2 cross + term_k, 0)); s_cut = s / max(1 - P, 1e-4); s^2 */
-      for (int k = 0; k < n_cand; ++k) {
-        float cr = 0.0f;
-        for (int i = 0; i < 64; ++i) cr = fmaf(Mvq[i], Vb[(long long)k * 64 + i], cr);
-        cr = rs_bf(cr, big);
-        float qd = rs_bf(rs_bf(tq - rs_bf(2.0f * cr, big), big) + termk[k], big);
-        qd = qd < 0.0f ? 0.0f : qd;
-        const float sq = rs_bf(sqrtf(qd), big);
-        s[k] = rs_bf(Pb[k] * sq, big);
-        float om = rs_bf(1.0f - Pb[k], big);
-        om = rs_bf(om < 1e-4f ? 1e-4f : om, big);
-        scut[k] = renorm ? rs_bf(s[k] / om, big) : s[k];
-        ssq[k] = rs_bf(s[k] * s[k], big);
-        if (s_out) s_out[row * n_cand + k] = s[k];
-      }
+      float vq[64], tm;
+      rs_row_setup(A + row * kb_p, Mb, Vb, termk, kb_p, n_cand, big, renorm, Pb, vq, &tm, s, scut, ssq);
+      if (s_out)
+        for (int k = 0; k < n_cand; ++k) s_out[row * n_cand + k] = s[k];
       /* initial one-shot cut: keep the top min(nts, n_cand) by s_cut (lowest under invert_cut) */
       int nkeep = nts[row];
       nkeep = nkeep < 0 ? 0 : (nkeep > n_cand ? n_cand : nkeep);
@@ -573,7 +610,7 @@ int oracle_restore_swap(const float* A, const float* V, const float* M, const in
         const double frac = remaining * decay;
         remaining -= frac;
         const int pic0 = (int)rintf((float)frac * (float)nts[row]);
-        const float J = rs_objective(Pb, drop, Vb, M32, vq, tm, n_cand, big, g, Mg, &gn, &K, &sp);
+        const float J = rs_round_qualities(Pb, drop, Vb, M32, vq, tm, ssq, n_cand, big, rq, cq);
         if (track) {
           const int better = maxim ? J > best_obj : J < best_obj;
           if (better) {
@@ -581,23 +618,11 @@ int oracle_restore_swap(const float* A, const float* V, const float* M, const in
             memcpy(best, drop, (size_t)n_cand);
           }
         }
-        float tqr = 0.0f, Mgb[64];
-        for (int d = 0; d < 64; ++d) tqr = tqr + vq[d] * Mg[d];
-        const float tqb = rs_bf(tqr, big);
-        for (int d = 0; d < 64; ++d) Mgb[d] = rs_bf(Mg[d], big);
         int n_drop = 0, n_kept = 0;
         float rmax = -INFINITY;
         for (int k = 0; k < n_cand; ++k) {
-          float tk = 0.0f;
-          for (int d = 0; d < 64; ++d) tk = fmaf(Vb[(long long)k * 64 + d], Mgb[d], tk);
-          tk = rs_bf(tk, big);
-          const float raw = rs_bf(Pb[k] * rs_bf(tk - tqb, big), big);
-          float r = rs_knorm(gn, K, 2.0f * raw + ssq[k], Pb[k]);
-          float c = rs_knorm(gn, K, ssq[k] - 2.0f * raw, -Pb[k]);
-          if (maxim) {
-            r = -r;
-            c = -c;
-          }
+          const float r = maxim ? -rq[k] : rq[k];
+          const float c = maxim ? -cq[k] : cq[k];
           rq[k] = drop[k] ? r : -INFINITY;
           cq[k] = drop[k] ? -INFINITY : c;
           if (drop[k]) {
@@ -634,6 +659,37 @@ int oracle_restore_swap(const float* A, const float* V, const float* M, const in
   }
   free(Vb); free(Mb); free(termk); free(Pb); free(s); free(scut); free(ssq); free(rq); free(cq);
   free(drop); free(best); free(sel); free(sel2); free(valid); free(keys); free(idx);
+  return 0;
+}
+
+/* The quantities oracle_restore_swap ranks by, for a caller-given drop set, through the same
+ * helpers (for checks against first principles): s and the initial cut's key scut
+ * [H][q_blk][n_cand], J [H][q_blk] of the drop set, and the round marginals rq / cq
+ * [H][q_blk][n_cand] (rs_round_qualities: every candidate, unmasked, minimisation sign).
+ * drop [H][q_blk][n_cand] uint8, 1 = dropped.
+ * flags as for oracle_restore_swap (only RS_BF16 and RS_NO_RENORM matter here). */
+int oracle_rs_probe(const float* A, const float* V, const float* M, const uint8_t* drop, int H, int q_blk, int kb_p,
+                    int n_cand, int flags, float* s_out, float* scut_out, float* J_out, float* rq_out,
+                    float* cq_out) {
+  const int big = (flags & RS_BF16) != 0, renorm = (flags & RS_NO_RENORM) == 0;
+  float* Vb = (float*)malloc(sizeof(float) * (size_t)kb_p * 64);
+  float* Mb = (float*)malloc(sizeof(float) * 64 * 64);
+  float* termk = (float*)malloc(sizeof(float) * (size_t)kb_p);
+  float* Pb = (float*)malloc(sizeof(float) * (size_t)kb_p);
+  float* ssq = (float*)malloc(sizeof(float) * (size_t)n_cand);
+  for (int h = 0; h < H; ++h) {
+    const float* M32 = M + (long long)h * 4096;
+    rs_head_setup(M32, V + (long long)h * kb_p * 64, kb_p, n_cand, big, Mb, Vb, termk);
+    for (int q = 0; q < q_blk; ++q) {
+      const long long row = (long long)h * q_blk + q;
+      float vq[64], tm;
+      rs_row_setup(A + row * kb_p, Mb, Vb, termk, kb_p, n_cand, big, renorm, Pb, vq, &tm, s_out + row * n_cand,
+                   scut_out + row * n_cand, ssq);
+      J_out[row] = rs_round_qualities(Pb, drop + row * n_cand, Vb, M32, vq, tm, ssq, n_cand, big,
+                                      rq_out + row * n_cand, cq_out + row * n_cand);
+    }
+  }
+  free(Vb); free(Mb); free(termk); free(Pb); free(ssq);
   return 0;
 }
 

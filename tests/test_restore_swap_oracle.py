@@ -7,7 +7,14 @@
   casts, on inputs whose dot products are exact in fp32 (so torch's summation order
   cannot matter and only the rounding points are compared);
 * invariants: the kept count is min(nts, n_cand); track_best never returns a set with a
-  larger J than the initial cut; the reported J is the float64 J of the returned set."""
+  larger J than the initial cut; the reported J is the float64 J of the returned set;
+* the identities the reference states, each computed from its definition in float64
+  through oracle_rs_probe (the helpers the rounds themselves rank with): the expanded
+  quadratic form equals the direct one and s_k^2 = ||e_k||^2_M (projected.py:259-288,
+  415-420); J({j}) = (s_j/(1-p_j))^2, the square of the cut key (:294-302); each round
+  marginal equals the brute-force J(D) - J(D -/+ {k}) (:191-211); M = I gives the
+  head-space damage p ||v_bar_query - V_k|| (attention.py:562-564). Planting a wrong sign,
+  grouping, index or mass term in the C oracle's score, objective or marginals fails them."""
 
 import numpy as np
 import pytest
@@ -80,3 +87,120 @@ def test_invariants_and_objective():
             J64 = ref.drift_objective64(A, V, M, keep, n_cand).numpy()
             if not bf:  # fp32 oracle arithmetic vs float64 on the same set
                 np.testing.assert_allclose(J, J64, rtol=2e-4, atol=1e-9)
+
+
+# ---- first-principles identities (float64), through oracle_rs_probe --------------------
+# The probe runs the helpers oracle_restore_swap itself ranks with (rs_row_setup for s,
+# rs_round_qualities for J and the round marginals), so these pin the rounds' arithmetic
+# against the definitions in src/ress/scoring/projected.py, not against a second
+# transcription of its expanded formulas.
+
+
+def _softmax_problem(seed, H=2, q_blk=3, kb_p=40, sinks=2, identity_M=False, partial_mass=False):
+    """Rows of A are full softmaxes over all kb_p blocks (total mass 1, the last `sinks`
+    blocks never droppable), V random, M = W^T W (PSD) or the identity. partial_mass: each
+    row scaled to a total mass in [0.5, 0.95], as when part of the mass lies outside the
+    map, so K = total mass - dropped mass differs from 1 - dropped mass."""
+    rng = np.random.default_rng(seed)
+    logits = rng.normal(size=(H, q_blk, kb_p)) * rng.uniform(0.5, 2.5, size=(H, q_blk, 1))
+    A = np.exp(logits - logits.max(-1, keepdims=True))
+    A = A / A.sum(-1, keepdims=True)
+    if partial_mass:
+        A = A * rng.uniform(0.5, 0.95, size=(H, q_blk, 1))
+    A = A.astype(np.float32)
+    V = rng.normal(size=(H, kb_p, 64)).astype(np.float32)
+    if identity_M:
+        M = np.broadcast_to(np.eye(64, dtype=np.float32), (H, 64, 64)).copy()
+    else:
+        W = (rng.normal(size=(H, 64, 64)) / 8).astype(np.float32)
+        M = np.einsum("hji,hjk->hik", W, W).astype(np.float32)
+    return A, V, M, kb_p - sinks
+
+
+def _J64(A, V, M, drop, n_cand):
+    """J(D) = ||g||^2_M / K^2 by its definition (projected.py:290-302): g = sum_{j in D}
+    p_j (v_bar_query - V_j) with v_bar_query = sum over all blocks of p V, K = total mass
+    minus the dropped mass; float64, direct (no expansion). drop (..., n_cand) bool."""
+    A64, V64, M64 = A.astype(np.float64), V.astype(np.float64), M.astype(np.float64)
+    vq = np.einsum("hqk,hkd->hqd", A64, V64)
+    Pd = A64[..., :n_cand] * drop
+    g = Pd.sum(-1)[..., None] * vq - np.einsum("hqk,hkd->hqd", Pd, V64[:, :n_cand])
+    G = np.einsum("hqi,hij,hqj->hq", g, M64, g)
+    K = A64.sum(-1) - Pd.sum(-1)
+    return G / K ** 2
+
+
+def test_score_is_direct_quadratic_form():
+    """s_k = p_k sqrt((v_bar_query - V_k)^T M (v_bar_query - V_k)): the oracle's expanded
+    term_q - 2 cross + term_k (quadratic_deviation, projected.py:259-288) equals the direct
+    form, and s_k^2 = ||e_k||^2_M for e_k = p_k (v_bar_query - V_k) (projected.py:415-420).
+    Tolerance: fp32 cancellation of the expansion, eps32-scaled by its three terms."""
+    for seed in range(6):
+        A, V, M, n = _softmax_problem(seed)
+        s, _, _, _, _ = oracle.rs_probe(A, V, M, np.zeros(A.shape[:2] + (n,), bool), n)
+        A64, V64, M64 = A.astype(np.float64), V.astype(np.float64), M.astype(np.float64)
+        vq = np.einsum("hqk,hkd->hqd", A64, V64)
+        e = vq[:, :, None, :] - V64[:, None, :n, :]
+        quad = np.einsum("hqki,hij,hqkj->hqk", e, M64, e)
+        p = A64[..., :n]
+        tq = np.einsum("hqi,hij,hqj->hq", vq, M64, vq)[..., None]
+        tk = np.einsum("hki,hij,hkj->hk", V64[:, :n], M64, V64[:, :n])[:, None, :]
+        cr = np.abs(np.einsum("hqi,hij,hkj->hqk", vq, M64, V64[:, :n]))
+        tol = p ** 2 * 4e-6 * (tq + 2 * cr + tk) + 1e-30
+        assert (np.abs(s.astype(np.float64) ** 2 - p ** 2 * quad) <= tol).all(), seed
+
+
+def test_single_drop_objective_is_renormalized_score():
+    """J({j}) = (s_j / (1 - p_j))^2 (projected.py:294-302): the objective of dropping one
+    candidate alone, by definition and as the oracle's rs_objective computes it, equals the
+    square of the renormalised cut key the initial cut ranks by."""
+    for seed in range(3):
+        A, V, M, n = _softmax_problem(50 + seed, kb_p=24)
+        H, Q = A.shape[:2]
+        for j in range(n):
+            drop = np.zeros((H, Q, n), bool)
+            drop[..., j] = True
+            s, scut, J, _, _ = oracle.rs_probe(A, V, M, drop, n)
+            p = A[..., j].astype(np.float64)
+            closed = (s[..., j].astype(np.float64) / (1.0 - p)) ** 2
+            np.testing.assert_allclose(J, closed, rtol=2e-5, atol=1e-30)
+            np.testing.assert_allclose(J, scut[..., j].astype(np.float64) ** 2, rtol=2e-5, atol=1e-30)
+            np.testing.assert_allclose(J, _J64(A, V, M, drop, n), rtol=2e-5, atol=1e-30)
+
+
+def test_round_qualities_are_bruteforce_objective_differences():
+    """kept_mass_norm_quality (projected.py:191-211) as the round uses it: restoring dropped
+    k scores J(D) - J(D - {k}), dropping kept k scores J(D) - J(D + {k}), both by the
+    float64 definition of J. Tolerance: the fp32 grouped form's rounding, relative to the
+    row's largest marginal."""
+    rng = np.random.default_rng(7)
+    for seed in range(6):
+        A, V, M, n = _softmax_problem(80 + seed, kb_p=36, partial_mass=seed % 2 == 1)
+        H, Q = A.shape[:2]
+        drop = rng.random((H, Q, n)) < rng.uniform(0.3, 0.8)
+        _, _, J, rq, cq = oracle.rs_probe(A, V, M, drop, n)
+        J0 = _J64(A, V, M, drop, n)
+        np.testing.assert_allclose(J, J0, rtol=2e-5, atol=1e-30)
+        want = np.zeros((H, Q, n))
+        for k in range(n):
+            d2 = drop.copy()
+            d2[..., k] = ~drop[..., k]
+            want[..., k] = J0 - _J64(A, V, M, d2, n)
+        got = np.where(drop, rq, cq).astype(np.float64)
+        scale = np.abs(want).max(-1, keepdims=True)
+        assert (np.abs(got - want) <= 2e-4 * scale + 1e-6 * np.abs(J0)[..., None]).all(), seed
+        # the marginal has the sign of the change of J, so a beneficial move is a positive one
+        big = np.abs(want) > 1e-2 * scale
+        assert (np.sign(got[big]) == np.sign(want[big])).all(), seed
+
+
+def test_identity_metric_is_head_space_damage():
+    """M = I reduces the score to the head-space damage p_k ||v_bar_query - V_k||_2
+    (src/ress/models/attention.py:562-564, the _nowo recipes)."""
+    for seed in range(4):
+        A, V, M, n = _softmax_problem(120 + seed, identity_M=True)
+        s, _, _, _, _ = oracle.rs_probe(A, V, M, np.zeros(A.shape[:2] + (n,), bool), n)
+        A64, V64 = A.astype(np.float64), V.astype(np.float64)
+        vq = np.einsum("hqk,hkd->hqd", A64, V64)
+        dmg = A64[..., :n] * np.linalg.norm(vq[:, :, None, :] - V64[:, None, :n, :], axis=-1)
+        np.testing.assert_allclose(s, dmg, rtol=5e-5, atol=1e-7)
