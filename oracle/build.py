@@ -14,7 +14,8 @@ LIB = os.path.join(HERE, "liboracle.so")
 def build_oracle():
     src = os.path.join(HERE, "ress_oracle.c")
     tmp = LIB + ".tmp"
-    cmd = ["gcc", "-O2", "-std=c11", "-ffp-contract=off", "-fno-fast-math", "-fPIC", "-shared", "-o", tmp, src, "-lm"]
+    cmd = ["gcc", "-O2", "-std=c11", "-fopenmp", "-ffp-contract=off", "-fno-fast-math", "-fPIC", "-shared", "-o", tmp, src,
+           "-lm"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"oracle build failed:\n{' '.join(cmd)}\n{r.stderr}")

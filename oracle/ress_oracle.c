@@ -13,7 +13,10 @@
  * only as the checker. The product library never links or calls it.
  *
  * Tensors are contiguous row-major. bf16 values are passed as uint16_t bit patterns.
+ * Rows (heads, query blocks) are independent; the loops over them run under OpenMP, which
+ * changes no row's arithmetic.
  */
+#define _GNU_SOURCE /* qsort_r */
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -121,8 +124,9 @@ void oracle_prep_qkv(const uint16_t* q, const uint16_t* k, const uint16_t* v, in
   const int N = frames * P, Tk = N;
   const int qbp = cdiv(m.T_p, 128), qbs = cdiv(m.T_s, 128), qbt = qbp + qbs;
   const int kbt = cdiv(Tk, 64), kbp = cdiv(m.T_p, 64);
-  int rows[128];
+#pragma omp parallel for schedule(dynamic, 1)
   for (int bh = 0; bh < BH; ++bh) {
+    int rows[128];
     const uint16_t* qh = q + (long long)bh * N * 64;
     const uint16_t* kh = k + (long long)bh * N * 64;
     const uint16_t* vh = v + (long long)bh * N * 64;
@@ -222,9 +226,12 @@ static float sum64(const float* x, int n) {
 
 void oracle_pooled_scores(const float* pooled_q, const float* pooled_k, int BH, int q_blk, int kb_p, int n_cand,
                           float scale, float* attn_full, float* attn_cond) {
+#pragma omp parallel
+  {
   float* s = (float*)malloc(sizeof(float) * (kb_p > 0 ? kb_p : 1));
-  for (int bh = 0; bh < BH; ++bh)
-    for (int qb = 0; qb < q_blk; ++qb) {
+#pragma omp for schedule(dynamic, 4)
+  for (long long row = 0; row < (long long)BH * q_blk; ++row) {
+      const int bh = (int)(row / q_blk), qb = (int)(row % q_blk);
       const float* pq = pooled_q + ((long long)bh * q_blk + qb) * 64;
       float m = -INFINITY;
       for (int kb = 0; kb < kb_p; ++kb) {
@@ -244,6 +251,7 @@ void oracle_pooled_scores(const float* pooled_q, const float* pooled_k, int BH, 
       for (int kb = 0; kb < n_cand; ++kb) cond[kb] = full[kb] / rs;
     }
   free(s);
+  }
 }
 
 /* ---- baseline budget ------------------------------------------------------------------
@@ -256,8 +264,11 @@ static int cmp_desc(const void* a, const void* b) {
   return (x < y) - (x > y);
 }
 void oracle_baseline_budget(const float* attn_cond, long long rows, int n, float cdf_threshold, int topk, int* out) {
-  float* v = (float*)malloc(sizeof(float) * (n > 0 ? n : 1));
   const float thr = cdf_threshold + 0x1.4f8b58p-17f;
+#pragma omp parallel
+  {
+  float* v = (float*)malloc(sizeof(float) * (n > 0 ? n : 1));
+#pragma omp for schedule(dynamic, 16)
   for (long long r = 0; r < rows; ++r) {
     if (cdf_threshold < 0.0f) {
       out[r] = topk;
@@ -274,6 +285,7 @@ void oracle_baseline_budget(const float* attn_cond, long long rows, int n, float
     out[r] = count > topk ? count : topk;
   }
   free(v);
+  }
 }
 
 /* ---- HeSS head reallocation -----------------------------------------------------------
@@ -343,19 +355,22 @@ int oracle_head_budget(const int* baseline, int B, int H, int q_blk, const float
  * sorting indices -- then the trailing sink columns (always kept) and any leading
  * attention_sink columns (external/patches/spargeattn.patch:61-65). LUT = ascending kept
  * columns (block_map_lut_triton, attention.py:224). Rows q_blk_sel..q_blk_total-1 are dense. */
-static const float* g_keys;
-static int cmp_rank(const void* a, const void* b) {
+static int cmp_rank(const void* a, const void* b, void* ctx) {
+  const float* keys = (const float*)ctx;
   int i = *(const int*)a, j = *(const int*)b;
-  uint32_t ki = order_key(g_keys[i]), kj = order_key(g_keys[j]);
+  uint32_t ki = order_key(keys[i]), kj = order_key(keys[j]);
   if (ki != kj) return ki > kj ? -1 : 1;
   return (i > j) - (i < j);
 }
 void oracle_select_blocks(const float* rank_key, const int* counts, int BH, int q_blk_sel, int q_blk_total,
                           int n_cand, int kb_tot, int sink_lead, int min_select, uint8_t* map, int* lut, int* nvalid) {
+#pragma omp parallel
+  {
   int* idx = (int*)malloc(sizeof(int) * (n_cand > 0 ? n_cand : 1));
   uint8_t* keep = (uint8_t*)malloc(kb_tot);
-  for (int bh = 0; bh < BH; ++bh)
-    for (int qb = 0; qb < q_blk_total; ++qb) {
+#pragma omp for schedule(dynamic, 4)
+  for (long long row = 0; row < (long long)BH * q_blk_total; ++row) {
+      const int bh = (int)(row / q_blk_total), qb = (int)(row % q_blk_total);
       if (qb >= q_blk_sel) {
         for (int c = 0; c < kb_tot; ++c) keep[c] = 1;
       } else {
@@ -363,9 +378,8 @@ void oracle_select_blocks(const float* rank_key, const int* counts, int BH, int 
         int n = counts[srow];
         n = n < min_select ? min_select : n;
         n = n < 0 ? 0 : (n > n_cand ? n_cand : n);
-        g_keys = rank_key + srow * n_cand;
         for (int i = 0; i < n_cand; ++i) idx[i] = i;
-        qsort(idx, n_cand, sizeof(int), cmp_rank);
+        qsort_r(idx, n_cand, sizeof(int), cmp_rank, (void*)(rank_key + srow * n_cand));
         memset(keep, 0, kb_tot);
         for (int i = 0; i < n; ++i) keep[idx[i]] = 1;
         for (int c = n_cand; c < kb_tot; ++c) keep[c] = 1;
@@ -380,6 +394,7 @@ void oracle_select_blocks(const float* rank_key, const int* counts, int BH, int 
     }
   free(idx);
   free(keep);
+  }
 }
 
 /* vectorised helpers for tests */
@@ -425,10 +440,10 @@ static inline uint32_t rs_key(float x) {
   uint32_t u = fbits(x);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
-static const uint32_t* g_rs_keys;
-static int cmp_rs(const void* a, const void* b) {
+static int cmp_rs(const void* a, const void* b, void* ctx) {
+  const uint32_t* keys = (const uint32_t*)ctx;
   int i = *(const int*)a, j = *(const int*)b;
-  if (g_rs_keys[i] != g_rs_keys[j]) return g_rs_keys[i] > g_rs_keys[j] ? -1 : 1;
+  if (keys[i] != keys[j]) return keys[i] > keys[j] ? -1 : 1;
   return (i > j) - (i < j);
 }
 /* top-m of key among valid (ties: lowest index) -> sel[] = 1 */
@@ -439,8 +454,7 @@ static void rs_top_m(const float* q, const uint8_t* valid, int n, int m, uint8_t
     keys[i] = rs_key(q[i]);
     if (valid[i]) idx[c++] = i;
   }
-  g_rs_keys = keys;
-  qsort(idx, c, sizeof(int), cmp_rs);
+  qsort_r(idx, c, sizeof(int), cmp_rs, keys);
   for (int i = 0; i < m && i < c; ++i) sel[idx[i]] = 1;
 }
 /* kept_mass_norm_quality (projected.py:191-211), grouping ((G*u)*(2K+u))/(K*K) - dG, / Kn^2 */
@@ -486,6 +500,7 @@ static void rs_head_setup(const float* M32, const float* Vh, int kb_p, int n_can
                           float* termk) {
   for (int i = 0; i < 4096; ++i) Mb[i] = rs_bf(M32[i], big);
   for (long long i = 0; i < (long long)kb_p * 64; ++i) Vb[i] = rs_bf(Vh[i], big);
+#pragma omp parallel for schedule(static)
   for (int k = 0; k < n_cand; ++k) {
     float tk = 0.0f;
     for (int i = 0; i < 64; ++i) {
@@ -559,106 +574,140 @@ static float rs_round_qualities(const float* Pb, const uint8_t* drop, const floa
   return J;
 }
 
-int oracle_restore_swap(const float* A, const float* V, const float* M, const int* nts, int H, int q_blk, int kb_p,
-                        int n_cand, int n_iters, double restore_frac, double decay, int flags, uint8_t* keep,
-                        float* obj_out, float* s_out) {
+/* Per-row scratch of oracle_restore_swap (one per thread). */
+typedef struct {
+  float *Pb, *s, *scut, *ssq, *rq, *cq;
+  uint8_t *drop, *best, *sel, *sel2, *valid;
+  uint32_t* keys;
+  int* idx;
+} rs_scratch;
+
+static void rs_scratch_alloc(rs_scratch* w, int kb_p, int n_cand) {
+  const size_t n = (size_t)(n_cand > 0 ? n_cand : 1);
+  w->Pb = (float*)malloc(sizeof(float) * (size_t)(kb_p > 0 ? kb_p : 1));
+  w->s = (float*)malloc(sizeof(float) * n);
+  w->scut = (float*)malloc(sizeof(float) * n);
+  w->ssq = (float*)malloc(sizeof(float) * n);
+  w->rq = (float*)malloc(sizeof(float) * n);
+  w->cq = (float*)malloc(sizeof(float) * n);
+  w->drop = (uint8_t*)malloc(n);
+  w->best = (uint8_t*)malloc(n);
+  w->sel = (uint8_t*)malloc(n);
+  w->sel2 = (uint8_t*)malloc(n);
+  w->valid = (uint8_t*)malloc(n);
+  w->keys = (uint32_t*)malloc(sizeof(uint32_t) * n);
+  w->idx = (int*)malloc(sizeof(int) * n);
+}
+
+static void rs_scratch_free(rs_scratch* w) {
+  free(w->Pb); free(w->s); free(w->scut); free(w->ssq); free(w->rq); free(w->cq);
+  free(w->drop); free(w->best); free(w->sel); free(w->sel2); free(w->valid); free(w->keys); free(w->idx);
+}
+
+/* One (head, query-block) row: initial cut, n_iters rounds, track-best (projected.py:756-1058). */
+static void rs_row(const float* Arow, const float* Mb, const float* Vb, const float* termk, const float* M32, int nts_row,
+                   int kb_p, int n_cand, int n_iters, double restore_frac, double decay, int flags, rs_scratch* w,
+                   uint8_t* keep_row, float* obj, float* s_row) {
   const int big = (flags & RS_BF16) != 0, track = (flags & RS_TRACK_BEST) != 0;
   const int renorm = (flags & RS_NO_RENORM) == 0;
   const int maxim = (flags & RS_MAXIMIZE) != 0, inv = (flags & RS_INVERT_CUT) != 0;
-  float* Vb = (float*)malloc(sizeof(float) * (size_t)kb_p * 64);
+  float *Pb = w->Pb, *s = w->s, *scut = w->scut, *ssq = w->ssq, *rq = w->rq, *cq = w->cq;
+  uint8_t *drop = w->drop, *best = w->best, *sel = w->sel, *sel2 = w->sel2, *valid = w->valid;
+  float vq[64], tm;
+  rs_row_setup(Arow, Mb, Vb, termk, kb_p, n_cand, big, renorm, Pb, vq, &tm, s, scut, ssq);
+  if (s_row)
+    for (int k = 0; k < n_cand; ++k) s_row[k] = s[k];
+  /* initial one-shot cut: keep the top min(nts, n_cand) by s_cut (lowest under invert_cut) */
+  int nkeep = nts_row;
+  nkeep = nkeep < 0 ? 0 : (nkeep > n_cand ? n_cand : nkeep);
+  for (int k = 0; k < n_cand; ++k) {
+    valid[k] = 1;
+    rq[k] = inv ? -scut[k] : scut[k];
+  }
+  rs_top_m(rq, valid, n_cand, nkeep, sel, w->keys, w->idx);
+  for (int k = 0; k < n_cand; ++k) drop[k] = !sel[k];
+  float g[64], Mg[64], gn, K, sp;
+  float best_obj = 0.0f;
+  if (track) {
+    best_obj = rs_objective(Pb, drop, Vb, M32, vq, tm, n_cand, big, g, Mg, &gn, &K, &sp);
+    memcpy(best, drop, (size_t)n_cand);
+  }
+  double remaining = restore_frac;
+  for (int it = 0; it < n_iters; ++it) {
+    const double frac = remaining * decay;
+    remaining -= frac;
+    const int pic0 = (int)rintf((float)frac * (float)nts_row);
+    const float J = rs_round_qualities(Pb, drop, Vb, M32, vq, tm, ssq, n_cand, big, rq, cq);
+    if (track) {
+      const int better = maxim ? J > best_obj : J < best_obj;
+      if (better) {
+        best_obj = J;
+        memcpy(best, drop, (size_t)n_cand);
+      }
+    }
+    int n_drop = 0, n_kept = 0;
+    float rmax = -INFINITY;
+    for (int k = 0; k < n_cand; ++k) {
+      const float r = maxim ? -rq[k] : rq[k];
+      const float c = maxim ? -cq[k] : cq[k];
+      rq[k] = drop[k] ? r : -INFINITY;
+      cq[k] = drop[k] ? -INFINITY : c;
+      if (drop[k]) {
+        ++n_drop;
+        rmax = rq[k] > rmax ? rq[k] : rmax;
+      } else {
+        ++n_kept;
+      }
+    }
+    const int beneficial = rmax > 0.0f;
+    int pic = pic0;
+    if (beneficial && pic < 1) pic = 1;
+    int cnt = pic < n_drop ? pic : n_drop;
+    cnt = cnt < n_kept ? cnt : n_kept;
+    if (!beneficial) cnt = 0;
+    for (int k = 0; k < n_cand; ++k) valid[k] = drop[k];
+    rs_top_m(rq, valid, n_cand, cnt, sel, w->keys, w->idx);
+    for (int k = 0; k < n_cand; ++k) valid[k] = !drop[k];
+    rs_top_m(cq, valid, n_cand, cnt, sel2, w->keys, w->idx);
+    for (int k = 0; k < n_cand; ++k) drop[k] = (uint8_t)((drop[k] && !sel[k]) || sel2[k]);
+  }
+  float fin = 0.0f;
+  if (track || obj) fin = rs_objective(Pb, drop, Vb, M32, vq, tm, n_cand, big, g, Mg, &gn, &K, &sp);
+  if (track) {
+    const int better = maxim ? fin > best_obj : fin < best_obj;
+    if (!better) {
+      memcpy(drop, best, (size_t)n_cand);
+      fin = best_obj;
+    }
+  }
+  if (obj) *obj = fin;
+  for (int k = 0; k < n_cand; ++k) keep_row[k] = (uint8_t)!drop[k];
+}
+
+int oracle_restore_swap(const float* A, const float* V, const float* M, const int* nts, int H, int q_blk, int kb_p,
+                        int n_cand, int n_iters, double restore_frac, double decay, int flags, uint8_t* keep,
+                        float* obj_out, float* s_out) {
+  const int big = (flags & RS_BF16) != 0;
+  float* Vb = (float*)malloc(sizeof(float) * (size_t)(kb_p > 0 ? kb_p : 1) * 64);
   float* Mb = (float*)malloc(sizeof(float) * 64 * 64);
-  float* termk = (float*)malloc(sizeof(float) * (size_t)kb_p);
-  float* Pb = (float*)malloc(sizeof(float) * (size_t)kb_p);
-  float* s = (float*)malloc(sizeof(float) * (size_t)n_cand);
-  float* scut = (float*)malloc(sizeof(float) * (size_t)n_cand);
-  float* ssq = (float*)malloc(sizeof(float) * (size_t)n_cand);
-  float* rq = (float*)malloc(sizeof(float) * (size_t)n_cand);
-  float* cq = (float*)malloc(sizeof(float) * (size_t)n_cand);
-  uint8_t* drop = (uint8_t*)malloc((size_t)n_cand);
-  uint8_t* best = (uint8_t*)malloc((size_t)n_cand);
-  uint8_t* sel = (uint8_t*)malloc((size_t)n_cand);
-  uint8_t* sel2 = (uint8_t*)malloc((size_t)n_cand);
-  uint8_t* valid = (uint8_t*)malloc((size_t)n_cand);
-  uint32_t* keys = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)n_cand);
-  int* idx = (int*)malloc(sizeof(int) * (size_t)n_cand);
+  float* termk = (float*)malloc(sizeof(float) * (size_t)(kb_p > 0 ? kb_p : 1));
   for (int h = 0; h < H; ++h) {
     const float* M32 = M + (long long)h * 4096;
     rs_head_setup(M32, V + (long long)h * kb_p * 64, kb_p, n_cand, big, Mb, Vb, termk);
-    for (int q = 0; q < q_blk; ++q) {
-      const long long row = (long long)h * q_blk + q;
-      float vq[64], tm;
-      rs_row_setup(A + row * kb_p, Mb, Vb, termk, kb_p, n_cand, big, renorm, Pb, vq, &tm, s, scut, ssq);
-      if (s_out)
-        for (int k = 0; k < n_cand; ++k) s_out[row * n_cand + k] = s[k];
-      /* initial one-shot cut: keep the top min(nts, n_cand) by s_cut (lowest under invert_cut) */
-      int nkeep = nts[row];
-      nkeep = nkeep < 0 ? 0 : (nkeep > n_cand ? n_cand : nkeep);
-      for (int k = 0; k < n_cand; ++k) {
-        valid[k] = 1;
-        rq[k] = inv ? -scut[k] : scut[k];
+#pragma omp parallel
+    {
+      rs_scratch w;
+      rs_scratch_alloc(&w, kb_p, n_cand);
+#pragma omp for schedule(dynamic, 1)
+      for (int q = 0; q < q_blk; ++q) {
+        const long long row = (long long)h * q_blk + q;
+        rs_row(A + row * kb_p, Mb, Vb, termk, M32, nts[row], kb_p, n_cand, n_iters, restore_frac, decay, flags, &w,
+               keep + row * n_cand, obj_out ? obj_out + row : NULL, s_out ? s_out + row * n_cand : NULL);
       }
-      rs_top_m(rq, valid, n_cand, nkeep, sel, keys, idx);
-      for (int k = 0; k < n_cand; ++k) drop[k] = !sel[k];
-      float g[64], Mg[64], gn, K, sp;
-      float best_obj = 0.0f;
-      if (track) {
-        best_obj = rs_objective(Pb, drop, Vb, M32, vq, tm, n_cand, big, g, Mg, &gn, &K, &sp);
-        memcpy(best, drop, (size_t)n_cand);
-      }
-      double remaining = restore_frac;
-      for (int it = 0; it < n_iters; ++it) {
-        const double frac = remaining * decay;
-        remaining -= frac;
-        const int pic0 = (int)rintf((float)frac * (float)nts[row]);
-        const float J = rs_round_qualities(Pb, drop, Vb, M32, vq, tm, ssq, n_cand, big, rq, cq);
-        if (track) {
-          const int better = maxim ? J > best_obj : J < best_obj;
-          if (better) {
-            best_obj = J;
-            memcpy(best, drop, (size_t)n_cand);
-          }
-        }
-        int n_drop = 0, n_kept = 0;
-        float rmax = -INFINITY;
-        for (int k = 0; k < n_cand; ++k) {
-          const float r = maxim ? -rq[k] : rq[k];
-          const float c = maxim ? -cq[k] : cq[k];
-          rq[k] = drop[k] ? r : -INFINITY;
-          cq[k] = drop[k] ? -INFINITY : c;
-          if (drop[k]) {
-            ++n_drop;
-            rmax = rq[k] > rmax ? rq[k] : rmax;
-          } else {
-            ++n_kept;
-          }
-        }
-        const int beneficial = rmax > 0.0f;
-        int pic = pic0;
-        if (beneficial && pic < 1) pic = 1;
-        int cnt = pic < n_drop ? pic : n_drop;
-        cnt = cnt < n_kept ? cnt : n_kept;
-        if (!beneficial) cnt = 0;
-        for (int k = 0; k < n_cand; ++k) valid[k] = drop[k];
-        rs_top_m(rq, valid, n_cand, cnt, sel, keys, idx);
-        for (int k = 0; k < n_cand; ++k) valid[k] = !drop[k];
-        rs_top_m(cq, valid, n_cand, cnt, sel2, keys, idx);
-        for (int k = 0; k < n_cand; ++k) drop[k] = (uint8_t)((drop[k] && !sel[k]) || sel2[k]);
-      }
-      float fin = 0.0f;
-      if (track || obj_out) fin = rs_objective(Pb, drop, Vb, M32, vq, tm, n_cand, big, g, Mg, &gn, &K, &sp);
-      if (track) {
-        const int better = maxim ? fin > best_obj : fin < best_obj;
-        if (!better) {
-          memcpy(drop, best, (size_t)n_cand);
-          fin = best_obj;
-        }
-      }
-      if (obj_out) obj_out[row] = fin;
-      for (int k = 0; k < n_cand; ++k) keep[row * n_cand + k] = (uint8_t)!drop[k];
+      rs_scratch_free(&w);
     }
   }
-  free(Vb); free(Mb); free(termk); free(Pb); free(s); free(scut); free(ssq); free(rq); free(cq);
-  free(drop); free(best); free(sel); free(sel2); free(valid); free(keys); free(idx);
+  free(Vb); free(Mb); free(termk);
   return 0;
 }
 

@@ -72,13 +72,35 @@ class LayerResult:
     lut: torch.Tensor = None
     nvalid: torch.Tensor = None
     blocks: kernels.Blocks = None
+    # device-side budget status: number of HeSS columns that did not converge (0-dim int32)
+    unconverged: torch.Tensor = None
+    max_iters: int = None
+
+    def _raise_unconverged(self, n):
+        if n:
+            raise RuntimeError(f"adjust_attention_selection did not converge in {self.max_iters} iterations "
+                               f"({int(n)} query-block columns)")
+
+    def check(self):
+        """Raise RuntimeError if the layer's HeSS budget did not converge (reference
+        _proportional.py:112-113). Synchronises with the device."""
+        if self.unconverged is not None:
+            self._raise_unconverged(int(self.unconverged.item()))
 
     def sparsity(self):
         """Realized sparsity 1 - mean(final_map), sinks included (reference
-        attention.py:242). Synchronises with the device."""
+        attention.py:242). Synchronises with the device once, and raises there if the
+        layer's HeSS budget did not converge (see check)."""
         if self.final_map is None:
+            self.check()
             return 0.0
-        return 1.0 - self.final_map.float().mean().item()
+        vals = [1.0 - self.final_map.float().mean()]
+        if self.unconverged is not None:
+            vals.append(self.unconverged.float())
+        got = torch.stack(vals).tolist()
+        if len(got) > 1:
+            self._raise_unconverged(got[1])
+        return got[0]
 
 
 def _rank_key(block_criterion, attn_cond, attn_full, v_bar_full, counts, grid, M, hd):
@@ -147,10 +169,22 @@ def protect_own_frame_swap(final_map, attn_pooled, grid):
     return torch.cat([new_kept, fm[..., n:]], dim=-1)
 
 
+def sink_lead_blocks(attention_sink, grid):
+    """Leading key blocks forced on by an attention sink of `attention_sink` leading
+    tokens: ceil(attention_sink / 64) (SpargeAttn get_block_map_meansim_fuse_quant as
+    patched, external/patches/spargeattn.patch:61-65), at most the candidate count. On the
+    kernel's cat(patch, special) key grid the leading blocks hold the first frame's patch
+    keys; its special keys are already in the always-kept trailing blocks."""
+    n = int(attention_sink or 0)
+    if n < 0:
+        raise ValueError(f"attention_sink must be a token count >= 0, got {attention_sink!r}")
+    return min(-(-n // KBLK), grid.n_cand)
+
+
 def sparse_global_attention(q, k, v, grid, *, num_to_select=None, budget_fn=None, perhead_budget_fn=None,
                             joint_select_fn=None, block_criterion="probability", M=None, out=None,
                             out_dtype=torch.float32, keep_intermediates=False, qk_mode=None,
-                            protect_own_frame=False):
+                            protect_own_frame=False, attention_sink=0):
     """One layer's block-sparse global attention on the GPU.
 
     q, k, v: bf16 (B, H, frames*P, 64) in storage order (per frame S special then P-S
@@ -159,14 +193,21 @@ def sparse_global_attention(q, k, v, grid, *, num_to_select=None, budget_fn=None
     446-491, 510-581, 625). qk_mode: the QK^T operands, "bf16" (default), "i8x2" or
     "i8" (see kernels.Blocks); the block map does not depend on it. protect_own_frame:
     the budget-neutral own-frame swap on the selected map (protect_own_frame_swap).
+    attention_sink: leading tokens whose key blocks every row keeps on top of its budget
+    (sink_lead_blocks; 0 = none, the reference's ReSS default).
     Returns a LayerResult whose `out` is (B, H, frames*P, 64) in storage order."""
+    sink_lead = sink_lead_blocks(attention_sink, grid)
     blocks = kernels.prepare_blocks(q, k, v, grid, mode=qk_mode or DEFAULT_QK_MODE)
     attn_full, attn_cond = kernels.pooled_scores(blocks)
     v_bar_full = blocks.pooled_v.view(grid.B, grid.H, grid.kb_p, 64)
     counts = None
     final_map = None
+    unconverged, max_iters = None, None
     if joint_select_fn is not None:
         final_map = joint_select_fn(attn_cond, v_bar_full[..., :grid.n_cand, :], grid.sink_blocks)
+        if sink_lead and not protect_own_frame:
+            final_map = final_map.clone()
+            final_map[..., :sink_lead] = True
         lut, nvalid = kernels.lut_from_map(final_map, grid)
     else:
         if perhead_budget_fn is not None:
@@ -178,18 +219,23 @@ def sparse_global_attention(q, k, v, grid, *, num_to_select=None, budget_fn=None
         if counts is None:
             raise AssertionError("num_to_select (or budget_fn/perhead_budget_fn) required unless dense=True "
                                  "or joint_select_fn is given")
+        unconverged = getattr(counts, "ress_unconverged", None)
+        max_iters = getattr(counts, "ress_max_iters", None)
         if not torch.is_tensor(counts):
             counts = torch.full((grid.B, grid.H, grid.q_blk_p), int(counts), dtype=torch.int32, device=q.device)
         counts = counts.reshape(grid.B, grid.H, grid.q_blk_p)
         rank = _rank_key(block_criterion, attn_cond, attn_full, v_bar_full,
                          counts.clamp(min=min(MIN_NUM_TO_SELECT, grid.n_cand)) if block_criterion != "probability"
                          else counts, grid, M, 64)
-        final_map, lut, nvalid = kernels.select_blocks(rank, counts, grid, min(MIN_NUM_TO_SELECT, grid.n_cand))
+        final_map, lut, nvalid = kernels.select_blocks(rank, counts, grid, min(MIN_NUM_TO_SELECT, grid.n_cand),
+                                                       sink_lead=0 if protect_own_frame else sink_lead)
     if protect_own_frame and grid.q_blk_p:  # after either selection path, as the reference does
         final_map = protect_own_frame_swap(final_map, attn_full[..., :grid.n_cand], grid)
+        if sink_lead:  # forced blocks go on last, so the swap never trades one away
+            final_map[..., :sink_lead] = True
         lut, nvalid = kernels.lut_from_map(final_map, grid)
     o = kernels.sparse_attention(blocks, lut, nvalid, out=out, out_dtype=out_dtype)
-    res = LayerResult(out=o, final_map=final_map)
+    res = LayerResult(out=o, final_map=final_map, unconverged=unconverged, max_iters=max_iters)
     if keep_intermediates:
         res.attn_full, res.attn_cond, res.v_bar_full = attn_full, attn_cond, v_bar_full
         res.counts, res.lut, res.nvalid, res.blocks = counts, lut, nvalid, blocks
@@ -213,9 +259,15 @@ def _dense_storage(q, k, v, shp):
 def ress_attention_forward(self, x, pos, num_to_select=None, budget_fn=None, perhead_budget_fn=None,
                            joint_select_fn=None, block_criterion="probability", pool_mode="avg",
                            num_special_tokens=5, num_heads=16, shape=None, aux_store=None, aux_full=True,
-                           dense=False, retain_output_grad=False, pooled_fallback=False, protect_own_frame=False):
+                           dense=False, retain_output_grad=False, pooled_fallback=False, protect_own_frame=False,
+                           attention_sink=0):
     """Replacement forward of a global-attention block (reference attention.py:296-659),
-    same arguments and return value: (B, N*P, dim) after the W_O projection."""
+    same arguments and return value: (B, N*P, dim) after the W_O projection.
+    attention_sink (not a reference argument; default 0 = the reference's behaviour):
+    leading tokens whose key blocks every row keeps, as sparse_global_attention. When
+    aux_store is given the forward synchronises once for the realized sparsity and raises
+    there if the HeSS budget did not converge; without it the forward does not synchronise
+    (LayerResult.check is the deferred check)."""
     if pool_mode != "avg":
         raise NotImplementedError("only avg pooling (the reference default) is implemented")
     q, k, v, shp = compute_qkv(self, x, pos, num_special_tokens=num_special_tokens, num_heads=num_heads,
@@ -233,7 +285,8 @@ def ress_attention_forward(self, x, pos, num_to_select=None, budget_fn=None, per
         res = sparse_global_attention(
             qb, kbf, vbf, grid, num_to_select=num_to_select, budget_fn=budget_fn, perhead_budget_fn=perhead_budget_fn,
             joint_select_fn=joint_select_fn, block_criterion=block_criterion, M=getattr(self, "M", None),
-            keep_intermediates=aux_store is not None and aux_full, protect_own_frame=protect_own_frame)
+            keep_intermediates=aux_store is not None and aux_full, protect_own_frame=protect_own_frame,
+            attention_sink=attention_sink)
         x_out = res.out
         sparsity = res.sparsity() if aux_store is not None else None
     if aux_store is not None:

@@ -92,7 +92,7 @@ class HessBudget:
     score_cam / score_pc: (3, n_layers, n_heads) tables, as tensors or `.pt` paths (read
     with torch.load(weights_only=True)); index `qkv_idx` (0 = W_Q) is used."""
 
-    def __init__(self, score_cam, score_pc, lam=0.5, qkv_idx=0, floor_frac=None, layer_slice=None):
+    def __init__(self, score_cam, score_pc, lam=0.5, qkv_idx=0, floor_frac=None, layer_slice=None, max_iters=1000):
         raw_cam = _load_table(score_cam, qkv_idx)
         raw_pc = _load_table(score_pc, qkv_idx)
         if layer_slice is not None:
@@ -104,6 +104,7 @@ class HessBudget:
         if floor_frac is not None:
             raise NotImplementedError("floor_frac is not on the HeSS path")
         self.floor_frac = None
+        self.max_iters = max_iters
         self._norm_cache = {}
 
     @property
@@ -119,8 +120,19 @@ class HessBudget:
         return t
 
     def num_to_select(self, layer_idx, attn_pooled, sparse_ratio=None, cdf_threshold=None, beta=1.0):
+        """Counts (B, nh, q_blk) int32 on the device, without a host sync. The reference
+        raises RuntimeError when the redistribution does not converge within max_iters
+        (_proportional.py:112-113), which costs it a sync per iteration. Here the kernel
+        reports each column's iteration count on the device and the returned tensor carries
+        the number of non-converged columns as `ress_unconverged` (0-dim int32); the layer
+        raises at its next host sync (LayerResult.check / .sparsity)."""
         baseline = compute_baseline_num_to_select(attn_pooled, sparse_ratio, cdf_threshold)
         max_val = attn_pooled.shape[-1]
         nts = baseline if baseline.dim() == 3 else baseline.unsqueeze(0)
-        out = kernels.head_budget(nts, self._scores_norm(layer_idx, attn_pooled.device), beta, max_val)
-        return out if baseline.dim() == 3 else out.squeeze(0)
+        iters = torch.empty(nts.shape[0], nts.shape[2], dtype=torch.int32, device=nts.device)
+        out = kernels.head_budget(nts, self._scores_norm(layer_idx, attn_pooled.device), beta, max_val,
+                                  max_iters=self.max_iters, iters_out=iters)
+        out = out if baseline.dim() == 3 else out.squeeze(0)
+        out.ress_unconverged = (iters < 0).sum(dtype=torch.int32)
+        out.ress_max_iters = self.max_iters
+        return out

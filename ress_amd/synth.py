@@ -11,7 +11,9 @@ GPU host build identical tensors; bf16 only at the end):
   axis and divides by its in-bounds cell count), then each channel rescaled to unit
   standard deviation over the whole field
 * per head, Q/K/V = z @ W + noise * N(0,1), W (rank x 64) ~ N(0, 1/rank), with
-  W_K = W_Q + 0.5 * N(0, 1/rank) so nearby tokens attend to each other; noise = 0.1
+  W_K = W_Q + 0.5 * N(0, 1/rank) so nearby tokens attend to each other; noise = 0.1.
+  Each (batch, head) draws from its own stream, SeedSequence([seed, 1, b*H + h]), so the
+  heads are generated in parallel and head h is the same tensor whatever H is.
 * 5 special tokens per frame (1 camera + 4 register) projected from N(0,1) latents
 * patch tokens of every frame in generalized-Hilbert order; storage per frame is
   [5 special, 1369 patch] -> tensors (B, H, frames*1374, 64) bf16.
@@ -20,7 +22,9 @@ The Hilbert order is the generalized Hilbert ("gilbert") curve for arbitrary rec
 (J. Cerveny's published construction), computed here with an explicit work stack.
 """
 
+import concurrent.futures
 import math
+import os
 
 import numpy as np
 import torch
@@ -95,12 +99,22 @@ def _box_blur(z, k=8):
     return out
 
 
-def _project(z, W):
-    """z (..., rank) @ W (rank, D) as an explicit sum over rank (deterministic order)."""
-    out = np.zeros(z.shape[:-1] + (W.shape[1],))
-    for r in range(W.shape[0]):
-        out += z[..., r:r + 1] * W[r]
-    return out
+def _project(z, W, chunk=512):
+    """z (..., rank) @ W (rank, D) as an explicit sum over rank (deterministic order:
+    ((z_0 W_0 + z_1 W_1) + z_2 W_2) + ..., each product rounded before its add), in
+    place over cache-sized row chunks."""
+    zf = z.reshape(-1, z.shape[-1])
+    out = np.empty((zf.shape[0], W.shape[1]))
+    tmp = np.empty((min(chunk, zf.shape[0]), W.shape[1]))
+    for i in range(0, zf.shape[0], chunk):
+        o = out[i:i + chunk]
+        t = tmp[:o.shape[0]]
+        zc = zf[i:i + chunk]
+        np.multiply(zc[:, 0:1], W[0], out=o)
+        for r in range(1, W.shape[0]):
+            np.multiply(zc[:, r:r + 1], W[r], out=t)
+            np.add(o, t, out=o)
+    return out.reshape(z.shape[:-1] + (W.shape[1],))
 
 
 def make_layer_qkv(frames, H=16, D=64, B=1, rank=16, seed=0, corr="shared", rho=0.6, ar=0.98, noise=0.1,
@@ -129,20 +143,26 @@ def make_layer_qkv(frames, H=16, D=64, B=1, rank=16, seed=0, corr="shared", rho=
     special = rng.standard_normal((frames, S, rank))
     lat = np.concatenate([special, patch], axis=1)  # (frames, P, rank)
     P = G * G + S
-    out = []
-    for _ in range(3):
-        out.append(np.empty((B, H, frames * P, D), dtype=np.float32))
-    for b in range(B):
-        for h in range(H):
+    out = [torch.empty((B, H, frames * P, D), dtype=torch.bfloat16) for _ in range(3)]
+
+    def one_head(bh):
+        b, h = divmod(bh, H)
+        hrng = np.random.default_rng(np.random.SeedSequence([seed, 1, bh]))
+        Wq = hrng.standard_normal((rank, D)) / math.sqrt(rank)
+        Wk = Wq + 0.5 * hrng.standard_normal((rank, D)) / math.sqrt(rank)
+        Wv = hrng.standard_normal((rank, D)) / math.sqrt(rank)
+        for t, W in enumerate((Wq, Wk, Wv)):
+            x = _project(lat, W)
+            x += noise * hrng.standard_normal((frames, P, D))
+            out[t][b, h] = torch.from_numpy(x.reshape(frames * P, D).astype(np.float32))
+        return bh
+
+    workers = max(1, min(B * H, os.cpu_count() or 1, 16))
+    with concurrent.futures.ThreadPoolExecutor(workers) as ex:
+        for i, _ in enumerate(ex.map(one_head, range(B * H))):
             if progress:
-                progress(f"head {b * H + h + 1}/{B * H}")
-            Wq = rng.standard_normal((rank, D)) / math.sqrt(rank)
-            Wk = Wq + 0.5 * rng.standard_normal((rank, D)) / math.sqrt(rank)
-            Wv = rng.standard_normal((rank, D)) / math.sqrt(rank)
-            for t, W in enumerate((Wq, Wk, Wv)):
-                x = _project(lat, W) + noise * rng.standard_normal((frames, P, D))
-                out[t][b, h] = x.reshape(frames * P, D)
-    q, k, v = (torch.from_numpy(a).to(torch.bfloat16).to(device) for a in out)
+                progress(f"head {i + 1}/{B * H}")
+    q, k, v = (a.to(device) for a in out)
     return q, k, v, {"frames": frames, "P": P, "S": S}
 
 

@@ -1,57 +1,77 @@
 """Installing the block-sparse forward on a model's global-attention blocks
-(reference src/ress/models/wiring.py)."""
+(the interface of the reference's src/ress/models/wiring.py:33-109).
 
-from types import MethodType
+`wire_ress_attention(model, blocks)` gives each block's attention module a
+`SparseAttentionForward` as its `forward`. The object reads the module's per-call
+configuration attributes (set by set_static_budget) at every call, from one table,
+`CALL_ATTRIBUTES`, and hands them to `ress_attention_forward`. The block list is recorded
+on the model for `global_blocks`.
+"""
 
 from ress_amd.attention import ress_attention_forward
+
+# Module attribute read at call time -> its value when the attribute is absent. Each is
+# passed to ress_attention_forward under the same name.
+CALL_ATTRIBUTES = (
+    ("num_to_select", None),
+    ("budget_fn", None),
+    ("perhead_budget_fn", None),
+    ("joint_select_fn", None),
+    ("block_criterion", "probability"),
+    ("dense", False),
+    ("retain_output_grad", False),
+    ("pooled_fallback", False),
+    ("protect_own_frame", False),
+    ("attention_sink", 0),
+)
 
 
 def global_blocks(model):
     """The blocks whose `.attn` is sparsified, in layer order: the list recorded by
     wire_ress_attention, else VGGT's `model.aggregator.global_blocks`
     (reference wiring.py:33-40)."""
-    blocks = getattr(model, "ress_global_blocks", None)
-    if blocks is not None:
-        return blocks
-    return model.aggregator.global_blocks
+    recorded = getattr(model, "ress_global_blocks", None)
+    return recorded if recorded is not None else model.aggregator.global_blocks
 
 
 def global_attns(model):
-    return [block.attn for block in global_blocks(model)]
+    """The attention modules of global_blocks(model) (reference wiring.py:43-46)."""
+    return [b.attn for b in global_blocks(model)]
+
+
+class SparseAttentionForward:
+    """Callable installed as `attn.forward`: (x, pos=None, xpos=None, attn_bias=None,
+    attn_mask=None) -> (B, N*P, dim). The positional encoding is accepted under VGGT's name
+    (`pos`) or Pi3's (`xpos`); a mask or bias cannot be honoured by a forward that builds its
+    own block mask, so a non-None one is refused (reference wiring.py:76-81)."""
+
+    def __init__(self, attn, aux_store=None, aux_full=True, num_special_tokens=5):
+        self.attn = attn
+        self.aux_store = aux_store
+        self.aux_full = aux_full
+        self.num_special_tokens = num_special_tokens
+
+    def config(self):
+        """The call-time configuration read off the module."""
+        return {name: getattr(self.attn, name, default) for name, default in CALL_ATTRIBUTES}
+
+    def __call__(self, x, pos=None, xpos=None, attn_bias=None, attn_mask=None):
+        if attn_bias is not None or attn_mask is not None:
+            raise AssertionError("the block-sparse attention forward builds its own block mask; attn_bias and "
+                                 "attn_mask must be None")
+        return ress_attention_forward(
+            self.attn, x, xpos if pos is None else pos, num_special_tokens=self.num_special_tokens,
+            num_heads=self.attn.num_heads, shape=getattr(self.attn, "ress_shape", None), aux_store=self.aux_store,
+            aux_full=self.aux_full, **self.config())
 
 
 def wire_ress_attention(model, blocks, aux_output_store=None, aux_full=True, num_special_tokens=5):
-    """Replace each block's `attn.forward` with the block-sparse forward and record the
-    block list on the model (reference wiring.py:49-109). Per-call configuration is read
-    from attributes of each attn module at forward time (set by set_static_budget). The
-    positional encoding is accepted as `pos=` (VGGT) or `xpos=` (Pi3); `attn_bias` and
-    `attn_mask` must be None."""
+    """Install SparseAttentionForward on every block's attention module and record the block
+    list as `model.ress_global_blocks` (reference wiring.py:49-109). aux_output_store: one
+    dict per block (or None) that receives the layer's AttentionAux."""
     blocks = list(blocks)
     for i, block in enumerate(blocks):
-        store_i = aux_output_store[i] if aux_output_store is not None else None
-
-        def _fwd(self, x, pos=None, xpos=None, attn_bias=None, attn_mask=None, _store=store_i, _attn=block.attn):
-            assert attn_bias is None and attn_mask is None, (
-                "ress_attention_forward builds its own block mask and cannot honor an "
-                "externally supplied attn_bias/attn_mask")
-            return ress_attention_forward(
-                _attn, x, pos if pos is not None else xpos,
-                num_to_select=getattr(_attn, "num_to_select", None),
-                budget_fn=getattr(_attn, "budget_fn", None),
-                perhead_budget_fn=getattr(_attn, "perhead_budget_fn", None),
-                joint_select_fn=getattr(_attn, "joint_select_fn", None),
-                block_criterion=getattr(_attn, "block_criterion", "probability"),
-                num_special_tokens=num_special_tokens,
-                num_heads=_attn.num_heads,
-                shape=getattr(_attn, "ress_shape", None),
-                aux_store=_store,
-                aux_full=aux_full,
-                dense=getattr(_attn, "dense", False),
-                retain_output_grad=getattr(_attn, "retain_output_grad", False),
-                pooled_fallback=getattr(_attn, "pooled_fallback", False),
-                protect_own_frame=getattr(_attn, "protect_own_frame", False),
-            )
-
-        block.attn.forward = MethodType(_fwd, block.attn)
+        store = None if aux_output_store is None else aux_output_store[i]
+        block.attn.forward = SparseAttentionForward(block.attn, store, aux_full, num_special_tokens)
     model.ress_global_blocks = blocks
     return blocks
