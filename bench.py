@@ -333,9 +333,11 @@ def main():
 
     projected.restore_swap_keep = timed_restore_swap
 
+    sink = cfg.get("attention_sink", 0)
+
     def step():
         return sparse_global_attention(q, k, v, grid, budget_fn=budget_fn, out=out, qk_mode=args.qk_mode,
-                                       block_criterion=criterion, M=M)
+                                       block_criterion=criterion, M=M, attention_sink=sink)
 
     for _ in range(args.warmup):
         step()
@@ -359,7 +361,7 @@ def main():
 
     # work actually done (same map every step)
     res = sparse_global_attention(q, k, v, grid, budget_fn=budget_fn, out=out, keep_intermediates=True,
-                                  qk_mode=args.qk_mode, block_criterion=criterion, M=M)
+                                  qk_mode=args.qk_mode, block_criterion=criterion, M=M, attention_sink=sink)
     torch.cuda.synchronize()
     lut, nvalid = res.lut.cpu().numpy(), res.nvalid.cpu().numpy()
     flops_kept = retained_flops(nvalid, lut, grid)
@@ -404,7 +406,8 @@ def main():
         "data": "synthetic (seeded smoothed-field Q/K/V, Hilbert order; synthetic HeSS tables)",
         "config": {"workload": f"BASELINE configs[{args.config}]: one global-attention layer, {cfg['mode']} budget",
                    "frames": frames, "tokens": N, "heads": 16, "head_dim": 64, "sparse_ratio": sr,
-                   "cdf_threshold": cdf, "realized_sparsity": round(sparsity, 4), "qk_mode": args.qk_mode},
+                   "cdf_threshold": cdf, "attention_sink": sink, "realized_sparsity": round(sparsity, 4),
+                   "qk_mode": args.qk_mode},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": round(peak, 1), "unit": "TFLOP/s",
                      "frac": round(achieved / peak, 4),
                      "traffic": measured_traffic(f"k_sparse_attn_{args.qk_mode}") if args.config == 1 else None,

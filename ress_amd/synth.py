@@ -181,10 +181,11 @@ def make_w_o(dim=1024, seed=2):
     return torch.from_numpy((rng.standard_normal((dim, dim)) / math.sqrt(dim)).astype(np.float32))
 
 
-# BASELINE.json configurations (frames, sparse_ratio, cdf_threshold, mode)
+# BASELINE.json configurations (frames, sparse_ratio, cdf_threshold, budget mode, frame
+# correlation, attention_sink = leading tokens whose key blocks every row keeps)
 CONFIGS = {
-    0: dict(frames=4, sparse_ratio=0.5, cdf_threshold=0.9, mode="sparse_vggt", corr="shared"),
+    0: dict(frames=4, sparse_ratio=0.5, cdf_threshold=0.9, mode="sparse_vggt", corr="shared", attention_sink=1374),
     1: dict(frames=16, sparse_ratio=0.7, cdf_threshold=None, mode="hess", corr="shared"),
     2: dict(frames=32, sparse_ratio=0.8, cdf_threshold=None, mode="ress", corr="shared", n_iters=5),
-    4: dict(frames=200, sparse_ratio=0.9, cdf_threshold=None, mode="sparse_vggt", corr="ar1"),
+    4: dict(frames=200, sparse_ratio=0.9, cdf_threshold=None, mode="sparse_vggt", corr="ar1", attention_sink=1374),
 }

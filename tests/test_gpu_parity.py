@@ -334,3 +334,77 @@ def test_attention_writes_every_row(B, H, frames, mode, dev):
     assert not torch.isnan(out).any()
     rows = row_sample(nv.cpu().numpy(), 12)
     _check_attention(out, q, k, v, frames, P, S, lut.cpu().numpy(), nv.cpu().numpy(), rows)
+
+
+def test_random_criterion_layer(dev):
+    """block_criterion="random" (reference attention.py:177-196, 576-578): the rank key is the
+    per-device generator's next draw (seed 20260826 on first use); the map is the oracle's
+    selection of that key, every row keeps exactly max(counts, 2) candidates plus the sinks."""
+    from ress_amd import attention as attn_mod
+    frames, sr = 4, 0.6
+    q, k, v, meta = synth.make_layer_qkv(frames)
+    P, S = meta["P"], meta["S"]
+    g = LayerGrid(1, 16, frames, P, S)
+    bud = budget.UniformBudget()
+    saved = dict(attn_mod._random_gens)
+    try:
+        attn_mod._random_gens.clear()
+        res = sparse_global_attention(q.to(dev), k.to(dev), v.to(dev), g,
+                                      budget_fn=lambda a: bud.num_to_select(0, a, sr, None, 1.0),
+                                      block_criterion="random", keep_intermediates=True)
+        torch.cuda.synchronize()
+        gen = torch.Generator(device=dev).manual_seed(20260826)
+        key = torch.rand((1, 16, g.q_blk_p, g.n_cand), device=dev, dtype=torch.float32, generator=gen)
+        assert torch.equal(attn_mod._random_gens[dev].get_state(), gen.get_state())
+    finally:
+        attn_mod._random_gens.clear()
+        attn_mod._random_gens.update(saved)
+    o = oracle_layer(q, k, v, frames, P, S, sparse_ratio=sr, criterion="key", rank_key=key.cpu().numpy())
+    fmap = _np(res.final_map).reshape(o["map"].shape)
+    assert np.array_equal(fmap, o["map"])
+    want = np.maximum(o["counts"].reshape(-1, g.q_blk_p), 2) + g.sink_blocks
+    assert np.array_equal(fmap.sum(-1), want)
+
+
+def test_hess_non_convergence_raises_at_layer_sync(dev):
+    """A HeSS budget that cannot converge within its iteration cap makes the layer's deferred
+    check raise RuntimeError (reference _proportional.py:112-113). The cap is forced to 1
+    from the host: two heads' ideal budgets exceed the candidate count, so every column needs
+    one redistribution step and the loop ends before the pass that finds no excess left. The
+    default cap converges on the same input."""
+    frames, sr = 4, 0.2
+    q, k, v, meta = synth.make_layer_qkv(frames)
+    P, S = meta["P"], meta["S"]
+    g = LayerGrid(1, 16, frames, P, S)
+    scores = torch.full((3, 1, 16), 1.0)
+    scores[0, 0, :2] = 50.0   # two heads want far more than max_val -> repeated caps
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    for cap, ok in ((1, False), (1000, True)):
+        hb = budget.HessBudget(scores, scores, lam=0.5, max_iters=cap)
+        res = sparse_global_attention(qd, kd, vd, g, budget_fn=lambda a: hb.num_to_select(0, a, sr, None, 1.0))
+        if ok:
+            res.check()
+            assert 0.0 < res.sparsity() < 1.0
+        else:
+            with pytest.raises(RuntimeError, match="did not converge in 1 iterations"):
+                res.sparsity()
+            with pytest.raises(RuntimeError, match="did not converge"):
+                res.check()
+
+
+@pytest.mark.parametrize("name", ["vggt", "pi3", "da3"])
+def test_head_budget_on_shipped_tables(name, dev):
+    """k_head_budget with every layer's head scores from the shipped calibration tables, at
+    the backbone's tuned lambda, against the oracle, with budgets that force caps."""
+    from ress_amd import backbones
+    spec = backbones.get_backbone(name)
+    pcd, cam = spec.calibration_paths()
+    hb = budget.HessBudget(cam, pcd, lam=spec.hess_lam)
+    rng = np.random.default_rng(len(name))
+    H, n_cand = spec.n_heads, 342
+    for layer in range(spec.n_global_blocks):
+        base = rng.integers(0, n_cand, size=(1, H, 40)).astype(np.int32)
+        got = kernels.head_budget(torch.from_numpy(base).to(dev), hb._scores_norm(layer, dev), 1.0, n_cand)
+        want, it = oracle.head_budget(base, oracle.scores_norm_seq(hb.head_scores[layer].numpy()), 1.0, n_cand)
+        assert it >= 0
+        assert np.array_equal(_np(got), want), (name, layer)
