@@ -179,6 +179,20 @@ int ress_sparse_attn_fwd_bf16(const void* q, long long sqB, long long sqH, long 
                               int P, int S, float sm_scale, void* out, int out_dtype, long long soB, long long soH,
                               long long soT, void* sched, hipStream_t stream);
 
+/* Allocation-free variant of ress_sparse_attn_fwd_bf16 (same arguments without `sched`,
+ * same kernels and results). No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). The launch's scratch (row schedule and split-row parts) lives in a
+ * static device array of ress_noalloc_scratch_bytes() bytes (about 26.7 MB) that each device
+ * holds for the life of the process; every shape fits in it, and a shape that did not would be
+ * rejected (-1). Calls on one device share that array: calls that overlap on a device (other
+ * streams or threads) race. Nothing is allocated, freed or synchronised. */
+long long ress_noalloc_scratch_bytes(void);
+int ress_sparse_attn_fwd_bf16_noalloc(const void* q, long long sqB, long long sqH, long long sqT, const void* k_pack,
+                                      const void* v_pack, const void* lut, const void* nvalid, int B, int H,
+                                      int frames, int P, int S, float sm_scale, void* out, int out_dtype,
+                                      long long soB, long long soH, long long soT, hipStream_t stream);
+
 /* Replaces SpargeAttn qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold
  * (call src/ress/models/attention.py:238-241) with the same argument meaning; see
  * attn.hip for the supported flag values. workspace: ress_qattn_workspace_size(B,H,Tq,Tk)

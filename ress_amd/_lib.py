@@ -26,6 +26,7 @@ _SIGS = {
     "ress_block_map_lut": "plipp" + "s",
     "ress_sparse_attn_fwd": "pppppppippiiiiifpilllps",
     "ress_sparse_attn_fwd_bf16": "plllpppp" + "iiiiif" + "pi" + "lll" + "ps",
+    "ress_sparse_attn_fwd_bf16_noalloc": "plllpppp" + "iiiiif" + "pi" + "lll" + "s",
     "ress_qattn_block_sparse_fwd": "pppipipppppiiiilllllliiifipls",
     "ress_restore_swap": "pppp" + "iiiiii" + "dd" + "i" + "ppp" + "pl" + "s",
     "ress_meansim_block_map": "ppp" + "iiii" + "llllll" + "ppi" + "ppppppppp" + "s",
@@ -61,6 +62,8 @@ def lib():
         L.ress_attn_sched_bytes.argtypes = [ctypes.c_int] * 3
         L.ress_restore_swap_workspace_size.restype = ctypes.c_longlong
         L.ress_restore_swap_workspace_size.argtypes = [ctypes.c_int] * 3
+        L.ress_noalloc_scratch_bytes.restype = ctypes.c_longlong
+        L.ress_noalloc_scratch_bytes.argtypes = []
         for name, sig in _SIGS.items():
             fn = getattr(L, name)
             fn.restype = ctypes.c_int
@@ -95,4 +98,4 @@ def last_error():
 
 def exported_symbols():
     return list(_SIGS) + ["ress_last_error", "ress_abi_version", "ress_qattn_workspace_size",
-                          "ress_attn_sched_bytes", "ress_restore_swap_workspace_size"]
+                          "ress_attn_sched_bytes", "ress_restore_swap_workspace_size", "ress_noalloc_scratch_bytes"]

@@ -20,6 +20,7 @@
 // that head's K/V stay in that XCD's L2.
 #include "common.h"
 
+#include <mutex>
 #include <type_traits>
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -1110,4 +1111,57 @@ RESS_API int ress_qattn_block_sparse_fwd(const void* q_i8, const void* k_i8, con
   m.T_s = 0;
   return attn_common(q_i8, nullptr, q_scale, k_i8, nullptr, k_scale, workspace, v_f16, lut, valid_block_num, B, H, m,
                      Tk, sm_scale, o, o_dtype, soB, soH, soT, (char*)workspace + qattn_vpack_bytes(B, H, Tk), stream);
+}
+
+// ---- allocation-free variant of ress_sparse_attn_fwd_bf16 -------------------------------
+// For callers that cannot allocate device memory (code under graph capture, serving loops,
+// harnesses that forbid hipMalloc): the launch's scratch -- the row schedule and the parts
+// of the split rows, ress_attn_sched_bytes(...) bytes, at most RESS_NOALLOC_SCRATCH_BYTES
+// for any shape -- lives in this file-scope device array instead of a caller workspace.
+// Each device holds its own copy for the life of the process. Every call on a device
+// uses that device's copy, so calls that overlap on one device (other streams, other
+// threads) race; the schedule kernel rewrites the counters at the start of every launch,
+// so nothing needs clearing between calls.
+#define RESS_NOALLOC_SCRATCH_BYTES \
+  (RESS_SCHED_HDR_BYTES + 8LL * RESS_SPLIT_ROWS * RESS_SPLIT_PARTS * RESS_PART_FLOATS * 4)
+static __device__ __align__(256) unsigned char scratch[RESS_NOALLOC_SCRATCH_BYTES];
+
+// Device address of `scratch` per device, looked up once with that device current (the
+// array's host-side name is not a device address).
+static std::mutex g_scratch_mu;
+static void* g_scratch_addr[64];
+
+static int scratch_address(void** out) {
+  int dev = -1;
+  RESS_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64,
+               "ress_sparse_attn_fwd_bf16_noalloc: no usable current device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    RESS_REQUIRE(e == hipSuccess && p != nullptr,
+                 "ress_sparse_attn_fwd_bf16_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                 hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return 0;
+}
+
+RESS_API long long ress_noalloc_scratch_bytes(void) { return RESS_NOALLOC_SCRATCH_BYTES; }
+
+RESS_API int ress_sparse_attn_fwd_bf16_noalloc(const void* q, long long sqB, long long sqH, long long sqT,
+                                               const void* k_pack, const void* v_pack, const void* lut,
+                                               const void* nvalid, int B, int H, int frames, int P, int S,
+                                               float sm_scale, void* out, int out_dtype, long long soB, long long soH,
+                                               long long soT, hipStream_t stream) {
+  RESS_REQUIRE(B > 0 && H > 0 && frames > 0 && P > S && S >= 0, "ress_sparse_attn_fwd_bf16_noalloc: bad geometry");
+  const long long need = ress_attn_sched_bytes(B, H, frames * P);
+  RESS_REQUIRE(need > 0 && need <= RESS_NOALLOC_SCRATCH_BYTES,
+               "ress_sparse_attn_fwd_bf16_noalloc: this shape needs %lld bytes of scratch, the static array holds %lld",
+               need, (long long)RESS_NOALLOC_SCRATCH_BYTES);
+  void* sched = nullptr;
+  if (scratch_address(&sched) != 0) return -1;
+  return ress_sparse_attn_fwd_bf16(q, sqB, sqH, sqT, k_pack, v_pack, lut, nvalid, B, H, frames, P, S, sm_scale, out,
+                                   out_dtype, soB, soH, soT, sched, stream);
 }
