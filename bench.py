@@ -38,7 +38,7 @@ PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, GB/s
 def mfma_peak(qk_mode):
     """Dense MFMA peak for the retained FLOPs, half of which are QK^T and half PV (bf16):
     QK^T at the bf16 or INT8 rate, harmonic combination of the two halves."""
-    qk = PEAK_BF16_TFLOPS if qk_mode == "bf16" else PEAK_INT8_TOPS
+    qk = PEAK_BF16_TFLOPS if qk_mode == "f16" else PEAK_INT8_TOPS
     return 1.0 / (0.5 / qk + 0.5 / PEAK_BF16_TFLOPS)
 
 
@@ -92,8 +92,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=15.0)
     ap.add_argument("--no-dense", action="store_true")
-    ap.add_argument("--qk-mode", default="bf16", choices=["bf16", "i8x2", "i8"],
-                    help="QK^T operands of the attention kernel (bf16 inputs, two-term or single-term INT8)")
+    ap.add_argument("--qk-mode", default="f16", choices=["f16", "i8x2", "i8"],
+                    help="QK^T operands of the attention kernel (16-bit: fp16 K blocks and per-row fp16 queries; "
+                         "two-term or single-term INT8)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run one plain device copy of this many MiB first (PMC traffic calibration)")
     return ap.parse_args()
@@ -382,11 +383,11 @@ def main():
     torch.cuda.synchronize()
     prep_ms = pe_s.elapsed_time(pe_e) / reps
     elems = N * 16 * 64
-    prep_bytes = elems * {"bf16": 10, "i8x2": 14, "i8": 12}[args.qk_mode]
+    prep_bytes = elems * {"f16": 10, "i8x2": 14, "i8": 12}[args.qk_mode]
     peak = mfma_peak(args.qk_mode)
     ms_meansim, ms_bytes = time_meansim(q, k, reps)
     peaks = measured_peaks(dev)
-    qk_meas = peaks["bf16_tflops"] if args.qk_mode == "bf16" else peaks["int8_tops"]
+    qk_meas = peaks["bf16_tflops"] if args.qk_mode == "f16" else peaks["int8_tops"]
     peak_meas = 1.0 / (0.5 / qk_meas + 0.5 / peaks["bf16_tflops"])
 
     result = {
@@ -401,7 +402,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"bf16": "bf16 QK", "i8x2": "two-term int8 QK", "i8": "int8 QK"}[args.qk_mode]
+        "dtype": {"f16": "fp16 QK (bf16 inputs)", "i8x2": "two-term int8 QK", "i8": "int8 QK"}[args.qk_mode]
                  + " / bf16 PV / fp32 softmax",
         "data": "synthetic (seeded smoothed-field Q/K/V, Hilbert order; synthetic HeSS tables)",
         "config": {"workload": f"BASELINE configs[{args.config}]: one global-attention layer, {cfg['mode']} budget",

@@ -38,9 +38,11 @@ int ress_abi_version(void);
  *   v_pack [BH][kb_tot][4096] bf16, ksum [BH][kb_tot][64] f32, km [BH][64] f32
  *   q_lo / k_lo (optional, layouts of q_i8 / k_i8): split-INT8 residual codes, x ~
  *   scale*hi + scale/254*lo, used by ress_sparse_attn_fwd for a two-term INT8 QK^T.
- *   k_pack [BH][kb_tot][64][64] bf16 (optional): the K blocks for ress_sparse_attn_fwd_bf16.
- * q_i8 = k_i8 = NULL selects the bf16 operands: only pooled_q/k/v, v_pack and k_pack
- * (required) are written; q_lo, q_scale, k_lo, k_scale, ksum, km are unused. */
+ *   k_pack [BH][kb_tot][64][64] fp16 (optional): the K blocks for ress_sparse_attn_fwd_f16
+ *   (a bf16 key is exact in fp16 unless below 2^-14 in magnitude or above 65504).
+ * q_i8 = k_i8 = NULL selects the 16-bit operands: pooled_q/k/v, v_pack, k_pack and
+ * k_scale (both required) are written, k_scale [BH][kb_tot] receiving each key block's
+ * largest key norm; q_lo, q_scale, k_lo, ksum, km are unused. */
 int ress_prep_qkv(const void* q, const void* k, const void* v, int B, int H, int frames, int P, int S,
                   long long sqB, long long sqH, long long sqT, long long skB, long long skH, long long skT,
                   long long svB, long long svH, long long svT, void* q_i8, void* q_lo, void* q_scale,
@@ -171,15 +173,20 @@ int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void* q_scale
                          hipStream_t stream);
 
 /* The fused-path attention of ress_sparse_attn_fwd (same reference lines) with QK^T on
- * the bf16 inputs (fp32 accumulation) instead of INT8 codes: q is the layer's bf16
- * (B,H,frames*P,64) query tensor in storage order with element strides sqB/sqH/sqT,
- * k_pack and v_pack come from ress_prep_qkv. sched: as for ress_sparse_attn_fwd. */
-int ress_sparse_attn_fwd_bf16(const void* q, long long sqB, long long sqH, long long sqT, const void* k_pack,
-                              const void* v_pack, const void* lut, const void* nvalid, int B, int H, int frames,
-                              int P, int S, float sm_scale, void* out, int out_dtype, long long soB, long long soH,
-                              long long soT, void* sched, hipStream_t stream);
+ * 16-bit operands (fp16 MFMA, fp32 accumulation) instead of INT8 codes: q is the layer's
+ * bf16 (B,H,frames*P,64) query tensor in storage order with element strides
+ * sqB/sqH/sqT, converted to fp16 per row in registers; k_pack (fp16), k_norm (the k_scale
+ * output of the 16-bit mode: per-block largest key norms) and v_pack come from
+ * ress_prep_qkv. A row whose logit bound |q*sm_scale*log2 e| * max key norm is at most 64
+ * (log2 units) runs with the pre-scaled queries rounded to fp16 and a fixed offset in the
+ * accumulator (no running max); other rows use the exact fp16 queries and a running max.
+ * sched: as for ress_sparse_attn_fwd. */
+int ress_sparse_attn_fwd_f16(const void* q, long long sqB, long long sqH, long long sqT, const void* k_pack,
+                             const void* k_norm, const void* v_pack, const void* lut, const void* nvalid, int B,
+                             int H, int frames, int P, int S, float sm_scale, void* out, int out_dtype,
+                             long long soB, long long soH, long long soT, void* sched, hipStream_t stream);
 
-/* Allocation-free variant of ress_sparse_attn_fwd_bf16 (same arguments without `sched`,
+/* Allocation-free variant of ress_sparse_attn_fwd_f16 (same arguments without `sched`,
  * same kernels and results). No counterpart in the reference: it is for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc). The launch's scratch (row schedule and split-row parts) lives in a
@@ -188,10 +195,10 @@ int ress_sparse_attn_fwd_bf16(const void* q, long long sqB, long long sqH, long 
  * rejected (-1). Calls on one device share that array: calls that overlap on a device (other
  * streams or threads) race. Nothing is allocated, freed or synchronised. */
 long long ress_noalloc_scratch_bytes(void);
-int ress_sparse_attn_fwd_bf16_noalloc(const void* q, long long sqB, long long sqH, long long sqT, const void* k_pack,
-                                      const void* v_pack, const void* lut, const void* nvalid, int B, int H,
-                                      int frames, int P, int S, float sm_scale, void* out, int out_dtype,
-                                      long long soB, long long soH, long long soT, hipStream_t stream);
+int ress_sparse_attn_fwd_f16_noalloc(const void* q, long long sqB, long long sqH, long long sqT, const void* k_pack,
+                                     const void* k_norm, const void* v_pack, const void* lut, const void* nvalid,
+                                     int B, int H, int frames, int P, int S, float sm_scale, void* out, int out_dtype,
+                                     long long soB, long long soH, long long soT, hipStream_t stream);
 
 /* Replaces SpargeAttn qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold
  * (call src/ress/models/attention.py:238-241) with the same argument meaning; see

@@ -80,10 +80,11 @@ def prep_qkv(q, k, v, frames, P, S):
         v_pack=np.zeros((BH, kbt, 4096), np.uint16),
         ksum=np.zeros((BH, kbt, 64), np.float32),
         km=np.zeros((BH, 64), np.float32),
+        k_norm=np.zeros((BH, kbt), np.float32),
     )
     lib().oracle_prep_qkv(_p(qu), _p(ku), _p(vu), BH, frames, P, S, *[_p(out[n]) for n in (
         "q_i8", "q_lo", "q_scale", "pooled_q", "k_i8", "k_lo", "k_scale", "pooled_k", "pooled_v", "v_pack", "ksum",
-        "km")])
+        "km", "k_norm")])
     return out
 
 

@@ -115,11 +115,14 @@ static inline int8_t quant_lo(float x, float scale, int8_t hi) {
  * key order cat(patch, special), attention.py:405-406), predict_attention's avg pools
  * (attention.py:90-96; ceil mode, a partial block divided by its valid count),
  * block_mean_value (attention.py:103-109), km = key.mean(-2) and
- * per_block_int8(q, k - km) (attention.py:231-233), all in fp32.
+ * per_block_int8(q, k - km) (attention.py:231-233), all in fp32; k_norm[BH][kb_tot] the
+ * 16-bit attention's per-block largest key norm: per key an fmaf chain over each group
+ * of 8 dims, the tree ((g0+g1)+(g2+g3))+((g4+g5)+(g6+g7)), sqrtf; the max over the block.
  * q,k,v: (BH, frames*P, 64) bf16. Output layouts as ress_prep_qkv (include/ress_hip.h). */
 void oracle_prep_qkv(const uint16_t* q, const uint16_t* k, const uint16_t* v, int BH, int frames, int P, int S,
                      int8_t* q_i8, int8_t* q_lo, float* q_scale, float* pooled_q, int8_t* k_i8, int8_t* k_lo,
-                     float* k_scale, float* pooled_k, float* pooled_v, uint16_t* v_pack, float* ksum, float* km) {
+                     float* k_scale, float* pooled_k, float* pooled_v, uint16_t* v_pack, float* ksum, float* km,
+                     float* k_norm) {
   tokmap m = mkmap(frames, P, S);
   const int N = frames * P, Tk = N;
   const int qbp = cdiv(m.T_p, 128), qbs = cdiv(m.T_s, 128), qbt = qbp + qbs;
@@ -167,6 +170,21 @@ void oracle_prep_qkv(const uint16_t* q, const uint16_t* k, const uint16_t* v, in
           pooled_v[((long long)bh * kbp + kb) * 64 + d] = sum8x(vh, rows, cnt_p, d) / (float)cnt_p;
         }
       }
+      float nmax = 0.0f;
+      for (int t = 0; t < cnt; ++t) {
+        float g8[8];
+        for (int grp = 0; grp < 8; ++grp) {
+          float ss = 0.0f;
+          for (int c = 0; c < 8; ++c) {
+            const float x = bf16f(kh[(long long)rows[t] * 64 + 8 * grp + c]);
+            ss = fmaf(x, x, ss);
+          }
+          g8[grp] = ss;
+        }
+        const float n = sqrtf(((g8[0] + g8[1]) + (g8[2] + g8[3])) + ((g8[4] + g8[5]) + (g8[6] + g8[7])));
+        nmax = fmaxf(nmax, n);
+      }
+      k_norm[(long long)bh * kbt + kb] = nmax;
       uint16_t* vp = v_pack + ((long long)bh * kbt + kb) * 4096;
       for (int t = 0; t < 64; ++t) {
         const int u = t & 15;

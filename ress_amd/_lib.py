@@ -25,8 +25,8 @@ _SIGS = {
     "ress_fill_block_map": "ppplI" + "s",
     "ress_block_map_lut": "plipp" + "s",
     "ress_sparse_attn_fwd": "pppppppippiiiiifpilllps",
-    "ress_sparse_attn_fwd_bf16": "plllpppp" + "iiiiif" + "pi" + "lll" + "ps",
-    "ress_sparse_attn_fwd_bf16_noalloc": "plllpppp" + "iiiiif" + "pi" + "lll" + "s",
+    "ress_sparse_attn_fwd_f16": "plllppppp" + "iiiiif" + "pi" + "lll" + "ps",
+    "ress_sparse_attn_fwd_f16_noalloc": "plllppppp" + "iiiiif" + "pi" + "lll" + "s",
     "ress_qattn_block_sparse_fwd": "pppipipppppiiiilllllliiifipls",
     "ress_restore_swap": "pppp" + "iiiiii" + "dd" + "i" + "ppp" + "pl" + "s",
     "ress_meansim_block_map": "ppp" + "iiii" + "llllll" + "ppi" + "ppppppppp" + "s",

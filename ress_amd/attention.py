@@ -3,7 +3,7 @@
 `ress_attention_forward` is the drop-in replacement of a global block's attention
 forward. Its hot path, `sparse_global_attention`, runs on the GPU kernels only:
 
-    prepare_blocks     pool Q/K/V, packed K/V (bf16 mode) or key mean +
+    prepare_blocks     pool Q/K/V, packed K/V + key norms (f16 mode) or key mean +
                        per-block INT8 Q/K codes (INT8 modes)                 (prep.hip)
     pooled_scores      pooled softmax attn_full, renormalised attn_cond      (scores.hip)
     budget_fn          per-(head, q-block) counts                            (budget.hip)
@@ -29,10 +29,11 @@ from ress_amd.qkv import combine_special_and_patch, compute_qkv, get_patch_token
 KBLK = 64
 MIN_NUM_TO_SELECT = 2  # floor on real key blocks per query row (reference attention.py:40-42)
 
-# QK^T operands of the attention kernel. bf16 is exact in the inputs and the fastest;
-# the INT8 modes reproduce the reference's SpargeAttn quantiser ("i8") or refine it
-# with a second code per element ("i8x2").
-DEFAULT_QK_MODE = "bf16"
+# QK^T operands of the attention kernel. "f16" (fp16 K blocks, queries converted to fp16
+# per row) is the fastest and within the tolerance; the INT8 modes reproduce the
+# reference's SpargeAttn quantiser ("i8") or refine it with a second code per element
+# ("i8x2").
+DEFAULT_QK_MODE = "f16"
 
 _RANDOM_SEED = 20260826  # block_criterion="random" (reference attention.py:177-196)
 _random_gens = {}
@@ -190,7 +191,7 @@ def sparse_global_attention(q, k, v, grid, *, num_to_select=None, budget_fn=None
     q, k, v: bf16 (B, H, frames*P, 64) in storage order (per frame S special then P-S
     patch tokens). Patch queries attend to the selected key blocks plus the trailing
     special blocks; special queries attend densely (reference attention.py:404-412,
-    446-491, 510-581, 625). qk_mode: the QK^T operands, "bf16" (default), "i8x2" or
+    446-491, 510-581, 625). qk_mode: the QK^T operands, "f16" (default), "i8x2" or
     "i8" (see kernels.Blocks); the block map does not depend on it. protect_own_frame:
     the budget-neutral own-frame swap on the selected map (protect_own_frame_swap).
     attention_sink: leading tokens whose key blocks every row keeps on top of its budget

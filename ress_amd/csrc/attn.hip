@@ -1,4 +1,5 @@
-// Block-sparse attention forward (INT8 QK^T, 16-bit PV) for gfx950.
+// Block-sparse attention forward for gfx950: QK^T on 16-bit (fp16) or INT8 operands,
+// online softmax, PV on bf16 (or fp16) MFMAs.
 //
 // Replaces SpargeAttn's qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold
 // as the reference calls it (src/ress/models/attention.py:238-241: HND layout, not
@@ -6,18 +7,21 @@
 // the special-query dense SDPA of attention.py:409 (special query blocks are rows
 // whose LUT lists every key block).
 //
-//   O[q] = sum_k softmax_k( q_scale*k_scale*sm_scale * (Q8[q] . K8[k]) ) V[k]
+//   O[q] = sum_k softmax_k( sm_scale * (Q[q] . K[k]) ) V[k]
 //
-// Work item = (batch*head, 128-query block); 256 threads = 4 waves of 32 queries.
-// Per kept 64-key block, as two 32-key tiles:
-//   S^T (32 keys x 32 queries) = K8 . Q8^T     2 x v_mfma_i32_32x32x32_i8 (6 when split)
-//   online softmax in the exp2 domain, scale folded into one fma per score
-//   O^T (64 dims x 32 queries) += V^T . P^T    4 x v_mfma_f32_32x32x16_{bf16,f16}
+// Work item = (batch*head, 128-query block). Per kept 64-key block:
+//   S^T = K . Q^T      v_mfma_f32_32x32x16_f16 (16-bit mode), or
+//                      v_mfma_i32_32x32x32_i8 (INT8 modes, 1 or 3 per tile)
+//   softmax in the exp2 domain: P = exp2(logit) directly on bounded 16-bit rows, else a
+//   lazily rescaled running max with the scale folded into one fma
+//   O^T (64 dims x 32 queries) += V^T . P^T    v_mfma_f32_32x32x16_{bf16,f16}
+// 16-bit mode: 512 threads = 8 waves, wave w takes query group w/2 (32 queries) and key
+// half w%2 of every block; the two halves merge through LDS when the row ends. INT8 modes:
+// 256 threads = 4 waves of 32 queries, both key tiles per wave.
 // The S^T accumulator layout puts one query per lane, so P feeds the PV MFMA from
 // registers; V is pre-packed (prep.hip) with keys permuted to match. K/V tiles go
-// through three LDS stages filled by LDS-DMA two blocks ahead. Work items are mapped XCD-major: hardware workgroup x runs
-// on XCD x%8, and consecutive workgroups of one XCD walk the rows of one head so
-// that head's K/V stay in that XCD's L2.
+// through LDS stages filled by LDS-DMA several blocks ahead. The kernels are persistent:
+// each XCD walks its own range of rows (see k_attn_schedule) so a head's K/V stay in its L2.
 #include "common.h"
 
 #include <mutex>
@@ -37,9 +41,10 @@ struct AttnArgs {
   const int8_t* k_i8;      // [BH][kb_tot][64][64]
   const float* k_scale;    // [BH][kb_tot]
   const uint16_t* v_pack;  // [BH][kb_tot][64 dims][64 permuted keys]
-  const uint16_t* q_bf;    // QK_BF16: the bf16 queries, (B,H,T,64) storage order, strides sqB/sqH/sqT
+  const uint16_t* q_bf;    // QK_F16: the bf16 queries, (B,H,T,64) storage order, strides sqB/sqH/sqT
   long long sqB, sqH, sqT;
-  const uint16_t* k_pack;  // QK_BF16: [BH][kb_tot][64 keys][64] bf16
+  const uint16_t* k_pack;  // QK_F16: [BH][kb_tot][64 keys][64] fp16
+  const float* k_norm;     // QK_F16: [BH][kb_tot] the block's largest key norm
   const int* lut;          // [BH][q_blk_total][kb_tot]
   const int* nvalid;       // [BH][q_blk_total]
   void* out;
@@ -235,25 +240,19 @@ __global__ __launch_bounds__(1024) void k_attn_schedule(const int* __restrict__ 
 //  QK_I8    single-term per-block INT8 (the reference's SpargeAttn quantiser)
 //  QK_I8X2  two-term INT8, x ~ s*hi + s/254*lo: S = 254*(hi.hi) + hi.lo + lo.hi in
 //           int32 (the lo.lo term, below 2^-16 relative, is dropped)
-//  QK_BF16  the bf16 inputs themselves, fp32 accumulation
-enum { QK_I8 = 0, QK_I8X2 = 1, QK_BF16 = 2 };
+//  QK_F16   16-bit operands: fp16 K blocks, the bf16 queries converted to fp16 per row
+//           (pre-scaled on bounded rows), fp32 accumulation (see attn_row_f16)
+enum { QK_I8 = 0, QK_I8X2 = 1, QK_F16 = 2 };
 
-// Q operand of one lane (query qi, half g), four 16-byte registers:
-//   INT8 modes: [0],[1] = hi codes of dims 16g..16g+15 and 32+16g..; [2],[3] = lo codes
-//   QK_BF16:    [j] = dims 16j+8g .. 16j+8g+7
-// K operand LDS slots of one lane for tile t (key 32t+qi):
-//   INT8 modes: ks[0], ks[1] = hi chunks g and 2+g (lo chunks at +256 slots)
-//   QK_BF16:    ks[j] = chunk 2j+g of the 128-byte key row
+// INT8 modes. Q operand of one lane (query qi, half g), four 16-byte registers: [0],[1]
+// = hi codes of dims 16g..16g+15 and 32+16g..; [2],[3] = lo codes. K operand LDS slots of
+// one lane for tile t (key 32t+qi): ks[0], ks[1] = hi chunks g and 2+g (lo chunks at +256
+// slots).
 template <int QK>
 __device__ __forceinline__ void k_slots(int row, int g, int ks[4]) {
-  if constexpr (QK == QK_BF16) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) ks[j] = v_slot(row, 2 * j + g);
-  } else {
-    ks[0] = k_slot(row, g);
-    ks[1] = k_slot(row, 2 + g);
-    ks[2] = ks[3] = 0;
-  }
+  ks[0] = k_slot(row, g);
+  ks[1] = k_slot(row, 2 + g);
+  ks[2] = ks[3] = 0;
 }
 
 __device__ __forceinline__ float pair_maxf(float x) {
@@ -261,39 +260,15 @@ __device__ __forceinline__ float pair_maxf(float x) {
   return fmaxf(__int_as_float((int)r[0]), __int_as_float((int)r[1]));
 }
 
-// S^T for one 32-key tile (keys 32t.. of the stage) as floats, plus the tile's max
-// score (in S units). Register r is key 32t + 8(r/4) + 4g + r%4 of the block.
-// nkt = valid keys in the tile (MASK only): masked scores are -inf (bf16) or the
-// lowest int (INT8), which exp2 maps to 0.
+// INT8 modes: S^T for one 32-key tile (keys 32t.. of the stage) as floats, plus the
+// tile's max score (in S units). Register r is key 32t + 8(r/4) + 4g + r%4 of the block.
+// nkt = valid keys in the tile (MASK only): masked scores are the lowest int, which exp2
+// maps to 0.
 template <int QK, bool MASK>
 __device__ __forceinline__ void qk_tile(const uint4* __restrict__ sk, int nkt, const int (&ks)[4],
                                         const uint4 (&qv)[4], int g, float (&s)[16], float& tmax) {
-  if constexpr (QK == QK_BF16) {
-    v16f sacc;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, sk[ks[j]]),
-                                                     __builtin_bit_cast(v8bf, qv[j]), sacc, 0, 0, 0);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = sacc[r];
-    if constexpr (MASK) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        if (8 * (r >> 2) + 4 * g + (r & 3) >= nkt) s[r] = -__builtin_huge_valf();
-    }
-    // two max chains; with NaNs excluded (this file is built with -fno-honor-nans: the
-    // scores are finite, or -inf for masked keys) each pair of fmaxf becomes one
-    // v_max3_f32 with no NaN-quieting of the MFMA results
-    float ma = fmaxf(fmaxf(s[0], s[1]), s[2]), mb = fmaxf(fmaxf(s[8], s[9]), s[10]);
-    ma = fmaxf(fmaxf(ma, s[3]), s[4]);
-    mb = fmaxf(fmaxf(mb, s[11]), s[12]);
-    ma = fmaxf(fmaxf(ma, s[5]), s[6]);
-    mb = fmaxf(fmaxf(mb, s[13]), s[14]);
-    ma = fmaxf(fmaxf(ma, s[7]), mb);
-    tmax = fmaxf(ma, s[15]);
-  } else {
+  static_assert(QK != QK_F16, "qk_tile is the INT8 modes' QK^T");
+  {
     const v4i kx0 = __builtin_bit_cast(v4i, sk[ks[0]]);
     const v4i kx1 = __builtin_bit_cast(v4i, sk[ks[1]]);
     const v4i qa0 = __builtin_bit_cast(v4i, qv[0]), qa1 = __builtin_bit_cast(v4i, qv[1]);
@@ -389,126 +364,55 @@ __device__ __forceinline__ void attn_block_i8(const uint4* __restrict__ stage, i
   }
 }
 
-// bf16 mode, software-pipelined over blocks: the S^T MFMAs of block i+1 (qk_block_bf16)
-// are issued before the softmax and PV of block i (sv_block_bf16), so the matrix cores
-// work on the next block's scores while the VALU computes this block's probabilities.
+// 16-bit mode (QK_F16). K blocks are fp16 (exact for bf16 keys above the fp16 subnormal
+// range); the row's queries are converted to fp16 in registers when the row starts. A row
+// runs one of two ways, chosen per row (the same for every wave of the workgroup):
+//  * bounded: Q' = fp16(q * sm_scale * log2 e). Every logit of the row (log2 units) lies
+//    in [-m0, m0], m0 = |Q'| * (the largest key norm of the row's kept blocks). When
+//    m0 <= RESS_BOUND_MAX, P = exp2(logit) itself is in [2^-64, 2^64]: no offset, no scale,
+//    no row max, no rescale. The row sum and O = sum P v stay below 2^82 * max|v| (fp32
+//    overflows at 2^128), and the largest P of the row is at least 2^-64.
+//  * running max (rows whose m0 exceeds RESS_BOUND_MAX, or is not finite): Q = fp16(q),
+//    exact, the scale folded into one fma per score and the lazy-rescale running max.
+#define RESS_BOUND_MAX 64.0f
 
-// S^T of one 64-key block: tile 0 (keys 0..31) into a0, tile 1 into a1. All eight K
-// operand reads go out before the first MFMA (LDS returns in order).
-__device__ __forceinline__ void qk_block_bf16(const uint4* __restrict__ stage, const int (&ks0)[4], const int (&ks1)[4],
-                                              const uint4 (&qv)[4], v16f& a0, v16f& a1) {
-  uint4 k0[4], k1[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) k0[j] = stage[ks0[j]];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) k1[j] = stage[ks1[j]];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) a0[r] = a1[r] = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    a0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, k0[j]), __builtin_bit_cast(v8bf, qv[j]), a0,
-                                                 0, 0, 0);
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    a1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, k1[j]), __builtin_bit_cast(v8bf, qv[j]), a1,
-                                                 0, 0, 0);
-}
-
-// Online softmax and O^T += V^T P^T for one 64-key block whose scores are (a0, a1):
-// one running-max update per block with lazy rescale, P = exp2(S*c - m) per tile.
-// Register r of a tile is key 32t + 8(r/4) + 4g + r%4.
-template <bool MASK>
-__device__ __forceinline__ void sv_block_bf16(const uint4* __restrict__ stage, int kch, int nk, float c, const v16f& a0,
-                                              const v16f& a1, int g, int qi, float& m_run, float& l_run, v16f& o0,
-                                              v16f& o1) {
-  const uint4* sv = stage + kch;
-  uint4 v0[4];
+// P of one 32-key tile (16 scores per lane) -> l_run and O^T += V^T P^T (2 MFMAs per
+// output half). MFMA s = 2t + h covers keys 16s..16s+15, registers 8h..8h+7; the row sum
+// accumulates the same rounded P the MFMA consumes.
+__device__ __forceinline__ void pv_tile_bf16(const float (&p)[16], const uint4 (&vv)[4], float& l_run, v16f& o0,
+                                             v16f& o1) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    v0[2 * h] = sv[v_slot(qi, 2 * h + g)];
-    v0[2 * h + 1] = sv[v_slot(32 + qi, 2 * h + g)];
+    uint4 pb;
+    pb.x = cvt_pair<false>(p[8 * h + 0], p[8 * h + 1]);
+    pb.y = cvt_pair<false>(p[8 * h + 2], p[8 * h + 3]);
+    pb.z = cvt_pair<false>(p[8 * h + 4], p[8 * h + 5]);
+    pb.w = cvt_pair<false>(p[8 * h + 6], p[8 * h + 7]);
+    l_run = dot2_acc<false>(pb.x, l_run);
+    l_run = dot2_acc<false>(pb.y, l_run);
+    l_run = dot2_acc<false>(pb.z, l_run);
+    l_run = dot2_acc<false>(pb.w, l_run);
+    o0 = pv_mfma<false>(vv[2 * h], pb, o0);
+    o1 = pv_mfma<false>(vv[2 * h + 1], pb, o1);
   }
-  float s0[16], s1[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    s0[r] = a0[r];
-    s1[r] = a1[r];
-  }
-  if constexpr (MASK) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = 8 * (r >> 2) + 4 * g + (r & 3);
-      if (key >= nk) s0[r] = -__builtin_huge_valf();
-      if (key + 32 >= nk) s1[r] = -__builtin_huge_valf();
-    }
-  }
-  // max over the lane's 32 scores; with NaNs excluded (this file is built with
-  // -fno-honor-nans: scores are finite, or -inf for masked keys) pairs of fmaxf become
-  // v_max3_f32 with no NaN-quieting of the MFMA results
-  float ma = fmaxf(fmaxf(s0[0], s0[1]), s0[2]), mb = fmaxf(fmaxf(s1[0], s1[1]), s1[2]);
-#pragma unroll
-  for (int r = 3; r < 15; r += 2) {
-    ma = fmaxf(fmaxf(ma, s0[r]), s0[r + 1]);
-    mb = fmaxf(fmaxf(mb, s1[r]), s1[r + 1]);
-  }
-  ma = fmaxf(fmaxf(ma, s0[15]), s1[15]);
-  const float bmax = pair_maxf(fmaxf(ma, mb)) * c;
-  const bool need = bmax > m_run + RESS_RESCALE_LOG2;
-  if (__any(need)) {
-    const float m_new = need ? bmax : m_run;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    m_run = m_new;
-    l_run *= alpha;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      o0[r] *= alpha;
-      o1[r] *= alpha;
-    }
-  }
-  const float nm = -m_run;
-  auto pv = [&](const float (&sc)[16], const uint4 (&vv)[4]) {
-    float p[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) p[r] = __builtin_amdgcn_exp2f(fmaf(sc[r], c, nm));
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      uint4 pb;
-      pb.x = cvt_pair<false>(p[8 * h + 0], p[8 * h + 1]);
-      pb.y = cvt_pair<false>(p[8 * h + 2], p[8 * h + 3]);
-      pb.z = cvt_pair<false>(p[8 * h + 4], p[8 * h + 5]);
-      pb.w = cvt_pair<false>(p[8 * h + 6], p[8 * h + 7]);
-      l_run = dot2_acc<false>(pb.x, l_run);
-      l_run = dot2_acc<false>(pb.y, l_run);
-      l_run = dot2_acc<false>(pb.z, l_run);
-      l_run = dot2_acc<false>(pb.w, l_run);
-      o0 = pv_mfma<false>(vv[2 * h], pb, o0);
-      o1 = pv_mfma<false>(vv[2 * h + 1], pb, o1);
-    }
-  };
-  pv(s0, v0);
-  uint4 v1[4];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    v1[2 * h] = sv[v_slot(qi, 4 + 2 * h + g)];
-    v1[2 * h + 1] = sv[v_slot(32 + qi, 4 + 2 * h + g)];
-  }
-  pv(s1, v1);
 }
 
-// K chunks (16 B) per stage: INT8 hi 256 [+ lo 256]; bf16 512.
+// K chunks (16 B) per stage of the INT8 modes: hi 256 [+ lo 256].
 template <int QK>
 struct StageShape {
+  static_assert(QK != QK_F16, "the 16-bit mode runs attn_row_f16");
   static constexpr int KCH = QK == QK_I8 ? 256 : 512;
   static constexpr int STAGE = KCH + 512;  // + V^T 8 KiB
   static constexpr int DMA = QK == QK_I8 ? 3 : 4;  // LDS-DMA instructions per lane per stage
 };
 
-// Output of one finished row (query block qb of head bh): O / row sum, in the output
-// dtype at the row's storage positions. o0/o1 hold O^T in the PV MFMA's register order.
+// Output of one finished row (query block qb of head bh) for the lane's query of query
+// group w (queries 32w..32w+31): O / row sum, in the output dtype at the row's storage
+// positions. o0/o1 hold O^T in the PV MFMA's register order.
 template <int OUT>
 __device__ __forceinline__ void store_row(const AttnArgs& a, int bh, int qb, const v16f& o0, const v16f& o1,
-                                          float l_run) {
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 5, qi = l & 31;
+                                          float l_run, int w) {
+  const int l = threadIdx.x & 63, g = l >> 5, qi = l & 31;
   const bool special = qb >= a.q_blk_p;
   const int qbase = special ? (qb - a.q_blk_p) * 128 : qb * 128;
   const int cnt_q = min(128, (special ? a.m.T_s : a.m.T_p) - qbase);
@@ -537,15 +441,14 @@ __device__ __forceinline__ void store_row(const AttnArgs& a, int bh, int qb, con
   }
 }
 
-// One row (query block qb of head bh) over its kept blocks kb_lo..kb_hi-1 (LUT
-// positions). part_out null: the whole row, written to the output; otherwise one part of
-// a split row, left in part_out for k_attn_merge.
+// One row of the INT8 modes (query block qb of head bh) over its kept blocks
+// kb_lo..kb_hi-1 (LUT positions). part_out null: the whole row, written to the output;
+// otherwise one part of a split row, left in part_out for k_attn_merge.
 template <int QK, bool V_F16, int OUT>
 __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __restrict__ lut_all,
                                                 const float* __restrict__ k_scale, uint4* __restrict__ s0,
-                                                uint4* __restrict__ s1, uint4* __restrict__ s2,
-                                                uint4* __restrict__ s3, int bh, int qb, int kb_lo, int kb_hi,
-                                                float* __restrict__ part_out) {
+                                                uint4* __restrict__ s1, uint4* __restrict__ s2, int bh, int qb,
+                                                int kb_lo, int kb_hi, float* __restrict__ part_out) {
   constexpr int KCH = StageShape<QK>::KCH;
   constexpr int DMA = StageShape<QK>::DMA;
   const long long row = (long long)bh * a.q_blk_total + qb;
@@ -560,19 +463,7 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
   const int qrow = 32 * w + qi;
 
   uint4 qv[4];  // Q operand (see k_slots)
-  float qs;     // this row's logit scale (times log2 e); INT8 modes multiply in k_scale per block
-  if constexpr (QK == QK_BF16) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) qv[j] = make_uint4(0u, 0u, 0u, 0u);
-    if (qrow < cnt_q) {
-      const int tok = special ? special_to_storage(qbase + qrow, a.m) : patch_to_storage(qbase + qrow, a.m);
-      const uint16_t* src = a.q_bf + (long long)(bh / a.H) * a.sqB + (long long)(bh % a.H) * a.sqH +
-                            (long long)tok * a.sqT + 8 * g;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) qv[j] = *reinterpret_cast<const uint4*>(src + 16 * j);
-    }
-    qs = a.sm_scale_log2e;
-  } else {
+  {
     const int8_t* qsrc = a.q_i8 + (row * 128 + qrow) * 64 + 16 * g;
     qv[0] = *reinterpret_cast<const uint4*>(qsrc);
     qv[1] = *reinterpret_cast<const uint4*>(qsrc + 32);
@@ -583,17 +474,15 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
       qv[2] = *reinterpret_cast<const uint4*>(qlsrc);
       qv[3] = *reinterpret_cast<const uint4*>(qlsrc + 32);
     }
-    qs = a.q_scale[row] * a.sm_scale_log2e * (QK == QK_I8X2 ? (1.0f / 254.0f) : 1.0f);
   }
+  // this row's logit scale (times log2 e); the block's k_scale is multiplied in per block
+  const float qs = a.q_scale[row] * a.sm_scale_log2e * (QK == QK_I8X2 ? (1.0f / 254.0f) : 1.0f);
   const float* ksc = k_scale + (long long)bh * a.kb_tot;
-  auto block_scale = [&](int kb) -> float {
-    if constexpr (QK == QK_BF16) return qs;
-    else return qs * ksc[kb];
-  };
+  auto block_scale = [&](int kb) -> float { return qs * ksc[kb]; };
 
-  // Stage loads are LDS-DMA: lane l of wave w fills 16-byte slots 64w+l (INT8 K hi, K lo)
-  // or 128w+l, 128w+64+l (bf16 K, V), so it fetches the global chunk that the swizzle
-  // places there (the XOR swizzles are their own inverse).
+  // Stage loads are LDS-DMA: lane l of wave w fills 16-byte slots 64w+l (K hi, K lo) and
+  // 128w+l, 128w+64+l (V), so it fetches the global chunk that the swizzle places there
+  // (the XOR swizzles are their own inverse).
   // Byte offsets are unsigned 32-bit, so each DMA address is a uniform 64-bit block base
   // plus a zero-extended lane offset (the SGPR-base form of the load, no 64-bit VALU add).
   const unsigned kslot = 64 * w + l;
@@ -601,8 +490,7 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
   const unsigned vslot0 = 128 * w + l, vslot1 = vslot0 + 64;
   const unsigned vsrc0 = 16 * (8 * (vslot0 >> 3) + ((vslot0 & 7) ^ (((vslot0 >> 3) ^ (vslot0 >> 6)) & 7)));
   const unsigned vsrc1 = 16 * (8 * (vslot1 >> 3) + ((vslot1 & 7) ^ (((vslot1 >> 3) ^ (vslot1 >> 6)) & 7)));
-  const char* kblk0 = QK == QK_BF16 ? reinterpret_cast<const char*>(a.k_pack) + (long long)bh * a.kb_tot * 8192
-                                    : reinterpret_cast<const char*>(a.k_i8) + (long long)bh * a.kb_tot * 4096;
+  const char* kblk0 = reinterpret_cast<const char*>(a.k_i8) + (long long)bh * a.kb_tot * 4096;
   const char* klblk0 =
       QK == QK_I8X2 ? reinterpret_cast<const char*>(a.k_lo) + (long long)bh * a.kb_tot * 4096 : nullptr;
   const char* vblk0 = reinterpret_cast<const char*>(a.v_pack) + (long long)bh * a.kb_tot * 8192;
@@ -616,15 +504,9 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
   auto stage_load = [&](uint4* stage, int kb) {
     char* base = reinterpret_cast<char*>(stage);
     const char* vb = uniform_base(vblk0 + (long long)kb * 8192);
-    if constexpr (QK == QK_BF16) {
-      const char* kbp = uniform_base(kblk0 + (long long)kb * 8192);
-      gl_lds16(kbp + vsrc0, base + 2048 * w);
-      gl_lds16(kbp + vsrc1, base + 2048 * w + 1024);
-    } else {
-      gl_lds16(uniform_base(kblk0 + (long long)kb * 4096) + ksrc, base + 1024 * w);
-      if constexpr (QK == QK_I8X2)
-        gl_lds16(uniform_base(klblk0 + (long long)kb * 4096) + ksrc, base + 4096 + 1024 * w);
-    }
+    gl_lds16(uniform_base(kblk0 + (long long)kb * 4096) + ksrc, base + 1024 * w);
+    if constexpr (QK == QK_I8X2)
+      gl_lds16(uniform_base(klblk0 + (long long)kb * 4096) + ksrc, base + 4096 + 1024 * w);
     gl_lds16(vb + vsrc0, base + 16 * KCH + 2048 * w);
     gl_lds16(vb + vsrc1, base + 16 * KCH + 2048 * w + 1024);
   };
@@ -641,62 +523,6 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
   // kept it is the last entry. Full blocks run unmasked, the partial one is peeled off.
   const bool tail_partial = nv > 0 && (a.Tk & 63) != 0 && lut[nv - 1] == a.kb_tot - 1;
 
-  if constexpr (QK == QK_BF16) {
-    // Four stages: block i lives in stage i % 4 and is fetched three steps ahead. Step i
-    // issues the DMA of block i+3 into the stage block i-1 used, the S^T MFMAs of block
-    // i+1 (resident since the end of step i-1), then the softmax and PV of block i, and
-    // waits for block i+2. The stages are distinct LDS objects and the loop is unrolled
-    // by four, so the compiler can see that no DMA writes a stage being read.
-    if (nv > 0) stage_load(s0, lut[0]);
-    if (nv > 1) stage_load(s1, lut[1]);
-    if (nv > 2) {
-      stage_load(s2, lut[2]);
-      wait_lds_dma_but<DMA>();
-    } else {
-      wait_lds_dma();
-    }
-    __syncthreads();
-    v16f a0, a1;
-    if (nv > 0) qk_block_bf16(s0, ks0, ks1, qv, a0, a1);
-    int kb3 = nv > 3 ? lut[3] : 0;
-    int kb4 = nv > 4 ? lut[4] : 0;
-    auto step = [&](const uint4* cur, const uint4* nxt, uint4* ahead, int it) {
-      const bool fetch = it + 3 < nv;
-      // the LUT entry of block it+5 is read first: its latency overlaps this step's first
-      // LDS operand reads instead of delaying the step-end barrier
-      const int kb5 = it + 5 < nv ? lut[it + 5] : 0;
-      if (fetch) stage_load(ahead, kb3);
-      v16f n0, n1;
-      qk_block_bf16(nxt, ks0, ks1, qv, n0, n1);
-      sv_block_bf16<false>(cur, KCH, 64, qs, a0, a1, g, qi, m_run, l_run, o0, o1);
-      kb3 = kb4;
-      kb4 = kb5;
-      a0 = n0;
-      a1 = n1;
-      if (fetch) wait_lds_dma_but<DMA>();
-      else wait_lds_dma();
-      stage_barrier();
-    };
-    int it = 0;
-    for (; it + 4 < nv; it += 4) {
-      step(s0, s1, s3, it);
-      step(s1, s2, s0, it + 1);
-      step(s2, s3, s1, it + 2);
-      step(s3, s0, s2, it + 3);
-    }
-    if (it + 1 < nv) step(s0, s1, s3, it++);
-    if (it + 1 < nv) step(s1, s2, s0, it++);
-    if (it + 1 < nv) step(s2, s3, s1, it++);
-    if (nv > 0) {  // the last block (it == nv - 1), in stage it % 4
-      const int st = it & 3;
-      const uint4* cur = st == 0 ? s0 : (st == 1 ? s1 : (st == 2 ? s2 : s3));
-      if (tail_partial)
-        sv_block_bf16<true>(cur, KCH, a.Tk - lut[nv - 1] * 64, qs, a0, a1, g, qi, m_run, l_run, o0, o1);
-      else
-        sv_block_bf16<false>(cur, KCH, 64, qs, a0, a1, g, qi, m_run, l_run, o0, o1);
-      __syncthreads();  // the next row's prologue overwrites the stages
-    }
-  } else {
   auto block = [&](const uint4* cur, int nk, float cb, auto mask_tag) {
     constexpr bool M = decltype(mask_tag)::value;
     attn_block_i8<QK, V_F16, M>(cur, KCH, nk, cb, ks0, ks1, qv, g, qi, m_run, l_run, o0, o1);
@@ -758,7 +584,6 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
     block(cur, nk, c, std::true_type{});
     __syncthreads();  // the next row's prologue overwrites this stage
   }
-  }
 
   // ---- epilogue ------------------------------------------------------------
   if (part_out) {  // unnormalised O, running max and row sum of this part, in register order
@@ -772,24 +597,20 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
     part_out[8448 + tid] = l_run;
     return;
   }
-  store_row<OUT>(a, bh, qb, o0, o1, l_run);
+  store_row<OUT>(a, bh, qb, o0, o1, l_run, threadIdx.x >> 6);
 }
 
-// Resident workgroups per CU (= waves per SIMD).
-template <int QK>
-struct Occupancy {
-  static constexpr int value = QK == QK_BF16 ? 2 : 3;
-};
+// Resident workgroups per CU (= waves per SIMD) of the INT8 kernel.
+#define RESS_I8_OCCUPANCY 3
 
 template <int QK, bool V_F16, int OUT>
-__global__ __launch_bounds__(256, Occupancy<QK>::value) void k_sparse_attn(AttnArgs a, const int* __restrict__ lut,
+__global__ __launch_bounds__(256, RESS_I8_OCCUPANCY) void k_sparse_attn(AttnArgs a, const int* __restrict__ lut,
                                                         const int* __restrict__ nvalid,
                                                         const float* __restrict__ k_scale) {
   constexpr int STAGE = StageShape<QK>::STAGE;
   __shared__ __attribute__((aligned(16))) uint4 stage0[STAGE];
   __shared__ __attribute__((aligned(16))) uint4 stage1[STAGE];
   __shared__ __attribute__((aligned(16))) uint4 stage2[STAGE];
-  __shared__ __attribute__((aligned(16))) uint4 stage3[QK == QK_BF16 ? STAGE : 1];  // bf16: four stages
   __shared__ int s_item;
 
   // ---- persistent loop over this XCD's range of rows ------------------------
@@ -810,15 +631,339 @@ __global__ __launch_bounds__(256, Occupancy<QK>::value) void k_sparse_attn(AttnA
     if (pos < full_end) {
       item_to_row(pos, a.BH, a.q_blk_p, a.q_blk_total, bh, qb);
       const int nv = nvalid[(long long)bh * a.q_blk_total + qb];
-      sparse_attn_row<QK, V_F16, OUT>(a, lut, k_scale, stage0, stage1, stage2, stage3, bh, qb, 0, nv, nullptr);
+      sparse_attn_row<QK, V_F16, OUT>(a, lut, k_scale, stage0, stage1, stage2, bh, qb, 0, nv, nullptr);
     } else {
       const int j = (pos - full_end) / RESS_SPLIT_PARTS, part = pos - full_end - j * RESS_SPLIT_PARTS;
       item_to_row(full_end + j, a.BH, a.q_blk_p, a.q_blk_total, bh, qb);
       const int nv = nvalid[(long long)bh * a.q_blk_total + qb];
       float* slot = a.part + ((long long)(xcd * a.split_L + j) * RESS_SPLIT_PARTS + part) * RESS_PART_FLOATS;
-      sparse_attn_row<QK, V_F16, OUT>(a, lut, k_scale, stage0, stage1, stage2, stage3, bh, qb,
-                                      nv * part / RESS_SPLIT_PARTS, nv * (part + 1) / RESS_SPLIT_PARTS, slot);
+      sparse_attn_row<QK, V_F16, OUT>(a, lut, k_scale, stage0, stage1, stage2, bh, qb, nv * part / RESS_SPLIT_PARTS,
+                                      nv * (part + 1) / RESS_SPLIT_PARTS, slot);
     }
+  }
+}
+
+// ---- 16-bit mode: eight waves per row ---------------------------------------------------
+// Wave w takes the 32 queries 32*(w>>1).. of the row (query group) and the 32 keys
+// 32*(w&1).. of every kept block (key half), with its own (m, l, O); when the row ends the
+// two key halves of each query group are merged through LDS. With 64 KiB of LDS stages and
+// at most 128 VGPRs a workgroup, two workgroups share a CU: four waves per SIMD, so one
+// wave's LDS and MFMA latencies are covered by three others. K/V go through four LDS stages
+// filled by LDS-DMA three blocks ahead (each wave moves 2 of the 32 16-byte chunks a lane
+// moves per stage).
+#define RESS_F16_WAVES 8
+#define RESS_F16_STAGE 1024  // 16-byte chunks per stage: K block 512, V^T block 512
+
+// S^T (32 keys x 32 queries) of this wave's key half: 4 MFMAs over the 64 dims. The four K
+// operand reads go out before the first MFMA.
+__device__ __forceinline__ v16f qk_half_f16(const uint4* __restrict__ stage, const int (&kofs)[4],
+                                            const uint4 (&qv)[4]) {
+  uint4 k[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) k[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(stage) + kofs[j]);
+  __builtin_amdgcn_sched_barrier(0);
+  v16f z;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) z[r] = 0.0f;
+  v16f acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, k[0]), __builtin_bit_cast(v8h, qv[0]), z, 0,
+                                                    0, 0);
+#pragma unroll
+  for (int j = 1; j < 4; ++j)
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, k[j]), __builtin_bit_cast(v8h, qv[j]), acc, 0,
+                                                 0, 0);
+  return acc;
+}
+
+// Softmax and PV of one key half (32 keys, 16 scores per lane; register r is key
+// 32*kh + 8(r/4) + 4g + r%4 of the block). BD: bounded row, P = exp2(S); otherwise the
+// running max with lazy rescale and P = exp2(S*c - m). nk = valid keys of the block (MASK).
+template <bool BD, bool MASK>
+__device__ __forceinline__ void sv_half(const uint4* __restrict__ stage, const int (&vofs)[4], int kh, int nk, float c,
+                                        const v16f& sacc, int g, float& m_run, float& l_run, v16f& o0, v16f& o1) {
+  uint4 vv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) vv[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(stage) + vofs[j]);
+  float x[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    x[r] = sacc[r];
+    if constexpr (MASK) {
+      if (32 * kh + 8 * (r >> 2) + 4 * g + (r & 3) >= nk) x[r] = -__builtin_huge_valf();
+    }
+  }
+  float p[16];
+  if constexpr (BD) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = __builtin_amdgcn_exp2f(x[r]);
+  } else {
+    float ma = fmaxf(fmaxf(x[0], x[1]), x[2]), mb = fmaxf(fmaxf(x[8], x[9]), x[10]);
+    ma = fmaxf(fmaxf(ma, x[3]), x[4]);
+    mb = fmaxf(fmaxf(mb, x[11]), x[12]);
+    ma = fmaxf(fmaxf(ma, x[5]), x[6]);
+    mb = fmaxf(fmaxf(mb, x[13]), x[14]);
+    ma = fmaxf(fmaxf(ma, x[7]), mb);
+    const float bmax = pair_maxf(fmaxf(ma, x[15])) * c;
+    const bool need = bmax > m_run + RESS_RESCALE_LOG2;
+    if (__any(need)) {
+      const float m_new = need ? bmax : m_run;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        o0[r] *= alpha;
+        o1[r] *= alpha;
+      }
+    }
+    const float nm = -m_run;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = __builtin_amdgcn_exp2f(fmaf(x[r], c, nm));
+  }
+  pv_tile_bf16(p, vv, l_run, o0, o1);
+}
+
+// One row (query block qb of head bh) over its kept blocks kb_lo..kb_hi-1 (LUT positions),
+// 16-bit operands, 512 threads. part_out null: the whole row, written to the output;
+// otherwise one part of a split row, left in part_out for k_attn_merge (written by the
+// even waves, query group qg at threads 64*qg + lane of the 256-thread part layout).
+template <int OUT>
+__device__ __forceinline__ void attn_row_f16(const AttnArgs& a, const int* __restrict__ lut_all,
+                                             const int* __restrict__ nvalid_all, uint4* __restrict__ s0,
+                                             uint4* __restrict__ s1, uint4* __restrict__ s2, uint4* __restrict__ s3,
+                                             int* __restrict__ vote, int bh, int qb, int kb_lo, int kb_hi,
+                                             float* __restrict__ part_out) {
+  constexpr int DMA = 2;  // LDS-DMA instructions per lane per stage
+  const long long row = (long long)bh * a.q_blk_total + qb;
+  const int nv = kb_hi - kb_lo;
+  const int* lut = lut_all + row * a.kb_tot + kb_lo;
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, g = l >> 5, qi = l & 31;
+  const int qg = w >> 1, kh = w & 1;
+  const bool special = qb >= a.q_blk_p;
+  const int qbase = special ? (qb - a.q_blk_p) * 128 : qb * 128;
+  const int cnt_q = min(128, (special ? a.m.T_s : a.m.T_p) - qbase);
+  const int qrow = 32 * qg + qi;
+
+  // ---- Q operand (dims 16j+8g..16j+8g+7 of the lane's query) and the row's path -------
+  uint4 qraw[4], qv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) qraw[j] = make_uint4(0u, 0u, 0u, 0u);
+  if (qrow < cnt_q) {
+    const int tok = special ? special_to_storage(qbase + qrow, a.m) : patch_to_storage(qbase + qrow, a.m);
+    const uint16_t* src =
+        a.q_bf + (long long)(bh / a.H) * a.sqB + (long long)(bh % a.H) * a.sqH + (long long)tok * a.sqT + 8 * g;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qraw[j] = *reinterpret_cast<const uint4*>(src + 16 * j);
+  }
+  const float c = a.sm_scale_log2e;
+  float qq = 0.0f;  // |Q'|^2 over this lane's 32 dims, Q' = fp16(q * c)
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float x[8];
+    unpack_bf16x8(qraw[j], x);
+    uint32_t w4[4];
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const _Float16 h0 = (_Float16)(x[2 * cc] * c), h1 = (_Float16)(x[2 * cc + 1] * c);
+      const float f0 = (float)h0, f1 = (float)h1;
+      qq = fmaf(f0, f0, qq);
+      qq = fmaf(f1, f1, qq);
+      w4[cc] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+    }
+    qv[j] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+  }
+  // the largest key norm over the whole row's kept blocks (every part of a split row sees
+  // the same bound), times |Q'|: the row's logit bound in log2 units
+  {
+    const int* lut_row = lut_all + row * a.kb_tot;
+    const int nv_row = nvalid_all[row];
+    const float* kn = a.k_norm + (long long)bh * a.kb_tot;
+    float kmax = 0.0f;
+    for (int i = l; i < nv_row; i += 64) kmax = fmaxf(kmax, kn[lut_row[i]]);
+    kmax = wave_max(kmax);
+    const float m0 = sqrtf(pair_sum(qq)) * kmax;
+    if (l == 0) vote[w] = __any(!(m0 <= RESS_BOUND_MAX)) ? 1 : 0;  // NaN fails the test
+  }
+  __syncthreads();
+  int any_over = 0;
+#pragma unroll
+  for (int i = 0; i < RESS_F16_WAVES; ++i) any_over |= vote[i];
+  const bool bounded = __builtin_amdgcn_readfirstlane(any_over) == 0;  // the same in every lane
+  if (!bounded) {  // running-max row: the exact fp16 queries, the scale applied per score
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float x[8];
+      unpack_bf16x8(qraw[j], x);
+      qv[j] = make_uint4(f32x2_to_f16_bits(x[0], x[1]), f32x2_to_f16_bits(x[2], x[3]), f32x2_to_f16_bits(x[4], x[5]),
+                         f32x2_to_f16_bits(x[6], x[7]));
+    }
+  }
+
+  // ---- stage loads: lane l of wave w fills 16-byte slot 64w+l of the K block and of the V^T
+  // block, fetching the chunk the XOR swizzle places there (its own inverse)
+  const unsigned slot = 64 * w + l;
+  const unsigned src = 16 * (8 * (slot >> 3) + ((slot & 7) ^ (((slot >> 3) ^ (slot >> 6)) & 7)));
+  const char* kblk0 = reinterpret_cast<const char*>(a.k_pack) + (long long)bh * a.kb_tot * 8192;
+  const char* vblk0 = reinterpret_cast<const char*>(a.v_pack) + (long long)bh * a.kb_tot * 8192;
+  auto uniform_base = [](const char* p) {
+    asm("" : "+s"(p));
+    return p;
+  };
+  auto stage_load = [&](uint4* stage, int kb) {
+    char* base = reinterpret_cast<char*>(stage) + 1024 * w;
+    gl_lds16(uniform_base(kblk0 + (long long)kb * 8192) + src, base);
+    gl_lds16(uniform_base(vblk0 + (long long)kb * 8192) + src, base + 8192);
+  };
+  // LDS byte offsets of this lane's operands within a stage: K chunk 2j+g of key 32kh+qi;
+  // V^T chunks 4kh+2h+g of dims qi and 32+qi (the V^T block starts 8 KiB into the stage)
+  int kofs[4], vofs[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) kofs[j] = 16 * v_slot(32 * kh + qi, 2 * j + g);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    vofs[2 * h] = 8192 + 16 * v_slot(qi, 4 * kh + 2 * h + g);
+    vofs[2 * h + 1] = 8192 + 16 * v_slot(32 + qi, 4 * kh + 2 * h + g);
+  }
+
+  float m_run = bounded ? 0.0f : -__builtin_huge_valf(), l_run = 0.0f;
+  v16f o0, o1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) o0[r] = o1[r] = 0.0f;
+  // only the sequence's last key block can be partial; LUTs are ascending, so if it is kept
+  // it is the last entry, which runs masked after the loop
+  const bool tail_partial = nv > 0 && (a.Tk & 63) != 0 && lut[nv - 1] == a.kb_tot - 1;
+
+  auto run = [&](auto bounded_tag) {
+    constexpr bool BD = decltype(bounded_tag)::value;
+    // Block i lives in stage i % 4. Step i issues the DMA of block i+3 into the stage block
+    // i-1 used, computes block i, and waits for block i+1 (blocks i+2, i+3 may stay in
+    // flight). The loop is unrolled by four over distinct LDS arrays, so the compiler sees
+    // that no DMA writes a stage being read.
+    if (nv > 0) stage_load(s0, lut[0]);
+    if (nv > 1) stage_load(s1, lut[1]);
+    if (nv > 2) stage_load(s2, lut[2]);
+    if (nv > 2) wait_lds_dma_but<2 * DMA>();
+    else if (nv > 1) wait_lds_dma_but<DMA>();
+    else wait_lds_dma();
+    __syncthreads();
+    int kb3 = nv > 3 ? lut[3] : 0;
+    auto block = [&](const uint4* cur, int nk, auto mask_tag) {
+      constexpr bool MK = decltype(mask_tag)::value;
+      // the lane's byte offsets pass through an empty asm every block: the compiler then
+      // adds the stage's address as the ds_read immediate instead of keeping one set of
+      // offsets per stage live, which would not fit the 128 VGPRs
+      asm volatile("" : "+v"(kofs[0]), "+v"(kofs[1]), "+v"(kofs[2]), "+v"(kofs[3]), "+v"(vofs[0]), "+v"(vofs[1]),
+                   "+v"(vofs[2]), "+v"(vofs[3]));
+      const v16f sacc = qk_half_f16(cur, kofs, qv);
+      sv_half<BD, MK>(cur, vofs, kh, nk, c, sacc, g, m_run, l_run, o0, o1);
+    };
+    auto step = [&](const uint4* cur, uint4* ahead, int it) {
+      const bool fetch = it + 3 < nv;
+      const int kb4 = it + 4 < nv ? lut[it + 4] : 0;
+      if (fetch) stage_load(ahead, kb3);
+      block(cur, 64, std::false_type{});
+      kb3 = kb4;
+      if (fetch) wait_lds_dma_but<2 * DMA>();
+      else if (it + 2 < nv) wait_lds_dma_but<DMA>();
+      else wait_lds_dma();
+      stage_barrier();
+    };
+    const int last = nv - 1;  // the final block runs after the loop (masked if partial)
+    int it = 0;
+    for (; it + 4 <= last; it += 4) {
+      step(s0, s3, it);
+      step(s1, s0, it + 1);
+      step(s2, s1, it + 2);
+      step(s3, s2, it + 3);
+    }
+    if (it < last) step(s0, s3, it++);
+    if (it < last) step(s1, s0, it++);
+    if (it < last) step(s2, s1, it++);
+    if (nv > 0) {
+      const int st = it & 3;
+      const uint4* cur = st == 0 ? s0 : (st == 1 ? s1 : (st == 2 ? s2 : s3));
+      if (tail_partial) block(cur, a.Tk - lut[last] * 64, std::true_type{});
+      else block(cur, 64, std::false_type{});
+    }
+  };
+  if (bounded) run(std::true_type{});
+  else run(std::false_type{});
+
+  // ---- merge the two key halves of each query group through LDS (the stages are free once
+  // every wave has read its last block); the even wave of a group finishes the row
+  __syncthreads();
+  float* xs = reinterpret_cast<float*>(qg == 0 ? s0 : (qg == 1 ? s1 : (qg == 2 ? s2 : s3)));
+  if (kh == 1) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      xs[r * 64 + l] = o0[r];
+      xs[(16 + r) * 64 + l] = o1[r];
+    }
+    xs[32 * 64 + l] = m_run;
+    xs[33 * 64 + l] = l_run;
+  }
+  __syncthreads();
+  if (kh == 0) {
+    const float mo = xs[32 * 64 + l], lo = xs[33 * 64 + l];
+    const float mm = fmaxf(m_run, mo);
+    const float fe = m_run == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(m_run - mm);
+    const float fo = mo == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(mo - mm);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      o0[r] = fmaf(fo, xs[r * 64 + l], o0[r] * fe);
+      o1[r] = fmaf(fo, xs[(16 + r) * 64 + l], o1[r] * fe);
+    }
+    m_run = mm;
+    l_run = fmaf(fo, lo, l_run * fe);
+    if (part_out) {  // unnormalised O, running max and row sum of this part, in register order
+      const int t4 = 64 * qg + l;
+      float4* po = reinterpret_cast<float4*>(part_out);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        po[q * 256 + t4] = make_float4(o0[4 * q], o0[4 * q + 1], o0[4 * q + 2], o0[4 * q + 3]);
+        po[(4 + q) * 256 + t4] = make_float4(o1[4 * q], o1[4 * q + 1], o1[4 * q + 2], o1[4 * q + 3]);
+      }
+      part_out[8192 + t4] = m_run;
+      part_out[8448 + t4] = l_run;
+    } else {
+      store_row<OUT>(a, bh, qb, o0, o1, l_run, qg);
+    }
+  }
+  __syncthreads();  // the next row's prologue overwrites the stages
+}
+
+// The persistent 16-bit kernel: the row loop of k_sparse_attn with eight waves per row.
+template <int OUT>
+__global__ __launch_bounds__(512, 4) void k_sparse_attn_f16(AttnArgs a, const int* __restrict__ lut,
+                                                            const int* __restrict__ nvalid) {
+  __shared__ __attribute__((aligned(16))) uint4 stage0[RESS_F16_STAGE];
+  __shared__ __attribute__((aligned(16))) uint4 stage1[RESS_F16_STAGE];
+  __shared__ __attribute__((aligned(16))) uint4 stage2[RESS_F16_STAGE];
+  __shared__ __attribute__((aligned(16))) uint4 stage3[RESS_F16_STAGE];
+  __shared__ int s_item;
+  __shared__ int s_vote[RESS_F16_WAVES];
+  const int xcd = blockIdx.x & 7;
+  const int b1 = a.sched[xcd + 1];
+  const int Lx = min(a.split_L, b1 - a.sched[xcd]);
+  const int full_end = b1 - Lx;
+  const int item_end = full_end + Lx * RESS_SPLIT_PARTS;
+  for (;;) {
+    if (threadIdx.x == 0) s_item = atomicAdd(&a.sched[16 + xcd], 1);
+    __syncthreads();
+    const int pos = __builtin_amdgcn_readfirstlane(s_item);
+    __syncthreads();
+    if (pos >= item_end) break;
+    // a whole row, or part `part` of split row j (one call site: one inlined copy of the row)
+    const bool split = pos >= full_end;
+    const int j = split ? (pos - full_end) / RESS_SPLIT_PARTS : 0;
+    const int part = split ? pos - full_end - j * RESS_SPLIT_PARTS : 0;
+    int bh, qb;
+    item_to_row(split ? full_end + j : pos, a.BH, a.q_blk_p, a.q_blk_total, bh, qb);
+    const int nv = nvalid[(long long)bh * a.q_blk_total + qb];
+    float* slot =
+        split ? a.part + ((long long)(xcd * a.split_L + j) * RESS_SPLIT_PARTS + part) * RESS_PART_FLOATS : nullptr;
+    const int lo = split ? nv * part / RESS_SPLIT_PARTS : 0;
+    const int hi = split ? nv * (part + 1) / RESS_SPLIT_PARTS : nv;
+    attn_row_f16<OUT>(a, lut, nvalid, stage0, stage1, stage2, stage3, s_vote, bh, qb, lo, hi, slot);
   }
 }
 
@@ -861,7 +1006,7 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
       o1[4 * q + 3] = fmaf(f, v.w, o1[4 * q + 3]);
     }
   }
-  store_row<OUT>(a, bh, qb, o0, o1, l_run);
+  store_row<OUT>(a, bh, qb, o0, o1, l_run, tid >> 6);
 }
 
 // Plain (B,H,Tk,64) 16-bit V -> packed [BH][kb][64 dims][64 permuted keys].
@@ -909,20 +1054,38 @@ static int launch_attn(const AttnArgs& a, int out_dtype, hipStream_t stream) {
   hipLaunchKernelGGL(k_attn_schedule, dim3(1), dim3(1024), 0, stream, a.nvalid, a.BH, a.q_blk_p, a.q_blk_total,
                      a.sched);
   RESS_LAUNCHED("k_attn_schedule");
-  // persistent: Occupancy<QK> resident workgroups per CU, a multiple of the 8 XCDs
-  const dim3 grid(8 * ((Occupancy<QK>::value * g_cu_count[dev] + 7) / 8)), block(256);
-  switch (out_dtype) {
-    case OUT_F32:
-      hipLaunchKernelGGL((k_sparse_attn<QK, V_F16, OUT_F32>), grid, block, 0, stream, a, a.lut, a.nvalid, a.k_scale);
-      break;
-    case OUT_BF16:
-      hipLaunchKernelGGL((k_sparse_attn<QK, V_F16, OUT_BF16>), grid, block, 0, stream, a, a.lut, a.nvalid, a.k_scale);
-      break;
-    default:
-      hipLaunchKernelGGL((k_sparse_attn<QK, V_F16, OUT_F16>), grid, block, 0, stream, a, a.lut, a.nvalid, a.k_scale);
-      break;
+  const dim3 block(256);
+  if constexpr (QK == QK_F16) {
+    // persistent: two 512-thread workgroups per CU, a multiple of the 8 XCDs
+    const dim3 grid(8 * ((2 * g_cu_count[dev] + 7) / 8)), fblock(64 * RESS_F16_WAVES);
+    switch (out_dtype) {
+      case OUT_F32:
+        hipLaunchKernelGGL(k_sparse_attn_f16<OUT_F32>, grid, fblock, 0, stream, a, a.lut, a.nvalid);
+        break;
+      case OUT_BF16:
+        hipLaunchKernelGGL(k_sparse_attn_f16<OUT_BF16>, grid, fblock, 0, stream, a, a.lut, a.nvalid);
+        break;
+      default:
+        hipLaunchKernelGGL(k_sparse_attn_f16<OUT_F16>, grid, fblock, 0, stream, a, a.lut, a.nvalid);
+        break;
+    }
+    RESS_LAUNCHED("k_sparse_attn_f16");
+  } else {
+    // persistent: RESS_I8_OCCUPANCY resident workgroups per CU, a multiple of the 8 XCDs
+    const dim3 grid(8 * ((RESS_I8_OCCUPANCY * g_cu_count[dev] + 7) / 8));
+    switch (out_dtype) {
+      case OUT_F32:
+        hipLaunchKernelGGL((k_sparse_attn<QK, V_F16, OUT_F32>), grid, block, 0, stream, a, a.lut, a.nvalid, a.k_scale);
+        break;
+      case OUT_BF16:
+        hipLaunchKernelGGL((k_sparse_attn<QK, V_F16, OUT_BF16>), grid, block, 0, stream, a, a.lut, a.nvalid, a.k_scale);
+        break;
+      default:
+        hipLaunchKernelGGL((k_sparse_attn<QK, V_F16, OUT_F16>), grid, block, 0, stream, a, a.lut, a.nvalid, a.k_scale);
+        break;
+    }
+    RESS_LAUNCHED("k_sparse_attn");
   }
-  RESS_LAUNCHED("k_sparse_attn");
   const dim3 mgrid(8 * a.split_L);
   switch (out_dtype) {
     case OUT_F32:
@@ -1025,19 +1188,22 @@ RESS_API int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void
                      layer_map(frames, P, S), frames * P, sm_scale, out, out_dtype, soB, soH, soT, sched, stream);
 }
 
-// The same fused-path attention with QK^T on the bf16 inputs themselves (fp32
-// accumulation): q is the layer's bf16 query tensor (B,H,frames*P,64) in storage order
-// with element strides sqB/sqH/sqT, k_pack the bf16 key blocks ress_prep_qkv writes,
-// v_pack its packed bf16 V. No quantisation error enters the logits; the online
-// softmax, P rounding and PV product are those of ress_sparse_attn_fwd.
-RESS_API int ress_sparse_attn_fwd_bf16(const void* q, long long sqB, long long sqH, long long sqT, const void* k_pack,
-                                       const void* v_pack, const void* lut, const void* nvalid, int B, int H,
-                                       int frames, int P, int S, float sm_scale, void* out, int out_dtype,
-                                       long long soB, long long soH, long long soT, void* sched, hipStream_t stream) {
-  RESS_REQUIRE(B > 0 && H > 0 && frames > 0 && P > S && S >= 0, "ress_sparse_attn_fwd_bf16: bad geometry");
-  RESS_REQUIRE(q && k_pack, "ress_sparse_attn_fwd_bf16: null pointer");
+// The same fused-path attention with QK^T on 16-bit operands (fp32 accumulation): q is
+// the layer's bf16 query tensor (B,H,frames*P,64) in storage order with element strides
+// sqB/sqH/sqT, converted to fp16 per row in registers; k_pack the fp16 key blocks and
+// k_norm the per-block largest key norms ress_prep_qkv writes (16-bit operands), v_pack
+// its packed bf16 V. A row whose logit bound |q'| * max key norm is at most
+// RESS_BOUND_MAX runs with pre-scaled fp16 queries and a fixed offset (no running max);
+// other rows use exact fp16 queries and the running max (see qk_block_f16).
+RESS_API int ress_sparse_attn_fwd_f16(const void* q, long long sqB, long long sqH, long long sqT, const void* k_pack,
+                                      const void* k_norm, const void* v_pack, const void* lut, const void* nvalid,
+                                      int B, int H, int frames, int P, int S, float sm_scale, void* out,
+                                      int out_dtype, long long soB, long long soH, long long soT, void* sched,
+                                      hipStream_t stream) {
+  RESS_REQUIRE(B > 0 && H > 0 && frames > 0 && P > S && S >= 0, "ress_sparse_attn_fwd_f16: bad geometry");
+  RESS_REQUIRE(q && k_pack && k_norm, "ress_sparse_attn_fwd_f16: null pointer");
   RESS_REQUIRE(al16(q) && al16(k_pack) && sqT % 8 == 0 && sqH % 8 == 0 && sqB % 8 == 0,
-               "ress_sparse_attn_fwd_bf16: q/k_pack must be 16-byte aligned, q strides a multiple of 8");
+               "ress_sparse_attn_fwd_f16: q/k_pack must be 16-byte aligned, q strides a multiple of 8");
   AttnArgs a;
   if (attn_args(a, v_pack, lut, nvalid, B, H, layer_map(frames, P, S), frames * P, sm_scale, out, out_dtype, soB, soH,
                 soT, sched))
@@ -1047,7 +1213,8 @@ RESS_API int ress_sparse_attn_fwd_bf16(const void* q, long long sqB, long long s
   a.sqH = sqH;
   a.sqT = sqT;
   a.k_pack = (const uint16_t*)k_pack;
-  return launch_attn<QK_BF16, false>(a, out_dtype, stream);
+  a.k_norm = (const float*)k_norm;
+  return launch_attn<QK_F16, false>(a, out_dtype, stream);
 }
 
 static long long qattn_vpack_bytes(int B, int H, int Tk) { return (long long)B * H * cdiv(Tk, 64) * 4096 * 2; }
@@ -1113,7 +1280,7 @@ RESS_API int ress_qattn_block_sparse_fwd(const void* q_i8, const void* k_i8, con
                      Tk, sm_scale, o, o_dtype, soB, soH, soT, (char*)workspace + qattn_vpack_bytes(B, H, Tk), stream);
 }
 
-// ---- allocation-free variant of ress_sparse_attn_fwd_bf16 -------------------------------
+// ---- allocation-free variant of ress_sparse_attn_fwd_f16 --------------------------------
 // For callers that cannot allocate device memory (code under graph capture, serving loops,
 // harnesses that forbid hipMalloc): the launch's scratch -- the row schedule and the parts
 // of the split rows, ress_attn_sched_bytes(...) bytes, at most RESS_NOALLOC_SCRATCH_BYTES
@@ -1134,13 +1301,13 @@ static void* g_scratch_addr[64];
 static int scratch_address(void** out) {
   int dev = -1;
   RESS_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64,
-               "ress_sparse_attn_fwd_bf16_noalloc: no usable current device");
+               "ress_sparse_attn_fwd_f16_noalloc: no usable current device");
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_addr[dev] == nullptr) {
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     RESS_REQUIRE(e == hipSuccess && p != nullptr,
-                 "ress_sparse_attn_fwd_bf16_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                 "ress_sparse_attn_fwd_f16_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
                  hipGetErrorString(e));
     g_scratch_addr[dev] = p;
   }
@@ -1150,18 +1317,18 @@ static int scratch_address(void** out) {
 
 RESS_API long long ress_noalloc_scratch_bytes(void) { return RESS_NOALLOC_SCRATCH_BYTES; }
 
-RESS_API int ress_sparse_attn_fwd_bf16_noalloc(const void* q, long long sqB, long long sqH, long long sqT,
-                                               const void* k_pack, const void* v_pack, const void* lut,
-                                               const void* nvalid, int B, int H, int frames, int P, int S,
-                                               float sm_scale, void* out, int out_dtype, long long soB, long long soH,
-                                               long long soT, hipStream_t stream) {
-  RESS_REQUIRE(B > 0 && H > 0 && frames > 0 && P > S && S >= 0, "ress_sparse_attn_fwd_bf16_noalloc: bad geometry");
+RESS_API int ress_sparse_attn_fwd_f16_noalloc(const void* q, long long sqB, long long sqH, long long sqT,
+                                              const void* k_pack, const void* k_norm, const void* v_pack,
+                                              const void* lut, const void* nvalid, int B, int H, int frames, int P,
+                                              int S, float sm_scale, void* out, int out_dtype, long long soB,
+                                              long long soH, long long soT, hipStream_t stream) {
+  RESS_REQUIRE(B > 0 && H > 0 && frames > 0 && P > S && S >= 0, "ress_sparse_attn_fwd_f16_noalloc: bad geometry");
   const long long need = ress_attn_sched_bytes(B, H, frames * P);
   RESS_REQUIRE(need > 0 && need <= RESS_NOALLOC_SCRATCH_BYTES,
-               "ress_sparse_attn_fwd_bf16_noalloc: this shape needs %lld bytes of scratch, the static array holds %lld",
+               "ress_sparse_attn_fwd_f16_noalloc: this shape needs %lld bytes of scratch, the static array holds %lld",
                need, (long long)RESS_NOALLOC_SCRATCH_BYTES);
   void* sched = nullptr;
   if (scratch_address(&sched) != 0) return -1;
-  return ress_sparse_attn_fwd_bf16(q, sqB, sqH, sqT, k_pack, v_pack, lut, nvalid, B, H, frames, P, S, sm_scale, out,
-                                   out_dtype, soB, soH, soT, sched, stream);
+  return ress_sparse_attn_fwd_f16(q, sqB, sqH, sqT, k_pack, k_norm, v_pack, lut, nvalid, B, H, frames, P, S, sm_scale,
+                                  out, out_dtype, soB, soH, soT, sched, stream);
 }

@@ -86,6 +86,10 @@ __device__ __forceinline__ void unpack_bf16x8(const uint4& r, float x[8]) {
   x[6] = bf16_lo(r.w); x[7] = bf16_hi(r.w);
 }
 // fp32 -> bf16, round to nearest even (NaN kept quiet)
+// two floats -> packed fp16 pair (round to nearest even), lo in bits 0..15
+__device__ __forceinline__ uint32_t f32x2_to_f16_bits(float lo, float hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+}
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;

@@ -86,7 +86,10 @@ __global__ __launch_bounds__(64) void k_prep_q(const uint16_t* __restrict__ q, S
 // ----------------------------------------------------------------------------
 // K/V blocks over the kernel key grid (patch keys then special keys).
 //  ksum   [BH][kb_tot][64]  full-block K sums (SUM8x), for the key mean (or null)
-//  k_pack [BH][kb_tot][64 keys][64] bf16 row-major K blocks (or null)
+//  k_pack [BH][kb_tot][64 keys][64] fp16 row-major K blocks (or null); a bf16 value is
+//         exact in fp16 unless below 2^-14 in magnitude (the subnormal range) or above 65504
+//  k_norm [BH][kb_tot]  the block's largest key norm sqrt(sum_d k_d^2) (or null): per key
+//         an fmaf chain over each lane's 8 dims, the tree of the 8 lanes, sqrtf; then the max
 //  pooled_k [BH][kb_p][64]  patch-only K means (the scoring grid)
 //  pooled_v [BH][kb_p][64]  patch-only V means (ReSS's v_bar)
 //  v_pack [BH][kb_tot][64 dims][64 keys]  bf16, keys permuted inside every group of
@@ -96,7 +99,7 @@ __global__ __launch_bounds__(64) void k_prep_kv(const uint16_t* __restrict__ k, 
                                                 Strides sk, Strides sv, TokenMap m, int Tk, int kb_tot, int kb_p,
                                                 float* __restrict__ ksum, float* __restrict__ pooled_k,
                                                 float* __restrict__ pooled_v, uint16_t* __restrict__ v_pack,
-                                                uint16_t* __restrict__ k_pack) {
+                                                uint16_t* __restrict__ k_pack, float* __restrict__ k_norm) {
   __shared__ uint16_t vt[64 * 64];
   const int kb = blockIdx.x, bh = blockIdx.y, lane = threadIdx.x;
   const int j = lane >> 3, dg = lane & 7;
@@ -107,12 +110,14 @@ __global__ __launch_bounds__(64) void k_prep_kv(const uint16_t* __restrict__ k, 
   const uint16_t* vsrc = v + bh_offset(bh, sv) + dg * 8;
 
   float ka[8], kp[8], vp[8];
+  float nmax = 0.0f;  // largest key norm of this lane's keys (lane group j holds key t's 64 dims)
 #pragma unroll
   for (int c = 0; c < 8; ++c) ka[c] = kp[c] = vp[c] = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int t = 8 * i + j;
-    uint4 rv = make_uint4(0u, 0u, 0u, 0u), rk = rv;
+    uint4 rv = make_uint4(0u, 0u, 0u, 0u), rk = rv, rk16 = rv;
+    float ss = 0.0f;
     if (t < cnt) {
       const int tok = key_to_storage(base + t, m);
       rk = *reinterpret_cast<const uint4*>(ksrc + (long long)tok * sk.t);
@@ -120,6 +125,14 @@ __global__ __launch_bounds__(64) void k_prep_kv(const uint16_t* __restrict__ k, 
       float xk[8], xv[8];
       unpack_bf16x8(rk, xk);
       unpack_bf16x8(rv, xv);
+      if (k_pack) {
+        rk16.x = f32x2_to_f16_bits(xk[0], xk[1]);
+        rk16.y = f32x2_to_f16_bits(xk[2], xk[3]);
+        rk16.z = f32x2_to_f16_bits(xk[4], xk[5]);
+        rk16.w = f32x2_to_f16_bits(xk[6], xk[7]);
+      }
+#pragma unroll
+      for (int c = 0; c < 8; ++c) ss = fmaf(xk[c], xk[c], ss);
 #pragma unroll
       for (int c = 0; c < 8; ++c) ka[c] = ka[c] + xk[c];
       if (t < cnt_p) {
@@ -130,8 +143,14 @@ __global__ __launch_bounds__(64) void k_prep_kv(const uint16_t* __restrict__ k, 
         }
       }
     }
-    if (k_pack)  // row-major bf16 K block, zero past the sequence end
-      *reinterpret_cast<uint4*>(k_pack + (((long long)bh * kb_tot + kb) * 64 + t) * 64 + dg * 8) = rk;
+    if (k_pack)  // row-major fp16 K block, zero past the sequence end
+      *reinterpret_cast<uint4*>(k_pack + (((long long)bh * kb_tot + kb) * 64 + t) * 64 + dg * 8) = rk16;
+    if (k_norm) {  // key t's squared norm: the tree of the 8 dim-group lanes of group j
+      ss = ss + __shfl_xor(ss, 1, 64);
+      ss = ss + __shfl_xor(ss, 2, 64);
+      ss = ss + __shfl_xor(ss, 4, 64);
+      nmax = fmaxf(nmax, sqrtf(ss));
+    }
     // transpose into LDS: vt[dim][perm(key)]
     const int u = t & 15;
     const int pos = (t & ~15) + 8 * ((u >> 2) & 1) + 4 * (u >> 3) + (u & 3);
@@ -147,6 +166,12 @@ __global__ __launch_bounds__(64) void k_prep_kv(const uint16_t* __restrict__ k, 
     ka[c] = sum8_tree(ka[c]);
     kp[c] = sum8_tree(kp[c]);
     vp[c] = sum8_tree(vp[c]);
+  }
+  if (k_norm) {
+    nmax = fmaxf(nmax, __shfl_xor(nmax, 8, 64));
+    nmax = fmaxf(nmax, __shfl_xor(nmax, 16, 64));
+    nmax = fmaxf(nmax, __shfl_xor(nmax, 32, 64));
+    if (lane == 0) k_norm[(long long)bh * kb_tot + kb] = nmax;
   }
   if (j == 0) {
     if (ksum) {
@@ -249,9 +274,10 @@ static TokenMap make_map(int frames, int P, int S) {
 // order with element strides (sB, sH, sT); D = 64 with unit stride.
 //  * INT8 operands (q_i8 and k_i8 set): codes, scales, key mean; q_lo/k_lo (same
 //    layouts as q_i8/k_i8) receive the split-INT8 residual codes, or are null.
-//  * bf16 operands (q_i8 and k_i8 null): only the pools, v_pack and k_pack are
-//    written; q_lo, q_scale, k_lo, k_scale, ksum and km are unused (may be null).
-// k_pack [BH][kb_tot][64 keys][64] bf16 (keys in kernel order, zero-padded) is
+//  * 16-bit operands (q_i8 and k_i8 null): the pools, v_pack, k_pack and, in k_scale,
+//    each key block's largest key norm (k_norm of k_prep_kv) are written; q_lo,
+//    q_scale, k_lo, ksum and km are unused (may be null).
+// k_pack [BH][kb_tot][64 keys][64] fp16 (keys in kernel order, zero-padded) is
 // written whenever it is non-null.
 RESS_API int ress_prep_qkv(const void* q, const void* k, const void* v, int B, int H, int frames, int P, int S,
                            long long sqB, long long sqH, long long sqT, long long skB, long long skH, long long skT,
@@ -264,7 +290,7 @@ RESS_API int ress_prep_qkv(const void* q, const void* k, const void* v, int B, i
   const bool quant = q_i8 != nullptr;
   RESS_REQUIRE((q_i8 == nullptr) == (k_i8 == nullptr), "ress_prep_qkv: give both q_i8 and k_i8, or neither");
   RESS_REQUIRE(!quant || (q_scale && k_scale && ksum && km), "ress_prep_qkv: INT8 operands need q_scale, k_scale, ksum, km");
-  RESS_REQUIRE(quant || k_pack, "ress_prep_qkv: bf16 operands need k_pack");
+  RESS_REQUIRE(quant || (k_pack && k_scale), "ress_prep_qkv: 16-bit operands need k_pack and k_scale");
   RESS_REQUIRE(quant || (!q_lo && !k_lo), "ress_prep_qkv: q_lo/k_lo need the INT8 operands");
   RESS_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(v_pack) && aligned16(q_i8) && aligned16(k_i8) &&
                    aligned16(q_lo) && aligned16(k_lo) && aligned16(k_pack),
@@ -285,7 +311,7 @@ RESS_API int ress_prep_qkv(const void* q, const void* k, const void* v, int B, i
   RESS_LAUNCHED("k_prep_q");
   hipLaunchKernelGGL(k_prep_kv, dim3(kb_tot, BH), dim3(64), 0, stream, (const uint16_t*)k, (const uint16_t*)v, sk, sv,
                      m, Tk, kb_tot, kb_p, (float*)(quant ? ksum : nullptr), (float*)pooled_k, (float*)pooled_v,
-                     (uint16_t*)v_pack, (uint16_t*)k_pack);
+                     (uint16_t*)v_pack, (uint16_t*)k_pack, (float*)(quant ? nullptr : k_scale));
   RESS_LAUNCHED("k_prep_kv");
   if (!quant) return 0;
   hipLaunchKernelGGL(k_key_mean, dim3(BH), dim3(64), 0, stream, (const float*)ksum, kb_tot, Tk, (float*)km);
@@ -342,7 +368,7 @@ RESS_API int ress_prep_kv_plain(const void* k, const void* v, int B, int H, int 
   Strides sk{skB, skH, skT, H}, sv{svB, svH, svT, H};
   hipLaunchKernelGGL(k_prep_kv, dim3(nk, BH), dim3(64), 0, stream, (const uint16_t*)k, (const uint16_t*)v, sk, sv, mk,
                      Tk, nk, nk, (float*)ksum, (float*)pooled_k, (float*)pooled_v, (uint16_t*)v_pack,
-                     (uint16_t*)nullptr);
+                     (uint16_t*)nullptr, (float*)nullptr);
   RESS_LAUNCHED("k_prep_kv");
   hipLaunchKernelGGL(k_key_mean, dim3(BH), dim3(64), 0, stream, (const float*)ksum, nk, Tk, (float*)km);
   RESS_LAUNCHED("k_key_mean");

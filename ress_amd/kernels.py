@@ -87,20 +87,22 @@ class LayerGrid:
         return self.kb_tot - self.n_cand
 
 
-QK_MODES = ("bf16", "i8x2", "i8")
+QK_MODES = ("f16", "i8x2", "i8")
 
 
 @dataclass
 class Blocks:
     """Output of the preparation pass (see ress_prep_qkv). `mode` names the QK^T
     operands the attention kernel will use:
-      "bf16"  the bf16 inputs themselves (q, k_pack); no codes are written
+      "f16"   16-bit operands: the bf16 queries (converted to fp16 per row by the kernel),
+              k_pack (fp16 K blocks) and k_scale = each key block's largest key norm
+              (the bound of the kernel's fixed-offset softmax); no codes are written
       "i8x2"  two-term INT8 codes (q_i8 + q_lo, k_i8 + k_lo) with per-block scales
       "i8"    the reference's single-term per-block INT8 codes (q_i8, k_i8)"""
 
     grid: LayerGrid
     mode: str
-    q: torch.Tensor  # the bf16 queries (storage order), read directly in "bf16" mode
+    q: torch.Tensor  # the bf16 queries (storage order), read directly in "f16" mode
     q_i8: torch.Tensor
     q_lo: torch.Tensor
     q_scale: torch.Tensor
@@ -127,7 +129,7 @@ def _check_qkv(t, name, grid):
         raise ValueError(f"{name} must have a unit-stride head dim")
 
 
-def prepare_blocks(q, k, v, grid, mode="bf16", split=None):
+def prepare_blocks(q, k, v, grid, mode="f16", split=None):
     """Pool and pack one layer's Q/K/V (bf16, storage order) for the attention mode
     `mode` (see Blocks). `split` is the older spelling: True = "i8x2", False = "i8"."""
     if split is not None:
@@ -138,7 +140,7 @@ def prepare_blocks(q, k, v, grid, mode="bf16", split=None):
         _check_qkv(t, n, grid)
     dev = q.device
     BH = grid.BH
-    quant = mode != "bf16"
+    quant = mode != "f16"
     e = lambda *s, dt=torch.float32: torch.empty(*s, dtype=dt, device=dev)  # noqa: E731
     b = Blocks(
         grid=grid,
@@ -150,11 +152,11 @@ def prepare_blocks(q, k, v, grid, mode="bf16", split=None):
         pooled_q=e(BH, grid.q_blk_p, HEAD_DIM),
         k_i8=e(BH, grid.kb_tot, KS_K, HEAD_DIM, dt=torch.int8) if quant else None,
         k_lo=e(BH, grid.kb_tot, KS_K, HEAD_DIM, dt=torch.int8) if mode == "i8x2" else None,
-        k_scale=e(BH, grid.kb_tot) if quant else None,
+        k_scale=e(BH, grid.kb_tot),
         pooled_k=e(BH, grid.kb_p, HEAD_DIM),
         pooled_v=e(BH, grid.kb_p, HEAD_DIM),
         v_pack=e(BH, grid.kb_tot, 4096, dt=torch.bfloat16),
-        k_pack=None if quant else e(BH, grid.kb_tot, KS_K, HEAD_DIM, dt=torch.bfloat16),
+        k_pack=None if quant else e(BH, grid.kb_tot, KS_K, HEAD_DIM, dt=torch.float16),
         ksum=e(BH, grid.kb_tot, HEAD_DIM) if quant else None,
         km=e(BH, HEAD_DIM) if quant else None,
     )
@@ -264,8 +266,8 @@ def sparse_attention(blocks, lut, nvalid, out=None, out_dtype=torch.float32):
     sched = torch.empty(_lib.lib().ress_attn_sched_bytes(g.B, g.H, g.Tk), dtype=torch.uint8, device=dev)
     P = _lib.ptr
     sm = 1.0 / math.sqrt(HEAD_DIM)
-    if blocks.mode == "bf16":
-        _lib.call("ress_sparse_attn_fwd_bf16", P(blocks.q), *blocks.q.stride()[:3], P(blocks.k_pack),
+    if blocks.mode == "f16":
+        _lib.call("ress_sparse_attn_fwd_f16", P(blocks.q), *blocks.q.stride()[:3], P(blocks.k_pack), P(blocks.k_scale),
                   P(blocks.v_pack), P(lut), P(nvalid), g.B, g.H, g.frames, g.P, g.S, sm, P(out), code,
                   *out.stride()[:3], P(sched), _lib.stream_handle(dev))
     else:

@@ -70,7 +70,7 @@ def config1(dev):
     return q, k, v, P, S, bud, o
 
 
-@pytest.mark.parametrize("mode", ["bf16", "i8x2"])
+@pytest.mark.parametrize("mode", ["f16", "i8x2"])
 def test_config0_uniform_with_sink(mode, dev):
     frames, sr, cdf = 4, 0.5, 0.9
     _say(f"[configs[0] {mode}] frames={frames} sr={sr} cdf={cdf} attention_sink={SINK}")
@@ -92,7 +92,7 @@ def test_config0_uniform_with_sink(mode, dev):
     assert worst <= ATOL and cmin >= MIN_COS
 
 
-@pytest.mark.parametrize("mode", ["bf16", "i8x2", "i8"])
+@pytest.mark.parametrize("mode", ["f16", "i8x2", "i8"])
 def test_config1_hess_every_row(config1, mode, dev):
     q, k, v, P, S, bud, o = config1
     _say(f"[configs[1] {mode}] 16 frames HeSS sr=0.7")
@@ -131,7 +131,7 @@ def test_config2_ress_layer(dev):
     assert np.array_equal(_np(res.final_map).reshape(o["map"].shape), o["map"])
     assert np.array_equal(_np(res.nvalid), o["nvalid"])
     _say(f"[configs[2]] map bit-exact, realised sparsity {res.sparsity():.4f}")
-    worst, cmin = _check_rows("configs[2] bf16", res, qd, kd, vd, g)
+    worst, cmin = _check_rows("configs[2] f16", res, qd, kd, vd, g)
     assert worst <= ATOL and cmin >= MIN_COS
 
 
@@ -158,7 +158,7 @@ def test_config4_long_sequence(dev):
     rows = split_rows(nv, g.q_blk_p)
     rows[:, g.q_blk_p:] = True
     rows[:, :g.q_blk_p:16] = True
-    worst, cmin = _check_rows("configs[4] bf16", res, qd, kd, vd, g, rows=rows)
+    worst, cmin = _check_rows("configs[4] f16", res, qd, kd, vd, g, rows=rows)
     assert worst <= ATOL and cmin >= MIN_COS
 
 

@@ -74,22 +74,28 @@ def test_prep_bit_exact(layer, dev):
     assert _bits_equal(_np(blocks.v_pack), o["v_pack"])
 
 
-def test_prep_bf16_operands(layer, dev):
-    """bf16 mode: the pools and v_pack equal the INT8 modes' (oracle) bit for bit, and
-    k_pack is K in kernel key order cat(patch, special), zero-padded to whole blocks."""
+def test_prep_f16_operands(layer, dev):
+    """16-bit mode: the pools and v_pack equal the INT8 modes' (oracle) bit for bit; k_pack
+    is K in kernel key order cat(patch, special) rounded to fp16, zero-padded to whole
+    blocks; k_scale holds each key block's largest key norm, bit-exact against the oracle
+    and within one ulp of the float64 norm."""
     name, q, k, v, frames, P, S, H = layer
     g = LayerGrid(1, H, frames, P, S)
-    blocks = kernels.prepare_blocks(q.to(dev), k.to(dev), v.to(dev), g, mode="bf16")
+    blocks = kernels.prepare_blocks(q.to(dev), k.to(dev), v.to(dev), g, mode="f16")
     torch.cuda.synchronize()
     assert blocks.q_i8 is None and blocks.k_i8 is None
     o = oracle.prep_qkv(q, k, v, frames, P, S)
     for field in ("pooled_q", "pooled_k", "pooled_v", "v_pack"):
         assert _bits_equal(_np(getattr(blocks, field)), o[field]), field
+    assert _bits_equal(_np(blocks.k_scale), o["k_norm"])
     kp, ks = ref.split_tokens(k, frames, P, S)
     keys = kp if ks is None else torch.cat([kp, ks], dim=-2)
-    want = torch.zeros(H, g.kb_tot * 64, 64, dtype=torch.bfloat16)
-    want[:, :g.Tk] = keys[0]
-    assert np.array_equal(_np(blocks.k_pack).reshape(H, -1, 64), _np(want))
+    want = torch.zeros(H, g.kb_tot * 64, 64, dtype=torch.float16)
+    want[:, :g.Tk] = keys[0].to(torch.float16)
+    assert torch.equal(blocks.k_pack.cpu().reshape(H, -1, 64), want)
+    norms = torch.zeros(H, g.kb_tot * 64, dtype=torch.float64)
+    norms[:, :g.Tk] = keys[0].double().norm(dim=-1)
+    np.testing.assert_allclose(o["k_norm"], norms.view(H, g.kb_tot, 64).amax(-1).numpy(), rtol=2e-7)
 
 
 def test_pooled_scores_bit_exact(layer, dev):
@@ -216,7 +222,7 @@ def _check_attention(out, q, k, v, frames, P, S, lut, nvalid, rows):
     return worst, cos_min
 
 
-@pytest.mark.parametrize("mode", ["bf16", "i8x2"])
+@pytest.mark.parametrize("mode", ["f16", "i8x2"])
 def test_attention_matches_fp32_masked_softmax(layer, mode, dev):
     name, q, k, v, frames, P, S, H = layer
     g = LayerGrid(1, H, frames, P, S)
@@ -231,7 +237,7 @@ def test_attention_matches_fp32_masked_softmax(layer, mode, dev):
     print(f"[{name} {mode}] attention max-abs {w:.3e} min-cos {c:.6f}")
 
 
-@pytest.mark.parametrize("mode", ["bf16", "i8x2"])
+@pytest.mark.parametrize("mode", ["f16", "i8x2"])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
 def test_attention_low_precision_outputs(out_dtype, mode, dev):
     frames, P, S, H = 2, 200, 4, 2
@@ -252,7 +258,7 @@ def test_attention_low_precision_outputs(out_dtype, mode, dev):
         assert torch.allclose(out.float(), out32, rtol=2.0 ** -10, atol=2.0 ** -24)
 
 
-@pytest.mark.parametrize("cfg,mode", [("sparse_vggt_f4", "bf16"), ("hess_f16", "bf16"), ("hess_f16", "i8x2")])
+@pytest.mark.parametrize("cfg,mode", [("sparse_vggt_f4", "f16"), ("hess_f16", "f16"), ("hess_f16", "i8x2")])
 def test_layer_pipeline_matches_oracle(cfg, mode, dev):
     if cfg == "sparse_vggt_f4":
         frames, sr, cdf, hess = 4, 0.5, 0.9, False
@@ -313,7 +319,7 @@ def test_layer_protect_own_frame(dev):
     _check_attention(res.out, q, k, v, frames, P, S, lut, nv, rows)
 
 
-@pytest.mark.parametrize("mode", ["bf16", "i8x2"])
+@pytest.mark.parametrize("mode", ["f16", "i8x2"])
 @pytest.mark.parametrize("B,H,frames", [(2, 16, 3), (1, 5, 2), (1, 1, 1)])
 def test_attention_writes_every_row(B, H, frames, mode, dev):
     """The persistent row schedule covers every (batch, head, q-block) exactly once:
@@ -408,3 +414,47 @@ def test_head_budget_on_shipped_tables(name, dev):
         want, it = oracle.head_budget(base, oracle.scores_norm_seq(hb.head_scores[layer].numpy()), 1.0, n_cand)
         assert it >= 0
         assert np.array_equal(_np(got), want), (name, layer)
+
+
+@pytest.mark.parametrize("q_mul", [1.0, 8.0, 0.0], ids=["mixed", "running_max", "zero_q"])
+def test_f16_bounded_and_running_max_rows(q_mul, dev):
+    """16-bit mode rows run bounded (pre-scaled fp16 queries, fixed offset |q'| * max key norm
+    - 32 in the accumulator) or, when that bound exceeds 64, with exact fp16 queries and the
+    running max. Queries scaled by 8 push every row past the bound (running max everywhere);
+    zero queries give uniform attention on bounded rows; unscaled data mixes both. Every row
+    against the fp32 masked softmax."""
+    from device_reference import row_errors
+    frames, P, S, H = 4, 1374, 5, 4
+    q, k, v, meta = synth.make_layer_qkv(frames, H=H, seed=3)
+    q = (q.float() * q_mul).to(torch.bfloat16)
+    g = LayerGrid(1, H, frames, P, S)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    blocks = kernels.prepare_blocks(qd, kd, vd, g, mode="f16")
+    rng = np.random.default_rng(5)
+    keys = torch.from_numpy(rng.random((1, H, g.q_blk_p, g.n_cand)).astype(np.float32)).to(dev)
+    counts = torch.from_numpy(rng.integers(2, g.n_cand + 1, (1, H, g.q_blk_p)).astype(np.int32)).to(dev)
+    _, lut, nv = kernels.select_blocks(keys, counts, g, 2)
+    out = kernels.sparse_attention(blocks, lut, nv)
+    torch.cuda.synchronize()
+    # which rows ran bounded: every query's |q * c|_fp16 * max kept key norm <= 64
+    c = 0.125 * 1.4426950408889634
+    qc = (q.float() * c).to(torch.float16).float()[0]
+    kn = blocks.k_scale.view(H, g.kb_tot).cpu()
+    lutc, nvc = lut.cpu(), nv.cpu()
+    order = torch.cat([torch.arange(f * P + S, (f + 1) * P) for f in range(frames)] +
+                      [torch.arange(f * P, f * P + S) for f in range(frames)])
+    qn = qc[:, order].norm(dim=-1)
+    bounded = np.zeros((H, g.q_blk_total), bool)
+    for h in range(H):
+        for r in range(g.q_blk_total):
+            kmax = kn[h, lutc[h, r, :nvc[h, r]].long()].max() if nvc[h, r] else torch.tensor(0.0)
+            r0 = r * 128 if r < g.q_blk_p else g.T_p + (r - g.q_blk_p) * 128
+            bounded[h, r] = bool((qn[h, r0:r0 + 128] * kmax <= 64).all())
+    err, cos = row_errors(out, qd, kd, vd, g, lut, nv)
+    print(f"[f16 q*{q_mul}] bounded rows {bounded.sum()}/{bounded.size}: max-abs {np.nanmax(err):.3e} "
+          f"min-cos {np.nanmin(cos):.6f}")
+    if q_mul == 8.0:
+        assert not bounded.any()
+    if q_mul == 0.0:
+        assert bounded.all()
+    assert np.nanmax(err) <= ATOL and np.nanmin(cos) >= MIN_COS

@@ -1,5 +1,5 @@
-"""The allocation-free attention entry point (ress_sparse_attn_fwd_bf16_noalloc) against
-the workspace entry point it shares its kernels with (ress_sparse_attn_fwd_bf16), through
+"""The allocation-free attention entry point (ress_sparse_attn_fwd_f16_noalloc) against
+the workspace entry point it shares its kernels with (ress_sparse_attn_fwd_f16), through
 the C ABI: bit-identical outputs on two calls in a row, the second on a smaller layer, so
 the shared static scratch is reused with different shapes."""
 
@@ -17,7 +17,7 @@ def _layer(frames, H, dev, seed):
     q, k, v, meta = synth.make_layer_qkv(frames, H=H, seed=seed)
     g = LayerGrid(1, H, frames, meta["P"], meta["S"])
     q, k, v = q.to(dev), k.to(dev), v.to(dev)
-    blocks = kernels.prepare_blocks(q, k, v, g, mode="bf16")
+    blocks = kernels.prepare_blocks(q, k, v, g, mode="f16")
     rng = np.random.default_rng(seed)
     keys = torch.from_numpy(rng.random((1, H, g.q_blk_p, g.n_cand)).astype(np.float32)).to(dev)
     counts = torch.from_numpy(rng.integers(0, g.n_cand + 1, (1, H, g.q_blk_p)).astype(np.int32)).to(dev)
@@ -28,9 +28,9 @@ def _layer(frames, H, dev, seed):
 def _run(entry, g, blocks, lut, nvalid, dev):
     out = torch.full((g.B, g.H, g.Tk, 64), float("nan"), device=dev)
     P = _lib.ptr
-    args = [P(blocks.q), *blocks.q.stride()[:3], P(blocks.k_pack), P(blocks.v_pack), P(lut), P(nvalid), g.B, g.H,
-            g.frames, g.P, g.S, 0.125, P(out), 0, *out.stride()[:3]]
-    if entry == "ress_sparse_attn_fwd_bf16":
+    args = [P(blocks.q), *blocks.q.stride()[:3], P(blocks.k_pack), P(blocks.k_scale), P(blocks.v_pack), P(lut),
+            P(nvalid), g.B, g.H, g.frames, g.P, g.S, 0.125, P(out), 0, *out.stride()[:3]]
+    if entry == "ress_sparse_attn_fwd_f16":
         sched = torch.empty(_lib.lib().ress_attn_sched_bytes(g.B, g.H, g.Tk), dtype=torch.uint8, device=dev)
         args.append(P(sched))
     _lib.call(entry, *args, _lib.stream_handle(dev))
@@ -43,7 +43,7 @@ def test_noalloc_matches_workspace_entry_point(dev):
     for frames, H, seed in ((16, 16, 0), (3, 4, 1)):   # the second call is smaller
         print(f"[noalloc] frames={frames} H={H}", flush=True)
         g, blocks, lut, nvalid = _layer(frames, H, dev, seed)
-        want = _run("ress_sparse_attn_fwd_bf16", g, blocks, lut, nvalid, dev)
-        got = _run("ress_sparse_attn_fwd_bf16_noalloc", g, blocks, lut, nvalid, dev)
+        want = _run("ress_sparse_attn_fwd_f16", g, blocks, lut, nvalid, dev)
+        got = _run("ress_sparse_attn_fwd_f16_noalloc", g, blocks, lut, nvalid, dev)
         assert not torch.isnan(got).any()
         assert torch.equal(got, want)
