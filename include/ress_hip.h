@@ -202,12 +202,19 @@ int ress_sparse_attn_fwd_f16_noalloc(const void* q, long long sqB, long long sqH
 
 /* Replaces SpargeAttn qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold
  * (call src/ress/models/attention.py:238-241) with the same argument meaning; see
- * attn.hip for the supported flag values. workspace: ress_qattn_workspace_size(B,H,Tq,Tk)
- * bytes (packed V, then the attention's sched workspace), 16-byte aligned. */
+ * attn.hip for the supported flag values. pv_threshold: H floats in device memory (or
+ * null), read on the device. workspace: ress_qattn_workspace_size(B,H,Tq,Tk) bytes,
+ * 16-byte aligned: a status word (int32 at offset 0), packed V, a checked copy of the LUT,
+ * the attention's sched workspace. The LUT contract is SpargeAttn's: per row, nvalid in
+ * [0, ceil(Tk/64)] and that many strictly ascending block indices below ceil(Tk/64). The
+ * call checks it on the device without synchronising: the attention runs on a copy
+ * clamped into range, and the status word gets 1 (an nvalid out of range), 2 (a listed
+ * block out of range or not ascending) or 4 (a pv_threshold below 1e9: PV-threshold skipping
+ * is not implemented), OR-ed, for the caller to read at its next synchronisation. */
 long long ress_qattn_workspace_size(int B, int H, int Tq, int Tk);
 int ress_qattn_block_sparse_fwd(const void* q_i8, const void* k_i8, const void* v, int v_f16, void* o,
                                 int o_dtype, const void* lut, const void* valid_block_num,
-                                const float* pv_threshold_host, const void* q_scale, const void* k_scale,
+                                const float* pv_threshold, const void* q_scale, const void* k_scale,
                                 int B, int H, int Tq, int Tk, long long svB, long long svH, long long svT,
                                 long long soB, long long soH, long long soT, int tensor_layout, int is_causal,
                                 int qk_quant_gran, float sm_scale, int return_pv_count, void* workspace,

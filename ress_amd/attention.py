@@ -397,7 +397,11 @@ def compute_baseline_num_to_select(pooled_score, sparse_ratio=None, cdf_threshol
 def run_block_sparse_kernel(query, key, value, final_map, dtype=torch.float16, out_dtype=torch.float32):
     """Reference attention.py:217-243 on the GPU kernels: LUT of final_map, key mean,
     per-block INT8 Q and K - km, block-sparse attention. query (B,nh,Tq,64), key/value
-    (B,nh,Tk,64), final_map (B,nh,ceil(Tq/128),ceil(Tk/64)). Returns (o, sparsity)."""
+    (B,nh,Tk,64), final_map (B,nh,ceil(Tq/128),ceil(Tk/64)). Returns (o, sparsity).
+    One stated deviation: the reference casts q and k to `dtype` (fp16 by default) and takes
+    km and k - km in that dtype; here q and k are taken in bf16 and km, k - km in fp32 before
+    the per-block quantiser, so the INT8 codes can differ in the last code step from the
+    reference's on the same inputs. V and o follow `dtype` as in the reference."""
     from ress_amd import sparge
     B, nh, Tq, C = query.shape
     q = query.contiguous().to(torch.bfloat16)
@@ -406,9 +410,13 @@ def run_block_sparse_kernel(query, key, value, final_map, dtype=torch.float16, o
     lut, valid_block_num = sparge.block_map_lut_triton(final_map)
     km = sparge.key_mean(k)
     q_int8, q_scale, k_int8, k_scale = sparge.per_block_int8(q, k, km=km)
-    o = torch.empty(B, nh, Tq, C, dtype=out_dtype, device=q.device)
+    # o in `dtype` then out_dtype, as the reference rounds it (empty_like(query), .to(out_dtype))
+    o = torch.empty(B, nh, Tq, C, dtype=dtype if dtype in (torch.float16, torch.bfloat16) else out_dtype,
+                    device=q.device)
     sparge.qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold(
         q_int8, k_int8, v, o, lut, valid_block_num, sparge.hyperparameter_check(1e10, nh, q.device), q_scale,
         k_scale, 1, 0, 1, 1.0 / math.sqrt(C), 0)
-    sparsity = 1 - final_map.float().mean().item()
-    return o, sparsity
+    # one synchronisation for the sparsity the reference returns and the mirror's input check
+    mean, status = torch.stack([final_map.float().mean(), sparge.last_call_status()[0].float()]).tolist()
+    sparge.raise_for_status(int(status))
+    return o.to(out_dtype), 1 - mean

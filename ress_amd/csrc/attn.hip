@@ -1218,6 +1218,52 @@ RESS_API int ress_sparse_attn_fwd_f16(const void* q, long long sqB, long long sq
 }
 
 static long long qattn_vpack_bytes(int B, int H, int Tk) { return (long long)B * H * cdiv(Tk, 64) * 4096 * 2; }
+// Mirror workspace: [status 256 B][packed V][checked LUT][checked nvalid][row schedule], each
+// part 256-byte aligned.
+static long long round256(long long x) { return (x + 255) / 256 * 256; }
+static long long qattn_lut_bytes(int B, int H, int Tq, int Tk) {
+  return round256((long long)B * H * cdiv(Tq, 128) * cdiv(Tk, 64) * 4);
+}
+static long long qattn_nv_bytes(int B, int H, int Tq) { return round256((long long)B * H * cdiv(Tq, 128) * 4); }
+
+// Status bits of the SpargeAttn mirror (word 0 of its workspace), set on the device.
+#define RESS_QATTN_BAD_NVALID 1    // a valid_block_num outside [0, ceil(Tk/64)]
+#define RESS_QATTN_BAD_LUT 2       // a listed block outside [0, ceil(Tk/64)) or not strictly ascending
+#define RESS_QATTN_PV_THRESHOLD 4  // a pv_threshold below 1e9 (PV skipping is not implemented)
+
+__global__ void k_qattn_status_clear(int* status) {
+  if (threadIdx.x == 0) status[0] = 0;
+}
+
+// Checks one (batch*head, q-block) row of a caller-supplied LUT and copies it clamped into
+// range (listed blocks to [0, nk), the count to [0, nk]), so the attention kernel reads in
+// bounds whatever the caller passed; what was wrong is OR-ed into *status for the host to
+// report. One wave per row.
+__global__ __launch_bounds__(64) void k_qattn_check(const int* __restrict__ lut, const int* __restrict__ nvalid,
+                                                    const float* __restrict__ pv_threshold, int H, int nq, int nk,
+                                                    int* __restrict__ lut_out, int* __restrict__ nv_out,
+                                                    int* __restrict__ status) {
+  const int qb = blockIdx.x, bh = blockIdx.y, lane = threadIdx.x;
+  const long long row = (long long)bh * nq + qb;
+  const int nv = nvalid[row];
+  const int nvc = min(max(nv, 0), nk);
+  int bad = (nv < 0 || nv > nk) ? RESS_QATTN_BAD_NVALID : 0;
+  const float thr = pv_threshold ? pv_threshold[bh % H] : 1e10f;
+  if (!(thr >= 1e9f)) bad |= RESS_QATTN_PV_THRESHOLD;  // NaN included
+  const int* src = lut + row * nk;
+  int* dst = lut_out + row * nk;
+  bool lut_bad = false;
+  for (int i = lane; i < nk; i += 64) {
+    const int e = src[i];
+    dst[i] = min(max(e, 0), nk - 1);
+    if (i < nvc) lut_bad |= e < 0 || e >= nk || (i > 0 && e <= src[i - 1]);
+  }
+  if (__any(lut_bad)) bad |= RESS_QATTN_BAD_LUT;
+  if (lane == 0) {
+    nv_out[row] = nvc;
+    if (bad) atomicOr(status, bad);
+  }
+}
 
 // Workspace of the attention entry points for B*H heads of Tq query rows: the row
 // schedule (header) and the parts of the rows split at the end of each XCD's range
@@ -1231,7 +1277,8 @@ RESS_API long long ress_attn_sched_bytes(int B, int H, int Tq) {
 
 RESS_API long long ress_qattn_workspace_size(int B, int H, int Tq, int Tk) {
   if (B <= 0 || H <= 0 || Tq < 0 || Tk < 0) return -1;
-  return qattn_vpack_bytes(B, H, Tk) + ress_attn_sched_bytes(B, H, Tq);
+  return 256 + round256(qattn_vpack_bytes(B, H, Tk)) + qattn_lut_bytes(B, H, Tq, Tk) + qattn_nv_bytes(B, H, Tq) +
+         ress_attn_sched_bytes(B, H, Tq);
 }
 
 // Mirror of SpargeAttn's qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold
@@ -1242,10 +1289,14 @@ RESS_API long long ress_qattn_workspace_size(int B, int H, int Tq, int Tk) {
 // q_scale [B*H][ceil(Tq/128)], k_scale [B*H][ceil(Tk/64)]; o (B,H,Tq,64) with strides.
 // Supported: tensor_layout 1 (HND), is_causal 0, qk_quant_gran 1 (per block),
 // return_pv_count 0, pv_threshold disabled (>= 1e9, the reference passes 1e10).
-// workspace: ress_qattn_workspace_size(B,H,Tq,Tk) bytes (packed V + the row schedule).
+// pv_threshold: H floats in device memory (or null = disabled), read on the device.
+// workspace: ress_qattn_workspace_size(B,H,Tq,Tk) bytes: a status word (int32 at offset 0),
+// packed V, the checked LUT copy, the row schedule. The status word gets the
+// RESS_QATTN_* bits of what was wrong with lut / valid_block_num / pv_threshold; the call
+// itself never synchronises, so the caller reads the word when it next synchronises.
 RESS_API int ress_qattn_block_sparse_fwd(const void* q_i8, const void* k_i8, const void* v, int v_f16, void* o,
                                          int o_dtype, const void* lut, const void* valid_block_num,
-                                         const float* pv_threshold_host, const void* q_scale, const void* k_scale,
+                                         const float* pv_threshold, const void* q_scale, const void* k_scale,
                                          int B, int H, int Tq, int Tk, long long svB, long long svH, long long svT,
                                          long long soB, long long soH, long long soT, int tensor_layout, int is_causal,
                                          int qk_quant_gran, float sm_scale, int return_pv_count, void* workspace,
@@ -1254,21 +1305,27 @@ RESS_API int ress_qattn_block_sparse_fwd(const void* q_i8, const void* k_i8, con
   RESS_REQUIRE(is_causal == 0, "ress_qattn_block_sparse_fwd: is_causal must be 0");
   RESS_REQUIRE(qk_quant_gran == 1, "ress_qattn_block_sparse_fwd: only per-block quantisation (qk_quant_gran=1)");
   RESS_REQUIRE(return_pv_count == 0, "ress_qattn_block_sparse_fwd: return_pv_count must be 0");
-  if (pv_threshold_host)
-    for (int h = 0; h < H; ++h)
-      RESS_REQUIRE(pv_threshold_host[h] >= 1e9f,
-                   "ress_qattn_block_sparse_fwd: PV-threshold skipping is not implemented (got %g; the reference "
-                   "passes 1e10 = disabled)",
-                   (double)pv_threshold_host[h]);
   RESS_REQUIRE(B > 0 && H > 0 && Tq > 0 && Tk > 0, "ress_qattn_block_sparse_fwd: bad geometry");
+  RESS_REQUIRE(lut && valid_block_num, "ress_qattn_block_sparse_fwd: null lut / valid_block_num");
   RESS_REQUIRE(v && workspace && workspace_bytes >= ress_qattn_workspace_size(B, H, Tq, Tk),
                "ress_qattn_block_sparse_fwd: workspace of %lld bytes required",
                ress_qattn_workspace_size(B, H, Tq, Tk));
   RESS_REQUIRE(((uintptr_t)v & 15u) == 0 && svT % 8 == 0 && svH % 8 == 0 && svB % 8 == 0,
                "ress_qattn_block_sparse_fwd: v must be 16-byte aligned with strides a multiple of 8");
-  const int kb_tot = cdiv(Tk, 64);
+  const int kb_tot = cdiv(Tk, 64), nq = cdiv(Tq, 128);
+  char* ws = (char*)workspace;
+  int* status = (int*)ws;
+  char* vpack = ws + 256;
+  int* lut_c = (int*)(vpack + round256(qattn_vpack_bytes(B, H, Tk)));
+  int* nv_c = (int*)((char*)lut_c + qattn_lut_bytes(B, H, Tq, Tk));
+  char* sched = (char*)nv_c + qattn_nv_bytes(B, H, Tq);
+  hipLaunchKernelGGL(k_qattn_status_clear, dim3(1), dim3(64), 0, stream, status);
+  RESS_LAUNCHED("k_qattn_status_clear");
+  hipLaunchKernelGGL(k_qattn_check, dim3(nq, B * H), dim3(64), 0, stream, (const int*)lut, (const int*)valid_block_num,
+                     pv_threshold, H, nq, kb_tot, lut_c, nv_c, status);
+  RESS_LAUNCHED("k_qattn_check");
   hipLaunchKernelGGL(k_pack_v, dim3(kb_tot, B * H), dim3(64), 0, stream, (const uint16_t*)v, svB, svH, svT, H, Tk,
-                     kb_tot, (uint16_t*)workspace);
+                     kb_tot, (uint16_t*)vpack);
   RESS_LAUNCHED("k_pack_v");
   TokenMap m;
   m.P = Tq;
@@ -1276,8 +1333,8 @@ RESS_API int ress_qattn_block_sparse_fwd(const void* q_i8, const void* k_i8, con
   m.HW = Tq;
   m.T_p = Tq;
   m.T_s = 0;
-  return attn_common(q_i8, nullptr, q_scale, k_i8, nullptr, k_scale, workspace, v_f16, lut, valid_block_num, B, H, m,
-                     Tk, sm_scale, o, o_dtype, soB, soH, soT, (char*)workspace + qattn_vpack_bytes(B, H, Tk), stream);
+  return attn_common(q_i8, nullptr, q_scale, k_i8, nullptr, k_scale, vpack, v_f16, lut_c, nv_c, B, H, m, Tk, sm_scale,
+                     o, o_dtype, soB, soH, soT, sched, stream);
 }
 
 // ---- allocation-free variant of ress_sparse_attn_fwd_f16 --------------------------------

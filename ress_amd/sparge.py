@@ -141,8 +141,10 @@ def qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold(
         v = v.to(torch.float16)
     if lut.shape[-2:] != (nq, nk):
         raise ValueError(f"lut must be (B,H,{nq},{nk})")
-    pv_host = torch.as_tensor(pv_threshold, dtype=torch.float32).detach().cpu().reshape(-1).contiguous()
-    if pv_host.numel() != H:
+    # the thresholds stay on the device (no host copy, no synchronisation): the kernel's
+    # check records a non-disabled value in the status word
+    pv_dev = torch.as_tensor(pv_threshold, dtype=torch.float32, device=dev).reshape(-1).contiguous()
+    if pv_dev.numel() != H:
         raise ValueError("pv_threshold must have one value per head")
     ws_bytes = _lib.lib().ress_qattn_workspace_size(B, H, Tq, Tk)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
@@ -152,10 +154,42 @@ def qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold(
     qs = q_scale.float().contiguous()
     ks = k_scale.float().contiguous()
     _lib.call("ress_qattn_block_sparse_fwd", _lib.ptr(q8), _lib.ptr(k8), _lib.ptr(v), int(v.dtype == torch.float16),
-              _lib.ptr(o), code, _lib.ptr(lut_c), _lib.ptr(nv_c), pv_host.data_ptr(), _lib.ptr(qs), _lib.ptr(ks),
+              _lib.ptr(o), code, _lib.ptr(lut_c), _lib.ptr(nv_c), _lib.ptr(pv_dev), _lib.ptr(qs), _lib.ptr(ks),
               B, H, Tq, Tk, *v.stride()[:3], *o.stride()[:3], int(tensor_layout), int(is_causal), int(qk_quant_gran),
               float(sm_scale), int(return_pv_count), _lib.ptr(ws), ws_bytes, _lib.stream_handle(dev))
+    global _last_status
+    _last_status = ws[:4].view(torch.int32).clone()  # kept past the workspace; read at the next sync
     return None
+
+
+# Status word of the last mirror call (device int32), and what its bits mean.
+_last_status = None
+_STATUS_BITS = (
+    (1, "valid_block_num outside [0, ceil(Tk/64)]"),
+    (2, "a LUT entry outside [0, ceil(Tk/64)) or not strictly ascending within valid_block_num"),
+    (4, "pv_threshold below 1e9: PV-threshold skipping is not implemented (the reference passes 1e10)"),
+)
+
+
+def raise_for_status(status):
+    """Raise ValueError naming every problem the status word `status` (an int) records."""
+    status = int(status)
+    if status:
+        msgs = [m for bit, m in _STATUS_BITS if status & bit]
+        raise ValueError("qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold: " + "; ".join(msgs))
+
+
+def last_call_status():
+    """The status word of the last mirror call as a device tensor (0 = the LUT, counts and
+    thresholds were valid); None before the first call."""
+    return _last_status
+
+
+def check_last_call():
+    """Synchronise on the last mirror call's status word and raise if its inputs were invalid
+    (the call itself never synchronises; it ran on a copy of the LUT clamped into range)."""
+    if _last_status is not None:
+        raise_for_status(_last_status.item())
 
 
 def get_block_map_meansim_fuse_quant(q, k, km=None, is_causal=False, BLKQ=BLKQ, BLKK=BLKK, simthreshd1=0.1,

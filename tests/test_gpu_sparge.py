@@ -126,9 +126,33 @@ def test_qattn_mirror_matches_emulation(v_dtype, o_dtype, dev):
     for (h, r), e in emu.items():
         got = o[0, h, r * 128:r * 128 + e.shape[0]].float().cpu()
         assert (got - e).abs().max().item() <= 1.5e-2
-    with pytest.raises(RuntimeError, match="PV-threshold"):
-        sparge.qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold(
-            q8, k8, v.to(dev), o, lut, nv, sparge.hyperparameter_check(50.0, H, dev), qs, ks, 1, 0, 1, 0.125, 0)
+    sparge.check_last_call()  # a valid call records no problem
+    # invalid inputs are found on the device without a synchronisation; the attention runs on
+    # a copy clamped into range, and the problem is raised at the caller's next check
+    sparge.qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold(
+        q8, k8, v.to(dev), o, lut, nv, sparge.hyperparameter_check(50.0, H, dev), qs, ks, 1, 0, 1, 0.125, 0)
+    with pytest.raises(ValueError, match="pv_threshold below 1e9"):
+        sparge.check_last_call()
+    bad_nv = nv.clone()
+    bad_nv[0, 1, 2] = 7  # more than the 6 key blocks
+    sparge.qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold(
+        q8, k8, v.to(dev), o, lut, bad_nv, sparge.hyperparameter_check(1e10, H, dev), qs, ks, 1, 0, 1, 0.125, 0)
+    with pytest.raises(ValueError, match="valid_block_num outside"):
+        sparge.check_last_call()
+    bad_lut = lut.clone()
+    bad_lut[0, 0, 0, 0] = 6  # a block past the last one
+    sparge.qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold(
+        q8, k8, v.to(dev), o, bad_lut, nv, sparge.hyperparameter_check(1e10, H, dev), qs, ks, 1, 0, 1, 0.125, 0)
+    with pytest.raises(ValueError, match="LUT entry"):
+        sparge.check_last_call()
+    unsorted = lut.clone()
+    row = int(torch.nonzero(nv[0, 0] >= 2)[0, 0])
+    unsorted[0, 0, row, :2] = unsorted[0, 0, row, :2].flip(0)  # two listed blocks swapped
+    sparge.qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold(
+        q8, k8, v.to(dev), o, unsorted, nv, sparge.hyperparameter_check(1e10, H, dev), qs, ks, 1, 0, 1, 0.125, 0)
+    with pytest.raises(ValueError, match="not strictly ascending"):
+        sparge.check_last_call()
+    torch.cuda.synchronize()
     with pytest.raises(RuntimeError, match="is_causal"):
         sparge.qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold(
             q8, k8, v.to(dev), o, lut, nv, sparge.hyperparameter_check(1e10, H, dev), qs, ks, 1, 1, 1, 0.125, 0)

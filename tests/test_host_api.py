@@ -330,3 +330,17 @@ def test_random_criterion_generator():
     assert torch.equal(a1, b1) and torch.equal(a2, b2) and not torch.equal(a1, a2)
     assert a1.shape == cond.shape and a1.dtype == torch.float32
     assert torch.equal(torch.cat([a1.flatten(), a2.flatten()]), want)
+
+
+def test_mirror_status_word_names_every_problem():
+    """The SpargeAttn mirror's device-side input check (status word bits 1, 2, 4: counts,
+    LUT entries, PV threshold) is decoded into one ValueError naming each problem."""
+    from ress_amd import sparge
+    sparge.raise_for_status(0)  # a clean call
+    with pytest.raises(ValueError, match="valid_block_num outside"):
+        sparge.raise_for_status(1)
+    with pytest.raises(ValueError, match="not strictly ascending"):
+        sparge.raise_for_status(2)
+    with pytest.raises(ValueError, match="pv_threshold below 1e9") as e:
+        sparge.raise_for_status(7)
+    assert "valid_block_num" in str(e.value) and "LUT entry" in str(e.value)

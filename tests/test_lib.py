@@ -63,8 +63,10 @@ def test_workspace_sizes(library):
     assert library.ress_attn_sched_bytes(1, 16, 21984) == 256 + 8 * 32 * part
     assert library.ress_attn_sched_bytes(2, 3, 0) == 256 + 8 * 6 * part
     assert library.ress_attn_sched_bytes(0, 3, 10) == -1
-    # SpargeAttn mirror: packed V (64x64 bf16 per key block) + the attention's workspace
-    assert library.ress_qattn_workspace_size(1, 2, 300, 200) == 2 * 4 * 4096 * 2 + 256 + 8 * 8 * part
+    # SpargeAttn mirror: status word (256 B), packed V (64x64 bf16 per key block), the checked
+    # LUT and counts (each rounded to 256 B), then the attention's workspace
+    assert library.ress_qattn_workspace_size(1, 2, 300, 200) == (256 + 2 * 4 * 4096 * 2 + 256 + 256 + 256
+                                                                  + 8 * 8 * part)
     assert library.ress_qattn_workspace_size(1, 2, -1, 200) == -1
 
 
