@@ -42,9 +42,13 @@ int ress_abi_version(void);
  *   (a bf16 key is exact in fp16 unless below 2^-14 in magnitude or above 65504).
  * q_i8 = k_i8 = NULL selects the 16-bit operands: pooled_q/k/v, v_pack, k_pack and
  * k_scale (both required) are written, k_scale [BH][kb_tot] receiving each key block's
- * largest key norm; q_lo, q_scale, k_lo, ksum, km are unused. */
+ * largest key norm; q_lo, q_scale, k_lo, ksum, km are unused.
+ * patch_order: NULL, or P-S int32 in device memory, a permutation of the frame's patch
+ * tokens: block position j of every frame holds the frame's patch token patch_order[j]
+ * (replaces the gather of hilbert_permute, src/ress/models/hilbert.py:128-162, and its
+ * .contiguous() copy: the tokens are read in place). Give the attention call the same table. */
 int ress_prep_qkv(const void* q, const void* k, const void* v, int B, int H, int frames, int P, int S,
-                  long long sqB, long long sqH, long long sqT, long long skB, long long skH, long long skT,
+                  const int* patch_order, long long sqB, long long sqH, long long sqT, long long skB, long long skH, long long skT,
                   long long svB, long long svH, long long svT, void* q_i8, void* q_lo, void* q_scale,
                   void* pooled_q, void* k_i8, void* k_lo, void* k_scale, void* pooled_k, void* pooled_v,
                   void* v_pack, void* k_pack, void* ksum, void* km, hipStream_t stream);
@@ -168,9 +172,9 @@ int ress_restore_swap(const void* A, const void* V, const void* M, const void* n
 long long ress_attn_sched_bytes(int B, int H, int Tq);
 int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void* q_scale, const void* k_i8,
                          const void* k_lo, const void* k_scale, const void* v_pack, int v_f16, const void* lut,
-                         const void* nvalid, int B, int H, int frames, int P, int S, float sm_scale, void* out,
-                         int out_dtype, long long soB, long long soH, long long soT, void* sched,
-                         hipStream_t stream);
+                         const void* nvalid, int B, int H, int frames, int P, int S, const int* patch_order,
+                         float sm_scale, void* out, int out_dtype, long long soB, long long soH, long long soT,
+                         void* sched, hipStream_t stream);
 
 /* The fused-path attention of ress_sparse_attn_fwd (same reference lines) with QK^T on
  * 16-bit operands (fp16 MFMA, fp32 accumulation) instead of INT8 codes: q is the layer's
@@ -180,11 +184,13 @@ int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void* q_scale
  * ress_prep_qkv. A row whose logit bound |q*sm_scale*log2 e| * max key norm is at most 64
  * (log2 units) runs with the pre-scaled queries rounded to fp16 and a fixed offset in the
  * accumulator (no running max); other rows use the exact fp16 queries and a running max.
- * sched: as for ress_sparse_attn_fwd. */
+ * sched, patch_order: as for ress_sparse_attn_fwd (patch_order: the table given to
+ * ress_prep_qkv; each row is read and written at the storage positions of its tokens). */
 int ress_sparse_attn_fwd_f16(const void* q, long long sqB, long long sqH, long long sqT, const void* k_pack,
                              const void* k_norm, const void* v_pack, const void* lut, const void* nvalid, int B,
-                             int H, int frames, int P, int S, float sm_scale, void* out, int out_dtype,
-                             long long soB, long long soH, long long soT, void* sched, hipStream_t stream);
+                             int H, int frames, int P, int S, const int* patch_order, float sm_scale, void* out,
+                             int out_dtype, long long soB, long long soH, long long soT, void* sched,
+                             hipStream_t stream);
 
 /* Allocation-free variant of ress_sparse_attn_fwd_f16 (same arguments without `sched`,
  * same kernels and results). No counterpart in the reference: it is for callers that cannot
@@ -197,7 +203,8 @@ int ress_sparse_attn_fwd_f16(const void* q, long long sqB, long long sqH, long l
 long long ress_noalloc_scratch_bytes(void);
 int ress_sparse_attn_fwd_f16_noalloc(const void* q, long long sqB, long long sqH, long long sqT, const void* k_pack,
                                      const void* k_norm, const void* v_pack, const void* lut, const void* nvalid,
-                                     int B, int H, int frames, int P, int S, float sm_scale, void* out, int out_dtype,
+                                     int B, int H, int frames, int P, int S, const int* patch_order, float sm_scale,
+                                     void* out, int out_dtype,
                                      long long soB, long long soH, long long soT, hipStream_t stream);
 
 /* Replaces SpargeAttn qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(_HERE, "libress_hip.so")
 
 # argument codes: p = pointer, i = int, l = long long, f = float, d = double, s = stream
 _SIGS = {
-    "ress_prep_qkv": "pppiiiii" + "lllllllll" + "ppppppppppppp" + "s",
+    "ress_prep_qkv": "pppiiiii" + "p" + "lllllllll" + "ppppppppppppp" + "s",
     "ress_per_block_int8": "pppiiii" + "llllll" + "ppppp" + "s",
     "ress_prep_kv_plain": "ppiii" + "llllll" + "ppppp" + "s",
     "ress_pooled_scores": "ppiiiifpp" + "s",
@@ -24,9 +24,9 @@ _SIGS = {
     "ress_select_blocks": "ppiiiiiiippp" + "s",
     "ress_fill_block_map": "ppplI" + "s",
     "ress_block_map_lut": "plipp" + "s",
-    "ress_sparse_attn_fwd": "pppppppippiiiiifpilllps",
-    "ress_sparse_attn_fwd_f16": "plllppppp" + "iiiiif" + "pi" + "lll" + "ps",
-    "ress_sparse_attn_fwd_f16_noalloc": "plllppppp" + "iiiiif" + "pi" + "lll" + "s",
+    "ress_sparse_attn_fwd": "pppppppippiiiii" + "p" + "fpilllps",
+    "ress_sparse_attn_fwd_f16": "plllppppp" + "iiiii" + "pf" + "pi" + "lll" + "ps",
+    "ress_sparse_attn_fwd_f16_noalloc": "plllppppp" + "iiiii" + "pf" + "pi" + "lll" + "s",
     "ress_qattn_block_sparse_fwd": "pppipipppppiiiilllllliiifipls",
     "ress_restore_swap": "pppp" + "iiiiii" + "dd" + "i" + "ppp" + "pl" + "s",
     "ress_meansim_block_map": "ppp" + "iiii" + "llllll" + "ppi" + "ppppppppp" + "s",

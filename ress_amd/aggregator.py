@@ -17,6 +17,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from ress_amd.synth import hilbert_permutation
 from ress_amd.wiring import wire_ress_attention
 
 _IMAGENET_MEAN = (0.485, 0.456, 0.406)
@@ -133,6 +134,7 @@ class Aggregator(nn.Module):
         self.global_blocks = nn.ModuleList(Block(dim, num_heads, mlp_ratio, rope) for _ in range(depth))
         self.register_buffer("mean", torch.tensor(_IMAGENET_MEAN).view(1, 1, 3, 1, 1), persistent=False)
         self.register_buffer("std", torch.tensor(_IMAGENET_STD).view(1, 1, 3, 1, 1), persistent=False)
+        self._hilbert = {}  # (w, h) -> the patch grid's Hilbert gather table
 
     def _special(self, B, S):
         def pick(tok):  # frame 0 takes index 0, the other frames index 1
@@ -153,10 +155,22 @@ class Aggregator(nn.Module):
         weight = self.patch_embed.weight.reshape(self.patch_embed.out_channels, cin * p * p)
         return F.linear(x, weight, self.patch_embed.bias), h, w
 
-    def forward(self, images):
+    def forward(self, images, use_hilbert=False):
+        """use_hilbert: the reference aggregator's flag (src/ress/models/vggt.py:32, 62-64):
+        the global layers form their blocks along the per-frame Hilbert curve of the patch
+        grid. The tokens stay in raster order: each global attention reads them through the
+        curve's gather table (its patch_order) instead of the reference's permuted copy, and
+        frame attention, being per-frame dense, is unaffected by the order."""
         B, S, _, Hi, Wi = images.shape
         x = ((images - self.mean) / self.std).to(self.patch_embed.weight.dtype)
         x, h, w = self._embed_patches(x.reshape(B * S, 3, Hi, Wi))  # (B*S, h*w, dim)
+        order = None
+        if use_hilbert:
+            order = self._hilbert.get((w, h))
+            if order is None:
+                order = self._hilbert[(w, h)] = torch.from_numpy(hilbert_permutation(w, h))
+        for gb in self.global_blocks:
+            gb.attn.patch_order = order
         x = torch.cat([self._special(B, S).to(x.dtype), x], dim=1)
         P, C = x.shape[1], x.shape[2]
         yy, xx = torch.meshgrid(torch.arange(h, device=x.device), torch.arange(w, device=x.device), indexing="ij")
@@ -175,8 +189,8 @@ class VGGTLike(nn.Module):
         super().__init__()
         self.aggregator = Aggregator(**kw)
 
-    def forward(self, images):
-        return self.aggregator(images)
+    def forward(self, images, use_hilbert=False):
+        return self.aggregator(images, use_hilbert=use_hilbert)
 
 
 def build_vggt_aggregator(depth=24, dim=1024, num_heads=16, device="cuda", dtype=torch.bfloat16, seed=0,

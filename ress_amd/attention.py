@@ -185,7 +185,7 @@ def sink_lead_blocks(attention_sink, grid):
 def sparse_global_attention(q, k, v, grid, *, num_to_select=None, budget_fn=None, perhead_budget_fn=None,
                             joint_select_fn=None, block_criterion="probability", M=None, out=None,
                             out_dtype=torch.float32, keep_intermediates=False, qk_mode=None,
-                            protect_own_frame=False, attention_sink=0):
+                            protect_own_frame=False, attention_sink=0, patch_order=None):
     """One layer's block-sparse global attention on the GPU.
 
     q, k, v: bf16 (B, H, frames*P, 64) in storage order (per frame S special then P-S
@@ -195,10 +195,13 @@ def sparse_global_attention(q, k, v, grid, *, num_to_select=None, budget_fn=None
     "i8" (see kernels.Blocks); the block map does not depend on it. protect_own_frame:
     the budget-neutral own-frame swap on the selected map (protect_own_frame_swap).
     attention_sink: leading tokens whose key blocks every row keeps on top of its budget
-    (sink_lead_blocks; 0 = none, the reference's ReSS default).
+    (sink_lead_blocks; 0 = none, the reference's ReSS default). patch_order: None, or a
+    per-frame permutation of the P-S patch positions (kernels.patch_order_table): blocks are
+    formed in that order, as if the tokens had gone through the reference's hilbert_permute
+    (src/ress/models/hilbert.py:128-162), but read and written in place.
     Returns a LayerResult whose `out` is (B, H, frames*P, 64) in storage order."""
     sink_lead = sink_lead_blocks(attention_sink, grid)
-    blocks = kernels.prepare_blocks(q, k, v, grid, mode=qk_mode or DEFAULT_QK_MODE)
+    blocks = kernels.prepare_blocks(q, k, v, grid, mode=qk_mode or DEFAULT_QK_MODE, patch_order=patch_order)
     attn_full, attn_cond = kernels.pooled_scores(blocks)
     v_bar_full = blocks.pooled_v.view(grid.B, grid.H, grid.kb_p, 64)
     counts = None
@@ -261,11 +264,14 @@ def ress_attention_forward(self, x, pos, num_to_select=None, budget_fn=None, per
                            joint_select_fn=None, block_criterion="probability", pool_mode="avg",
                            num_special_tokens=5, num_heads=16, shape=None, aux_store=None, aux_full=True,
                            dense=False, retain_output_grad=False, pooled_fallback=False, protect_own_frame=False,
-                           attention_sink=0):
+                           attention_sink=0, patch_order=None):
     """Replacement forward of a global-attention block (reference attention.py:296-659),
     same arguments and return value: (B, N*P, dim) after the W_O projection.
     attention_sink (not a reference argument; default 0 = the reference's behaviour):
-    leading tokens whose key blocks every row keeps, as sparse_global_attention. When
+    leading tokens whose key blocks every row keeps, as sparse_global_attention.
+    patch_order (not a reference argument; the module attribute set by the aggregator's
+    use_hilbert): the per-frame patch order the blocks are formed in, read in place (the
+    reference permutes the token tensor itself, hilbert.py:128-162). When
     aux_store is given the forward synchronises once for the realized sparsity and raises
     there if the HeSS budget did not converge; without it the forward does not synchronise
     (LayerResult.check is the deferred check)."""
@@ -283,11 +289,12 @@ def ress_attention_forward(self, x, pos, num_to_select=None, budget_fn=None, per
         sparsity = 0.0
     else:
         qb, kbf, vbf = (t.to(torch.bfloat16) for t in (q, k, v))
+        order = _device_patch_order(self, patch_order, grid, q.device)
         res = sparse_global_attention(
             qb, kbf, vbf, grid, num_to_select=num_to_select, budget_fn=budget_fn, perhead_budget_fn=perhead_budget_fn,
             joint_select_fn=joint_select_fn, block_criterion=block_criterion, M=getattr(self, "M", None),
             keep_intermediates=aux_store is not None and aux_full, protect_own_frame=protect_own_frame,
-            attention_sink=attention_sink)
+            attention_sink=attention_sink, patch_order=order)
         x_out = res.out
         sparsity = res.sparsity() if aux_store is not None else None
     if aux_store is not None:
@@ -295,7 +302,7 @@ def ress_attention_forward(self, x, pos, num_to_select=None, budget_fn=None, per
             aux_store["value"] = AttentionAux(
                 attn_pooled=res.attn_full[..., :grid.n_cand], v_bar=res.v_bar_full[..., :grid.n_cand, :],
                 attn_full=res.attn_full, v_bar_full=res.v_bar_full, n_cand=grid.n_cand,
-                q_patch=get_patch_tokens(q, N, P, S), shape=shp, sparsity=sparsity)
+                q_patch=_in_block_order(get_patch_tokens(q, N, P, S), order, N), shape=shp, sparsity=sparsity)
         else:
             aux_store["value"] = AttentionAux(shape=shp, sparsity=sparsity)
     if retain_output_grad and x_out.requires_grad:
@@ -303,6 +310,29 @@ def ress_attention_forward(self, x, pos, num_to_select=None, budget_fn=None, per
     if aux_store is not None and aux_full:
         aux_store["value"].output = x_out
     return project_out(self, x_out.to(x.dtype) if x.dtype != x_out.dtype else x_out, B, N, P, nh, hd)
+
+
+def _device_patch_order(module, order, grid, device):
+    """The device table of a module's patch order, validated and copied once per (order,
+    device) and kept on the module (no host-to-device copy per call)."""
+    if order is None:
+        return None
+    cache = module.__dict__.setdefault("_ress_patch_order_tables", {})
+    key = (id(order), str(device))
+    hit = cache.get(key)
+    if hit is None or hit[0] is not order:
+        hit = (order, kernels.patch_order_table(order, grid, device))
+        cache[key] = hit
+    return hit[1]
+
+
+def _in_block_order(patch, order, frames):
+    """Patch tokens (..., frames*HW, C) in the order the blocks were formed in."""
+    if order is None:
+        return patch
+    hw = order.numel()
+    idx = (torch.arange(frames, device=patch.device)[:, None] * hw + order.long()[None]).reshape(-1)
+    return patch.index_select(-2, idx)
 
 
 # ---------------------------------------------------------------------------

@@ -1160,13 +1160,14 @@ static int attn_common(const void* q_i8, const void* q_lo, const void* q_scale, 
   return v_f16 ? launch_attn<QK_I8, true>(a, out_dtype, stream) : launch_attn<QK_I8, false>(a, out_dtype, stream);
 }
 
-static TokenMap layer_map(int frames, int P, int S) {
+static TokenMap layer_map(int frames, int P, int S, const int* perm) {
   TokenMap m;
   m.P = P;
   m.S = S;
   m.HW = P - S;
   m.T_p = frames * (P - S);
   m.T_s = frames * S;
+  m.perm = perm;
   return m;
 }
 
@@ -1178,14 +1179,18 @@ static TokenMap layer_map(int frames, int P, int S) {
 // (split-INT8 residual codes from ress_prep_qkv) QK^T is evaluated as a two-term INT8
 // product; without them it is the single-term per-block INT8 product of the reference.
 // sched: ress_attn_sched_bytes(B, H, frames*P) bytes of 16-byte aligned device workspace.
+// patch_order: the table given to ress_prep_qkv (or null), so rows are read and written at
+// the storage positions of the patch order the blocks were formed in.
 RESS_API int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void* q_scale, const void* k_i8,
                                   const void* k_lo, const void* k_scale, const void* v_pack, int v_f16, const void* lut,
-                                  const void* nvalid, int B, int H, int frames, int P, int S, float sm_scale, void* out,
+                                  const void* nvalid, int B, int H, int frames, int P, int S, const int* patch_order,
+                                  float sm_scale, void* out,
                                   int out_dtype, long long soB, long long soH, long long soT, void* sched,
                                   hipStream_t stream) {
   RESS_REQUIRE(B > 0 && H > 0 && frames > 0 && P > S && S >= 0, "ress_sparse_attn_fwd: bad geometry");
   return attn_common(q_i8, q_lo, q_scale, k_i8, k_lo, k_scale, v_pack, v_f16, lut, nvalid, B, H,
-                     layer_map(frames, P, S), frames * P, sm_scale, out, out_dtype, soB, soH, soT, sched, stream);
+                     layer_map(frames, P, S, patch_order), frames * P, sm_scale, out, out_dtype, soB, soH, soT, sched,
+                     stream);
 }
 
 // The same fused-path attention with QK^T on 16-bit operands (fp32 accumulation): q is
@@ -1194,10 +1199,12 @@ RESS_API int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void
 // k_norm the per-block largest key norms ress_prep_qkv writes (16-bit operands), v_pack
 // its packed bf16 V. A row whose logit bound |q'| * max key norm is at most
 // RESS_BOUND_MAX runs with pre-scaled fp16 queries and a fixed offset (no running max);
-// other rows use exact fp16 queries and the running max (see qk_block_f16).
+// other rows use exact fp16 queries and the running max (see attn_row_f16). patch_order:
+// as for ress_sparse_attn_fwd.
 RESS_API int ress_sparse_attn_fwd_f16(const void* q, long long sqB, long long sqH, long long sqT, const void* k_pack,
                                       const void* k_norm, const void* v_pack, const void* lut, const void* nvalid,
-                                      int B, int H, int frames, int P, int S, float sm_scale, void* out,
+                                      int B, int H, int frames, int P, int S, const int* patch_order, float sm_scale,
+                                      void* out,
                                       int out_dtype, long long soB, long long soH, long long soT, void* sched,
                                       hipStream_t stream) {
   RESS_REQUIRE(B > 0 && H > 0 && frames > 0 && P > S && S >= 0, "ress_sparse_attn_fwd_f16: bad geometry");
@@ -1205,8 +1212,8 @@ RESS_API int ress_sparse_attn_fwd_f16(const void* q, long long sqB, long long sq
   RESS_REQUIRE(al16(q) && al16(k_pack) && sqT % 8 == 0 && sqH % 8 == 0 && sqB % 8 == 0,
                "ress_sparse_attn_fwd_f16: q/k_pack must be 16-byte aligned, q strides a multiple of 8");
   AttnArgs a;
-  if (attn_args(a, v_pack, lut, nvalid, B, H, layer_map(frames, P, S), frames * P, sm_scale, out, out_dtype, soB, soH,
-                soT, sched))
+  if (attn_args(a, v_pack, lut, nvalid, B, H, layer_map(frames, P, S, patch_order), frames * P, sm_scale, out,
+                out_dtype, soB, soH, soT, sched))
     return -1;
   a.q_bf = (const uint16_t*)q;
   a.sqB = sqB;
@@ -1333,6 +1340,7 @@ RESS_API int ress_qattn_block_sparse_fwd(const void* q_i8, const void* k_i8, con
   m.HW = Tq;
   m.T_p = Tq;
   m.T_s = 0;
+  m.perm = nullptr;
   return attn_common(q_i8, nullptr, q_scale, k_i8, nullptr, k_scale, vpack, v_f16, lut_c, nv_c, B, H, m, Tk, sm_scale,
                      o, o_dtype, soB, soH, soT, sched, stream);
 }
@@ -1377,8 +1385,8 @@ RESS_API long long ress_noalloc_scratch_bytes(void) { return RESS_NOALLOC_SCRATC
 RESS_API int ress_sparse_attn_fwd_f16_noalloc(const void* q, long long sqB, long long sqH, long long sqT,
                                               const void* k_pack, const void* k_norm, const void* v_pack,
                                               const void* lut, const void* nvalid, int B, int H, int frames, int P,
-                                              int S, float sm_scale, void* out, int out_dtype, long long soB,
-                                              long long soH, long long soT, hipStream_t stream) {
+                                              int S, const int* patch_order, float sm_scale, void* out, int out_dtype,
+                                              long long soB, long long soH, long long soT, hipStream_t stream) {
   RESS_REQUIRE(B > 0 && H > 0 && frames > 0 && P > S && S >= 0, "ress_sparse_attn_fwd_f16_noalloc: bad geometry");
   const long long need = ress_attn_sched_bytes(B, H, frames * P);
   RESS_REQUIRE(need > 0 && need <= RESS_NOALLOC_SCRATCH_BYTES,
@@ -1386,6 +1394,6 @@ RESS_API int ress_sparse_attn_fwd_f16_noalloc(const void* q, long long sqB, long
                need, (long long)RESS_NOALLOC_SCRATCH_BYTES);
   void* sched = nullptr;
   if (scratch_address(&sched) != 0) return -1;
-  return ress_sparse_attn_fwd_f16(q, sqB, sqH, sqT, k_pack, k_norm, v_pack, lut, nvalid, B, H, frames, P, S, sm_scale,
-                                  out, out_dtype, soB, soH, soT, sched, stream);
+  return ress_sparse_attn_fwd_f16(q, sqB, sqH, sqT, k_pack, k_norm, v_pack, lut, nvalid, B, H, frames, P, S,
+                                  patch_order, sm_scale, out, out_dtype, soB, soH, soT, sched, stream);
 }

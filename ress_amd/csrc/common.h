@@ -61,11 +61,17 @@ struct TokenMap {
   int HW;   // patch tokens per frame (P - S)
   int T_p;  // total patch tokens (frames * HW)
   int T_s;  // total special tokens (frames * S)
+  // Patch order within a frame (null: storage order). The kernels' patch token j of a frame
+  // is the frame's patch token perm[j] in storage, so blocks are formed in this order (the
+  // reference's hilbert_permute, src/ress/models/hilbert.py:128-162, read in place instead
+  // of a permuted copy). perm must be a permutation of 0..HW-1; entries are clamped into
+  // range so a bad table cannot address outside the frame.
+  const int* perm;
 };
 
 __device__ __forceinline__ int patch_to_storage(int p, const TokenMap& m) {
-  int f = p / m.HW;
-  return f * m.P + m.S + (p - f * m.HW);
+  const int f = p / m.HW, j = p - f * m.HW;
+  return f * m.P + m.S + (m.perm ? min(max(m.perm[j], 0), m.HW - 1) : j);
 }
 __device__ __forceinline__ int special_to_storage(int s, const TokenMap& m) {
   int f = s / m.S;

@@ -259,13 +259,14 @@ __global__ __launch_bounds__(64) void k_quant_k(const uint16_t* __restrict__ k, 
 // ============================================================================
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-static TokenMap make_map(int frames, int P, int S) {
+static TokenMap make_map(int frames, int P, int S, const int* perm = nullptr) {
   TokenMap m;
   m.P = P;
   m.S = S;
   m.HW = P - S;
   m.T_p = frames * (P - S);
   m.T_s = frames * S;
+  m.perm = perm;
   return m;
 }
 
@@ -278,9 +279,11 @@ static TokenMap make_map(int frames, int P, int S) {
 //    each key block's largest key norm (k_norm of k_prep_kv) are written; q_lo,
 //    q_scale, k_lo, ksum and km are unused (may be null).
 // k_pack [BH][kb_tot][64 keys][64] fp16 (keys in kernel order, zero-padded) is
-// written whenever it is non-null.
+// written whenever it is non-null. patch_order: null, or HW = P-S int32 in device memory,
+// the frame's patch tokens in the order blocks are formed (the Hilbert order of
+// hilbert_permute), read in place; the same table must go to the attention call.
 RESS_API int ress_prep_qkv(const void* q, const void* k, const void* v, int B, int H, int frames, int P, int S,
-                           long long sqB, long long sqH, long long sqT, long long skB, long long skH, long long skT,
+                           const int* patch_order, long long sqB, long long sqH, long long sqT, long long skB, long long skH, long long skT,
                            long long svB, long long svH, long long svT, void* q_i8, void* q_lo, void* q_scale,
                            void* pooled_q, void* k_i8, void* k_lo, void* k_scale, void* pooled_k, void* pooled_v,
                            void* v_pack, void* k_pack, void* ksum, void* km, hipStream_t stream) {
@@ -298,7 +301,7 @@ RESS_API int ress_prep_qkv(const void* q, const void* k, const void* v, int B, i
   RESS_REQUIRE(sqT % 8 == 0 && skT % 8 == 0 && svT % 8 == 0 && sqH % 8 == 0 && skH % 8 == 0 && svH % 8 == 0 &&
                    sqB % 8 == 0 && skB % 8 == 0 && svB % 8 == 0,
                "ress_prep_qkv: strides must be multiples of 8 elements");
-  TokenMap m = make_map(frames, P, S);
+  TokenMap m = make_map(frames, P, S, patch_order);
   const int Tk = frames * P;
   const int BH = B * H;
   const int q_blk_p = cdiv(m.T_p, 128), q_blk_s = cdiv(m.T_s, 128);

@@ -116,6 +116,21 @@ class Blocks:
     k_pack: torch.Tensor
     ksum: torch.Tensor
     km: torch.Tensor
+    patch_order: torch.Tensor = None  # device int32 (P-S,) or None: the frame's patch order
+
+
+def patch_order_table(order, grid, device):
+    """Validate a per-frame patch order (a permutation of the P-S patch positions: block
+    position j holds the frame's patch token order[j], the gather of the reference's
+    hilbert_permute, src/ress/models/hilbert.py:128-162) on the host and return it as the
+    device int32 table the kernels read, or None for storage order."""
+    if order is None:
+        return None
+    o = torch.as_tensor(order).detach().to("cpu", torch.int64).reshape(-1)
+    hw = grid.P - grid.S
+    if o.numel() != hw or not torch.equal(torch.sort(o).values, torch.arange(hw)):
+        raise ValueError(f"patch_order must be a permutation of the {hw} patch positions of a frame")
+    return o.to(device=device, dtype=torch.int32)
 
 
 def _check_qkv(t, name, grid):
@@ -129,9 +144,13 @@ def _check_qkv(t, name, grid):
         raise ValueError(f"{name} must have a unit-stride head dim")
 
 
-def prepare_blocks(q, k, v, grid, mode="f16", split=None):
+def prepare_blocks(q, k, v, grid, mode="f16", split=None, patch_order=None):
     """Pool and pack one layer's Q/K/V (bf16, storage order) for the attention mode
-    `mode` (see Blocks). `split` is the older spelling: True = "i8x2", False = "i8"."""
+    `mode` (see Blocks). `split` is the older spelling: True = "i8x2", False = "i8".
+    patch_order: None, or a per-frame permutation of the patch positions (a device int32
+    table from patch_order_table, or anything it accepts): blocks are formed in that order
+    with the tokens read in place, and sparse_attention writes each row back to its
+    tokens' storage positions."""
     if split is not None:
         mode = "i8x2" if split else "i8"
     if mode not in QK_MODES:
@@ -139,6 +158,9 @@ def prepare_blocks(q, k, v, grid, mode="f16", split=None):
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
         _check_qkv(t, n, grid)
     dev = q.device
+    if patch_order is not None and not (torch.is_tensor(patch_order) and patch_order.is_cuda
+                                        and patch_order.dtype == torch.int32):
+        patch_order = patch_order_table(patch_order, grid, dev)
     BH = grid.BH
     quant = mode != "f16"
     e = lambda *s, dt=torch.float32: torch.empty(*s, dtype=dt, device=dev)  # noqa: E731
@@ -159,10 +181,11 @@ def prepare_blocks(q, k, v, grid, mode="f16", split=None):
         k_pack=None if quant else e(BH, grid.kb_tot, KS_K, HEAD_DIM, dt=torch.float16),
         ksum=e(BH, grid.kb_tot, HEAD_DIM) if quant else None,
         km=e(BH, HEAD_DIM) if quant else None,
+        patch_order=patch_order,
     )
     P = _lib.ptr
     _lib.call(
-        "ress_prep_qkv", P(q), P(k), P(v), grid.B, grid.H, grid.frames, grid.P, grid.S,
+        "ress_prep_qkv", P(q), P(k), P(v), grid.B, grid.H, grid.frames, grid.P, grid.S, P(patch_order),
         *q.stride()[:3], *k.stride()[:3], *v.stride()[:3],
         P(b.q_i8), P(b.q_lo), P(b.q_scale), P(b.pooled_q), P(b.k_i8), P(b.k_lo), P(b.k_scale), P(b.pooled_k),
         P(b.pooled_v), P(b.v_pack), P(b.k_pack), P(b.ksum), P(b.km), _lib.stream_handle(dev))
@@ -268,10 +291,12 @@ def sparse_attention(blocks, lut, nvalid, out=None, out_dtype=torch.float32):
     sm = 1.0 / math.sqrt(HEAD_DIM)
     if blocks.mode == "f16":
         _lib.call("ress_sparse_attn_fwd_f16", P(blocks.q), *blocks.q.stride()[:3], P(blocks.k_pack), P(blocks.k_scale),
-                  P(blocks.v_pack), P(lut), P(nvalid), g.B, g.H, g.frames, g.P, g.S, sm, P(out), code,
+                  P(blocks.v_pack), P(lut), P(nvalid), g.B, g.H, g.frames, g.P, g.S, P(blocks.patch_order), sm,
+                  P(out), code,
                   *out.stride()[:3], P(sched), _lib.stream_handle(dev))
     else:
         _lib.call("ress_sparse_attn_fwd", P(blocks.q_i8), P(blocks.q_lo), P(blocks.q_scale), P(blocks.k_i8),
                   P(blocks.k_lo), P(blocks.k_scale), P(blocks.v_pack), 0, P(lut), P(nvalid), g.B, g.H,
-                  g.frames, g.P, g.S, sm, P(out), code, *out.stride()[:3], P(sched), _lib.stream_handle(dev))
+                  g.frames, g.P, g.S, P(blocks.patch_order), sm, P(out), code, *out.stride()[:3], P(sched),
+                  _lib.stream_handle(dev))
     return out

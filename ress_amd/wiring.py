@@ -23,6 +23,7 @@ CALL_ATTRIBUTES = (
     ("pooled_fallback", False),
     ("protect_own_frame", False),
     ("attention_sink", 0),
+    ("patch_order", None),
 )
 
 

@@ -458,3 +458,37 @@ def test_f16_bounded_and_running_max_rows(q_mul, dev):
     if q_mul == 0.0:
         assert bounded.all()
     assert np.nanmax(err) <= ATOL and np.nanmin(cos) >= MIN_COS
+
+
+@pytest.mark.parametrize("mode", ["f16", "i8x2"])
+def test_patch_order_read_in_place_matches_permuted_copy(mode, dev):
+    """The Hilbert order read in place (patch_order) gives exactly what the reference's
+    hilbert_permute copy gives (src/ress/models/hilbert.py:128-162): the layer on raster-order
+    Q/K/V with the curve's gather table equals the layer on the permuted tensors with the
+    output permuted back, bit for bit (maps, LUTs, pools, attention)."""
+    from ress_amd.synth import hilbert_permutation
+    gw, gh, S, frames, H = 13, 11, 5, 3, 4
+    HW = gw * gh
+    P = HW + S
+    perm = torch.from_numpy(hilbert_permutation(gw, gh))
+    gen = torch.Generator().manual_seed(11)
+    q, k, v = (torch.randn(1, H, frames * P, 64, generator=gen).to(torch.bfloat16) for _ in range(3))
+    print(f"[patch_order {mode}] frames={frames} P={P} S={S} H={H}", flush=True)
+    # the reference's copy: per frame, the special tokens, then the patch tokens gathered
+    idx = torch.cat([torch.cat([f * P + torch.arange(S), f * P + S + perm]) for f in range(frames)])
+    g = LayerGrid(1, H, frames, P, S)
+    counts = torch.full((1, H, g.q_blk_p), max(2, g.n_cand // 3), dtype=torch.int32, device=dev)
+    a = sparse_global_attention(q.to(dev), k.to(dev), v.to(dev), g, num_to_select=counts, qk_mode=mode,
+                                keep_intermediates=True, patch_order=perm)
+    b = sparse_global_attention(q[:, :, idx].contiguous().to(dev), k[:, :, idx].contiguous().to(dev),
+                                v[:, :, idx].contiguous().to(dev), g, num_to_select=counts, qk_mode=mode,
+                                keep_intermediates=True)
+    torch.cuda.synchronize()
+    assert torch.equal(a.blocks.pooled_q, b.blocks.pooled_q) and torch.equal(a.blocks.pooled_k, b.blocks.pooled_k)
+    assert torch.equal(a.attn_full, b.attn_full)
+    assert torch.equal(a.final_map, b.final_map) and torch.equal(a.nvalid, b.nvalid)
+    listed = torch.arange(g.kb_tot, device=dev) < a.nvalid[..., None]  # entries past nvalid are unused
+    assert torch.equal(torch.where(listed, a.lut, -1), torch.where(listed, b.lut, -1))
+    back = torch.empty_like(b.out)
+    back[:, :, idx] = b.out
+    assert torch.equal(a.out, back)

@@ -344,3 +344,21 @@ def test_mirror_status_word_names_every_problem():
     with pytest.raises(ValueError, match="pv_threshold below 1e9") as e:
         sparge.raise_for_status(7)
     assert "valid_block_num" in str(e.value) and "LUT entry" in str(e.value)
+
+
+def test_patch_order_table_validates_the_permutation():
+    """kernels.patch_order_table: a per-frame permutation of the P-S patch positions becomes
+    the int32 table the kernels read; anything else is refused on the host."""
+    from ress_amd import kernels, synth
+    g = LayerGrid(B=1, H=2, frames=3, P=13 * 11 + 5, S=5)
+    perm = synth.hilbert_permutation(13, 11)
+    t = kernels.patch_order_table(perm, g, "cpu")
+    assert t.dtype == torch.int32 and torch.equal(t.long(), torch.from_numpy(perm))
+    assert kernels.patch_order_table(None, g, "cpu") is None
+    bad = perm.copy()
+    bad[3] = bad[4]
+    with pytest.raises(ValueError, match="permutation"):
+        kernels.patch_order_table(bad, g, "cpu")
+    with pytest.raises(ValueError, match="permutation"):
+        kernels.patch_order_table(perm[:-1], g, "cpu")
+    assert ("patch_order", None) in wiring.CALL_ATTRIBUTES

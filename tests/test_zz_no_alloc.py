@@ -29,7 +29,7 @@ def _run(entry, g, blocks, lut, nvalid, dev):
     out = torch.full((g.B, g.H, g.Tk, 64), float("nan"), device=dev)
     P = _lib.ptr
     args = [P(blocks.q), *blocks.q.stride()[:3], P(blocks.k_pack), P(blocks.k_scale), P(blocks.v_pack), P(lut),
-            P(nvalid), g.B, g.H, g.frames, g.P, g.S, 0.125, P(out), 0, *out.stride()[:3]]
+            P(nvalid), g.B, g.H, g.frames, g.P, g.S, None, 0.125, P(out), 0, *out.stride()[:3]]
     if entry == "ress_sparse_attn_fwd_f16":
         sched = torch.empty(_lib.lib().ress_attn_sched_bytes(g.B, g.H, g.Tk), dtype=torch.uint8, device=dev)
         args.append(P(sched))
