@@ -170,6 +170,22 @@ __device__ __forceinline__ int quant_i8(float x, float scale) {
   y = y + (y >= 0.0f ? 0.5f : -0.5f);
   return (int)y;
 }
+// quant_i8 without a division per element: rcp = 1/scale (IEEE, once per block). y = x*rcp
+// is within 2^-15 of x/scale for the codes' range (|x/scale| <= 127.5: two roundings of
+// relative size 2^-24); the code is trunc(|y| + 0.5) with y's sign, so it can differ from
+// quant_i8's only when |y| + 0.5 lies within that distance of an integer. Those elements
+// (fraction within 2^-12 of an integer), NaN and infinities take quant_i8 itself, so the
+// result is identical for every input.
+__device__ __forceinline__ int quant_i8_rcp(float x, float scale, float rcp) {
+  const float y = x * rcp;
+  const float a = fabsf(y) + 0.5f;
+  const float f = a - floorf(a);
+  if (scale != 0.0f && f > 0x1p-12f && f < 1.0f - 0x1p-12f) {
+    const int m = (int)a;
+    return y >= 0.0f ? m : -m;
+  }
+  return quant_i8(x, scale);
+}
 // Two-term ("split") INT8: x ~ scale*hi + (scale/254)*lo. hi is the per-block code
 // above; lo quantises the exact residual fmaf(-scale, hi, x) (|r| <= scale/2) with the
 // scale scale/254, so |lo| <= 127.

@@ -140,12 +140,13 @@ __global__ __launch_bounds__(256) void k_ms_stats(const uint16_t* __restrict__ x
   }
 
   // codes of the whole padded block (rows past the sequence end are zero)
+  const float rc = sc != 0.0f ? 1.0f / sc : 0.0f;
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) {
     const int t = tr + 32 * p;
     int c8[8];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) c8[c] = t < cnt ? quant_i8(xv[p][c], sc) : 0;
+    for (int c = 0; c < 8; ++c) c8[c] = t < cnt ? quant_i8_rcp(xv[p][c], sc, rc) : 0;
     *reinterpret_cast<uint2*>(codes + ((long long)bh * nb * BS + base + t) * 64 + 8 * g) = pack_i8x8(c8);
   }
 }
@@ -216,6 +217,12 @@ template <int E, int K>
 __device__ __forceinline__ void ms_bsort(uint32_t (&u)[E], uint32_t* kx, int w, int lane) {
   ms_bmerge<E, K, K / 2>(u, kx, w, lane);
   if constexpr (K < 256 * E) ms_bsort<E, K * 2>(u, kx, w, lane);
+}
+// The same network over one wave's 64E positions i = 64e + lane (no cross-wave stage).
+template <int E, int K>
+__device__ __forceinline__ void ms_bsort_wave(uint32_t (&u)[E], int lane) {
+  ms_bmerge<E, K, K / 2>(u, nullptr, 0, lane);
+  if constexpr (K < 64 * E) ms_bsort_wave<E, K * 2>(u, lane);
 }
 
 // One 256-thread workgroup per (head, q-block) row for nk > 1024, E keys per lane
@@ -442,8 +449,8 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
 //          prefix sums): a bitonic network over 32-bit keys in registers, partners 64
 //          positions or more apart in the same lane, closer ones one shuffle away.
 //  prefix  the sequential CDF chain of each row runs in one lane of wave 0 over the
-//          sorted values in LDS (the four rows' chains side by side), and every wave
-//          then counts its row's prefix sums <= th in parallel.
+//          sorted values in LDS (the four rows' chains side by side) up to the batch of 16
+//          where it first exceeds th; that position is the row's count.
 //  select  with v the n-th largest probability: every column with p > v, and of those
 //          with p == v the lowest-indexed ones up to n (a ballot prefix count).
 template <int E>
@@ -458,6 +465,7 @@ __global__ __launch_bounds__(256) void k_ms_map_wave(const float* __restrict__ p
   __shared__ __align__(16) float pq_l[4][64];
   __shared__ __align__(16) float sv_l[4][LDS_ROW];
   __shared__ int go_l[4];
+  __shared__ int n_l[4];
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int bh = blockIdx.y, r = blockIdx.x * 4 + w;
   const long long row_id = (long long)bh * nq + r;
@@ -545,32 +553,9 @@ __global__ __launch_bounds__(256) void k_ms_map_wave(const float* __restrict__ p
       pb[e] = __float_as_uint(s[e] / tot);
       u[e] = 64 * e + lane < nk ? ~pb[e] : ~0u;
     }
-#pragma unroll
-    for (int k = 2; k <= NP; k <<= 1) {
-#pragma unroll
-      for (int j = k >> 1; j > 0; j >>= 1) {
-        if (j >= 64) {
-          const int ej = j >> 6;
-#pragma unroll
-          for (int e = 0; e < E; ++e) {
-            if (e & ej) continue;
-            const uint32_t a = u[e], b = u[e | ej];
-            const bool asc = ((64 * e) & k) == 0;
-            u[e] = asc ? min(a, b) : max(a, b);
-            u[e | ej] = asc ? max(a, b) : min(a, b);
-          }
-        } else {
-          const bool lower = (lane & j) == 0;
-#pragma unroll
-          for (int e = 0; e < E; ++e) {
-            const bool asc = k >= 64 ? ((64 * e) & k) == 0 : (lane & k) == 0;
-            const uint32_t a = u[e];
-            const uint32_t b = (uint32_t)__shfl_xor((int)a, j, 64);
-            u[e] = (lower == asc) ? min(a, b) : max(a, b);
-          }
-        }
-      }
-    }
+    // bitonic network over positions 64e + lane: partners 64 or more apart are another
+    // register of the lane, closer ones one DPP / swizzle / half-swap permute away
+    ms_bsort_wave<E, 2>(u, lane);
 #pragma unroll
     for (int e = 0; e < E; ++e) sv_l[w][64 * e + lane] = __uint_as_float(~u[e]);
     if (lane == 0) go_l[w] = 1;
@@ -582,28 +567,49 @@ __global__ __launch_bounds__(256) void k_ms_map_wave(const float* __restrict__ p
   }
   __syncthreads();
   if (w == 0 && lane < 4 && go_l[lane]) {  // the four rows' sequential chains, side by side
-    float* v = sv_l[lane];
+    // n = #{sequential prefix sums of the sorted p that are <= th}; p >= 0, so the sums
+    // only grow and n is the position of the first sum above th (nk if none): the chain
+    // stops at the batch that crosses th
+    const float th = cdfth[bh % H];
+    const float* v = sv_l[lane];
     float cum = 0.0f;
-    int i = 0;
+    int n = nk, i = 0;
+    bool crossed = false;
     for (; i + 16 <= nk; i += 16) {  // 16 values per LDS round trip
       float4 x[4];
 #pragma unroll
       for (int g = 0; g < 4; ++g) x[g] = reinterpret_cast<const float4*>(v + i)[g];
+      float cv[16];
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        x[g].x = cum + x[g].x;
-        x[g].y = x[g].x + x[g].y;
-        x[g].z = x[g].y + x[g].z;
-        x[g].w = x[g].z + x[g].w;
-        cum = x[g].w;
+        cum = cum + x[g].x;
+        cv[4 * g] = cum;
+        cum = cum + x[g].y;
+        cv[4 * g + 1] = cum;
+        cum = cum + x[g].z;
+        cv[4 * g + 2] = cum;
+        cum = cum + x[g].w;
+        cv[4 * g + 3] = cum;
       }
+      if (!(cum <= th)) {
+        int first = 15;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) reinterpret_cast<float4*>(v + i)[g] = x[g];
+        for (int m = 14; m >= 0; --m) first = cv[m] <= th ? first : m;
+        n = i + first;
+        crossed = true;
+        break;
+      }
     }
-    for (; i < nk; ++i) {
-      cum = cum + v[i];
-      v[i] = cum;
+    if (!crossed) {
+      for (; i < nk; ++i) {
+        cum = cum + v[i];
+        if (!(cum <= th)) {
+          n = i;
+          break;
+        }
+      }
     }
+    n_l[lane] = n;
   }
   __syncthreads();
   if (!in_range) return;
@@ -612,14 +618,7 @@ __global__ __launch_bounds__(256) void k_ms_map_wave(const float* __restrict__ p
     for (int c = lane; c < nk; c += 64) row[c] = 1;
     return;
   }
-  const float th = cdfth[bh % H];
-  int cnt = 0;
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int i = 64 * e + lane;
-    cnt += (i < nk && sv_l[w][i] <= th) ? 1 : 0;
-  }
-  const int n = wave_sum_i(cnt);  // the sums only grow: the count is the prefix length
+  const int n = n_l[w];
   uint32_t vbits = 0;
   int n_gt = 0;
   if (n > 0) {  // v = the n-th largest p (sorted position n-1; s[] holds the sorted values)

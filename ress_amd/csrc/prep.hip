@@ -14,14 +14,18 @@
 #include "common.h"
 
 // hi (and, if lo_dst is set, split lo) codes of 8 values -> two 8-byte stores
+// (quant_i8 / quant_i8_lo through the division-free quant_i8_rcp: identical codes)
 __device__ __forceinline__ void store_codes(const float x[8], float scale, int8_t* hi_dst, int8_t* lo_dst) {
   int hi[8], lo[8];
+  const float rc = scale != 0.0f ? 1.0f / scale : 0.0f;
 #pragma unroll
-  for (int c = 0; c < 8; ++c) hi[c] = quant_i8(x[c], scale);
+  for (int c = 0; c < 8; ++c) hi[c] = quant_i8_rcp(x[c], scale, rc);
   *reinterpret_cast<uint2*>(hi_dst) = pack_i8x8(hi);
   if (lo_dst) {
+    const float s2 = scale / 254.0f;
+    const float rc2 = s2 != 0.0f ? 1.0f / s2 : 0.0f;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) lo[c] = quant_i8_lo(x[c], scale, hi[c]);
+    for (int c = 0; c < 8; ++c) lo[c] = scale == 0.0f ? 0 : quant_i8_rcp(fmaf(-scale, (float)hi[c], x[c]), s2, rc2);
     *reinterpret_cast<uint2*>(lo_dst) = pack_i8x8(lo);
   }
 }

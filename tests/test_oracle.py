@@ -336,3 +336,45 @@ def test_generator_is_deterministic_and_shaped():
     assert m == {"frames": 2, "P": 1374, "S": 5}
     cam, pc = synth.make_hess_tables()
     assert cam.shape == (3, 24, 16) and torch.all(cam > 0)
+
+
+def test_reciprocal_quantiser_fast_path_is_exact():
+    """The kernels quantise with x * (1/scale) and fall back to the division x / scale when
+    |y| + 0.5 has a fraction within 2^-12 of an integer (common.h quant_i8_rcp). In float32
+    (numpy, round to nearest like the GPU), the fast path's code equals the division's on
+    random blocks and on values placed at and around every half-integer boundary."""
+    rng = np.random.default_rng(3)
+    f32 = np.float32
+
+    def exact(x, s):
+        y = (x / s).astype(f32)
+        y = (y + np.where(y >= 0, f32(0.5), f32(-0.5))).astype(f32)
+        return np.trunc(y).astype(np.int64)
+
+    def fast(x, s):
+        r = (f32(1.0) / s).astype(f32)
+        y = (x * r).astype(f32)
+        a = (np.abs(y) + f32(0.5)).astype(f32)
+        f = (a - np.floor(a)).astype(f32)
+        ok = (f > f32(2.0 ** -12)) & (f < f32(1.0) - f32(2.0 ** -12))
+        m = np.trunc(a).astype(np.int64)
+        return np.where(ok, np.where(y >= 0, m, -m), exact(x, s)), ok
+
+    for trial in range(200):
+        x = (rng.standard_normal(4096) * 10.0 ** rng.uniform(-6, 4)).astype(f32)
+        s = f32(np.abs(x).max() / f32(127.0))
+        got, _ = fast(x, s)
+        assert np.array_equal(got, exact(x, s))
+    # adversarial: x just around (k + 1/2) * s for every k, a few ulps either side
+    for s in (f32(0.0137), f32(3.3e-5), f32(1.0), f32(7.77)):
+        k = np.arange(-127, 128, dtype=f32)
+        base = ((k + f32(0.5)) * s).astype(f32)
+        xs = [base]
+        for n in range(1, 6):
+            xs.append(np.nextafter(base, np.inf, dtype=f32))
+            xs.append(np.nextafter(base, -np.inf, dtype=f32))
+            base = xs[-2]
+        x = np.concatenate(xs)
+        got, ok = fast(x, s)
+        assert np.array_equal(got, exact(x, s))
+        assert not ok.all()  # the boundary values do take the division
