@@ -11,7 +11,9 @@ special-query rows dense, output in storage order.
 
 Prints one JSON line. value = effective TFLOP/s = 4 N^2 H D / t (dense-equivalent);
 ms_per_step = ms per layer (ms_per_step_median: the median of the per-step HIP-event
-times). roofline = the attention kernel's retained-block FLOPs over
+times), kernels launched eagerly; with --graph, ms_per_step_graph times the same step
+captured once in a HIP graph and replayed (its output checked bit for bit against an
+eager step first). roofline = the attention kernel's retained-block FLOPs over
 its own HIP-event-timed duration against the dense MFMA peak of its arithmetic (QK^T
 half at the bf16 or INT8 rate, PV half at the bf16 rate); frac_of_int8_peak prices the
 same FLOPs against the INT8 peak, frac_of_measured_peak against the rates measured on
@@ -92,6 +94,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=15.0)
     ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="also capture the step once in a HIP graph and time its replays (reported as "
+                         "ms_per_step_graph; on this ROCm stack the replay measured slower than eager launches)")
     ap.add_argument("--qk-mode", default="f16", choices=["f16", "i8x2", "i8"],
                     help="QK^T operands of the attention kernel (16-bit: fp16 K blocks and per-row fp16 queries; "
                          "two-term or single-term INT8)")
@@ -359,6 +364,33 @@ def main():
     rs_ms = sum(s.elapsed_time(e) for s, e in rs_ev) / len(rs_ev) if rs_ev else None
     attn_mod.kernels.sparse_attention = orig_attn
     projected.restore_swap_keep = orig_rs
+    # --graph: the same step captured once in a HIP graph and replayed (every kernel and
+    # buffer of the eager step); the replay's output is checked against an eager step bit
+    # for bit before it is timed. The eager step stays the headline figure.
+    ms_graph = ms_graph_median = None
+    if args.graph:
+        step()
+        torch.cuda.synchronize()
+        want = out.clone()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step()
+        for _ in range(args.warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        graph_checked = bool(torch.equal(out, want))
+        if not graph_checked:
+            raise RuntimeError("graph replay differs from the eager step")
+        gm = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+        gm[0].record()
+        for i in range(args.steps):
+            g.replay()
+            gm[i + 1].record()
+        torch.cuda.synchronize()
+        ms_graph = gm[0].elapsed_time(gm[-1]) / args.steps
+        g_ms = sorted(gm[i].elapsed_time(gm[i + 1]) for i in range(args.steps))
+        ms_graph_median = g_ms[len(g_ms) // 2]
+        del g
 
     # work actually done (same map every step)
     res = sparse_global_attention(q, k, v, grid, budget_fn=budget_fn, out=out, keep_intermediates=True,
@@ -399,6 +431,8 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
         "ms_per_step_median": round(ms_median, 4),
+        "ms_per_step_graph": None if ms_graph is None else round(ms_graph, 4),
+        "ms_per_step_graph_median": None if ms_graph is None else round(ms_graph_median, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -492,3 +492,35 @@ def test_patch_order_read_in_place_matches_permuted_copy(mode, dev):
     back = torch.empty_like(b.out)
     back[:, :, idx] = b.out
     assert torch.equal(a.out, back)
+
+
+def test_layer_step_replays_from_a_hip_graph(dev):
+    """The layer step (prep, pooled map, HeSS budget, selection, attention) captured once in
+    a HIP graph: every replay, with eager work and synchronisations between replays, equals
+    the eager step bit for bit (no memset nodes or host reads inside the step)."""
+    frames = 4
+    q, k, v, meta = synth.make_layer_qkv(frames)
+    g = LayerGrid(1, 16, frames, meta["P"], meta["S"])
+    cam, pc = synth.make_hess_tables()
+    bud = budget.HessBudget(cam, pc, lam=0.5)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    out = torch.empty(1, 16, g.Tk, 64, dtype=torch.float32, device=dev)
+
+    def step():
+        return sparse_global_attention(qd, kd, vd, g, budget_fn=lambda a: bud.num_to_select(0, a, 0.7, None, 1.0),
+                                       out=out, attention_sink=64)
+
+    step()
+    torch.cuda.synchronize()
+    want = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for rep in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {rep} differs from the eager step"
+        step()  # eager work between the replays
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)
