@@ -449,7 +449,8 @@ def main():
                      "mfma_busy_pct_pmc": measured_mfma_busy(f"k_sparse_attn_{args.qk_mode}") if args.config == 1 else None,
                      "frac_of_int8_peak": round(achieved / PEAK_INT8_TOPS, 4),
                      "measured_peak": round(peak_meas, 1), "frac_of_measured_peak": round(achieved / peak_meas, 4),
-                     "kernel": "k_sparse_attn", "kernel_ms": round(attn_ms, 4),
+                     "kernel": "k_sparse_attn_f16" if args.qk_mode == "f16" else "k_sparse_attn",
+                     "kernel_ms": round(attn_ms, 4),
                      "retained_flop_per_launch": flops_kept},
         "restore_swap_ms": None if rs_ms is None else round(rs_ms, 4),
         "measured_peaks": peaks,
