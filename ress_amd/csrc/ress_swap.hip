@@ -128,20 +128,24 @@ __device__ __forceinline__ uint32_t rs_top_m(const uint32_t (&key)[NPL], uint32_
     const int above = suf - own;  // keys in bins of higher lanes
     const int s3 = above + h3, s2 = s3 + h2, s1 = s2 + h1, s0 = s1 + h0;
     // the digit t with S(t) >= need > S(t+1) is unique
-    int t = -1, gt = 0;
-    if (s3 >= need && above < need) t = 3, gt = above;
-    else if (s2 >= need && s3 < need) t = 2, gt = s3;
-    else if (s1 >= need && s2 < need) t = 1, gt = s2;
-    else if (s0 >= need && s1 < need) t = 0, gt = s1;
+    int t = -1, gt = 0, inbin = 0;
+    if (s3 >= need && above < need) t = 3, gt = above, inbin = h3;
+    else if (s2 >= need && s3 < need) t = 2, gt = s3, inbin = h2;
+    else if (s1 >= need && s2 < need) t = 1, gt = s2, inbin = h1;
+    else if (s0 >= need && s1 < need) t = 0, gt = s1, inbin = h0;
     const unsigned long long hit = __ballot(t >= 0);
     const int src = __ffsll((long long)hit) - 1;
-    const int digit = __shfl(4 * lane + t, src), n_gt = __shfl(gt, src);
+    const int digit = __shfl(4 * lane + t, src), n_gt = __shfl(gt, src), n_in = __shfl(inbin, src);
     need -= n_gt;
     prefix |= (uint32_t)digit << shift;
     pmask |= 255u << shift;
     __builtin_amdgcn_wave_barrier();
+    // every key of the threshold bin is taken: the keys above prefix (lower digits zero)
+    // and the n_in >= (keys equal to prefix) ties below select exactly the same set as
+    // the full descent, so the remaining digits are skipped
+    if (n_in == need) break;
   }
-  const uint32_t thr = prefix;  // the m-th largest key; `need` of its ties are taken
+  const uint32_t thr = prefix;  // the m-th largest key's high digits; `need` of the ties at thr are taken
   uint32_t sel = 0u;
   int before = 0;
   const unsigned long long lower = lane ? (~0ull >> (64 - lane)) : 0ull;
