@@ -185,7 +185,11 @@ int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void* q_scale
  * (log2 units) runs with the pre-scaled queries rounded to fp16 and a fixed offset in the
  * accumulator (no running max); other rows use the exact fp16 queries and a running max.
  * sched, patch_order: as for ress_sparse_attn_fwd (patch_order: the table given to
- * ress_prep_qkv; each row is read and written at the storage positions of its tokens). */
+ * ress_prep_qkv; each row is read and written at the storage positions of its tokens).
+ * After the call, int32 word 24 of sched (byte 96) is 1 if a key and 2 if a query element
+ * (or 3 if both) lay outside fp16's range (|x| >= 65520, which bf16 can hold and fp16
+ * cannot): those rows are not meaningful and the caller should use the INT8 entry point.
+ * ress_prep_qkv marks such a key block by an infinite k_norm. */
 int ress_sparse_attn_fwd_f16(const void* q, long long sqB, long long sqH, long long sqT, const void* k_pack,
                              const void* k_norm, const void* v_pack, const void* lut, const void* nvalid, int B,
                              int H, int frames, int P, int S, const int* patch_order, float sm_scale, void* out,

@@ -173,15 +173,18 @@ void oracle_prep_qkv(const uint16_t* q, const uint16_t* k, const uint16_t* v, in
       float nmax = 0.0f;
       for (int t = 0; t < cnt; ++t) {
         float g8[8];
+        int over = 0;  // an element fp16 cannot hold (|x| >= 65520 rounds to inf): the norm is inf
         for (int grp = 0; grp < 8; ++grp) {
           float ss = 0.0f;
           for (int c = 0; c < 8; ++c) {
             const float x = bf16f(kh[(long long)rows[t] * 64 + 8 * grp + c]);
             ss = fmaf(x, x, ss);
+            over |= !(fabsf(x) < 65520.0f);
           }
           g8[grp] = ss;
         }
-        const float n = sqrtf(((g8[0] + g8[1]) + (g8[2] + g8[3])) + ((g8[4] + g8[5]) + (g8[6] + g8[7])));
+        const float n = over ? INFINITY
+                             : sqrtf(((g8[0] + g8[1]) + (g8[2] + g8[3])) + ((g8[4] + g8[5]) + (g8[6] + g8[7])));
         nmax = fmaxf(nmax, n);
       }
       k_norm[(long long)bh * kbt + kb] = nmax;

@@ -76,31 +76,55 @@ class LayerResult:
     # device-side budget status: number of HeSS columns that did not converge (0-dim int32)
     unconverged: torch.Tensor = None
     max_iters: int = None
+    # device-side 16-bit operand status (kernels.sparse_attention's ress_attn_status), or None
+    attn_status: torch.Tensor = None
 
     def _raise_unconverged(self, n):
         if n:
             raise RuntimeError(f"adjust_attention_selection did not converge in {self.max_iters} iterations "
                                f"({int(n)} query-block columns)")
 
+    @staticmethod
+    def _raise_range(st):
+        st = int(st)
+        if st:
+            what = " and ".join(n for bit, n in ((1, "key"), (2, "query")) if st & bit)
+            raise ValueError(f"a {what} element lies outside the fp16 range (|x| >= 65520), which the 16-bit "
+                             f"attention mode cannot represent; run the layer with qk_mode='i8x2'")
+
+    def _status_values(self):
+        vals = []
+        if self.unconverged is not None:
+            vals.append(self.unconverged.float().reshape(()))
+        if self.attn_status is not None:
+            vals.append(self.attn_status[0].float())
+        return vals
+
+    def _raise_status(self, got):
+        i = 0
+        if self.unconverged is not None:
+            self._raise_unconverged(got[i])
+            i += 1
+        if self.attn_status is not None:
+            self._raise_range(got[i])
+
     def check(self):
         """Raise RuntimeError if the layer's HeSS budget did not converge (reference
-        _proportional.py:112-113). Synchronises with the device."""
-        if self.unconverged is not None:
-            self._raise_unconverged(int(self.unconverged.item()))
+        _proportional.py:112-113), or ValueError if the 16-bit attention met an operand
+        outside fp16's range. Synchronises with the device once."""
+        vals = self._status_values()
+        if vals:
+            self._raise_status(torch.stack(vals).tolist())
 
     def sparsity(self):
         """Realized sparsity 1 - mean(final_map), sinks included (reference
-        attention.py:242). Synchronises with the device once, and raises there if the
-        layer's HeSS budget did not converge (see check)."""
+        attention.py:242). Synchronises with the device once, and raises there on what
+        check() reports."""
         if self.final_map is None:
             self.check()
             return 0.0
-        vals = [1.0 - self.final_map.float().mean()]
-        if self.unconverged is not None:
-            vals.append(self.unconverged.float())
-        got = torch.stack(vals).tolist()
-        if len(got) > 1:
-            self._raise_unconverged(got[1])
+        got = torch.stack([1.0 - self.final_map.float().mean()] + self._status_values()).tolist()
+        self._raise_status(got[1:])
         return got[0]
 
 
@@ -239,7 +263,8 @@ def sparse_global_attention(q, k, v, grid, *, num_to_select=None, budget_fn=None
             final_map[..., :sink_lead] = True
         lut, nvalid = kernels.lut_from_map(final_map, grid)
     o = kernels.sparse_attention(blocks, lut, nvalid, out=out, out_dtype=out_dtype)
-    res = LayerResult(out=o, final_map=final_map, unconverged=unconverged, max_iters=max_iters)
+    res = LayerResult(out=o, final_map=final_map, unconverged=unconverged, max_iters=max_iters,
+                      attn_status=getattr(o, "ress_attn_status", None))
     if keep_intermediates:
         res.attn_full, res.attn_cond, res.v_bar_full = attn_full, attn_cond, v_bar_full
         res.counts, res.lut, res.nvalid, res.blocks = counts, lut, nvalid, blocks

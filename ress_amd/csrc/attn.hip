@@ -155,6 +155,10 @@ __device__ __forceinline__ float pair_sum(float x) {
 // row of a head in the middle of a range would start late and end long after the rest.
 //   sched[0..8]   range bounds (sched[j] .. sched[j+1]-1 belong to XCD j)
 //   sched[16..23] per-XCD next-item counters (atomically advanced by the kernel)
+//   sched[24]     operand status of the 16-bit kernel: RESS_F16_KEY_RANGE |
+//                 RESS_F16_QUERY_RANGE when a key / query element was outside fp16's range
+#define RESS_F16_KEY_RANGE 1
+#define RESS_F16_QUERY_RANGE 2
 #define RESS_SCHED_INTS 32
 #define RESS_ROW_COST 2
 // Tail split. Workgroups run out of rows one by one at the end of a range; the spread of
@@ -195,6 +199,7 @@ __global__ __launch_bounds__(1024) void k_attn_schedule(const int* __restrict__ 
     s += nvalid[(long long)bh * q_blk_total + qb] + RESS_ROW_COST;
   }
   if (tid < 9) sched[tid] = tid == 0 ? 0 : n;
+  if (tid == 9) sched[24] = 0;  // operand status, set by the 16-bit kernel
   // inclusive scan of the threads' sums: lane shuffles within each wave, then the 16 wave
   // totals through LDS (one barrier)
   long long incl = s;
@@ -782,6 +787,18 @@ __device__ __forceinline__ void attn_row_f16(const AttnArgs& a, const int* __res
     kmax = wave_max(kmax);
     const float m0 = sqrtf(pair_sum(qq)) * kmax;
     if (l == 0) vote[w] = __any(!(m0 <= RESS_BOUND_MAX)) ? 1 : 0;  // NaN fails the test
+    // operands fp16 cannot hold (|x| >= 65520): an infinite key norm (prep's marker) or a
+    // query element; the row's result is not meaningful and the caller is told so
+    bool q_over = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float x[8];
+      unpack_bf16x8(qraw[j], x);
+#pragma unroll
+      for (int cc = 0; cc < 8; ++cc) q_over |= !(fabsf(x[cc]) < 65520.0f);
+    }
+    const int bad = (!(kmax < __builtin_huge_valf()) ? RESS_F16_KEY_RANGE : 0) | (__any(q_over) ? RESS_F16_QUERY_RANGE : 0);
+    if (bad && l == 0) atomicOr(&a.sched[24], bad);
   }
   __syncthreads();
   int any_over = 0;

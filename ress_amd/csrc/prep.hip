@@ -137,6 +137,12 @@ __global__ __launch_bounds__(64) void k_prep_kv(const uint16_t* __restrict__ k, 
       }
 #pragma unroll
       for (int c = 0; c < 8; ++c) ss = fmaf(xk[c], xk[c], ss);
+      if (k_norm) {  // an element fp16 cannot hold (|x| >= 65520 rounds to inf): the key's norm is inf
+        bool over = false;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) over |= !(fabsf(xk[c]) < 65520.0f);
+        if (over) ss = __builtin_huge_valf();
+      }
 #pragma unroll
       for (int c = 0; c < 8; ++c) ka[c] = ka[c] + xk[c];
       if (t < cnt_p) {

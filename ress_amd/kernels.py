@@ -280,7 +280,10 @@ def lut_from_map(final_map, grid):
 
 def sparse_attention(blocks, lut, nvalid, out=None, out_dtype=torch.float32):
     """Block-sparse attention over the prepared blocks; returns (B,H,frames*P,64) in
-    storage order (patch rows sparse, special rows dense)."""
+    storage order (patch rows sparse, special rows dense). In the "f16" mode the returned
+    tensor carries `ress_attn_status`, a device int32 (1,) that the kernel sets to 1 (a key)
+    or 2 (a query) or both when an operand element was outside fp16's range (|x| >= 65520):
+    read it at the next synchronisation (LayerResult.check does)."""
     g = blocks.grid
     dev = blocks.pooled_q.device
     if out is None:
@@ -292,8 +295,8 @@ def sparse_attention(blocks, lut, nvalid, out=None, out_dtype=torch.float32):
     if blocks.mode == "f16":
         _lib.call("ress_sparse_attn_fwd_f16", P(blocks.q), *blocks.q.stride()[:3], P(blocks.k_pack), P(blocks.k_scale),
                   P(blocks.v_pack), P(lut), P(nvalid), g.B, g.H, g.frames, g.P, g.S, P(blocks.patch_order), sm,
-                  P(out), code,
-                  *out.stride()[:3], P(sched), _lib.stream_handle(dev))
+                  P(out), code, *out.stride()[:3], P(sched), _lib.stream_handle(dev))
+        out.ress_attn_status = sched[96:100].view(torch.int32)  # word 24 of the schedule header
     else:
         _lib.call("ress_sparse_attn_fwd", P(blocks.q_i8), P(blocks.q_lo), P(blocks.q_scale), P(blocks.k_i8),
                   P(blocks.k_lo), P(blocks.k_scale), P(blocks.v_pack), 0, P(lut), P(nvalid), g.B, g.H,

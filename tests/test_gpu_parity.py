@@ -524,3 +524,24 @@ def test_layer_step_replays_from_a_hip_graph(dev):
         step()  # eager work between the replays
         torch.cuda.synchronize()
         assert torch.equal(out, want)
+
+
+@pytest.mark.parametrize("which", ["key", "query"])
+def test_f16_operand_outside_fp16_range_is_reported(which, dev):
+    """A key or query element fp16 cannot hold (|x| >= 65520; bf16 can) makes the 16-bit
+    layer raise at its next synchronisation instead of returning inf/NaN rows silently;
+    the same layer without it reports nothing."""
+    frames, H = 2, 4
+    q, k, v, meta = synth.make_layer_qkv(frames, H=H)
+    g = LayerGrid(1, H, frames, meta["P"], meta["S"])
+    counts = torch.full((1, H, g.q_blk_p), max(2, g.n_cand // 2), dtype=torch.int32, device=dev)
+    clean = sparse_global_attention(q.to(dev), k.to(dev), v.to(dev), g, num_to_select=counts)
+    clean.check()
+    q2, k2 = q.clone(), k.clone()
+    (k2 if which == "key" else q2)[0, 1, 7, 3] = 70000.0
+    print(f"[f16 range] {which} element 70000", flush=True)
+    res = sparse_global_attention(q2.to(dev), k2.to(dev), v.to(dev), g, num_to_select=counts)
+    with pytest.raises(ValueError, match=f"a {which} element lies outside the fp16 range"):
+        res.check()
+    with pytest.raises(ValueError, match="outside the fp16 range"):
+        res.sparsity()

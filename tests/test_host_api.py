@@ -362,3 +362,14 @@ def test_patch_order_table_validates_the_permutation():
     with pytest.raises(ValueError, match="permutation"):
         kernels.patch_order_table(perm[:-1], g, "cpu")
     assert ("patch_order", None) in wiring.CALL_ATTRIBUTES
+
+
+def test_layer_result_reports_fp16_operand_range():
+    """LayerResult decodes the 16-bit kernel's operand status (1 key, 2 query)."""
+    attention.LayerResult._raise_range(0)
+    with pytest.raises(ValueError, match="a key element"):
+        attention.LayerResult._raise_range(1)
+    with pytest.raises(ValueError, match="a query element"):
+        attention.LayerResult._raise_range(2)
+    with pytest.raises(ValueError, match="a key and query element"):
+        attention.LayerResult._raise_range(3)
