@@ -321,6 +321,10 @@ def ress_attention_forward(self, x, pos, num_to_select=None, budget_fn=None, per
             keep_intermediates=aux_store is not None and aux_full, protect_own_frame=protect_own_frame,
             attention_sink=attention_sink, patch_order=order)
         x_out = res.out
+        # the forward does not synchronise: the layer's device-side status (HeSS convergence,
+        # 16-bit operand range) stays on the module for check_layers
+        self._ress_status = LayerResult(out=None, unconverged=res.unconverged, max_iters=res.max_iters,
+                                        attn_status=res.attn_status)
         sparsity = res.sparsity() if aux_store is not None else None
     if aux_store is not None:
         if aux_full and res is not None:
@@ -335,6 +339,24 @@ def ress_attention_forward(self, x, pos, num_to_select=None, budget_fn=None, per
     if aux_store is not None and aux_full:
         aux_store["value"].output = x_out
     return project_out(self, x_out.to(x.dtype) if x.dtype != x_out.dtype else x_out, B, N, P, nh, hd)
+
+
+def check_layers(model_or_modules):
+    """Synchronise once and raise what the last forward of each block-sparse attention
+    module left unreported: RuntimeError if a HeSS budget did not converge (reference
+    _proportional.py:112-113), ValueError if the 16-bit attention met an operand outside
+    fp16's range. Takes a model (every submodule) or an iterable of modules."""
+    mods = model_or_modules.modules() if hasattr(model_or_modules, "modules") else model_or_modules
+    results = [m._ress_status for m in mods if getattr(m, "_ress_status", None) is not None]
+    vals = [v for r in results for v in r._status_values()]
+    if not vals:
+        return
+    got = torch.stack(vals).tolist()
+    i = 0
+    for r in results:
+        n = len(r._status_values())
+        r._raise_status(got[i:i + n])
+        i += n
 
 
 def _device_patch_order(module, order, grid, device):

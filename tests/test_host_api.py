@@ -373,3 +373,22 @@ def test_layer_result_reports_fp16_operand_range():
         attention.LayerResult._raise_range(2)
     with pytest.raises(ValueError, match="a key and query element"):
         attention.LayerResult._raise_range(3)
+
+
+def test_check_layers_raises_what_the_forwards_left():
+    """ress_amd.check_layers: one synchronisation over the status the last forward of each
+    block-sparse attention module kept (HeSS convergence, 16-bit operand range)."""
+    class Mod(nn.Module):
+        pass
+
+    ok, bad_range, bad_hess = Mod(), Mod(), Mod()
+    ok._ress_status = attention.LayerResult(out=None, unconverged=torch.tensor(0, dtype=torch.int32),
+                                            attn_status=torch.zeros(1, dtype=torch.int32))
+    ress.check_layers([ok])
+    bad_range._ress_status = attention.LayerResult(out=None, attn_status=torch.tensor([2], dtype=torch.int32))
+    with pytest.raises(ValueError, match="a query element"):
+        ress.check_layers([ok, bad_range])
+    bad_hess._ress_status = attention.LayerResult(out=None, unconverged=torch.tensor(3, dtype=torch.int32),
+                                                  max_iters=1000)
+    with pytest.raises(RuntimeError, match="did not converge"):
+        ress.check_layers(nn.ModuleList([ok, bad_hess]))
