@@ -238,7 +238,8 @@ def run_aggregator(args):
         "metric": "ms per end-to-end aggregator forward (24 global layers under ReSS) + global-attention share",
         "value": round(ms, 2), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 2), "ms_per_step_median": round(step_ms[len(step_ms) // 2], 2),
-        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 model; global attention fp16 QK (bf16 inputs) / bf16 PV / fp32 softmax",
         "data": "synthetic (64 frames 518x518: uniform [0,1] pixels + a shared low-frequency pattern); random weights",
         "config": {"workload": "BASELINE configs[3]: VGGT-1B-style aggregator, ReSS on all 24 global layers",
                    "frames": S, "tokens": S * 1374, "layers": depth, "dim": 1024, "heads": 16, "sparse_ratio": 0.8,
