@@ -770,7 +770,8 @@ int oracle_rs_probe(const float* A, const float* V, const float* M, const uint8_
  * quant_per_block, :38-41). SpargeAttn itself is not in the reference; this is the
  * build's restatement (parity unpinned against SpargeAttn):
  *  per block (Q 128, K 64 tokens; K smoothed by km when given), x the fp32 values:
- *    pooled  = mean_t x_t                                  (SUM8x order)
+ *    pooled  = mean_t x_t   (token lane r < 32 sums rows r, r+32, ... in order, tree8 over
+ *              lanes 8w..8w+7, then (W0 + W1) + (W2 + W3); rows past the end add 0)
  *    sim     = ||sum_t x_t/||x_t|| ||^2 / n^2, the mean pairwise cosine similarity
  *              (self pairs included; a zero row contributes 0); similar = sim > simthreshd1[h]
  *    codes   = the per-block INT8 quantiser (scale = amax/127)
@@ -807,15 +808,27 @@ static void ms_block(const uint16_t* x, const float* km, int T, int b, int BS, f
     const float inv = n2 > 0.0f ? 1.0f / sqrtf(n2) : 0.0f;
     for (int d = 0; d < 64; ++d) xh[t][d] = xs[t][d] * inv;
   }
+  /* per dim, over the BS padded rows (zeros past cnt): token lane r < 32 adds rows r + 32p
+   * in p order, lanes 8w..8w+7 combine by tree8, the four groups as (W0 + W1) + (W2 + W3) */
   float ssum[64];
   for (int d = 0; d < 64; ++d) {
-    float pp[8] = {0, 0, 0, 0, 0, 0, 0, 0}, ph[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int t = 0; t < cnt; ++t) {
-      pp[t & 7] = pp[t & 7] + xs[t][d];
-      ph[t & 7] = ph[t & 7] + xh[t][d];
+    float wp[4], wh[4];
+    for (int w = 0; w < 4; ++w) {
+      float lp[8], lh[8];
+      for (int tl = 0; tl < 8; ++tl) {
+        float a = 0.0f, h = 0.0f;
+        for (int t = 8 * w + tl; t < BS; t += 32) {
+          a = a + (t < cnt ? xs[t][d] : 0.0f);
+          h = h + (t < cnt ? xh[t][d] : 0.0f);
+        }
+        lp[tl] = a;
+        lh[tl] = h;
+      }
+      wp[w] = tree8(lp);
+      wh[w] = tree8(lh);
     }
-    pooled[d] = tree8(pp) / (float)cnt;
-    ssum[d] = tree8(ph);
+    pooled[d] = ((wp[0] + wp[1]) + (wp[2] + wp[3])) / (float)cnt;
+    ssum[d] = (wh[0] + wh[1]) + (wh[2] + wh[3]);
   }
   float part[8];
   for (int g = 0; g < 8; ++g) {

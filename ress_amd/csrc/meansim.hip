@@ -11,7 +11,10 @@
 //   per block of n tokens (Q 128, K 64; K minus km when km is given), x_t in fp32:
 //     n2_t    = tree8 over dim groups g of fmaf(x, x) chains over dims 8g..8g+7
 //     xh_t    = x_t * (n2_t > 0 ? 1/sqrt(n2_t) : 0)
-//     pooled  = SUM8x(x) / n,  ssum = SUM8x(xh)
+//     pooled  = TSUM(x) / n,  ssum = TSUM(xh), where per dim TSUM over the block's
+//               padded token rows (zeros past the sequence end) is: a[r] = the sum of
+//               tokens r, r+32, r+64, r+96 in that order (r < 32; Q has 4 terms, K 2),
+//               W[w] = tree8(a[8w..8w+7]), TSUM = (W[0] + W[1]) + (W[2] + W[3])
 //     sim     = tree8 over g of fmaf chains of ssum^2  /  (n*n)   (the mean pairwise
 //               cosine similarity, self pairs included); similar = sim > simthreshd1[h]
 //     codes   = the per-block quantiser, scale = amax/127
@@ -22,9 +25,10 @@
 //     map = the first n of that order | non-similar c | every c of a non-similar row
 //           | c < ceil(attention_sink/64)
 //
-// k_ms_stats: one 256-thread workgroup per (block, batch*head). Thread (token lane
-// tid>>3, dim group tid&7) loads 8 bf16 per token pass (BS/32 passes), keeps them in
-// registers for the codes, and stages fp32 copies in LDS for the per-dim column pass.
+// k_ms_stats: one 256-thread workgroup per (block, batch*head), Q's and K's blocks in one
+// launch. Thread (token lane tid>>3, dim group tid&7) loads 8 bf16 per token pass (BS/32
+// passes) and keeps them in registers for the sums and the codes; the token-lane sums are
+// lane butterflies, and only the 4 waves' partial sums go through LDS.
 // k_ms_map_wave (nk <= 1024): one wave per (q-block, batch*head) row, four rows per
 // workgroup; details at the kernel.
 // k_ms_map_long (nk > 1024): one 256-thread workgroup per row: the same value sort with
@@ -34,121 +38,11 @@
 
 namespace {
 
-constexpr int MS_LD = 68;          // LDS row stride (floats) of the staged block: 16-byte rows, offset banks
 constexpr int MS_MAX_NK = 6144;    // key blocks per row of the map kernels (<= 32 KiB keys + 24 KiB p in LDS)
 constexpr int MS_CH_LD = 17;       // k_ms_map_long score chunks: 64 columns x 16 dims, odd row stride
 // front LDS region of k_ms_map_long: the NP2 sort keys, or the four waves' score chunks
 __host__ __device__ constexpr size_t ms_long_front_bytes(int np2) {
   return (size_t)np2 * 4 > 4 * 64 * MS_CH_LD * 4 ? (size_t)np2 * 4 : 4 * 64 * MS_CH_LD * 4;
-}
-
-template <int BS>
-__global__ __launch_bounds__(256) void k_ms_stats(const uint16_t* __restrict__ x, Strides sx, int T,
-                                                  const float* __restrict__ km, const float* __restrict__ simth,
-                                                  int nb, int8_t* __restrict__ codes, float* __restrict__ scale,
-                                                  float* __restrict__ pooled, uint8_t* __restrict__ sim) {
-  constexpr int PASSES = BS / 32;
-  __shared__ __align__(16) float xs_l[BS * MS_LD];
-  __shared__ float inv_l[BS];
-  __shared__ float ssum_l[64];
-  __shared__ float amax_l[4];
-  const int blk = blockIdx.x, bh = blockIdx.y;
-  const int tid = threadIdx.x, g = tid & 7, tr = tid >> 3, lane = tid & 63, w = tid >> 6;
-  const int base = blk * BS, cnt = min(BS, T - base);
-  const uint16_t* xb = x + bh_offset(bh, sx);
-
-  float kmv[8];
-#pragma unroll
-  for (int c = 0; c < 8; ++c) kmv[c] = km ? km[(long long)bh * 64 + 8 * g + c] : 0.0f;
-
-  // token pass: values, squared norm (fmaf chain per dim group, tree8 across the 8 lanes of a token)
-  float xv[PASSES][8];
-  float amax = 0.0f;
-#pragma unroll
-  for (int p = 0; p < PASSES; ++p) {
-    const int t = tr + 32 * p;
-    if (t < cnt) {
-      const uint4 r = *reinterpret_cast<const uint4*>(xb + (long long)(base + t) * sx.t + 8 * g);
-      unpack_bf16x8(r, xv[p]);
-#pragma unroll
-      for (int c = 0; c < 8; ++c) xv[p][c] = xv[p][c] - kmv[c];
-    } else {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) xv[p][c] = 0.0f;
-    }
-    float part = 0.0f;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      part = fmaf(xv[p][c], xv[p][c], part);
-      amax = fmaxf(amax, fabsf(xv[p][c]));
-    }
-    part = part + __shfl_xor(part, 1, 64);
-    part = part + __shfl_xor(part, 2, 64);
-    part = part + __shfl_xor(part, 4, 64);
-    if (t < cnt) {
-      float4* dst = reinterpret_cast<float4*>(xs_l + t * MS_LD + 8 * g);
-      dst[0] = make_float4(xv[p][0], xv[p][1], xv[p][2], xv[p][3]);
-      dst[1] = make_float4(xv[p][4], xv[p][5], xv[p][6], xv[p][7]);
-      if (g == 0) inv_l[t] = part > 0.0f ? 1.0f / sqrtf(part) : 0.0f;
-    }
-  }
-  amax = wave_max(amax);
-  if (lane == 0) amax_l[w] = amax;
-  __syncthreads();
-
-  // column pass: lane (j = lane>>3, dims d0, d0+1); SUM8x over token lanes j
-  {
-    const int j = lane >> 3, d0 = w * 16 + (lane & 7) * 2;
-    float pp0 = 0.0f, pp1 = 0.0f, ph0 = 0.0f, ph1 = 0.0f;
-    for (int t = j; t < cnt; t += 8) {
-      const float2 v = *reinterpret_cast<const float2*>(xs_l + t * MS_LD + d0);
-      const float iv = inv_l[t];
-      pp0 = pp0 + v.x;
-      pp1 = pp1 + v.y;
-      ph0 = ph0 + v.x * iv;
-      ph1 = ph1 + v.y * iv;
-    }
-    pp0 = sum8_tree(pp0);
-    pp1 = sum8_tree(pp1);
-    ph0 = sum8_tree(ph0);
-    ph1 = sum8_tree(ph1);
-    if (j == 0) {
-      float* pd = pooled + ((long long)bh * nb + blk) * 64 + d0;
-      pd[0] = pp0 / (float)cnt;
-      pd[1] = pp1 / (float)cnt;
-      ssum_l[d0] = ph0;
-      ssum_l[d0 + 1] = ph1;
-    }
-  }
-  const float bamax = fmaxf(fmaxf(amax_l[0], amax_l[1]), fmaxf(amax_l[2], amax_l[3]));
-  const float sc = bamax / 127.0f;
-  __syncthreads();
-
-  if (w == 0) {
-    const int gg = lane & 7;
-    float part = 0.0f;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) part = fmaf(ssum_l[8 * gg + c], ssum_l[8 * gg + c], part);
-    part = part + __shfl_xor(part, 1, 64);
-    part = part + __shfl_xor(part, 2, 64);
-    part = part + __shfl_xor(part, 4, 64);
-    if (lane == 0) {
-      const float s = part / ((float)cnt * (float)cnt);
-      sim[(long long)bh * nb + blk] = s > simth[bh % sx.H] ? 1 : 0;
-      scale[(long long)bh * nb + blk] = sc;
-    }
-  }
-
-  // codes of the whole padded block (rows past the sequence end are zero)
-  const float rc = sc != 0.0f ? 1.0f / sc : 0.0f;
-#pragma unroll
-  for (int p = 0; p < PASSES; ++p) {
-    const int t = tr + 32 * p;
-    int c8[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) c8[c] = t < cnt ? quant_i8_rcp(xv[p][c], sc, rc) : 0;
-    *reinterpret_cast<uint2*>(codes + ((long long)bh * nb * BS + base + t) * 64 + 8 * g) = pack_i8x8(c8);
-  }
 }
 
 // Bitonic network of k_ms_map_long over sort positions i = 64E*w + 64e + lane (lane
@@ -169,6 +63,139 @@ __device__ __forceinline__ uint32_t ms_xor_lane(uint32_t a, int lane) {
     const auto r = __builtin_amdgcn_permlane32_swap(a, a, false, false);  // {lo,lo}, {hi,hi}
     return lane < 32 ? (uint32_t)r[1] : (uint32_t)r[0];
   }
+}
+
+// One butterfly step of the token-lane sums: lanes that differ in bit J of the lane id
+// each send the half of their N partial sums that the other keeps, and keep the pairwise
+// sums of their own half (the lane with bit J clear keeps the lower half).
+template <int J, int N>
+__device__ __forceinline__ void ms_halve(float (&v)[N], int lane) {
+  const bool hi = (lane & J) != 0;
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    const float send = hi ? v[i] : v[N / 2 + i];
+    const float keep = hi ? v[N / 2 + i] : v[i];
+    v[i] = keep + __uint_as_float(ms_xor_lane<J>(__float_as_uint(send), lane));
+  }
+}
+
+// Statistics and codes of one block (BS = 128 query or 64 key tokens) by a 256-thread
+// workgroup. Thread (token lane tr = tid>>3, dim group g = tid&7) holds dims 8g..8g+7 of
+// tokens tr + 32p (p < BS/32; zeros past the sequence end) in registers. Per dim, the
+// sums over tokens are: each thread adds its tokens in p order, the 8 token lanes of a
+// wave combine as tree8 (lane bits 3, 4, 5: a reduce-scatter, so each lane ends with 2 of
+// the wave's 128 sums), and the 4 waves as (w0 + w1) + (w2 + w3) through LDS.
+template <int BS>
+__device__ __forceinline__ void ms_stats_block(const uint16_t* __restrict__ x, const Strides& sx, int T,
+                                               const float* __restrict__ km, const float* __restrict__ simth, int nb,
+                                               int blk, int bh, int8_t* __restrict__ codes, float* __restrict__ scale,
+                                               float* __restrict__ pooled, uint8_t* __restrict__ sim,
+                                               float (&part_l)[4][2][64], float (&ssum_l)[64], float (&amax_l)[4]) {
+  constexpr int PASSES = BS / 32;
+  const int tid = threadIdx.x, g = tid & 7, tr = tid >> 3, lane = tid & 63, w = tid >> 6;
+  const int base = blk * BS, cnt = min(BS, T - base);
+  const uint16_t* xb = x + bh_offset(bh, sx);
+
+  float kmv[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) kmv[c] = km ? km[(long long)bh * 64 + 8 * g + c] : 0.0f;
+  float xv[PASSES][8];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int t = tr + 32 * p;
+    uint4 r = make_uint4(0u, 0u, 0u, 0u);
+    if (t < cnt) r = *reinterpret_cast<const uint4*>(xb + (long long)(base + t) * sx.t + 8 * g);
+    unpack_bf16x8(r, xv[p]);
+    if (t < cnt) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) xv[p][c] = xv[p][c] - kmv[c];
+    }
+  }
+  // token norms (fmaf chain per dim group, tree8 across the token's 8 lanes), then the
+  // per-thread sums of x and of x/||x|| in p order
+  float acc[16], amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 16; ++c) acc[c] = 0.0f;
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    float n2 = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      n2 = fmaf(xv[p][c], xv[p][c], n2);
+      amax = fmaxf(amax, fabsf(xv[p][c]));
+    }
+    n2 = n2 + __shfl_xor(n2, 1, 64);
+    n2 = n2 + __shfl_xor(n2, 2, 64);
+    n2 = n2 + __shfl_xor(n2, 4, 64);
+    const float inv = n2 > 0.0f ? 1.0f / sqrtf(n2) : 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      acc[c] = acc[c] + xv[p][c];
+      acc[8 + c] = acc[8 + c] + xv[p][c] * inv;
+    }
+  }
+  ms_halve<8, 16>(acc, lane);
+  ms_halve<16, 8>(reinterpret_cast<float(&)[8]>(acc), lane);
+  ms_halve<32, 4>(reinterpret_cast<float(&)[4]>(acc), lane);
+  {  // acc[0..1]: sums (x if lane bit 3 is clear, else x/||x||) of dims 8g + 4*bit4 + 2*bit5 + {0, 1}
+    const int d = 8 * g + 4 * ((lane >> 4) & 1) + 2 * ((lane >> 5) & 1);
+    *reinterpret_cast<float2*>(&part_l[w][(lane >> 3) & 1][d]) = make_float2(acc[0], acc[1]);
+  }
+  amax = wave_max(amax);
+  if (lane == 0) amax_l[w] = amax;
+  __syncthreads();
+  const float bamax = fmaxf(fmaxf(amax_l[0], amax_l[1]), fmaxf(amax_l[2], amax_l[3]));
+  const float sc = bamax / 127.0f;
+  if (w < 2) {  // wave 0: the pooled mean of dim `lane`; wave 1: the sum of x/||x|| of dim `lane`
+    const float s = (part_l[0][w][lane] + part_l[1][w][lane]) + (part_l[2][w][lane] + part_l[3][w][lane]);
+    if (w == 0) {
+      pooled[((long long)bh * nb + blk) * 64 + lane] = s / (float)cnt;
+    } else {
+      ssum_l[lane] = s;
+      const int gg = lane & 7;
+      float q = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) q = fmaf(ssum_l[8 * gg + c], ssum_l[8 * gg + c], q);
+      q = q + __shfl_xor(q, 1, 64);
+      q = q + __shfl_xor(q, 2, 64);
+      q = q + __shfl_xor(q, 4, 64);
+      if (lane == 0) {
+        const float si = q / ((float)cnt * (float)cnt);
+        sim[(long long)bh * nb + blk] = si > simth[bh % sx.H] ? 1 : 0;
+        scale[(long long)bh * nb + blk] = sc;
+      }
+    }
+  }
+  // codes of the whole padded block (rows past the sequence end are zero)
+  const float rc = sc != 0.0f ? 1.0f / sc : 0.0f;
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int t = tr + 32 * p;
+    int c8[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) c8[c] = t < cnt ? quant_i8_rcp(xv[p][c], sc, rc) : 0;
+    *reinterpret_cast<uint2*>(codes + ((long long)bh * nb * BS + base + t) * 64 + 8 * g) = pack_i8x8(c8);
+  }
+}
+
+// Both operands' blocks in one launch: x = 0..nq-1 are Q's 128-token blocks, nq..nq+nk-1
+// K's 64-token blocks (K minus km when km is given).
+__global__ __launch_bounds__(256) void k_ms_stats(const uint16_t* __restrict__ q, Strides sq, int Tq,
+                                                  const uint16_t* __restrict__ k, Strides sk, int Tk,
+                                                  const float* __restrict__ km, const float* __restrict__ simth,
+                                                  int nq, int nk, int8_t* __restrict__ q_i8,
+                                                  float* __restrict__ q_scale, float* __restrict__ pooled_q,
+                                                  uint8_t* __restrict__ sim_q, int8_t* __restrict__ k_i8,
+                                                  float* __restrict__ k_scale, float* __restrict__ pooled_k,
+                                                  uint8_t* __restrict__ sim_k) {
+  __shared__ __align__(16) float part_l[4][2][64];
+  __shared__ float ssum_l[64];
+  __shared__ float amax_l[4];
+  const int bx = blockIdx.x, bh = blockIdx.y;
+  if (bx < nq)
+    ms_stats_block<128>(q, sq, Tq, nullptr, simth, nq, bx, bh, q_i8, q_scale, pooled_q, sim_q, part_l, ssum_l, amax_l);
+  else
+    ms_stats_block<64>(k, sk, Tk, km, simth, nk, bx - nq, bh, k_i8, k_scale, pooled_k, sim_k, part_l, ssum_l, amax_l);
 }
 
 template <int E, int K, int J>
@@ -670,14 +697,11 @@ RESS_API int ress_meansim_block_map(const void* q, const void* k, const void* km
   const int nq = cdiv(Tq, 128), nk = cdiv(Tk, 64), BH = B * H;
   RESS_REQUIRE(nk <= MS_MAX_NK, "ress_meansim_block_map: %d key blocks exceed %d", nk, MS_MAX_NK);
   const Strides sq{sqB, sqH, sqT, H}, sk{skB, skH, skT, H};
-  hipLaunchKernelGGL(k_ms_stats<128>, dim3(nq, BH), dim3(256), 0, stream, (const uint16_t*)q, sq, Tq,
-                     (const float*)nullptr, (const float*)simthreshd1, nq, (int8_t*)q_i8, (float*)q_scale,
-                     (float*)pooled_q, (uint8_t*)sim_q);
-  RESS_LAUNCHED("k_ms_stats<128>");
-  hipLaunchKernelGGL(k_ms_stats<64>, dim3(nk, BH), dim3(256), 0, stream, (const uint16_t*)k, sk, Tk,
-                     (const float*)km, (const float*)simthreshd1, nk, (int8_t*)k_i8, (float*)k_scale,
+  hipLaunchKernelGGL(k_ms_stats, dim3(nq + nk, BH), dim3(256), 0, stream, (const uint16_t*)q, sq, Tq,
+                     (const uint16_t*)k, sk, Tk, (const float*)km, (const float*)simthreshd1, nq, nk, (int8_t*)q_i8,
+                     (float*)q_scale, (float*)pooled_q, (uint8_t*)sim_q, (int8_t*)k_i8, (float*)k_scale,
                      (float*)pooled_k, (uint8_t*)sim_k);
-  RESS_LAUNCHED("k_ms_stats<64>");
+  RESS_LAUNCHED("k_ms_stats");
   const int n_sink = attention_sink > 0 ? cdiv(attention_sink, 64) : 0;
   const dim3 wgrid(cdiv(nq, 4), BH);
   const float* pq = (const float*)pooled_q;
