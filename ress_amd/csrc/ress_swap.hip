@@ -220,7 +220,14 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
   float* t3 = t2 + 64;
   int* hist = reinterpret_cast<int*>(t0);
   float* outl = t3 + 64;            // STREAM: [NPL][64] candidate products, slot-major
-  const int bh = blockIdx.y;
+  // Workgroup gl = x + gx*y runs on XCD gl % 8. With a multiple of 8 heads, XCD x takes
+  // heads x, x+8, ... whole (every row group of each), so each XCD's L2 holds the V and A
+  // rows of its own heads only: at kb_p = 1369 the 16 heads' V (5.6 MB in fp32) no longer
+  // all pass through every XCD's 4 MB L2.
+  const int gx = gridDim.x, gl = blockIdx.x + gx * blockIdx.y;
+  const bool xmap = (gridDim.y & 7) == 0;
+  const int bh = xmap ? (gl & 7) + 8 * ((gl >> 3) / gx) : blockIdx.y;
+  const int bgrp = xmap ? (gl >> 3) % gx : blockIdx.x;  // this workgroup's row group of head bh
   const bool big = a.flags & RS_BF16, track = a.flags & RS_TRACK_BEST;
   const bool maxim = a.flags & RS_MAXIMIZE, inv = a.flags & RS_INVERT_CUT;
   const bool renorm = !(a.flags & RS_NO_RENORM);
@@ -491,7 +498,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_restore_swap(RsArgs a, int rows_
     return acc;
   };
 
-  const int q_begin = blockIdx.x * rows_per_wg, q_end = min(a.q_blk, (blockIdx.x + 1) * rows_per_wg);
+  const int q_begin = bgrp * rows_per_wg, q_end = min(a.q_blk, (bgrp + 1) * rows_per_wg);
   // STREAM: every wave makes the same number of passes (a wave without a row of its own
   // repeats the last one and writes nothing), so the collective calls line up
   const int passes = STREAM ? (q_end - q_begin + WAVES - 1) / WAVES : 0x7fffffff;
