@@ -418,7 +418,7 @@ def main():
     elems = N * 16 * 64
     prep_bytes = elems * {"f16": 10, "i8x2": 14, "i8": 12}[args.qk_mode]
     peak = mfma_peak(args.qk_mode)
-    ms_meansim, ms_bytes = time_meansim(q, k, reps)
+    ms_meansim, ms_bytes = time_meansim(q, k, 100)
     peaks = measured_peaks(dev)
     qk_meas = peaks["bf16_tflops"] if args.qk_mode == "f16" else peaks["int8_tops"]
     peak_meas = 1.0 / (0.5 / qk_meas + 0.5 / peaks["bf16_tflops"])
