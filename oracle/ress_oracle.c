@@ -777,7 +777,8 @@ int oracle_rs_probe(const float* A, const float* V, const float* M, const uint8_
  *    codes   = the per-block INT8 quantiser (scale = amax/127)
  *  per (head, q-block) row: scores = DOT64(pooled_q, pooled_k)/8 over the similar K
  *  blocks (the others -inf), softmax (ress exp, SUM64 sum), keep the top-n by (p desc,
- *  index asc) with n = #{prefix sums of the sorted p <= cdfthreshd[h]}, then force on
+ *  index asc) with n = #{prefix sums of the sorted p <= cdfthreshd[h]}, the prefix sums
+ *  taken exactly over q = floor(p * 2^50) (uint64) against floor(min(th, 8192) * 2^50), then force on
  *  the non-similar K blocks, every block of a non-similar Q row, and the sinks.
  * q, k: (BH, T, 64) bf16; km [BH][64] or NULL; simth, cdfth [H].
  * Outputs: map [BH][nq][nk] uint8, q_i8 [BH][nq*128][64], q_scale [BH][nq],
@@ -892,12 +893,18 @@ void oracle_meansim_map(const uint16_t* q, const uint16_t* k, const float* km, i
         for (int c = 0; c < nk; ++c) idx[c] = c;
         g_ms_p = sc;
         qsort(idx, nk, sizeof(int), cmp_ms);
-        float cum = 0.0f;
+        /* n = #{k : S_k <= T}: S_k the exact sum of the k largest q = floor(p * 2^50) (uint64),
+           T = floor(min(cdfth, 8192) * 2^50); a negative (or NaN) threshold keeps none */
         int n = 0;
-        for (int i = 0; i < nk; ++i) {
-          cum = cum + sc[idx[i]];
-          if (cum <= cdfth[h]) n = i + 1;
-          else break;
+        const float th = cdfth[h];
+        if (th >= 0.0f) {
+          const uint64_t T = (uint64_t)((double)(th < 8192.0f ? th : 8192.0f) * 1125899906842624.0);
+          uint64_t cum = 0;
+          for (int i = 0; i < nk; ++i) {
+            cum += (uint64_t)((double)sc[idx[i]] * 1125899906842624.0);
+            if (cum <= T) n = i + 1;
+            else break;
+          }
         }
         for (int i = 0; i < n; ++i) row[idx[i]] = 1;
       }

@@ -21,9 +21,12 @@
 //   per (head, q-block) row, over the nk key blocks:
 //     s_c = DOT64(pooled_q, pooled_k[c]) * 0.125 for similar c, -inf otherwise
 //     p_c = ress_expf(s_c - max) / SUM64(e)
-//     n   = #{prefix sums (SEQ) of p in (p desc, index asc) order that are <= cdfthreshd[h]}
-//     map = the first n of that order | non-similar c | every c of a non-similar row
-//           | c < ceil(attention_sink/64)
+//     n   = #{k : S_k <= T}, S_k = the exact (uint64) sum of the k largest q(p_c) =
+//           floor(p_c * 2^50), T = floor(min(cdfthreshd[h], 8192) * 2^50); n = 0 when
+//           cdfthreshd[h] < 0 (the prefix sums of the sorted p, evaluated exactly at 2^-50
+//           resolution, so the count depends on the values alone, not on a summation order)
+//     map = the first n of the (p desc, index asc) order | non-similar c | every c of a
+//           non-similar row | c < ceil(attention_sink/64)
 //
 // k_ms_stats: one 256-thread workgroup per (block, batch*head), Q's and K's blocks in one
 // launch. Thread (token lane tid>>3, dim group tid&7) loads 8 bf16 per token pass (BS/32
@@ -31,24 +34,19 @@
 // lane butterflies, and only the 4 waves' partial sums go through LDS.
 // k_ms_map_wave (nk <= 1024): one wave per (q-block, batch*head) row, four rows per
 // workgroup; details at the kernel.
-// k_ms_map_long (nk > 1024): one 256-thread workgroup per row: the same value sort with
-// the keys in registers (cross-wave stages through LDS), one lane's CDF chain, and the
-// tie rank by a workgroup scan.
+// k_ms_map_long (nk > 1024): one 256-thread workgroup per row.
+// Both find n without sorting: an MSB-first radix descent over the bits of p (four 8-bit
+// digits) with per-digit counts and uint64 sums of q, and the tie rank by index.
 #include "common.h"
 
 namespace {
 
-constexpr int MS_MAX_NK = 6144;    // key blocks per row of the map kernels (<= 32 KiB keys + 24 KiB p in LDS)
+constexpr int MS_MAX_NK = 6144;    // key blocks per row of the map kernels (24 KiB of p in LDS)
 constexpr int MS_CH_LD = 17;       // k_ms_map_long score chunks: 64 columns x 16 dims, odd row stride
-// front LDS region of k_ms_map_long: the NP2 sort keys, or the four waves' score chunks
-__host__ __device__ constexpr size_t ms_long_front_bytes(int np2) {
-  return (size_t)np2 * 4 > 4 * 64 * MS_CH_LD * 4 ? (size_t)np2 * 4 : 4 * 64 * MS_CH_LD * 4;
-}
+constexpr float MS_Q_SCALE = 1125899906842624.0f;  // 2^50: q(p) = floor(p * 2^50)
+// front LDS region of k_ms_map_long: the four waves' score chunks
+constexpr size_t MS_LONG_FRONT_BYTES = 4 * 64 * MS_CH_LD * 4;
 
-// Bitonic network of k_ms_map_long over sort positions i = 64E*w + 64e + lane (lane
-// (w, lane) holds u[e]), stages as compile-time (K, J) so every register index is static:
-// J >= 64E pairs positions of two waves (through LDS), 64 <= J < 64E two registers of a
-// lane, J < 64 two lanes (shuffle).
 // the value of lane ^ J (J < 64): DPP quad permutes for 1 and 2, a bit-mode ds_swizzle
 // (source lane ((l & 31) ^ J) within each 32-lane half) for 4..16, the half swap for 32
 template <int J>
@@ -198,86 +196,155 @@ __global__ __launch_bounds__(256) void k_ms_stats(const uint16_t* __restrict__ q
     ms_stats_block<64>(k, sk, Tk, km, simth, nk, bx - nq, bh, k_i8, k_scale, pooled_k, sim_k, part_l, ssum_l, amax_l);
 }
 
-template <int E, int K, int J>
-__device__ __forceinline__ void ms_bstage(uint32_t (&u)[E], uint32_t* kx, int w, int lane) {
-  constexpr int NW = 64 * E;
-  if constexpr (J >= NW) {
+__device__ __forceinline__ uint32_t ms_wave_min_u32(uint32_t v) {
 #pragma unroll
-    for (int e = 0; e < E; ++e) kx[NW * w + 64 * e + lane] = u[e];
-    __syncthreads();
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const int i = NW * w + 64 * e + lane;
-      const uint32_t b = kx[i ^ J];
-      const bool asc = (i & K) == 0, lower = (i & J) == 0;
-      u[e] = (lower == asc) ? min(u[e], b) : max(u[e], b);
-    }
-    __syncthreads();  // every wave has read before the next exchange overwrites
-  } else if constexpr (J >= 64) {
-    constexpr int EJ = J / 64;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      if (e & EJ) continue;
-      const uint32_t a = u[e], b = u[e | EJ];
-      const bool asc = ((NW * w + 64 * e) & K) == 0;
-      u[e] = asc ? min(a, b) : max(a, b);
-      u[e | EJ] = asc ? max(a, b) : min(a, b);
-    }
-  } else {
-    const bool lower = (lane & J) == 0;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const int i = NW * w + 64 * e + lane;
-      const bool asc = (i & K) == 0;
-      const uint32_t a = u[e];
-      const uint32_t b = ms_xor_lane<J>(a, lane);
-      u[e] = (lower == asc) ? min(a, b) : max(a, b);
-    }
-  }
-}
-template <int E, int K, int J>
-__device__ __forceinline__ void ms_bmerge(uint32_t (&u)[E], uint32_t* kx, int w, int lane) {
-  ms_bstage<E, K, J>(u, kx, w, lane);
-  if constexpr (J > 1) ms_bmerge<E, K, J / 2>(u, kx, w, lane);
-}
-template <int E, int K>
-__device__ __forceinline__ void ms_bsort(uint32_t (&u)[E], uint32_t* kx, int w, int lane) {
-  ms_bmerge<E, K, K / 2>(u, kx, w, lane);
-  if constexpr (K < 256 * E) ms_bsort<E, K * 2>(u, kx, w, lane);
-}
-// The same network over one wave's 64E positions i = 64e + lane (no cross-wave stage).
-template <int E, int K>
-__device__ __forceinline__ void ms_bsort_wave(uint32_t (&u)[E], int lane) {
-  ms_bmerge<E, K, K / 2>(u, nullptr, 0, lane);
-  if constexpr (K < 64 * E) ms_bsort_wave<E, K * 2>(u, lane);
+  for (int off = 32; off > 0; off >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, off, 64));
+  return v;
 }
 
-// One 256-thread workgroup per (head, q-block) row for nk > 1024, E keys per lane
-// (NP2 = 256E sort positions):
+// One digit of the CDF radix descent, by one wave over the 256 bins (hc counts, hs uint64
+// sums of q) of the keys in the current range: bins are taken from the highest down while
+// the running total stays <= T. Returns false if every bin fits (above, n_above then
+// include them all); otherwise the crossing bin with its count and sum, and above /
+// n_above advanced over the bins before it. Every lane gets the same results.
+__device__ __forceinline__ bool ms_cdf_digit(const int* hc, const unsigned long long* hs, unsigned long long T,
+                                             unsigned long long& above, int& n_above, int lane, int& bin,
+                                             int& bcnt, unsigned long long& bsum) {
+  int c4[4];
+  unsigned long long s4[4], ls = 0ull;
+  int lc = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {  // lane l: bins 255-4l down to 252-4l
+    c4[j] = hc[255 - 4 * lane - j];
+    s4[j] = hs[255 - 4 * lane - j];
+    ls += s4[j];
+    lc += c4[j];
+  }
+  unsigned long long in = ls;  // inclusive scan over lanes (lane 0 = highest bins)
+  int inc = lc;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const unsigned long long y = __shfl_up(in, off, 64);
+    const int yc = __shfl_up(inc, off, 64);
+    if (lane >= off) {
+      in += y;
+      inc += yc;
+    }
+  }
+  unsigned long long base = above + (in - ls);
+  int basec = n_above + (inc - lc), jx = 4, cx = 0;
+  unsigned long long sx = 0ull;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (jx == 4) {
+      if (base + s4[j] > T) {
+        jx = j;
+        cx = c4[j];
+        sx = s4[j];
+      } else {
+        base += s4[j];
+        basec += c4[j];
+      }
+    }
+  }
+  const unsigned long long has = __ballot(jx < 4);
+  if (has == 0ull) {
+    above = __shfl(base, 63, 64);
+    n_above = __shfl(basec, 63, 64);
+    return false;
+  }
+  const int src = __ffsll((long long)has) - 1;
+  bin = 255 - 4 * src - __shfl(jx, src, 64);
+  above = __shfl(base, src, 64);
+  n_above = __shfl(basec, src, 64);
+  bcnt = __shfl(cx, src, 64);
+  bsum = __shfl(sx, src, 64);
+  return true;
+}
+
+// The row's CDF cut by one wave: key[e] = bits of p at column 64e + lane (p >= +0, so the
+// bits order like the values). Returns n and the n-th largest key (vbits, for n > 0).
+// hc / hs: this wave's 256-bin LDS histogram.
+template <int E>
+__device__ __forceinline__ int ms_cdf_wave(const uint32_t (&key)[E], int nk, float th, int lane, int* hc,
+                                           unsigned long long* hs, uint32_t& vbits) {
+  vbits = 0u;
+  if (!(th >= 0.0f)) return 0;
+  const unsigned long long T = (unsigned long long)(fminf(th, 8192.0f) * MS_Q_SCALE);
+  unsigned long long q[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    q[e] = 64 * e + lane < nk ? (unsigned long long)(__uint_as_float(key[e]) * MS_Q_SCALE) : 0ull;
+  uint32_t prefix = 0u, pmask = 0u;
+  unsigned long long above = 0ull, bsum = 0ull;
+  int n_above = 0, bcnt = 0;
+  bool crossed = true;
+#pragma unroll
+  for (int level = 0; level < 4; ++level) {
+    const int shift = 24 - 8 * level;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      hc[64 * j + lane] = 0;
+      hs[64 * j + lane] = 0ull;
+    }
+    asm volatile("" ::: "memory");  // this wave's LDS accesses stay in program order
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      if (64 * e + lane < nk && (key[e] & pmask) == prefix) {
+        const int b = (key[e] >> shift) & 255;
+        atomicAdd(&hc[b], 1);
+        atomicAdd(&hs[b], q[e]);
+      }
+    }
+    asm volatile("" ::: "memory");
+    int bin = 0;
+    if (!ms_cdf_digit(hc, hs, T, above, n_above, lane, bin, bcnt, bsum)) {
+      crossed = false;
+      break;
+    }
+    prefix |= (uint32_t)bin << shift;
+    pmask |= 0xFFu << shift;
+    asm volatile("" ::: "memory");
+  }
+  // every key fits: n = all of them, the n-th largest the smallest; otherwise the crossing
+  // key's ties (equal p, equal q) fit floor((T - above) / q) times
+  const int m = crossed ? (int)((T - above) / (bsum / (unsigned long long)bcnt)) : 0;
+  const int n = n_above + m;
+  if (crossed && m > 0) {
+    vbits = prefix;
+  } else {
+    uint32_t mn = 0xFFFFFFFFu;
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      if (64 * e + lane < nk && (!crossed || key[e] > prefix)) mn = min(mn, key[e]);
+    vbits = ms_wave_min_u32(mn);
+  }
+  return n;
+}
+
+// One 256-thread workgroup per (head, q-block) row for nk > 1024:
 //  scores  wave w scores columns c = 256i + 64w + lane, each lane reading its column's
 //          pooled K (64 floats) straight from L2 (DOT64 chain, pooled Q in registers).
-//  sort    lane (w, lane) holds sort positions i = 64Ew + 64e + lane in registers; a
-//          bitonic network over i: partners 64 positions or more apart and in the same
-//          wave are another register of the lane, closer ones one shuffle away, and only
-//          the 3 stages whose partner is in another wave go through LDS.
-//  prefix  the sequential CDF chain over the sorted values in one lane, as in k_ms_map_wave.
+//  cut     the CDF radix descent over p in LDS (column order): a workgroup histogram per
+//          digit, scanned by wave 0 (ms_cdf_digit).
 //  select  contiguous column chunks per thread and a workgroup scan for the tie rank.
-template <int E>
 __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ pooled_q,
                                                      const float* __restrict__ pooled_k,
                                                      const uint8_t* __restrict__ sim_q,
                                                      const uint8_t* __restrict__ sim_k, int H, int nq, int nk,
                                                      const float* __restrict__ cdfth, int n_sink,
                                                      uint8_t* __restrict__ map) {
-  constexpr int NW = 64 * E, NP2 = 4 * NW;
   extern __shared__ __align__(16) unsigned char ms_dyn[];
-  // front region (ms_long_front_bytes): the waves' score chunks, later the sort exchange
-  uint32_t* kx = reinterpret_cast<uint32_t*>(ms_dyn);  // [NP2] exchange, then the sorted keys
+  // front region (MS_LONG_FRONT_BYTES): the waves' score chunks
   float* scw = reinterpret_cast<float*>(ms_dyn) + (threadIdx.x >> 6) * (64 * MS_CH_LD);  // [64][MS_CH_LD]
-  float* p = reinterpret_cast<float*>(ms_dyn + ms_long_front_bytes(NP2));  // [nk] scores -> p, column order
+  float* p = reinterpret_cast<float*>(ms_dyn + MS_LONG_FRONT_BYTES);  // [nk] scores -> p, column order
   __shared__ float red[4];
   __shared__ int ired[4];
-  __shared__ int n_sel;
+  __shared__ int hc[256];
+  __shared__ unsigned long long hs[256];
+  __shared__ unsigned long long cut_l[2];  // the digit's result: above, then bsum
+  __shared__ int cut_i[4];                 // crossed, bin, n_above, bcnt
+  __shared__ uint32_t vmin_l;
   const int r = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   uint8_t* row = map + ((long long)bh * nq + r) * nk;
   const uint8_t* sk = sim_k + (long long)bh * nk;
@@ -363,70 +430,69 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
   const float tot = red[0];
   for (int c = tid; c < nk; c += 256) p[c] = p[c] / tot;
   __syncthreads();
-  // every p is >= +0, so its bit pattern orders like the value; only the values are
-  // sorted (equal values are interchangeable in the prefix sums). Ascending keys ~bits(p):
-  // descending p, padding (~0) last.
-  uint32_t u[E];
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int i = NW * w + 64 * e + lane;
-    u[e] = i < nk ? ~__float_as_uint(p[i]) : ~0u;
-  }
-  ms_bsort<E, 2>(u, kx, w, lane);
-#pragma unroll
-  for (int e = 0; e < E; ++e) kx[NW * w + 64 * e + lane] = ~u[e];  // the sorted p (descending), as bits
-  __syncthreads();
-  if (tid == 0) {  // n = #{sequential prefix sums of the sorted p that are <= th}
-    // p >= 0, so the sums only grow: n is the position of the first sum above th (nk if
-    // none). One add per key; the batch that crosses th is searched once; the next 16
-    // keys are read while a batch is summed. Keys past nk are p = 0 (padding).
-    const float th = cdfth[bh % H];
-    const float4* v4 = reinterpret_cast<const float4*>(kx);
-    float cum = 0.0f;
-    int n = nk;
-    // 16 values a batch, the next two batches' reads in flight (v4[4b .. 4b+3] is batch b;
-    // batches up to NP2/16 exist, NP2 >= 2048)
-    float4 x[4], y[4], z[4];
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      x[g] = v4[g];
-      y[g] = v4[4 + g];
+  // the CDF cut: p >= +0, so its bits order like the value (ms_cdf_wave has the steps)
+  int n = 0;
+  uint32_t vbits = 0u;
+  const float th = cdfth[bh % H];
+  if (th >= 0.0f) {
+    const unsigned long long T = (unsigned long long)(fminf(th, 8192.0f) * MS_Q_SCALE);
+    uint32_t prefix = 0u, pmask = 0u;
+    unsigned long long above = 0ull, bsum = 0ull;
+    int n_above = 0, bcnt = 0;
+    bool crossed = true;
+    for (int level = 0; level < 4; ++level) {
+      const int shift = 24 - 8 * level;
+      hc[tid] = 0;
+      hs[tid] = 0ull;
+      __syncthreads();
+      for (int c = tid; c < nk; c += 256) {
+        const uint32_t b = __float_as_uint(p[c]);
+        if ((b & pmask) == prefix) {
+          atomicAdd(&hc[(b >> shift) & 255], 1);
+          atomicAdd(&hs[(b >> shift) & 255], (unsigned long long)(p[c] * MS_Q_SCALE));
+        }
+      }
+      __syncthreads();
+      if (w == 0) {
+        int bin = 0;
+        const bool x = ms_cdf_digit(hc, hs, T, above, n_above, lane, bin, bcnt, bsum);
+        if (lane == 0) {
+          cut_i[0] = x;
+          cut_i[1] = bin;
+          cut_i[2] = n_above;
+          cut_i[3] = bcnt;
+          cut_l[0] = above;
+          cut_l[1] = bsum;
+        }
+      }
+      __syncthreads();
+      crossed = cut_i[0] != 0;
+      n_above = cut_i[2];
+      bcnt = cut_i[3];
+      above = cut_l[0];
+      bsum = cut_l[1];
+      if (!crossed) break;
+      prefix |= (uint32_t)cut_i[1] << shift;
+      pmask |= 0xFFu << shift;
     }
-    for (int i = 0; i < nk; i += 16) {
-      if (i + 32 < nk) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) z[g] = v4[(i + 32) / 4 + g];  // i + 48 <= NP2
+    const int m = crossed ? (int)((T - above) / (bsum / (unsigned long long)bcnt)) : 0;
+    n = n_above + m;
+    if (crossed && m > 0) {
+      vbits = prefix;
+    } else {  // the smallest key (every key fits) or the smallest above the crossing key
+      if (tid == 0) vmin_l = 0xFFFFFFFFu;
+      uint32_t mn = 0xFFFFFFFFu;
+      for (int c = tid; c < nk; c += 256) {
+        const uint32_t b = __float_as_uint(p[c]);
+        if (!crossed || b > prefix) mn = min(mn, b);
       }
-      float cv[16];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        cum = cum + x[g].x;
-        cv[4 * g] = cum;
-        cum = cum + x[g].y;
-        cv[4 * g + 1] = cum;
-        cum = cum + x[g].z;
-        cv[4 * g + 2] = cum;
-        cum = cum + x[g].w;
-        cv[4 * g + 3] = cum;
-      }
-      if (!(cum <= th)) {
-        int first = 15;
-#pragma unroll
-        for (int m = 14; m >= 0; --m) first = cv[m] <= th ? first : m;
-        n = min(nk, i + first);
-        break;
-      }
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        x[g] = y[g];
-        y[g] = z[g];
-      }
+      mn = ms_wave_min_u32(mn);
+      __syncthreads();
+      if (lane == 0) atomicMin(&vmin_l, mn);
+      __syncthreads();
+      vbits = vmin_l;
     }
-    n_sel = n;
   }
-  __syncthreads();
-  const int n = n_sel;
-  const uint32_t vbits = n > 0 ? kx[n - 1] : 0u;  // the n-th largest p
   // contiguous column chunks: p > v is kept; of the p == v columns, the lowest-indexed
   // n - #{p > v} (an exclusive scan of the per-chunk counts gives each one's rank)
   const int chunk = cdiv(nk, 256), c0 = min(nk, tid * chunk), c1 = min(nk, c0 + chunk);
@@ -472,12 +538,8 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
 // rows of one head per workgroup.
 //  scores  pooled K goes through LDS in coalesced 64-block tiles that the four rows
 //          share; lane l keeps the scores of columns c = 64e + l (also the SUM64 order).
-//  sort    only the probabilities are sorted (equal values are interchangeable in the
-//          prefix sums): a bitonic network over 32-bit keys in registers, partners 64
-//          positions or more apart in the same lane, closer ones one shuffle away.
-//  prefix  the sequential CDF chain of each row runs in one lane of wave 0 over the
-//          sorted values in LDS (the four rows' chains side by side) up to the batch of 16
-//          where it first exceeds th; that position is the row's count.
+//  cut     n and the n-th largest p by the CDF radix descent (ms_cdf_wave), each wave on
+//          its own LDS histogram: no sort, no cross-wave step after the scores.
 //  select  with v the n-th largest probability: every column with p > v, and of those
 //          with p == v the lowest-indexed ones up to n (a ballot prefix count).
 template <int E>
@@ -487,12 +549,11 @@ __global__ __launch_bounds__(256) void k_ms_map_wave(const float* __restrict__ p
                                                      const uint8_t* __restrict__ sim_k, int H, int nq, int nk,
                                                      const float* __restrict__ cdfth, int n_sink,
                                                      uint8_t* __restrict__ map) {
-  constexpr int NP = 64 * E, LDK = 65, LDS_ROW = NP + 4;  // LDK / LDS_ROW: padded strides
+  constexpr int LDK = 65;  // padded stride of the pooled-K tile
   __shared__ float pk_l[64 * LDK];
   __shared__ __align__(16) float pq_l[4][64];
-  __shared__ __align__(16) float sv_l[4][LDS_ROW];
-  __shared__ int go_l[4];
-  __shared__ int n_l[4];
+  __shared__ int hc_l[4][256];                 // per-wave CDF digit histograms
+  __shared__ unsigned long long hs_l[4][256];
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int bh = blockIdx.y, r = blockIdx.x * 4 + w;
   const long long row_id = (long long)bh * nq + r;
@@ -563,97 +624,26 @@ __global__ __launch_bounds__(256) void k_ms_map_wave(const float* __restrict__ p
   // the CDF path runs for a similar row with at least one similar key block; otherwise
   // every block of the row is on
   const bool go = active && mx > -__builtin_huge_valf();
-  uint32_t pb[E];  // bits of p at the lane's own columns (p >= +0: bits order like values)
-#pragma unroll
-  for (int e = 0; e < E; ++e) pb[e] = 0;
-  if (go) {
-    float part = 0.0f;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      s[e] = simc[e] ? ress_expf(s[e] - mx) : 0.0f;
-      if (64 * e + lane < nk) part = part + s[e];
-    }
-    const float tot = sum64_tree(part);
-    uint32_t u[E];  // ascending sort keys ~bits(p): descending p; padding (~0) last
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      pb[e] = __float_as_uint(s[e] / tot);
-      u[e] = 64 * e + lane < nk ? ~pb[e] : ~0u;
-    }
-    // bitonic network over positions 64e + lane: partners 64 or more apart are another
-    // register of the lane, closer ones one DPP / swizzle / half-swap permute away
-    ms_bsort_wave<E, 2>(u, lane);
-#pragma unroll
-    for (int e = 0; e < E; ++e) sv_l[w][64 * e + lane] = __uint_as_float(~u[e]);
-    if (lane == 0) go_l[w] = 1;
-    // s[] now holds the sorted values (position 64e + lane): the chain overwrites sv_l
-#pragma unroll
-    for (int e = 0; e < E; ++e) s[e] = __uint_as_float(~u[e]);
-  } else if (lane == 0) {
-    go_l[w] = 0;
-  }
-  __syncthreads();
-  if (w == 0 && lane < 4 && go_l[lane]) {  // the four rows' sequential chains, side by side
-    // n = #{sequential prefix sums of the sorted p that are <= th}; p >= 0, so the sums
-    // only grow and n is the position of the first sum above th (nk if none): the chain
-    // stops at the batch that crosses th
-    const float th = cdfth[bh % H];
-    const float* v = sv_l[lane];
-    float cum = 0.0f;
-    int n = nk, i = 0;
-    bool crossed = false;
-    for (; i + 16 <= nk; i += 16) {  // 16 values per LDS round trip
-      float4 x[4];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) x[g] = reinterpret_cast<const float4*>(v + i)[g];
-      float cv[16];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        cum = cum + x[g].x;
-        cv[4 * g] = cum;
-        cum = cum + x[g].y;
-        cv[4 * g + 1] = cum;
-        cum = cum + x[g].z;
-        cv[4 * g + 2] = cum;
-        cum = cum + x[g].w;
-        cv[4 * g + 3] = cum;
-      }
-      if (!(cum <= th)) {
-        int first = 15;
-#pragma unroll
-        for (int m = 14; m >= 0; --m) first = cv[m] <= th ? first : m;
-        n = i + first;
-        crossed = true;
-        break;
-      }
-    }
-    if (!crossed) {
-      for (; i < nk; ++i) {
-        cum = cum + v[i];
-        if (!(cum <= th)) {
-          n = i;
-          break;
-        }
-      }
-    }
-    n_l[lane] = n;
-  }
-  __syncthreads();
   if (!in_range) return;
   uint8_t* row = map + row_id * nk;
   if (!go) {
     for (int c = lane; c < nk; c += 64) row[c] = 1;
     return;
   }
-  const int n = n_l[w];
-  uint32_t vbits = 0;
-  int n_gt = 0;
-  if (n > 0) {  // v = the n-th largest p (sorted position n-1; s[] holds the sorted values)
-    const int pos = n - 1, slot = pos >> 6;
-    float sel = 0.0f;
+  float part = 0.0f;
 #pragma unroll
-    for (int e = 0; e < E; ++e) sel = e == slot ? s[e] : sel;
-    vbits = __float_as_uint(__shfl(sel, pos & 63, 64));
+  for (int e = 0; e < E; ++e) {
+    s[e] = simc[e] ? ress_expf(s[e] - mx) : 0.0f;
+    if (64 * e + lane < nk) part = part + s[e];
+  }
+  const float tot = sum64_tree(part);
+  uint32_t pb[E];  // bits of p at the lane's own columns (p >= +0: bits order like values)
+#pragma unroll
+  for (int e = 0; e < E; ++e) pb[e] = __float_as_uint(s[e] / tot);
+  uint32_t vbits;
+  const int n = ms_cdf_wave<E>(pb, nk, cdfth[bh % H], lane, hc_l[w], hs_l[w], vbits);
+  int n_gt = 0;
+  if (n > 0) {
     int gt = 0;
 #pragma unroll
     for (int e = 0; e < E; ++e) gt += (64 * e + lane < nk && pb[e] > vbits) ? 1 : 0;
@@ -720,16 +710,8 @@ RESS_API int ress_meansim_block_map(const void* q, const void* k, const void* km
   } else if (nk <= 1024) {
     hipLaunchKernelGGL(k_ms_map_wave<16>, wgrid, dim3(256), 0, stream, pq, pk, sq8, sk8, H, nq, nk, cd, n_sink, m8);
   } else {
-    const size_t lds4 = (size_t)nk * 4;
-    if (nk <= 2048)
-      hipLaunchKernelGGL(k_ms_map_long<8>, dim3(nq, BH), dim3(256), ms_long_front_bytes(2048) + lds4, stream, pq, pk, sq8, sk8, H, nq,
-                         nk, cd, n_sink, m8);
-    else if (nk <= 4096)
-      hipLaunchKernelGGL(k_ms_map_long<16>, dim3(nq, BH), dim3(256), ms_long_front_bytes(4096) + lds4, stream, pq, pk, sq8, sk8, H, nq,
-                         nk, cd, n_sink, m8);
-    else
-      hipLaunchKernelGGL(k_ms_map_long<32>, dim3(nq, BH), dim3(256), ms_long_front_bytes(8192) + lds4, stream, pq, pk, sq8, sk8, H, nq,
-                         nk, cd, n_sink, m8);
+    hipLaunchKernelGGL(k_ms_map_long, dim3(nq, BH), dim3(256), MS_LONG_FRONT_BYTES + (size_t)nk * 4, stream, pq, pk, sq8,
+                       sk8, H, nq, nk, cd, n_sink, m8);
   }
   RESS_LAUNCHED("k_ms_map");
   return 0;
