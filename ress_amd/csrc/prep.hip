@@ -34,11 +34,11 @@ __device__ __forceinline__ void store_codes(const float x[8], float scale, int8_
 // Q blocks: kernel q-blocks 0..q_blk_p-1 hold patch queries, q_blk_p.. the
 // special queries. Writes q_i8 [BH][q_blk_total][128][64], q_scale [BH][q_blk_total]
 // and, for patch blocks, pooled_q [BH][q_blk_p][64].
-__global__ __launch_bounds__(64) void k_prep_q(const uint16_t* __restrict__ q, Strides sq, TokenMap m,
-                                               int q_blk_p, int q_blk_total, int8_t* __restrict__ q_i8,
-                                               int8_t* __restrict__ q_lo, float* __restrict__ q_scale,
-                                               float* __restrict__ pooled_q) {
-  const int qb = blockIdx.x, bh = blockIdx.y, lane = threadIdx.x;
+__device__ __forceinline__ void prep_q_block(int qb, int bh, const uint16_t* __restrict__ q, const Strides& sq,
+                                             const TokenMap& m, int q_blk_p, int q_blk_total,
+                                             int8_t* __restrict__ q_i8, int8_t* __restrict__ q_lo,
+                                             float* __restrict__ q_scale, float* __restrict__ pooled_q) {
+  const int lane = threadIdx.x;
   const int j = lane >> 3, dg = lane & 7;
   const bool special = qb >= q_blk_p;
   const int base = special ? (qb - q_blk_p) * 128 : qb * 128;
@@ -86,6 +86,12 @@ __global__ __launch_bounds__(64) void k_prep_q(const uint16_t* __restrict__ q, S
     store_codes(x, scale, q_i8 + off + r, q_lo ? q_lo + off + r : nullptr);
   }
 }
+__global__ __launch_bounds__(64) void k_prep_q(const uint16_t* __restrict__ q, Strides sq, TokenMap m,
+                                               int q_blk_p, int q_blk_total, int8_t* __restrict__ q_i8,
+                                               int8_t* __restrict__ q_lo, float* __restrict__ q_scale,
+                                               float* __restrict__ pooled_q) {
+  prep_q_block(blockIdx.x, blockIdx.y, q, sq, m, q_blk_p, q_blk_total, q_i8, q_lo, q_scale, pooled_q);
+}
 
 // ----------------------------------------------------------------------------
 // K/V blocks over the kernel key grid (patch keys then special keys).
@@ -99,13 +105,14 @@ __global__ __launch_bounds__(64) void k_prep_q(const uint16_t* __restrict__ q, S
 //  v_pack [BH][kb_tot][64 dims][64 keys]  bf16, keys permuted inside every group of
 //         16 as 0-3,8-11,4-7,12-15 so that one 16-byte read per lane is an MFMA
 //         operand; keys past the sequence end are zero.
-__global__ __launch_bounds__(64) void k_prep_kv(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-                                                Strides sk, Strides sv, TokenMap m, int Tk, int kb_tot, int kb_p,
-                                                float* __restrict__ ksum, float* __restrict__ pooled_k,
-                                                float* __restrict__ pooled_v, uint16_t* __restrict__ v_pack,
-                                                uint16_t* __restrict__ k_pack, float* __restrict__ k_norm) {
-  __shared__ uint16_t vt[64 * 64];
-  const int kb = blockIdx.x, bh = blockIdx.y, lane = threadIdx.x;
+__device__ __forceinline__ void prep_kv_block(int kb, int bh, const uint16_t* __restrict__ k,
+                                              const uint16_t* __restrict__ v, const Strides& sk, const Strides& sv,
+                                              const TokenMap& m, int Tk, int kb_tot, int kb_p,
+                                              float* __restrict__ ksum, float* __restrict__ pooled_k,
+                                              float* __restrict__ pooled_v, uint16_t* __restrict__ v_pack,
+                                              uint16_t* __restrict__ k_pack, float* __restrict__ k_norm,
+                                              uint16_t* __restrict__ vt) {
+  const int lane = threadIdx.x;
   const int j = lane >> 3, dg = lane & 7;
   const int base = kb * 64;
   const int cnt = min(64, Tk - base);
@@ -205,6 +212,33 @@ __global__ __launch_bounds__(64) void k_prep_kv(const uint16_t* __restrict__ k, 
   const uint4* s4 = reinterpret_cast<const uint4*>(vt);
 #pragma unroll
   for (int i = 0; i < 8; ++i) dst[i * 64 + lane] = s4[i * 64 + lane];
+}
+__global__ __launch_bounds__(64) void k_prep_kv(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                                                Strides sk, Strides sv, TokenMap m, int Tk, int kb_tot, int kb_p,
+                                                float* __restrict__ ksum, float* __restrict__ pooled_k,
+                                                float* __restrict__ pooled_v, uint16_t* __restrict__ v_pack,
+                                                uint16_t* __restrict__ k_pack, float* __restrict__ k_norm) {
+  __shared__ uint16_t vt[64 * 64];
+  prep_kv_block(blockIdx.x, blockIdx.y, k, v, sk, sv, m, Tk, kb_tot, kb_p, ksum, pooled_k, pooled_v, v_pack, k_pack,
+                k_norm, vt);
+}
+
+// The layer's Q blocks and K/V blocks in one launch (they are independent): x < nqb is Q
+// block x, the rest K/V block x - nqb.
+__global__ __launch_bounds__(64) void k_prep_qkv(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                                 const uint16_t* __restrict__ v, Strides sq, Strides sk, Strides sv,
+                                                 TokenMap m, int nqb, int q_blk_p, int q_blk_total, int Tk, int kb_tot,
+                                                 int kb_p, int8_t* __restrict__ q_i8, int8_t* __restrict__ q_lo,
+                                                 float* __restrict__ q_scale, float* __restrict__ pooled_q,
+                                                 float* __restrict__ ksum, float* __restrict__ pooled_k,
+                                                 float* __restrict__ pooled_v, uint16_t* __restrict__ v_pack,
+                                                 uint16_t* __restrict__ k_pack, float* __restrict__ k_norm) {
+  __shared__ uint16_t vt[64 * 64];
+  if ((int)blockIdx.x < nqb)
+    prep_q_block(blockIdx.x, blockIdx.y, q, sq, m, q_blk_p, q_blk_total, q_i8, q_lo, q_scale, pooled_q);
+  else
+    prep_kv_block(blockIdx.x - nqb, blockIdx.y, k, v, sk, sv, m, Tk, kb_tot, kb_p, ksum, pooled_k, pooled_v, v_pack,
+                  k_pack, k_norm, vt);
 }
 
 // key mean over all Tk keys: km[d] = SEQ-sum of the block sums / Tk. The loads are
@@ -317,15 +351,14 @@ RESS_API int ress_prep_qkv(const void* q, const void* k, const void* v, int B, i
   const int q_blk_p = cdiv(m.T_p, 128), q_blk_s = cdiv(m.T_s, 128);
   const int kb_tot = cdiv(Tk, 64), kb_p = cdiv(m.T_p, 64);
   Strides sq{sqB, sqH, sqT, H}, sk{skB, skH, skT, H}, sv{svB, svH, svT, H};
-  // without codes only the patch blocks (the pooled ones) have work
-  hipLaunchKernelGGL(k_prep_q, dim3(quant ? q_blk_p + q_blk_s : q_blk_p, BH), dim3(64), 0, stream, (const uint16_t*)q,
-                     sq, m, q_blk_p, q_blk_p + q_blk_s, (int8_t*)q_i8, (int8_t*)q_lo, (float*)q_scale,
-                     (float*)pooled_q);
-  RESS_LAUNCHED("k_prep_q");
-  hipLaunchKernelGGL(k_prep_kv, dim3(kb_tot, BH), dim3(64), 0, stream, (const uint16_t*)k, (const uint16_t*)v, sk, sv,
-                     m, Tk, kb_tot, kb_p, (float*)(quant ? ksum : nullptr), (float*)pooled_k, (float*)pooled_v,
-                     (uint16_t*)v_pack, (uint16_t*)k_pack, (float*)(quant ? nullptr : k_scale));
-  RESS_LAUNCHED("k_prep_kv");
+  // without codes only the patch blocks (the pooled ones) have Q work
+  const int nqb = quant ? q_blk_p + q_blk_s : q_blk_p;
+  hipLaunchKernelGGL(k_prep_qkv, dim3(nqb + kb_tot, BH), dim3(64), 0, stream, (const uint16_t*)q, (const uint16_t*)k,
+                     (const uint16_t*)v, sq, sk, sv, m, nqb, q_blk_p, q_blk_p + q_blk_s, Tk, kb_tot, kb_p,
+                     (int8_t*)q_i8, (int8_t*)q_lo, (float*)q_scale, (float*)pooled_q,
+                     (float*)(quant ? ksum : nullptr), (float*)pooled_k, (float*)pooled_v, (uint16_t*)v_pack,
+                     (uint16_t*)k_pack, (float*)(quant ? nullptr : k_scale));
+  RESS_LAUNCHED("k_prep_qkv");
   if (!quant) return 0;
   hipLaunchKernelGGL(k_key_mean, dim3(BH), dim3(64), 0, stream, (const float*)ksum, kb_tot, Tk, (float*)km);
   RESS_LAUNCHED("k_key_mean");
