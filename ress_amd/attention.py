@@ -73,8 +73,11 @@ class LayerResult:
     lut: torch.Tensor = None
     nvalid: torch.Tensor = None
     blocks: kernels.Blocks = None
-    # device-side budget status: number of HeSS columns that did not converge (0-dim int32)
+    # device-side budget status: the number of HeSS columns that did not converge (0-dim
+    # int32), or the per-column iteration counts it is taken from (negative = not converged;
+    # counted at the sync, so the layer step launches no reduction for it)
     unconverged: torch.Tensor = None
+    budget_iters: torch.Tensor = None
     max_iters: int = None
     # device-side 16-bit operand status (kernels.sparse_attention's ress_attn_status), or None
     attn_status: torch.Tensor = None
@@ -96,6 +99,8 @@ class LayerResult:
         vals = []
         if self.unconverged is not None:
             vals.append(self.unconverged.float().reshape(()))
+        if self.budget_iters is not None:
+            vals.append((self.budget_iters < 0).sum().float())
         if self.attn_status is not None:
             vals.append(self.attn_status[0].float())
         return vals
@@ -103,6 +108,9 @@ class LayerResult:
     def _raise_status(self, got):
         i = 0
         if self.unconverged is not None:
+            self._raise_unconverged(got[i])
+            i += 1
+        if self.budget_iters is not None:
             self._raise_unconverged(got[i])
             i += 1
         if self.attn_status is not None:
@@ -230,7 +238,7 @@ def sparse_global_attention(q, k, v, grid, *, num_to_select=None, budget_fn=None
     v_bar_full = blocks.pooled_v.view(grid.B, grid.H, grid.kb_p, 64)
     counts = None
     final_map = None
-    unconverged, max_iters = None, None
+    budget_iters, max_iters = None, None
     if joint_select_fn is not None:
         final_map = joint_select_fn(attn_cond, v_bar_full[..., :grid.n_cand, :], grid.sink_blocks)
         if sink_lead and not protect_own_frame:
@@ -247,7 +255,7 @@ def sparse_global_attention(q, k, v, grid, *, num_to_select=None, budget_fn=None
         if counts is None:
             raise AssertionError("num_to_select (or budget_fn/perhead_budget_fn) required unless dense=True "
                                  "or joint_select_fn is given")
-        unconverged = getattr(counts, "ress_unconverged", None)
+        budget_iters = getattr(counts, "ress_iters", None)
         max_iters = getattr(counts, "ress_max_iters", None)
         if not torch.is_tensor(counts):
             counts = torch.full((grid.B, grid.H, grid.q_blk_p), int(counts), dtype=torch.int32, device=q.device)
@@ -263,7 +271,7 @@ def sparse_global_attention(q, k, v, grid, *, num_to_select=None, budget_fn=None
             final_map[..., :sink_lead] = True
         lut, nvalid = kernels.lut_from_map(final_map, grid)
     o = kernels.sparse_attention(blocks, lut, nvalid, out=out, out_dtype=out_dtype)
-    res = LayerResult(out=o, final_map=final_map, unconverged=unconverged, max_iters=max_iters,
+    res = LayerResult(out=o, final_map=final_map, budget_iters=budget_iters, max_iters=max_iters,
                       attn_status=getattr(o, "ress_attn_status", None))
     if keep_intermediates:
         res.attn_full, res.attn_cond, res.v_bar_full = attn_full, attn_cond, v_bar_full
@@ -323,8 +331,8 @@ def ress_attention_forward(self, x, pos, num_to_select=None, budget_fn=None, per
         x_out = res.out
         # the forward does not synchronise: the layer's device-side status (HeSS convergence,
         # 16-bit operand range) stays on the module for check_layers
-        self._ress_status = LayerResult(out=None, unconverged=res.unconverged, max_iters=res.max_iters,
-                                        attn_status=res.attn_status)
+        self._ress_status = LayerResult(out=None, unconverged=res.unconverged, budget_iters=res.budget_iters,
+                                        max_iters=res.max_iters, attn_status=res.attn_status)
         sparsity = res.sparsity() if aux_store is not None else None
     if aux_store is not None:
         if aux_full and res is not None:
@@ -348,15 +356,15 @@ def check_layers(model_or_modules):
     fp16's range. Takes a model (every submodule) or an iterable of modules."""
     mods = model_or_modules.modules() if hasattr(model_or_modules, "modules") else model_or_modules
     results = [m._ress_status for m in mods if getattr(m, "_ress_status", None) is not None]
-    vals = [v for r in results for v in r._status_values()]
+    per = [r._status_values() for r in results]
+    vals = [v for vs in per for v in vs]
     if not vals:
         return
     got = torch.stack(vals).tolist()
     i = 0
-    for r in results:
-        n = len(r._status_values())
-        r._raise_status(got[i:i + n])
-        i += n
+    for r, vs in zip(results, per):
+        r._raise_status(got[i:i + len(vs)])
+        i += len(vs)
 
 
 def _device_patch_order(module, order, grid, device):

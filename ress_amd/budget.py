@@ -123,9 +123,10 @@ class HessBudget:
         """Counts (B, nh, q_blk) int32 on the device, without a host sync. The reference
         raises RuntimeError when the redistribution does not converge within max_iters
         (_proportional.py:112-113), which costs it a sync per iteration. Here the kernel
-        reports each column's iteration count on the device and the returned tensor carries
-        the number of non-converged columns as `ress_unconverged` (0-dim int32); the layer
-        raises at its next host sync (LayerResult.check / .sparsity)."""
+        reports each column's iteration count on the device (negative where it did not
+        converge) and the returned tensor carries those counts as `ress_iters` ((B, q_blk)
+        int32); the layer counts them and raises at its next host sync (LayerResult.check /
+        .sparsity), so the budget itself launches nothing beyond its two kernels."""
         baseline = compute_baseline_num_to_select(attn_pooled, sparse_ratio, cdf_threshold)
         max_val = attn_pooled.shape[-1]
         nts = baseline if baseline.dim() == 3 else baseline.unsqueeze(0)
@@ -133,6 +134,6 @@ class HessBudget:
         out = kernels.head_budget(nts, self._scores_norm(layer_idx, attn_pooled.device), beta, max_val,
                                   max_iters=self.max_iters, iters_out=iters)
         out = out if baseline.dim() == 3 else out.squeeze(0)
-        out.ress_unconverged = (iters < 0).sum(dtype=torch.int32)
+        out.ress_iters = iters
         out.ress_max_iters = self.max_iters
         return out

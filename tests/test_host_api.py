@@ -309,6 +309,23 @@ def test_layer_result_raises_on_unconverged_budget():
     assert attention.LayerResult(out=None, final_map=fmap).sparsity() == 0.0
 
 
+def test_layer_result_counts_unconverged_columns_at_the_sync():
+    # HeSS budgets hand over per-column iteration counts (negative = not converged); the
+    # layer counts them only when it synchronises
+    fmap = torch.ones(1, 2, 3, 4, dtype=torch.uint8)
+    ok = attention.LayerResult(out=None, final_map=fmap, budget_iters=torch.tensor([[4, 9, 1]], dtype=torch.int32),
+                               max_iters=10)
+    assert ok.sparsity() == 0.0
+    bad = attention.LayerResult(out=None, final_map=fmap,
+                                budget_iters=torch.tensor([[4, -10, -10]], dtype=torch.int32), max_iters=10)
+    with pytest.raises(RuntimeError, match=r"did not converge in 10 iterations \(2 query-block columns\)"):
+        bad.check()
+    mod = torch.nn.Module()
+    mod._ress_status = bad
+    with pytest.raises(RuntimeError, match="did not converge"):
+        attention.check_layers([mod])
+
+
 def test_random_criterion_generator():
     """One generator per device, seeded 20260826 on first use and advanced by every draw: the
     same call order reproduces the same keys, consecutive layers get different keys
