@@ -106,6 +106,7 @@ class HessBudget:
         self.floor_frac = None
         self.max_iters = max_iters
         self._norm_cache = {}
+        self._uniform_baseline = {}
 
     @property
     def needs_v_bar(self):
@@ -126,8 +127,19 @@ class HessBudget:
         reports each column's iteration count on the device (negative where it did not
         converge) and the returned tensor carries those counts as `ress_iters` ((B, q_blk)
         int32); the layer counts them and raises at its next host sync (LayerResult.check /
-        .sparsity), so the budget itself launches nothing beyond its two kernels."""
-        baseline = compute_baseline_num_to_select(attn_pooled, sparse_ratio, cdf_threshold)
+        .sparsity), so the budget launches only its own kernels: the head budget, and the
+        baseline count when a CDF threshold makes it depend on the scores."""
+        if cdf_threshold is None and sparse_ratio is not None:
+            # a sparse-ratio baseline does not depend on the scores: every row gets
+            # int(k_blk * (1 - sparse_ratio)). It is made once per shape and device and
+            # only read afterwards, so the step launches no fill for it.
+            key = (tuple(attn_pooled.shape), float(sparse_ratio), str(attn_pooled.device))
+            baseline = self._uniform_baseline.get(key)
+            if baseline is None:
+                baseline = compute_baseline_num_to_select(attn_pooled, sparse_ratio, None)
+                self._uniform_baseline[key] = baseline
+        else:
+            baseline = compute_baseline_num_to_select(attn_pooled, sparse_ratio, cdf_threshold)
         max_val = attn_pooled.shape[-1]
         nts = baseline if baseline.dim() == 3 else baseline.unsqueeze(0)
         iters = torch.empty(nts.shape[0], nts.shape[2], dtype=torch.int32, device=nts.device)
