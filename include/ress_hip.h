@@ -136,7 +136,11 @@ int ress_qk_norm_rope(const void* qkv, int B, int T, int nh, const void* q_weigh
  * [B*H][nq][nk] uint8 (nq = ceil(Tq/128), nk = ceil(Tk/64) <= 6144), q_i8
  * [B*H][nq*128][64], q_scale [B*H][nq], k_i8 [B*H][nk*64][64], k_scale [B*H][nk], and the
  * intermediate pooled_q [B*H][nq][64], pooled_k [B*H][nk][64] f32, sim_q [B*H][nq],
- * sim_k [B*H][nk] uint8 (1 = similar block). Non-causal only. */
+ * sim_k [B*H][nk] uint8 (1 = similar block). Non-causal only. The CDF cut keeps the n
+ * largest probabilities of a row (ties to the lowest index), n = the number of prefix sums
+ * of the descending probabilities that are <= cdfthreshd[h], the sums taken exactly over
+ * floor(p * 2^50) in uint64 against floor(min(cdfthreshd, 8192) * 2^50) (n = 0 for a
+ * negative threshold): a value-only definition, within 2^-37 of the real-number sums. */
 int ress_meansim_block_map(const void* q, const void* k, const void* km, int B, int H, int Tq, int Tk,
                            long long sqB, long long sqH, long long sqT, long long skB, long long skH, long long skT,
                            const void* simthreshd1, const void* cdfthreshd, int attention_sink, void* map, void* q_i8,

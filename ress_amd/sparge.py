@@ -197,8 +197,9 @@ def get_block_map_meansim_fuse_quant(q, k, km=None, is_causal=False, BLKQ=BLKQ, 
     """SpargeAttn's fused block map, as the reference patches it (spargeattn.patch:50-67):
     per-block mean pooling, mean intra-block cosine similarity and INT8 quantisation of
     Q (128-token blocks) and K - km (64-token blocks), then per (head, q-block) row the
-    softmax of the pooled scores over the similar K blocks, the smallest prefix of
-    the sorted probabilities whose cumulative sum stays <= cdfthreshd, and the forced
+    softmax of the pooled scores over the similar K blocks, the longest prefix of the
+    sorted probabilities whose cumulative sum stays <= cdfthreshd (the sums taken exactly,
+    at 2^-50 resolution, so the cut depends on the values alone), and the forced
     blocks: non-similar K blocks, every block of a non-similar Q row, and the
     ceil(attention_sink/64) leading blocks (attention_sink counts tokens, :63-65).
 
