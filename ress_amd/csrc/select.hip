@@ -50,7 +50,7 @@ __global__ __launch_bounds__(64 * SEL_WAVES) void k_select(const float* __restri
                                                            int* __restrict__ lut, int* __restrict__ nvalid) {
   extern __shared__ uint32_t key[];  // n_cand order keys, then reused for the kept flags
   __shared__ int hist[256];
-  __shared__ int pick[2];
+  __shared__ int pick[3];
   __shared__ int wcnt[2][SEL_WAVES];
   const int qb = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -105,6 +105,7 @@ __global__ __launch_bounds__(64 * SEL_WAVES) void k_select(const float* __restri
           if (above < rank && above + hv[t] >= rank) {
             pick[0] = 4 * lane + t;
             pick[1] = rank - above;
+            pick[2] = rank - above == hv[t];  // the whole bin is taken
           }
           above += hv[t];
         }
@@ -113,6 +114,10 @@ __global__ __launch_bounds__(64 * SEL_WAVES) void k_select(const float* __restri
       prefix |= (uint32_t)pick[0] << shift;
       pmask |= 255u << shift;
       rank = pick[1];
+      // every key of the bin is taken: with the lower digits left zero, the keys above
+      // thr plus the ties at thr are exactly the bin's keys and those above it, the set
+      // the remaining digits would select, so they are skipped
+      if (pick[2]) break;
     }
     thr = prefix;
   }
