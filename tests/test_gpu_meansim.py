@@ -82,6 +82,28 @@ def test_meansim_bit_exact(dev, B, H, Tq, Tk, sink):
     assert 0 < fm.float().mean().item() < 1
 
 
+# Tied probabilities across most of a row and thresholds at the edges of the cut's
+# definition: negative (nothing cut in), 0, inside a tie group, exactly 1, above 1 and above
+# the 8192 clamp. Both map kernels: 63 key blocks (one wave per row) and 1094 (a workgroup).
+@pytest.mark.parametrize("Tk", [4000, 70000])
+def test_meansim_cut_with_ties_and_edge_thresholds(dev, Tk):
+    H, Tq = 6, 500
+    rng = np.random.default_rng(Tk)
+    q = rng.normal(size=(1, H, Tq, 64))
+    blk = rng.normal(size=(1, H, 64, 64)) + 2.0 * rng.normal(size=(1, H, 1, 64))
+    nk = -(-Tk // 64)
+    k = np.tile(blk, (1, 1, nk, 1))[:, :, :Tk]             # every key block the same ...
+    for j in (3, 17, nk - 2):                              # ... but three
+        k[:, :, 64 * j:64 * j + 64] += 1.5 * rng.normal(size=(1, H, 1, 64))
+    to = lambda a: torch.from_numpy(a.astype(np.float32)).to(torch.bfloat16)  # noqa: E731
+    q, k = to(q), to(k)
+    cdfth = [-0.5, 0.0, 0.37, 1.0, 5.0, 1.0e5]
+    fm, want = _check(q, k, None, [0.0] * H, cdfth, 0, dev)
+    kept = want["map"].reshape(H, -1, nk).sum(-1)
+    assert (kept[0] == 0).all()                           # tau < 0: nothing is cut in, nothing forced
+    assert (kept[5] == nk).all() and (kept[4] == nk).all()  # tau >= 1 keeps every block
+
+
 def test_meansim_longest_rows(dev):
     """4100 key blocks (the workgroup kernel's value sort over 8192 slots, scan tie-break)."""
     q, k = _qk(12, 1, 1, 1030, 4100 * 64, dup=True, zeros=True)
