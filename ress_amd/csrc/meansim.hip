@@ -275,12 +275,27 @@ __device__ __forceinline__ int ms_cdf_wave(const uint32_t (&key)[E], int nk, flo
 #pragma unroll
   for (int e = 0; e < E; ++e)
     q[e] = 64 * e + lane < nk ? (unsigned long long)(__uint_as_float(key[e]) * MS_Q_SCALE) : 0ull;
-  uint32_t prefix = 0u, pmask = 0u;
+  // digits every valid key shares need no histogram: start at the first one that differs
+  uint32_t kor = 0u, kand = 0xFFFFFFFFu;
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (64 * e + lane < nk) {
+      kor |= key[e];
+      kand &= key[e];
+    }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    kor |= (uint32_t)__shfl_xor((int)kor, off, 64);
+    kand &= (uint32_t)__shfl_xor((int)kand, off, 64);
+  }
+  const uint32_t diff = kor ^ kand;
+  const int start = diff == 0u ? 3 : __clz((int)diff) >> 3;
+  uint32_t pmask = start ? 0xFFFFFFFFu << (32 - 8 * start) : 0u;
+  uint32_t prefix = kand & pmask;
   unsigned long long above = 0ull, bsum = 0ull;
   int n_above = 0, bcnt = 0;
   bool crossed = true;
-#pragma unroll
-  for (int level = 0; level < 4; ++level) {
+  for (int level = start; level < 4; ++level) {
     const int shift = 24 - 8 * level;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -305,18 +320,21 @@ __device__ __forceinline__ int ms_cdf_wave(const uint32_t (&key)[E], int nk, flo
     prefix |= (uint32_t)bin << shift;
     pmask |= 0xFFu << shift;
     asm volatile("" ::: "memory");
+    if (bcnt == 1) break;  // one key in the crossing bin: it does not fit, and nothing below it
   }
-  // every key fits: n = all of them, the n-th largest the smallest; otherwise the crossing
-  // key's ties (equal p, equal q) fit floor((T - above) / q) times
-  const int m = crossed ? (int)((T - above) / (bsum / (unsigned long long)bcnt)) : 0;
+  // every key fits: n = all of them, the n-th largest the smallest; a lone crossing key
+  // fits 0 times; otherwise the crossing key's ties (equal p, equal q) fit
+  // floor((T - above) / q) times
+  const int m = crossed && bcnt > 1 ? (int)((T - above) / (bsum / (unsigned long long)bcnt)) : 0;
   const int n = n_above + m;
   if (crossed && m > 0) {
     vbits = prefix;
-  } else {
+  } else {  // the smallest key (all fit), or the smallest above the crossing key's range
+    const uint32_t top = prefix | ~pmask;
     uint32_t mn = 0xFFFFFFFFu;
 #pragma unroll
     for (int e = 0; e < E; ++e)
-      if (64 * e + lane < nk && (!crossed || key[e] > prefix)) mn = min(mn, key[e]);
+      if (64 * e + lane < nk && (!crossed || key[e] > top)) mn = min(mn, key[e]);
     vbits = ms_wave_min_u32(mn);
   }
   return n;
@@ -474,17 +492,19 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
       if (!crossed) break;
       prefix |= (uint32_t)cut_i[1] << shift;
       pmask |= 0xFFu << shift;
+      if (bcnt == 1) break;  // one key in the crossing bin: it does not fit, and nothing below it
     }
-    const int m = crossed ? (int)((T - above) / (bsum / (unsigned long long)bcnt)) : 0;
+    const int m = crossed && bcnt > 1 ? (int)((T - above) / (bsum / (unsigned long long)bcnt)) : 0;
     n = n_above + m;
     if (crossed && m > 0) {
       vbits = prefix;
-    } else {  // the smallest key (every key fits) or the smallest above the crossing key
+    } else {  // the smallest key (every key fits) or the smallest above the crossing key's range
       if (tid == 0) vmin_l = 0xFFFFFFFFu;
+      const uint32_t top = prefix | ~pmask;
       uint32_t mn = 0xFFFFFFFFu;
       for (int c = tid; c < nk; c += 256) {
         const uint32_t b = __float_as_uint(p[c]);
-        if (!crossed || b > prefix) mn = min(mn, b);
+        if (!crossed || b > top) mn = min(mn, b);
       }
       mn = ms_wave_min_u32(mn);
       __syncthreads();
