@@ -288,15 +288,20 @@ __device__ __forceinline__ int ms_cdf_wave(const uint32_t (&key)[E], int nk, flo
     kor |= (uint32_t)__shfl_xor((int)kor, off, 64);
     kand &= (uint32_t)__shfl_xor((int)kand, off, 64);
   }
+  // The digits start at the highest bit where the keys differ and take 8 bits at a time
+  // downward (the last one what is left): a digit aligned to the bytes of the key would
+  // put most keys of a row into the few bins of its exponent, and the histogram atomics
+  // of one bin serialise.
   const uint32_t diff = kor ^ kand;
-  const int start = diff == 0u ? 3 : __clz((int)diff) >> 3;
-  uint32_t pmask = start ? 0xFFFFFFFFu << (32 - 8 * start) : 0u;
+  int hi = diff == 0u ? 7 : 31 - __clz((int)diff);  // the next digit's highest bit
+  uint32_t pmask = hi >= 31 ? 0u : 0xFFFFFFFFu << (hi + 1);
   uint32_t prefix = kand & pmask;
   unsigned long long above = 0ull, bsum = 0ull;
   int n_above = 0, bcnt = 0;
   bool crossed = true;
-  for (int level = start; level < 4; ++level) {
-    const int shift = 24 - 8 * level;
+  while (hi >= 0) {
+    const int shift = max(hi - 7, 0);
+    const uint32_t dmask = (2u << (hi - shift)) - 1u;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       hc[64 * j + lane] = 0;
@@ -306,7 +311,7 @@ __device__ __forceinline__ int ms_cdf_wave(const uint32_t (&key)[E], int nk, flo
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       if (64 * e + lane < nk && (key[e] & pmask) == prefix) {
-        const int b = (key[e] >> shift) & 255;
+        const int b = (key[e] >> shift) & dmask;
         atomicAdd(&hc[b], 1);
         atomicAdd(&hs[b], q[e]);
       }
@@ -318,7 +323,8 @@ __device__ __forceinline__ int ms_cdf_wave(const uint32_t (&key)[E], int nk, flo
       break;
     }
     prefix |= (uint32_t)bin << shift;
-    pmask |= 0xFFu << shift;
+    pmask |= dmask << shift;
+    hi = shift - 1;
     asm volatile("" ::: "memory");
     if (bcnt == 1) break;  // one key in the crossing bin: it does not fit, and nothing below it
   }
@@ -363,6 +369,7 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
   __shared__ unsigned long long cut_l[2];  // the digit's result: above, then bsum
   __shared__ int cut_i[4];                 // crossed, bin, n_above, bcnt
   __shared__ uint32_t vmin_l;
+  __shared__ uint32_t kred[8];  // the waves' OR, then AND, of the keys
   const int r = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   uint8_t* row = map + ((long long)bh * nq + r) * nk;
   const uint8_t* sk = sim_k + (long long)bh * nk;
@@ -454,20 +461,44 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
   const float th = cdfth[bh % H];
   if (th >= 0.0f) {
     const unsigned long long T = (unsigned long long)(fminf(th, 8192.0f) * MS_Q_SCALE);
-    uint32_t prefix = 0u, pmask = 0u;
+    // the digits start at the highest bit where the row's keys differ and take 8 bits at a
+    // time downward (as in ms_cdf_wave)
+    uint32_t kor = 0u, kand = 0xFFFFFFFFu;
+    for (int c = tid; c < nk; c += 256) {
+      const uint32_t b = __float_as_uint(p[c]);
+      kor |= b;
+      kand &= b;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      kor |= (uint32_t)__shfl_xor((int)kor, off, 64);
+      kand &= (uint32_t)__shfl_xor((int)kand, off, 64);
+    }
+    if (lane == 0) {
+      kred[w] = kor;
+      kred[4 + w] = kand;
+    }
+    __syncthreads();
+    kor = (kred[0] | kred[1]) | (kred[2] | kred[3]);
+    kand = (kred[4] & kred[5]) & (kred[6] & kred[7]);
+    const uint32_t diff = kor ^ kand;
+    int hi = diff == 0u ? 7 : 31 - __clz((int)diff);  // the next digit's highest bit
+    uint32_t pmask = hi >= 31 ? 0u : 0xFFFFFFFFu << (hi + 1);
+    uint32_t prefix = kand & pmask;
     unsigned long long above = 0ull, bsum = 0ull;
     int n_above = 0, bcnt = 0;
     bool crossed = true;
-    for (int level = 0; level < 4; ++level) {
-      const int shift = 24 - 8 * level;
+    while (hi >= 0) {
+      const int shift = max(hi - 7, 0);
+      const uint32_t dmask = (2u << (hi - shift)) - 1u;
       hc[tid] = 0;
       hs[tid] = 0ull;
       __syncthreads();
       for (int c = tid; c < nk; c += 256) {
         const uint32_t b = __float_as_uint(p[c]);
         if ((b & pmask) == prefix) {
-          atomicAdd(&hc[(b >> shift) & 255], 1);
-          atomicAdd(&hs[(b >> shift) & 255], (unsigned long long)(p[c] * MS_Q_SCALE));
+          atomicAdd(&hc[(b >> shift) & dmask], 1);
+          atomicAdd(&hs[(b >> shift) & dmask], (unsigned long long)(p[c] * MS_Q_SCALE));
         }
       }
       __syncthreads();
@@ -491,7 +522,8 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
       bsum = cut_l[1];
       if (!crossed) break;
       prefix |= (uint32_t)cut_i[1] << shift;
-      pmask |= 0xFFu << shift;
+      pmask |= dmask << shift;
+      hi = shift - 1;
       if (bcnt == 1) break;  // one key in the crossing bin: it does not fit, and nothing below it
     }
     const int m = crossed && bcnt > 1 ? (int)((T - above) / (bsum / (unsigned long long)bcnt)) : 0;
@@ -569,65 +601,91 @@ __global__ __launch_bounds__(256) void k_ms_map_wave(const float* __restrict__ p
                                                      const uint8_t* __restrict__ sim_k, int H, int nq, int nk,
                                                      const float* __restrict__ cdfth, int n_sink,
                                                      uint8_t* __restrict__ map) {
-  constexpr int LDK = 65;  // padded stride of the pooled-K tile
-  __shared__ float pk_l[64 * LDK];
-  __shared__ __align__(16) float pq_l[4][64];
-  __shared__ int hc_l[4][256];                 // per-wave CDF digit histograms
-  __shared__ unsigned long long hs_l[4][256];
+  constexpr int LDK = 68;  // row stride of a pooled-K tile: 16-byte rows, 8 consecutive columns in distinct banks
+  constexpr int LDQ = 68;  // row stride of the pooled-Q rows
+  constexpr int TB = 64 * LDK;
+  // two pooled-K tiles; once the scores are done the same LDS holds the per-wave CDF digit
+  // histograms (counts, then uint64 sums)
+  __shared__ __align__(16) float pk_l[2 * TB];
+  __shared__ __align__(16) float pq_l[4 * LDQ];
+  __shared__ float sc_l[4][128];  // one pass's scores, row-major
+  int(*hc_l)[256] = reinterpret_cast<int(*)[256]>(pk_l);
+  unsigned long long(*hs_l)[256] = reinterpret_cast<unsigned long long(*)[256]>(pk_l + 4 * 256);
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int bh = blockIdx.y, r = blockIdx.x * 4 + w;
   const long long row_id = (long long)bh * nq + r;
   const bool in_range = r < nq;
   const bool active = in_range && sim_q[row_id];
-  if (in_range) pq_l[w][lane] = pooled_q[row_id * 64 + lane];
+  const float pq = in_range ? pooled_q[row_id * 64 + lane] : 0.0f;
   const float* pkh = pooled_k + (long long)bh * nk * 64;
   const uint8_t* sk = sim_k + (long long)bh * nk;
+  // the similarity flags of the lane's columns (0 past nk) and the row's threshold, loaded
+  // now so that their latency overlaps the scores
+  uint8_t skc[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) skc[e] = 64 * e + lane < nk ? sk[64 * e + lane] : 0;
+  const float th = cdfth[bh % H];
 
-  // tiles of 64 key blocks: tile e+1 is loaded into registers while tile e is computed
+  // Passes of two 64-key-block tiles; pass p+1 is loaded into registers while pass p is
+  // computed. Lane l of wave w scores row l/16 of the workgroup against column 16w + l%16
+  // of both tiles (two independent DOT64 chains, each over d = 0..63 in order), so the
+  // four rows share every pooled-K read; sc_l turns the scores back to one row per wave,
+  // one column per lane.
+  const int srow = lane >> 4, scol = 16 * w + (lane & 15);
   float s[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) s[e] = 0.0f;
-  const int tiles = cdiv(nk, 64);
-  float4 nxt[4];
-  auto load_tile = [&](int t) {
-    const int cols = min(64, nk - 64 * t);
+  const int passes = cdiv(cdiv(nk, 64), 2);
+  float4 nxt[8];
+  auto load_pass = [&](int pp) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int f4 = tid + 256 * i, col = f4 >> 4;
+    for (int i = 0; i < 8; ++i) {
+      const int t = 2 * pp + (i >> 2), cols = min(64, nk - 64 * t);  // cols <= 0: no such tile
+      const int f4 = tid + 256 * (i & 3), col = f4 >> 4;
       nxt[i] = col < cols ? reinterpret_cast<const float4*>(pkh + (long long)(64 * t + col) * 64)[f4 & 15]
                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
   };
-  load_tile(0);
+  load_pass(0);  // in flight together with the loads above
+  pq_l[w * LDQ + lane] = pq;
 #pragma unroll 1
-  for (int e = 0; e < tiles; ++e) {
-    __syncthreads();  // previous tile consumed (and pq_l written, first time)
+  for (int pp = 0; pp < passes; ++pp) {
+    __syncthreads();  // previous pass consumed (and pq_l written, first time)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int f4 = tid + 256 * i;
-      float* dst = pk_l + (f4 >> 4) * LDK + (f4 & 15) * 4;
-      dst[0] = nxt[i].x;
-      dst[1] = nxt[i].y;
-      dst[2] = nxt[i].z;
-      dst[3] = nxt[i].w;
+    for (int i = 0; i < 8; ++i) {
+      const int f4 = tid + 256 * (i & 3);
+      *reinterpret_cast<float4*>(pk_l + (i >> 2) * TB + (f4 >> 4) * LDK + (f4 & 15) * 4) = nxt[i];
     }
     __syncthreads();
-    if (e + 1 < tiles) load_tile(e + 1);
-    if (active && 64 * e + lane < nk) {
-      const float4* qv = reinterpret_cast<const float4*>(pq_l[w]);
-      const float* kc = pk_l + lane * LDK;
-      float a = 0.0f;
+    if (pp + 1 < passes) load_pass(pp + 1);
+    {
+      const float4* qv = reinterpret_cast<const float4*>(pq_l + srow * LDQ);
+      const float4* k0 = reinterpret_cast<const float4*>(pk_l + scol * LDK);
+      const float4* k1 = reinterpret_cast<const float4*>(pk_l + TB + scol * LDK);
+      float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
       for (int d4 = 0; d4 < 16; ++d4) {
-        const float4 qq = qv[d4];
-        a = fmaf(qq.x, kc[4 * d4 + 0], a);
-        a = fmaf(qq.y, kc[4 * d4 + 1], a);
-        a = fmaf(qq.z, kc[4 * d4 + 2], a);
-        a = fmaf(qq.w, kc[4 * d4 + 3], a);
+        const float4 qq = qv[d4], x0 = k0[d4], x1 = k1[d4];
+        a0 = fmaf(qq.x, x0.x, a0);
+        a1 = fmaf(qq.x, x1.x, a1);
+        a0 = fmaf(qq.y, x0.y, a0);
+        a1 = fmaf(qq.y, x1.y, a1);
+        a0 = fmaf(qq.z, x0.z, a0);
+        a1 = fmaf(qq.z, x1.z, a1);
+        a0 = fmaf(qq.w, x0.w, a0);
+        a1 = fmaf(qq.w, x1.w, a1);
       }
+      sc_l[srow][scol] = a0;
+      sc_l[srow][64 + scol] = a1;
+    }
+    __syncthreads();
+    const float b0 = sc_l[w][lane], b1 = sc_l[w][64 + lane];
+    if (active) {
 #pragma unroll
-      for (int e2 = 0; e2 < E; ++e2)
-        if (e2 == e) s[e2] = a;
+      for (int e2 = 0; e2 < E; ++e2) {
+        if (64 * e2 + lane < nk && e2 == 2 * pp) s[e2] = b0;
+        if (64 * e2 + lane < nk && e2 == 2 * pp + 1) s[e2] = b1;
+      }
     }
   }
 
@@ -635,8 +693,7 @@ __global__ __launch_bounds__(256) void k_ms_map_wave(const float* __restrict__ p
   float mx = -__builtin_huge_valf();
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const int c = 64 * e + lane;
-    simc[e] = c < nk && sk[c];
+    simc[e] = skc[e] != 0;
     s[e] = s[e] * 0.125f;
     if (simc[e]) mx = fmaxf(mx, s[e]);
   }
@@ -661,7 +718,7 @@ __global__ __launch_bounds__(256) void k_ms_map_wave(const float* __restrict__ p
 #pragma unroll
   for (int e = 0; e < E; ++e) pb[e] = __float_as_uint(s[e] / tot);
   uint32_t vbits;
-  const int n = ms_cdf_wave<E>(pb, nk, cdfth[bh % H], lane, hc_l[w], hs_l[w], vbits);
+  const int n = ms_cdf_wave<E>(pb, nk, th, lane, hc_l[w], hs_l[w], vbits);
   int n_gt = 0;
   if (n > 0) {
     int gt = 0;
@@ -679,7 +736,7 @@ __global__ __launch_bounds__(256) void k_ms_map_wave(const float* __restrict__ p
     const int rank_eq = eq_before + __popcll(m & lt_mask);
     eq_before += __popcll(m);
     const bool sel = n > 0 && c < nk && (pb[e] > vbits || (eq && rank_eq < n - n_gt));
-    if (c < nk) row[c] = (sel || !sk[c] || c < n_sink) ? 1 : 0;
+    if (c < nk) row[c] = (sel || !skc[e] || c < n_sink) ? 1 : 0;
   }
 }
 
