@@ -186,6 +186,27 @@ __device__ __forceinline__ int quant_i8_rcp(float x, float scale, float rcp) {
   }
   return quant_i8(x, scale);
 }
+// quant_i8_rcp over 8 elements: the fast codes of all 8, then, only if one of them is
+// not trusted (or scale is 0), quant_i8 for those. Identical to quant_i8 per element, with
+// one branch where quant_i8_rcp takes one per element.
+__device__ __forceinline__ void quant_i8x8_rcp(const float (&x)[8], float scale, float rcp, int (&c)[8]) {
+  bool fast[8], all = scale != 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float y = x[i] * rcp;
+    const float a = fabsf(y) + 0.5f;
+    const float f = a - floorf(a);
+    fast[i] = f > 0x1p-12f && f < 1.0f - 0x1p-12f;
+    all = all && fast[i];
+    const int m = (int)a;
+    c[i] = y >= 0.0f ? m : -m;
+  }
+  if (!all) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (!(scale != 0.0f && fast[i])) c[i] = quant_i8(x[i], scale);
+  }
+}
 // Two-term ("split") INT8: x ~ scale*hi + (scale/254)*lo. hi is the per-block code
 // above; lo quantises the exact residual fmaf(-scale, hi, x) (|r| <= scale/2) with the
 // scale scale/254, so |lo| <= 127.

@@ -109,9 +109,9 @@ __device__ __forceinline__ void ms_stats_block(const uint16_t* __restrict__ x, c
       for (int c = 0; c < 8; ++c) xv[p][c] = xv[p][c] - kmv[c];
     }
   }
-  // token norms (fmaf chain per dim group, tree8 across the token's 8 lanes), then the
-  // per-thread sums of x and of x/||x|| in p order
-  float acc[16], amax = 0.0f;
+  // token norms (fmaf chain per dim group, tree8 across the token's 8 lanes, which all end
+  // with the same sum), then the per-thread sums of x and of x/||x|| in p order
+  float acc[16], amax = 0.0f, n2v[PASSES];
 #pragma unroll
   for (int c = 0; c < 16; ++c) acc[c] = 0.0f;
 #pragma unroll
@@ -124,8 +124,18 @@ __device__ __forceinline__ void ms_stats_block(const uint16_t* __restrict__ x, c
     }
     n2 = n2 + __shfl_xor(n2, 1, 64);
     n2 = n2 + __shfl_xor(n2, 2, 64);
-    n2 = n2 + __shfl_xor(n2, 4, 64);
-    const float inv = n2 > 0.0f ? 1.0f / sqrtf(n2) : 0.0f;
+    n2v[p] = n2 + __shfl_xor(n2, 4, 64);
+  }
+  // 1/||x|| once per token: lane g of the token's 8 lanes computes it for pass g (g <
+  // PASSES), and every pass takes it from there
+  float n2own = n2v[0];
+#pragma unroll
+  for (int p = 1; p < PASSES; ++p)
+    if (g == p) n2own = n2v[p];
+  const float inv_own = n2own > 0.0f ? 1.0f / sqrtf(n2own) : 0.0f;
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const float inv = __shfl(inv_own, (lane & ~7) | p, 64);
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       acc[c] = acc[c] + xv[p][c];
@@ -164,14 +174,13 @@ __device__ __forceinline__ void ms_stats_block(const uint16_t* __restrict__ x, c
       }
     }
   }
-  // codes of the whole padded block (rows past the sequence end are zero)
+  // codes of the whole padded block (rows past the sequence end hold exact zeros: code 0)
   const float rc = sc != 0.0f ? 1.0f / sc : 0.0f;
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) {
     const int t = tr + 32 * p;
     int c8[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) c8[c] = t < cnt ? quant_i8_rcp(xv[p][c], sc, rc) : 0;
+    quant_i8x8_rcp(xv[p], sc, rc, c8);
     *reinterpret_cast<uint2*>(codes + ((long long)bh * nb * BS + base + t) * 64 + 8 * g) = pack_i8x8(c8);
   }
 }
