@@ -142,13 +142,16 @@ __device__ __forceinline__ long long bh_offset(int bh, const Strides& s) {
 
 // ---- int8 packing ------------------------------------------------------------
 __device__ __forceinline__ uint2 pack_i8x8(const int c[8]) {
-  uint32_t w0 = 0, w1 = 0;
+  // byte permutes (v_perm_b32: selector bytes 0-3 take the second operand's bytes, 4-7
+  // the first's, 0x0c a zero byte): the low bytes of c[0..3] in order, then of c[4..7]
+  uint32_t w[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    w0 |= ((uint32_t)(c[i] & 0xff)) << (8 * i);
-    w1 |= ((uint32_t)(c[4 + i] & 0xff)) << (8 * i);
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)c[4 * h + 1], (uint32_t)c[4 * h], 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)c[4 * h + 3], (uint32_t)c[4 * h + 2], 0x0c0c0400u);
+    w[h] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
   }
-  return make_uint2(w0, w1);
+  return make_uint2(w[0], w[1]);
 }
 
 // ---- order keys ------------------------------------------------------------
@@ -188,18 +191,19 @@ __device__ __forceinline__ int quant_i8_rcp(float x, float scale, float rcp) {
 }
 // quant_i8_rcp over 8 elements: the fast codes of all 8, then, only if one of them is
 // not trusted (or scale is 0), quant_i8 for those. Identical to quant_i8 per element, with
-// one branch where quant_i8_rcp takes one per element.
+// one branch where quant_i8_rcp takes one per element. a = y + copysign(0.5, y) is
+// sign(y) * (|y| + 0.5) with the same rounding, its truncation the code; the fraction of
+// |a| (exact) must lie at least 2^-12 away from 0 and 1.
 __device__ __forceinline__ void quant_i8x8_rcp(const float (&x)[8], float scale, float rcp, int (&c)[8]) {
   bool fast[8], all = scale != 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float y = x[i] * rcp;
-    const float a = fabsf(y) + 0.5f;
-    const float f = a - floorf(a);
-    fast[i] = f > 0x1p-12f && f < 1.0f - 0x1p-12f;
+    const float a = y + __builtin_copysignf(0.5f, y);
+    const float f = __builtin_amdgcn_fractf(fabsf(a));
+    fast[i] = fabsf(f - 0.5f) < 0.5f - 0x1p-12f;
     all = all && fast[i];
-    const int m = (int)a;
-    c[i] = y >= 0.0f ? m : -m;
+    c[i] = (int)a;
   }
   if (!all) {
 #pragma unroll

@@ -97,17 +97,19 @@ __device__ __forceinline__ void ms_stats_block(const uint16_t* __restrict__ x, c
   float kmv[8];
 #pragma unroll
   for (int c = 0; c < 8; ++c) kmv[c] = km ? km[(long long)bh * 64 + 8 * g + c] : 0.0f;
+  // every pass's row is loaded before any is used (tokens past the sequence end read the
+  // last token's row and become zeros), so the loads are in flight together
+  uint4 raw[PASSES];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p)
+    raw[p] = *reinterpret_cast<const uint4*>(xb + (long long)(base + min(tr + 32 * p, cnt - 1)) * sx.t + 8 * g);
   float xv[PASSES][8];
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) {
-    const int t = tr + 32 * p;
-    uint4 r = make_uint4(0u, 0u, 0u, 0u);
-    if (t < cnt) r = *reinterpret_cast<const uint4*>(xb + (long long)(base + t) * sx.t + 8 * g);
-    unpack_bf16x8(r, xv[p]);
-    if (t < cnt) {
+    const bool in = tr + 32 * p < cnt;
+    unpack_bf16x8(raw[p], xv[p]);
 #pragma unroll
-      for (int c = 0; c < 8; ++c) xv[p][c] = xv[p][c] - kmv[c];
-    }
+    for (int c = 0; c < 8; ++c) xv[p][c] = in ? xv[p][c] - kmv[c] : 0.0f;
   }
   // token norms (fmaf chain per dim group, tree8 across the token's 8 lanes, which all end
   // with the same sum), then the per-thread sums of x and of x/||x|| in p order
