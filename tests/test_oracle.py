@@ -340,9 +340,10 @@ def test_generator_is_deterministic_and_shaped():
 
 def test_reciprocal_quantiser_fast_path_is_exact():
     """The kernels quantise with x * (1/scale) and fall back to the division x / scale when
-    |y| + 0.5 has a fraction within 2^-12 of an integer (common.h quant_i8_rcp). In float32
-    (numpy, round to nearest like the GPU), the fast path's code equals the division's on
-    random blocks and on values placed at and around every half-integer boundary."""
+    |y| + 0.5 has a fraction within 2^-12 of an integer (common.h quant_i8_rcp, and the
+    equivalent form of quant_i8x8_rcp). In float32 (numpy, round to nearest like the GPU),
+    the fast path's code equals the division's on random blocks and on values placed at and
+    around every half-integer boundary, and both forms trust the same elements."""
     rng = np.random.default_rng(3)
     f32 = np.float32
 
@@ -360,11 +361,24 @@ def test_reciprocal_quantiser_fast_path_is_exact():
         m = np.trunc(a).astype(np.int64)
         return np.where(ok, np.where(y >= 0, m, -m), exact(x, s)), ok
 
+    def fast8(x, s):
+        """quant_i8x8_rcp's form: a = y + copysign(0.5, y) (sign(y) * (|y| + 0.5), the same
+        rounding), the fraction of |a| tested as |f - 0.5| < 0.5 - 2^-12, the code trunc(a)."""
+        r = (f32(1.0) / s).astype(f32)
+        y = (x * r).astype(f32)
+        a = (y + np.copysign(f32(0.5), y)).astype(f32)
+        aa = np.abs(a)
+        f = (aa - np.floor(aa)).astype(f32)
+        ok = np.abs((f - f32(0.5)).astype(f32)) < f32(0.5) - f32(2.0 ** -12)
+        return np.where(ok, np.trunc(a).astype(np.int64), exact(x, s)), ok
+
     for trial in range(200):
         x = (rng.standard_normal(4096) * 10.0 ** rng.uniform(-6, 4)).astype(f32)
         s = f32(np.abs(x).max() / f32(127.0))
-        got, _ = fast(x, s)
+        got, ok = fast(x, s)
         assert np.array_equal(got, exact(x, s))
+        got8, ok8 = fast8(x, s)
+        assert np.array_equal(got8, exact(x, s)) and np.array_equal(ok8, ok)
     # adversarial: x just around (k + 1/2) * s for every k, a few ulps either side
     for s in (f32(0.0137), f32(3.3e-5), f32(1.0), f32(7.77)):
         k = np.arange(-127, 128, dtype=f32)
@@ -378,3 +392,5 @@ def test_reciprocal_quantiser_fast_path_is_exact():
         got, ok = fast(x, s)
         assert np.array_equal(got, exact(x, s))
         assert not ok.all()  # the boundary values do take the division
+        got8, ok8 = fast8(x, s)
+        assert np.array_equal(got8, exact(x, s)) and np.array_equal(ok8, ok)
