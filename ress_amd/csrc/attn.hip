@@ -220,12 +220,7 @@ __global__ __launch_bounds__(1024) void k_attn_schedule(const int* __restrict__ 
   if (tid == 9) sched[24] = 0;  // operand status, set by the 16-bit kernel
   // inclusive scan of the threads' sums: lane shuffles within each wave, then the 16 wave
   // totals through LDS (one barrier)
-  long long incl = s;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const long long y = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += y;
-  }
+  long long incl = (long long)wave_scan_sum_u64((unsigned long long)s);
   if (lane == 63) wtot[wv] = incl;
   __syncthreads();
   long long W = 0;

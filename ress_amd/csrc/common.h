@@ -219,16 +219,64 @@ __device__ __forceinline__ int quant_i8_lo(float x, float scale, int hi) {
   return quant_i8(fmaf(-scale, (float)hi, x), scale / 254.0f);
 }
 
-// ---- wave reductions (wave64) ---------------------------------------------
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+// ---- wave scans and reductions (wave64, every lane active) -----------------
+// DPP moves (GFX9 encodings): row_shr:n (0x110 + n) within 16-lane rows, row_bcast:15 /
+// row_bcast:31 (0x142 / 0x143) carry lane 15 / 31 of a row pair into the rows the row mask
+// selects. A lane without a source (or outside the row mask) gets `old`. Four row shifts
+// and the two broadcasts make an inclusive scan over the 64 lanes; lane 63 then holds the
+// whole reduction. Used for integer sums and for maxima / minima, which are exact in any
+// order, so these return the same values as lane-shuffle trees without the LDS round trips
+// of ds_bpermute. Float sums keep their shuffle trees (their order is part of the result).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t old, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROWS, 0xf, false);
 }
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
-  return v;
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t x, uint32_t identity, Op op) {
+  x = op(x, dpp_u32<0x111, 0xf>(identity, x));
+  x = op(x, dpp_u32<0x112, 0xf>(identity, x));
+  x = op(x, dpp_u32<0x114, 0xf>(identity, x));
+  x = op(x, dpp_u32<0x118, 0xf>(identity, x));
+  x = op(x, dpp_u32<0x142, 0xa>(identity, x));
+  x = op(x, dpp_u32<0x143, 0xc>(identity, x));
+  return x;
+}
+__device__ __forceinline__ uint32_t lane63(uint32_t x) { return (uint32_t)__builtin_amdgcn_readlane((int)x, 63); }
+// inclusive prefix sum over lanes 0..l
+__device__ __forceinline__ int wave_scan_sum_i(int x) {
+  return (int)wave_scan_u32((uint32_t)x, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+}
+template <int C, int R>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
+  const uint32_t lo = dpp_u32<C, R>(0u, (uint32_t)v), hi = dpp_u32<C, R>(0u, (uint32_t)(v >> 32));
+  return ((unsigned long long)hi << 32) | lo;
+}
+__device__ __forceinline__ unsigned long long wave_scan_sum_u64(unsigned long long x) {
+  x += dpp_u64<0x111, 0xf>(x);
+  x += dpp_u64<0x112, 0xf>(x);
+  x += dpp_u64<0x114, 0xf>(x);
+  x += dpp_u64<0x118, 0xf>(x);
+  x += dpp_u64<0x142, 0xa>(x);
+  x += dpp_u64<0x143, 0xc>(x);
+  return x;
+}
+__device__ __forceinline__ unsigned long long lane63_u64(unsigned long long x) {
+  return ((unsigned long long)lane63((uint32_t)(x >> 32)) << 32) | lane63((uint32_t)x);
+}
+__device__ __forceinline__ float wave_max(float v) {
+  const uint32_t r = wave_scan_u32(__float_as_uint(v), 0xff800000u,  // -inf
+                                   [](uint32_t a, uint32_t b) { return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b))); });
+  return __uint_as_float(lane63(r));
+}
+__device__ __forceinline__ int wave_sum_i(int v) { return (int)lane63((uint32_t)wave_scan_sum_i(v)); }
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  return lane63(wave_scan_u32(v, ~0u, [](uint32_t a, uint32_t b) { return min(a, b); }));
+}
+__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
+  return lane63(wave_scan_u32(v, 0u, [](uint32_t a, uint32_t b) { return a | b; }));
+}
+__device__ __forceinline__ uint32_t wave_and_u32(uint32_t v) {
+  return lane63(wave_scan_u32(v, ~0u, [](uint32_t a, uint32_t b) { return a & b; }));
 }
 // the SUM64 butterfly over 64 lane partials
 __device__ __forceinline__ float sum64_tree(float v) {

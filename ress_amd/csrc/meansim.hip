@@ -124,9 +124,9 @@ __device__ __forceinline__ void ms_stats_block(const uint16_t* __restrict__ x, c
       n2 = fmaf(xv[p][c], xv[p][c], n2);
       amax = fmaxf(amax, fabsf(xv[p][c]));
     }
-    n2 = n2 + __shfl_xor(n2, 1, 64);
-    n2 = n2 + __shfl_xor(n2, 2, 64);
-    n2v[p] = n2 + __shfl_xor(n2, 4, 64);
+    n2 = n2 + __uint_as_float(ms_xor_lane<1>(__float_as_uint(n2), lane));
+    n2 = n2 + __uint_as_float(ms_xor_lane<2>(__float_as_uint(n2), lane));
+    n2v[p] = n2 + __uint_as_float(ms_xor_lane<4>(__float_as_uint(n2), lane));
   }
   // 1/||x|| once per token: lane g of the token's 8 lanes computes it for pass g (g <
   // PASSES), and every pass takes it from there
@@ -207,12 +207,6 @@ __global__ __launch_bounds__(256) void k_ms_stats(const uint16_t* __restrict__ q
     ms_stats_block<64>(k, sk, Tk, km, simth, nk, bx - nq, bh, k_i8, k_scale, pooled_k, sim_k, part_l, ssum_l, amax_l);
 }
 
-__device__ __forceinline__ uint32_t ms_wave_min_u32(uint32_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, off, 64));
-  return v;
-}
-
 // One digit of the CDF radix descent, by one wave over the 256 bins (hc counts, hs uint64
 // sums of q) of the keys in the current range: bins are taken from the highest down while
 // the running total stays <= T. Returns false if every bin fits (above, n_above then
@@ -231,17 +225,9 @@ __device__ __forceinline__ bool ms_cdf_digit(const int* hc, const unsigned long 
     ls += s4[j];
     lc += c4[j];
   }
-  unsigned long long in = ls;  // inclusive scan over lanes (lane 0 = highest bins)
-  int inc = lc;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const unsigned long long y = __shfl_up(in, off, 64);
-    const int yc = __shfl_up(inc, off, 64);
-    if (lane >= off) {
-      in += y;
-      inc += yc;
-    }
-  }
+  // inclusive scans over lanes (lane 0 = highest bins)
+  const unsigned long long in = wave_scan_sum_u64(ls);
+  const int inc = wave_scan_sum_i(lc);
   unsigned long long base = above + (in - ls);
   int basec = n_above + (inc - lc), jx = 4, cx = 0;
   unsigned long long sx = 0ull;
@@ -260,16 +246,18 @@ __device__ __forceinline__ bool ms_cdf_digit(const int* hc, const unsigned long 
   }
   const unsigned long long has = __ballot(jx < 4);
   if (has == 0ull) {
-    above = __shfl(base, 63, 64);
-    n_above = __shfl(basec, 63, 64);
+    above = lane63_u64(base);
+    n_above = (int)lane63((uint32_t)basec);
     return false;
   }
-  const int src = __ffsll((long long)has) - 1;
-  bin = 255 - 4 * src - __shfl(jx, src, 64);
-  above = __shfl(base, src, 64);
-  n_above = __shfl(basec, src, 64);
-  bcnt = __shfl(cx, src, 64);
-  bsum = __shfl(sx, src, 64);
+  const int src = __ffsll((long long)has) - 1;  // uniform
+  bin = 255 - 4 * src - __builtin_amdgcn_readlane(jx, src);
+  above = ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(base >> 32), src) << 32) |
+          (uint32_t)__builtin_amdgcn_readlane((int)base, src);
+  n_above = __builtin_amdgcn_readlane(basec, src);
+  bcnt = __builtin_amdgcn_readlane(cx, src);
+  bsum = ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(sx >> 32), src) << 32) |
+         (uint32_t)__builtin_amdgcn_readlane((int)sx, src);
   return true;
 }
 
@@ -294,11 +282,8 @@ __device__ __forceinline__ int ms_cdf_wave(const uint32_t (&key)[E], int nk, flo
       kor |= key[e];
       kand &= key[e];
     }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    kor |= (uint32_t)__shfl_xor((int)kor, off, 64);
-    kand &= (uint32_t)__shfl_xor((int)kand, off, 64);
-  }
+  kor = wave_or_u32(kor);
+  kand = wave_and_u32(kand);
   // The digits start at the highest bit where the keys differ and take 8 bits at a time
   // downward (the last one what is left): a digit aligned to the bytes of the key would
   // put most keys of a row into the few bins of its exponent, and the histogram atomics
@@ -352,7 +337,7 @@ __device__ __forceinline__ int ms_cdf_wave(const uint32_t (&key)[E], int nk, flo
 #pragma unroll
     for (int e = 0; e < E; ++e)
       if (64 * e + lane < nk && (!crossed || key[e] > top)) mn = min(mn, key[e]);
-    vbits = ms_wave_min_u32(mn);
+    vbits = wave_min_u32(mn);
   }
   return n;
 }
@@ -480,11 +465,8 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
       kor |= b;
       kand &= b;
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      kor |= (uint32_t)__shfl_xor((int)kor, off, 64);
-      kand &= (uint32_t)__shfl_xor((int)kand, off, 64);
-    }
+    kor = wave_or_u32(kor);
+    kand = wave_and_u32(kand);
     if (lane == 0) {
       kred[w] = kor;
       kred[4 + w] = kand;
@@ -549,7 +531,7 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
         const uint32_t b = __float_as_uint(p[c]);
         if (!crossed || b > top) mn = min(mn, b);
       }
-      mn = ms_wave_min_u32(mn);
+      mn = wave_min_u32(mn);
       __syncthreads();
       if (lane == 0) atomicMin(&vmin_l, mn);
       __syncthreads();
@@ -565,12 +547,7 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
     gt += b > vbits ? 1 : 0;
     eq += b == vbits ? 1 : 0;
   }
-  int incl = eq;  // inclusive scan of eq over the workgroup, in thread order
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += y;
-  }
+  const int incl = wave_scan_sum_i(eq);  // inclusive scan of eq over the wave, in thread order
   const int gsum = wave_sum_i(gt);
   if (lane == 63) ired[w] = incl;
   if (lane == 0) red[w] = __int_as_float(gsum);

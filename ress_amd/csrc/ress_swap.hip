@@ -120,12 +120,9 @@ __device__ __forceinline__ uint32_t rs_top_m(const uint32_t (&key)[NPL], uint32_
     // lane l owns bins 4l..4l+3; suffix counts S(t) = #{digit >= t}
     const int h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2], h3 = hist[4 * lane + 3];
     const int own = h0 + h1 + h2 + h3;
-    int suf = own;  // inclusive suffix over lanes >= l
-    for (int off = 1; off < 64; off <<= 1) {
-      const int y = __shfl_down(suf, off);
-      if (lane + off < 64) suf += y;
-    }
-    const int above = suf - own;  // keys in bins of higher lanes
+    // keys in bins of higher lanes: the total minus the inclusive prefix over lanes <= l
+    const int incl = wave_scan_sum_i(own);
+    const int above = (int)lane63((uint32_t)incl) - incl;
     const int s3 = above + h3, s2 = s3 + h2, s1 = s2 + h1, s0 = s1 + h0;
     // the digit t with S(t) >= need > S(t+1) is unique
     int t = -1, gt = 0, inbin = 0;
@@ -134,8 +131,9 @@ __device__ __forceinline__ uint32_t rs_top_m(const uint32_t (&key)[NPL], uint32_
     else if (s1 >= need && s2 < need) t = 1, gt = s2, inbin = h1;
     else if (s0 >= need && s1 < need) t = 0, gt = s1, inbin = h0;
     const unsigned long long hit = __ballot(t >= 0);
-    const int src = __ffsll((long long)hit) - 1;
-    const int digit = __shfl(4 * lane + t, src), n_gt = __shfl(gt, src), n_in = __shfl(inbin, src);
+    const int src = hit ? __ffsll((long long)hit) - 1 : 63;  // uniform
+    const int digit = __builtin_amdgcn_readlane(4 * lane + t, src), n_gt = __builtin_amdgcn_readlane(gt, src),
+              n_in = __builtin_amdgcn_readlane(inbin, src);
     need -= n_gt;
     prefix |= (uint32_t)digit << shift;
     pmask |= 255u << shift;

@@ -91,13 +91,8 @@ __global__ __launch_bounds__(64 * SEL_WAVES) void k_select(const float* __restri
         // lane l owns bins 4l..4l+3; above = matching keys in bins > 4l+3
         const int h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2], h3 = hist[4 * lane + 3];
         const int own = h0 + h1 + h2 + h3;
-        int incl = own;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          const int y = __shfl_up(incl, off, 64);
-          if (lane >= off) incl += y;
-        }
-        const int total = __shfl(incl, 63, 64);
+        const int incl = wave_scan_sum_i(own);
+        const int total = (int)lane63((uint32_t)incl);
         int above = total - incl;
         const int hv[4] = {h0, h1, h2, h3};
 #pragma unroll
