@@ -278,13 +278,48 @@ __device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
 __device__ __forceinline__ uint32_t wave_and_u32(uint32_t v) {
   return lane63(wave_scan_u32(v, ~0u, [](uint32_t a, uint32_t b) { return a & b; }));
 }
+// The value of lane ^ J (J a power of two below 64) without the LDS: DPP quad permutes for
+// 1 and 2, row shifts by 4 either way (the lane's bit 2 picks the direction), a rotate by
+// 8 within the 16-lane row, and the gfx950 row swaps (v_permlane16_swap,
+// v_permlane32_swap) for 16 and 32. The same partner as __shfl_xor(v, J), so butterflies
+// built on it add the same pairs in the same order.
+template <int J>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t a) {
+  if constexpr (J == 1) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)a, 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
+  } else if constexpr (J == 2) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)a, 0x4E, 0xF, 0xF, false);  // quad_perm 2,3,0,1
+  } else if constexpr (J == 4) {
+    const uint32_t below = (uint32_t)__builtin_amdgcn_mov_dpp((int)a, 0x114, 0xF, 0xF, false);  // row_shr:4
+    const uint32_t above = (uint32_t)__builtin_amdgcn_mov_dpp((int)a, 0x104, 0xF, 0xF, false);  // row_shl:4
+    return (threadIdx.x & 4) ? below : above;
+  } else if constexpr (J == 8) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)a, 0x128, 0xF, 0xF, false);  // row_ror:8
+  } else if constexpr (J == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(a, a, false, false);
+    return (threadIdx.x & 16) ? (uint32_t)r[0] : (uint32_t)r[1];
+  } else {
+    static_assert(J == 32, "xor_lane: J is 1, 2, 4, 8, 16 or 32");
+    const auto r = __builtin_amdgcn_permlane32_swap(a, a, false, false);
+    return (threadIdx.x & 32) ? (uint32_t)r[0] : (uint32_t)r[1];
+  }
+}
+template <int J>
+__device__ __forceinline__ float xor_lane_f(float a) {
+  return __uint_as_float(xor_lane<J>(__float_as_uint(a)));
+}
 // the SUM64 butterfly over 64 lane partials
 __device__ __forceinline__ float sum64_tree(float v) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) v = v + __shfl_xor(v, off, 64);
+  v = v + xor_lane_f<1>(v);
+  v = v + xor_lane_f<2>(v);
+  v = v + xor_lane_f<4>(v);
+  v = v + xor_lane_f<8>(v);
+  v = v + xor_lane_f<16>(v);
+  v = v + xor_lane_f<32>(v);
   return v;
 }
-// the SUM8x tree over token lanes j = lane>>3 (lane bits 3..5)
+// the SUM8x tree over token lanes j = lane>>3 (lane bits 3..5); lane shuffles (the LDS
+// unit) for the HBM-bound prep pass, whose VALU is the busier unit
 __device__ __forceinline__ float sum8_tree(float v) {
   v = v + __shfl_xor(v, 8, 64);
   v = v + __shfl_xor(v, 16, 64);

@@ -47,8 +47,10 @@ constexpr float MS_Q_SCALE = 1125899906842624.0f;  // 2^50: q(p) = floor(p * 2^5
 // front LDS region of k_ms_map_long: the four waves' score chunks
 constexpr size_t MS_LONG_FRONT_BYTES = 4 * 64 * MS_CH_LD * 4;
 
-// the value of lane ^ J (J < 64): DPP quad permutes for 1 and 2, a bit-mode ds_swizzle
-// (source lane ((l & 31) ^ J) within each 32-lane half) for 4..16, the half swap for 32
+// the value of lane ^ J (J < 64) for the stats kernel: DPP quad permutes for 1 and 2, a
+// bit-mode ds_swizzle (source lane ((l & 31) ^ J) within each 32-lane half) for 4..16, the
+// half swap for 32. The stats kernel's VALU is its busiest unit, so its middle exchanges
+// stay on the LDS unit (ds_swizzle) rather than in VALU moves (common.h xor_lane).
 template <int J>
 __device__ __forceinline__ uint32_t ms_xor_lane(uint32_t a, int lane) {
   if constexpr (J == 1) {

@@ -29,10 +29,10 @@ __device__ __forceinline__ void st_bf16x4(uint16_t* p, float a, float b, float c
       make_uint2(f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16), f32_to_bf16_bits(c) | (f32_to_bf16_bits(d) << 16));
 }
 __device__ __forceinline__ float sum16(float v) {
-  v = v + __shfl_xor(v, 1, 64);
-  v = v + __shfl_xor(v, 2, 64);
-  v = v + __shfl_xor(v, 4, 64);
-  v = v + __shfl_xor(v, 8, 64);
+  v = v + xor_lane_f<1>(v);
+  v = v + xor_lane_f<2>(v);
+  v = v + xor_lane_f<4>(v);
+  v = v + xor_lane_f<8>(v);
   return v;
 }
 
@@ -51,8 +51,8 @@ __device__ __forceinline__ float4 head_norm(float4 x, const uint16_t* w, const u
 
 // rotate-half RoPE of dims d0..d0+3 within a 32-dim half, given cos/sin of their angles
 __device__ __forceinline__ float4 rope4(float4 y, int d0, const float (&cs)[4], const float (&sn)[4]) {
-  const float4 o = make_float4(__shfl_xor(y.x, 4, 64), __shfl_xor(y.y, 4, 64), __shfl_xor(y.z, 4, 64),
-                               __shfl_xor(y.w, 4, 64));  // dims d0 +- 16
+  const float4 o = make_float4(xor_lane_f<4>(y.x), xor_lane_f<4>(y.y), xor_lane_f<4>(y.z),
+                               xor_lane_f<4>(y.w));  // dims d0 +- 16
   const bool lo = (d0 & 31) < 16;
   float r[4];
   const float yy[4] = {y.x, y.y, y.z, y.w}, oo[4] = {o.x, o.y, o.z, o.w};
