@@ -35,8 +35,9 @@
 // k_ms_map_wave (nk <= 1024): one wave per (q-block, batch*head) row, four rows per
 // workgroup; details at the kernel.
 // k_ms_map_long (nk > 1024): one 256-thread workgroup per row.
-// Both find n without sorting: an MSB-first radix descent over the bits of p (four 8-bit
-// digits) with per-digit counts and uint64 sums of q, and the tie rank by index.
+// Both find n without sorting: an MSB-first radix descent over the bits of p (8-bit
+// digits from the highest bit where the row's keys differ) with per-digit counts and
+// uint64 sums of q, and the tie rank by index.
 #include "common.h"
 
 namespace {
