@@ -282,7 +282,8 @@ __device__ __forceinline__ uint32_t wave_and_u32(uint32_t v) {
 // 1 and 2, row shifts by 4 either way (the lane's bit 2 picks the direction), a rotate by
 // 8 within the 16-lane row, and the gfx950 row swaps (v_permlane16_swap,
 // v_permlane32_swap) for 16 and 32. The same partner as __shfl_xor(v, J), so butterflies
-// built on it add the same pairs in the same order.
+// built on it add the same pairs in the same order. The lane bits come from threadIdx.x:
+// every kernel of this library runs one-dimensional workgroups.
 template <int J>
 __device__ __forceinline__ uint32_t xor_lane(uint32_t a) {
   if constexpr (J == 1) {
