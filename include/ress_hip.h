@@ -186,8 +186,9 @@ int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void* q_scale
  * sqB/sqH/sqT, converted to fp16 per row in registers; k_pack (fp16), k_norm (the k_scale
  * output of the 16-bit mode: per-block largest key norms) and v_pack come from
  * ress_prep_qkv. A row whose logit bound |q*sm_scale*log2 e| * max key norm is at most 64
- * (log2 units) runs with the pre-scaled queries rounded to fp16 and a fixed offset in the
- * accumulator (no running max); other rows use the exact fp16 queries and a running max.
+ * (log2 units) for every one of its queries runs with the pre-scaled queries rounded to fp16
+ * and P = exp2(logit) taken directly (no offset, no running max); other rows use the exact
+ * fp16 queries and a running max.
  * sched, patch_order: as for ress_sparse_attn_fwd (patch_order: the table given to
  * ress_prep_qkv; each row is read and written at the storage positions of its tokens).
  * After the call, int32 word 24 of sched (byte 96) is 1 if a key and 2 if a query element
@@ -214,6 +215,14 @@ int ress_sparse_attn_fwd_f16_noalloc(const void* q, long long sqB, long long sqH
                                      int B, int H, int frames, int P, int S, const int* patch_order, float sm_scale,
                                      void* out, int out_dtype,
                                      long long soB, long long soH, long long soT, hipStream_t stream);
+/* The fp16 operand-range report of ress_sparse_attn_fwd_f16_noalloc (no counterpart in the
+ * reference; for the same callers). ress_sparse_attn_fwd_f16 reports a key / query element
+ * outside fp16's range (|x| >= 65520) in word 24 of its `sched` workspace; the noalloc call
+ * keeps that word in its static array, whose device address (an int32, for the current
+ * device) this returns in *out. Each call clears the word when it starts and ORs in 1 (a
+ * key) or 2 (a query); read it after the call has completed and before the next call on the
+ * device. Looks the address up once per device; allocates nothing. */
+int ress_noalloc_status_address(void** out);
 
 /* Replaces SpargeAttn qk_int8_sv_f16_accum_f16_block_sparse_attn_inst_buf_with_pv_threshold
  * (call src/ress/models/attention.py:238-241) with the same argument meaning; see

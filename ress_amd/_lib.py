@@ -64,6 +64,8 @@ def lib():
         L.ress_restore_swap_workspace_size.argtypes = [ctypes.c_int] * 3
         L.ress_noalloc_scratch_bytes.restype = ctypes.c_longlong
         L.ress_noalloc_scratch_bytes.argtypes = []
+        L.ress_noalloc_status_address.restype = ctypes.c_int
+        L.ress_noalloc_status_address.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
         for name, sig in _SIGS.items():
             fn = getattr(L, name)
             fn.restype = ctypes.c_int
@@ -98,4 +100,5 @@ def last_error():
 
 def exported_symbols():
     return list(_SIGS) + ["ress_last_error", "ress_abi_version", "ress_qattn_workspace_size",
-                          "ress_attn_sched_bytes", "ress_restore_swap_workspace_size", "ress_noalloc_scratch_bytes"]
+                          "ress_attn_sched_bytes", "ress_restore_swap_workspace_size", "ress_noalloc_scratch_bytes",
+                          "ress_noalloc_status_address"]

@@ -297,7 +297,7 @@ def ress_attention_forward(self, x, pos, num_to_select=None, budget_fn=None, per
                            joint_select_fn=None, block_criterion="probability", pool_mode="avg",
                            num_special_tokens=5, num_heads=16, shape=None, aux_store=None, aux_full=True,
                            dense=False, retain_output_grad=False, pooled_fallback=False, protect_own_frame=False,
-                           attention_sink=0, patch_order=None):
+                           attention_sink=0, patch_order=None, eager_check=False):
     """Replacement forward of a global-attention block (reference attention.py:296-659),
     same arguments and return value: (B, N*P, dim) after the W_O projection.
     attention_sink (not a reference argument; default 0 = the reference's behaviour):
@@ -307,7 +307,10 @@ def ress_attention_forward(self, x, pos, num_to_select=None, budget_fn=None, per
     reference permutes the token tensor itself, hilbert.py:128-162). When
     aux_store is given the forward synchronises once for the realized sparsity and raises
     there if the HeSS budget did not converge; without it the forward does not synchronise
-    (LayerResult.check is the deferred check)."""
+    (check_layers / LayerResult.check is the deferred check). eager_check (not a reference
+    argument; the module attribute of the same name): synchronise at the end of the forward
+    and raise there, as the reference raises a non-converged HeSS budget at once
+    (_proportional.py:112-113)."""
     if pool_mode != "avg":
         raise NotImplementedError("only avg pooling (the reference default) is implemented")
     q, k, v, shp = compute_qkv(self, x, pos, num_special_tokens=num_special_tokens, num_heads=num_heads,
@@ -320,6 +323,7 @@ def ress_attention_forward(self, x, pos, num_to_select=None, budget_fn=None, per
     if dense:
         x_out = _dense_storage(q, k, v, shp).float()
         sparsity = 0.0
+        self._ress_status = None   # a dense forward leaves nothing to report
     else:
         qb, kbf, vbf = (t.to(torch.bfloat16) for t in (q, k, v))
         order = _device_patch_order(self, patch_order, grid, q.device)
@@ -334,6 +338,8 @@ def ress_attention_forward(self, x, pos, num_to_select=None, budget_fn=None, per
         self._ress_status = LayerResult(out=None, unconverged=res.unconverged, budget_iters=res.budget_iters,
                                         max_iters=res.max_iters, attn_status=res.attn_status)
         sparsity = res.sparsity() if aux_store is not None else None
+        if eager_check and aux_store is None:
+            res.check()
     if aux_store is not None:
         if aux_full and res is not None:
             aux_store["value"] = AttentionAux(

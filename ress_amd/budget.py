@@ -133,11 +133,15 @@ class HessBudget:
             # a sparse-ratio baseline does not depend on the scores: every row gets
             # int(k_blk * (1 - sparse_ratio)). It is made once per shape and device and
             # only read afterwards, so the step launches no fill for it.
+            # Under HIP graph capture the fill kernel would only be recorded, not run, and
+            # the tensor would belong to the graph's pool: such a baseline is made for the
+            # graph alone and not kept.
             key = (tuple(attn_pooled.shape), float(sparse_ratio), str(attn_pooled.device))
             baseline = self._uniform_baseline.get(key)
             if baseline is None:
                 baseline = compute_baseline_num_to_select(attn_pooled, sparse_ratio, None)
-                self._uniform_baseline[key] = baseline
+                if not (attn_pooled.is_cuda and torch.cuda.is_current_stream_capturing()):
+                    self._uniform_baseline[key] = baseline
         else:
             baseline = compute_baseline_num_to_select(attn_pooled, sparse_ratio, cdf_threshold)
         max_val = attn_pooled.shape[-1]

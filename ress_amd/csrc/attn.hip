@@ -799,7 +799,10 @@ __device__ __forceinline__ void attn_row_f16(const AttnArgs& a, const int* __res
     for (int i = l; i < nv_row; i += 64) kmax = fmaxf(kmax, kn[lut_row[i]]);
     kmax = wave_max(kmax);
     const float m0 = sqrtf(pair_sum(qq)) * kmax;
-    if (l == 0) vote[w] = __any(!(m0 <= RESS_BOUND_MAX)) ? 1 : 0;  // NaN fails the test
+    // the vote runs with every lane active (each lane pair holds one query of the wave's
+    // 32); NaN fails the test
+    const int over = __any(!(m0 <= RESS_BOUND_MAX)) ? 1 : 0;
+    if (l == 0) vote[w] = over;
     // operands fp16 cannot hold (|x| >= 65520): an infinite key norm (prep's marker) or a
     // query element; the row's result is not meaningful and the caller is told so
     bool q_over = false;
@@ -1232,7 +1235,7 @@ RESS_API int ress_sparse_attn_fwd(const void* q_i8, const void* q_lo, const void
 // sqB/sqH/sqT, converted to fp16 per row in registers; k_pack the fp16 key blocks and
 // k_norm the per-block largest key norms ress_prep_qkv writes (16-bit operands), v_pack
 // its packed bf16 V. A row whose logit bound |q'| * max key norm is at most
-// RESS_BOUND_MAX runs with pre-scaled fp16 queries and a fixed offset (no running max);
+// RESS_BOUND_MAX for every query runs with pre-scaled fp16 queries, P = exp2(logit) (no offset, no running max);
 // other rows use exact fp16 queries and the running max (see attn_row_f16). patch_order:
 // as for ress_sparse_attn_fwd.
 RESS_API int ress_sparse_attn_fwd_f16(const void* q, long long sqB, long long sqH, long long sqT, const void* k_pack,
@@ -1415,6 +1418,19 @@ static int scratch_address(void** out) {
 }
 
 RESS_API long long ress_noalloc_scratch_bytes(void) { return RESS_NOALLOC_SCRATCH_BYTES; }
+
+// Device address of the current device's operand-status word (int32) inside `scratch`:
+// word 24 of the schedule header, which every ress_sparse_attn_fwd_f16_noalloc call clears
+// when it starts and sets to RESS_F16_KEY_RANGE | RESS_F16_QUERY_RANGE for a key / query
+// element outside fp16's range. Read it (a 4-byte device-to-host copy) after the call has
+// completed and before the next call on the device.
+RESS_API int ress_noalloc_status_address(void** out) {
+  RESS_REQUIRE(out != nullptr, "ress_noalloc_status_address: null output pointer");
+  void* base = nullptr;
+  if (scratch_address(&base) != 0) return -1;
+  *out = reinterpret_cast<int*>(base) + 24;
+  return 0;
+}
 
 RESS_API int ress_sparse_attn_fwd_f16_noalloc(const void* q, long long sqB, long long sqH, long long sqT,
                                               const void* k_pack, const void* k_norm, const void* v_pack,

@@ -24,6 +24,7 @@ CALL_ATTRIBUTES = (
     ("protect_own_frame", False),
     ("attention_sink", 0),
     ("patch_order", None),
+    ("eager_check", False),
 )
 
 

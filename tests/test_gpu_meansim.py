@@ -105,7 +105,8 @@ def test_meansim_cut_with_ties_and_edge_thresholds(dev, Tk):
 
 
 def test_meansim_longest_rows(dev):
-    """4100 key blocks (the workgroup kernel's value sort over 8192 slots, scan tie-break)."""
+    """4100 key blocks (the workgroup kernel: radix CDF descent over the row in LDS, ties
+    ranked by a workgroup scan)."""
     q, k = _qk(12, 1, 1, 1030, 4100 * 64, dup=True, zeros=True)
     _check(q, k, k.float().mean(2, keepdim=True), 0.2, 0.95, 1374, dev)
 

@@ -14,7 +14,7 @@ import torch
 
 import ress_amd as ress
 import ress_amd.wiring as wiring
-from ress_amd import synth
+from ress_amd import budget, synth
 from ress_amd.aggregator import build_vggt_aggregator, synthetic_frames
 
 pytestmark = pytest.mark.gpu
@@ -129,3 +129,36 @@ def test_modes_do_not_leak(models):
         b = model(images)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+def test_eager_check_raises_in_the_forward_and_dense_clears_status(models):
+    """A HeSS budget that cannot converge (iteration cap 1, one head wanting far more than
+    the candidate count) is reported by check_layers after the forward by default, and by the
+    forward itself with the module attribute eager_check (the reference raises at once,
+    _proportional.py:112-113). A later dense forward leaves nothing to report."""
+    model, images, _ = models
+    scores = torch.full((3, DEPTH, HEADS), 1.0)
+    scores[0, :, 0] = 50.0
+    hb = budget.HessBudget(scores, scores, lam=0.5, max_iters=1)
+    attns = wiring.global_attns(model)
+    try:
+        with torch.no_grad():
+            ress.apply_hess(model, 0.2)
+            for a in attns:
+                a.budget_fn = lambda ap: hb.num_to_select(0, ap, 0.2, None, 1.0)
+            model(images)
+            with pytest.raises(RuntimeError, match="did not converge"):
+                ress.check_layers(model)
+            for a in attns:
+                a.eager_check = True
+            with pytest.raises(RuntimeError, match="did not converge"):
+                model(images)
+            for a in attns:
+                a.eager_check = False
+            ress.apply_dense(model)
+            model(images)
+        ress.check_layers(model)
+    finally:
+        for a in attns:
+            a.eager_check = False
+        ress.apply_dense(model)

@@ -418,9 +418,9 @@ def test_head_budget_on_shipped_tables(name, dev):
 
 @pytest.mark.parametrize("q_mul", [1.0, 8.0, 0.0], ids=["mixed", "running_max", "zero_q"])
 def test_f16_bounded_and_running_max_rows(q_mul, dev):
-    """16-bit mode rows run bounded (pre-scaled fp16 queries, fixed offset |q'| * max key norm
-    - 32 in the accumulator) or, when that bound exceeds 64, with exact fp16 queries and the
-    running max. Queries scaled by 8 push every row past the bound (running max everywhere);
+    """16-bit mode rows run bounded (pre-scaled fp16 queries, P = exp2(logit) with no offset
+    and no running max) when |q'| * max key norm is at most 64 for every query of the row, or
+    otherwise with exact fp16 queries and the running max. Queries scaled by 8 push every row past the bound (running max everywhere);
     zero queries give uniform attention on bounded rows; unscaled data mixes both. Every row
     against the fp32 masked softmax."""
     from device_reference import row_errors
@@ -457,6 +457,47 @@ def test_f16_bounded_and_running_max_rows(q_mul, dev):
         assert not bounded.any()
     if q_mul == 0.0:
         assert bounded.all()
+    assert np.nanmax(err) <= ATOL and np.nanmin(cos) >= MIN_COS
+
+
+def test_f16_outlier_query_off_the_vote_lane_takes_running_max(dev):
+    """The bounded/running-max vote covers all 128 queries of a row, not only the first query
+    of each 32-query group. Every patch row gets one outlier query at index 77 (lane 13 of its
+    query group) aligned with a kept key, so that its logits reach ~200 in log2 units while the
+    rest of the row stays far inside the bound. A row that ran bounded would give exp2 overflow
+    (inf/NaN) for that query; the running-max path gives the fp32 masked softmax."""
+    from device_reference import kernel_order, row_errors
+    frames, P, S, H = 4, 1374, 5, 2
+    q, k, v, meta = synth.make_layer_qkv(frames, H=H, seed=4)
+    q = (q.float() * 0.25).to(torch.bfloat16)
+    g = LayerGrid(1, H, frames, P, S)
+    rng = np.random.default_rng(6)
+    keys = torch.from_numpy(rng.random((1, H, g.q_blk_p, g.n_cand)).astype(np.float32)).to(dev)
+    counts = torch.from_numpy(rng.integers(2, g.n_cand + 1, (1, H, g.q_blk_p)).astype(np.int32)).to(dev)
+    _, lut, nv = kernels.select_blocks(keys, counts, g, 2)
+    lutc, nvc = lut.cpu(), nv.cpu()
+    order = kernel_order(frames, P, S, "cpu")
+    c = 0.125 * 1.4426950408889634
+    qf, kf = q.float(), k.float()
+    worst_logit = np.inf
+    for h in range(H):
+        for r in range(g.q_blk_p):
+            kb = int(lutc[h, r, 0])                    # a kept key block of the row
+            kk = kf[0, h, order[kb * 64]]              # its first key (kernel order)
+            scale = 200.0 / (c * float(kk.dot(kk)))
+            q[0, h, order[r * 128 + 77]] = (kk * scale).to(torch.bfloat16)
+            qo = q[0, h, order[r * 128 + 77]].float()
+            kept = torch.cat([torch.arange(int(b) * 64, min(int(b) * 64 + 64, g.Tk)) for b in lutc[h, r, :nvc[h, r]]])
+            worst_logit = min(worst_logit, float((kf[0, h, order[kept]] @ qo).max()) * c)
+    assert worst_logit > 128.0, worst_logit   # exp2 of the outlier's logits overflows fp32
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    blocks = kernels.prepare_blocks(qd, kd, vd, g, mode="f16")
+    out = kernels.sparse_attention(blocks, lut, nv)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    err, cos = row_errors(out, qd, kd, vd, g, lut, nv)
+    print(f"[f16 outlier q77] min outlier logit {worst_logit:.1f} log2 units: max-abs {np.nanmax(err):.3e} "
+          f"min-cos {np.nanmin(cos):.6f}")
     assert np.nanmax(err) <= ATOL and np.nanmin(cos) >= MIN_COS
 
 

@@ -47,3 +47,34 @@ def test_noalloc_matches_workspace_entry_point(dev):
         got = _run("ress_sparse_attn_fwd_f16_noalloc", g, blocks, lut, nvalid, dev)
         assert not torch.isnan(got).any()
         assert torch.equal(got, want)
+
+
+def _read_status_word():
+    """The noalloc call's operand-status word, read from its device address with a 4-byte
+    hipMemcpy (device to host)."""
+    import ctypes
+    addr = ctypes.c_void_p()
+    _lib.call("ress_noalloc_status_address", ctypes.byref(addr))
+    hip = ctypes.CDLL("libamdhip64.so")
+    word = ctypes.c_int(-1)
+    assert hip.hipMemcpy(ctypes.byref(word), addr, ctypes.c_size_t(4), 2) == 0   # hipMemcpyDeviceToHost
+    return word.value
+
+
+def test_noalloc_reports_fp16_range_through_its_status_word(dev):
+    """A key element fp16 cannot hold (70000; bf16 can) is reported in the noalloc call's
+    status word, as ress_sparse_attn_fwd_f16 reports it in its workspace; the next call on
+    clean data clears the word."""
+    frames, H, seed = 2, 4, 2
+    q, k, v, meta = synth.make_layer_qkv(frames, H=H, seed=seed)
+    g = LayerGrid(1, H, frames, meta["P"], meta["S"])
+    k_bad = k.clone()
+    k_bad[0, 1, 7, 3] = 70000.0
+    counts = torch.full((1, H, g.q_blk_p), max(2, g.n_cand // 2), dtype=torch.int32, device=dev)
+    keys = torch.ones(1, H, g.q_blk_p, g.n_cand, device=dev)
+    _, lut, nvalid = kernels.select_blocks(keys, counts, g, 2)
+    for kk, want in ((k_bad, 1), (k, 0)):
+        print(f"[noalloc status] key element {float(kk[0, 1, 7, 3]):.0f}", flush=True)
+        blocks = kernels.prepare_blocks(q.to(dev), kk.to(dev), v.to(dev), g, mode="f16")
+        _run("ress_sparse_attn_fwd_f16_noalloc", g, blocks, lut, nvalid, dev)
+        assert _read_status_word() == want
