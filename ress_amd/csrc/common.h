@@ -328,4 +328,4 @@ __device__ __forceinline__ float sum8_tree(float v) {
   return v;
 }
 
-__host__ __device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }
+__host__ __device__ constexpr __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }
