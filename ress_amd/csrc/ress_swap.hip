@@ -24,8 +24,8 @@
 //    restored (pd = -P) and compensated (pd = +P) candidates in four classes k mod 4, each
 //    a sequential chain over increasing k (fmaf for the products), combined as
 //    (d0 + d1) + (d2 + d3).
-//  * The 64-term products and sums of M (M v_bar_query, M g, ||g||^2_M, the term_q sums)
-//    are sequential fp32 chains in index order.
+//  * The 64-term products and sums of M (M v_bar_query, M g, ||g||^2_M, the term_q sums,
+//    and term_k once per head) are sequential fp32 chains in index order.
 #include <type_traits>
 
 #include "common.h"
@@ -69,6 +69,31 @@ template <int N>
 __device__ __forceinline__ float rs_tree(const float* x) {
   if constexpr (N == 1) return x[0];
   else return rs_tree<N / 2>(x) + rs_tree<N / 2>(x + N / 2);
+}
+
+// Sequential fmaf chain over j = 0..63 of lane i's column of an LDS matrix (col[64*j],
+// big-rounded when BF) and the broadcast vec[j]; sequential sum of a broadcast vector.
+template <bool BF>
+__device__ __forceinline__ float rs_dot_col(const float* col, const float* vec, bool big) {
+  float acc = 0.0f;
+#pragma unroll 8
+  for (int j = 0; j < 64; ++j) {
+    float m = col[j * 64];
+    if constexpr (BF) m = rs_bf(m, big);
+    acc = fmaf(m, vec[j], acc);
+  }
+  return acc;
+}
+__device__ __forceinline__ float rs_sum64(const float* vec) {
+  float acc = 0.0f;
+  for (int i = 0; i < 64; i += 4) {
+    const float4 x = *reinterpret_cast<const float4*>(vec + i);
+    acc = acc + x.x;
+    acc = acc + x.y;
+    acc = acc + x.z;
+    acc = acc + x.w;
+  }
+  return acc;
 }
 
 // Per-head preparation, 64 key blocks per workgroup: Vp = big(V) [kb_p][64] (bf16 bits when
@@ -185,6 +210,7 @@ __global__ __launch_bounds__(RsShape<B16>::TPB) void k_restore_swap(RsArgs a) {
   extern __shared__ __align__(16) unsigned char lds[];
   __shared__ __align__(16) float4 tb0[TB];
   __shared__ __align__(16) float4 tb1[TB];
+  __shared__ __align__(16) float4 tb2[TB];
   __shared__ int rowflag[2][RsShape<B16>::WAVES];
 
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -258,6 +284,26 @@ __global__ __launch_bounds__(RsShape<B16>::TPB) void k_restore_swap(RsArgs a) {
   };
   const uint32_t vsel = (lane & 1) ? 0x03020c0cu : 0x01000c0cu;  // B16: this lane's half as fp32
   auto vdim = [&](uint32_t word) -> float { return __uint_as_float(__builtin_amdgcn_perm(0u, word, vsel)); };
+  // Collective pass over T tiles, three buffers (tile t in buffer t % 3), the DMA two tiles
+  // ahead. Step t: wait for tile t (tile t+1 may stay in flight), barrier, pre(t) -- every
+  // access to dynamic LDS of the step --, the DMA of tile t+2 into the buffer of tile t-1,
+  // then body(tile, t), which reads the static tile buffer only: the compiler keeps an LDS
+  // access it cannot tell apart from an LDS-DMA target behind a wait for that DMA.
+  constexpr int DPT = (TB + TPB - 1) / TPB;  // DMA instructions per tile per wave (at most)
+  auto step3 = [&](int T, int t, const float4* cur, float4* ahead, auto&& pre, auto&& body) {
+    if (t + 1 < T) rs_wait_vmcnt<DPT>();
+    else rs_wait_vmcnt<0>();
+    rs_barrier();
+    pre(t);
+    if (t + 2 < T) tile_dma(ahead, t + 2);
+    body(cur, t);
+  };
+  auto stream_begin = [&](int T) {
+    rs_wait_vmcnt<0>();  // no other vector-memory operation of the wave is outstanding
+    rs_barrier();        // every wave is done with the tile buffers of the previous collective
+    tile_dma(tb0, 0);
+    if (T > 1) tile_dma(tb1, 1);
+  };
 
   // ---- SUMK over keys 0..64*T-1 of tile-streamed V: returns (dot = sum_k pd_k V[k][lane],
   // sum = sum_k pd_k), pd_k = PbL[k] (masked by the 64-bit word mask(t) of tile t when MASKED).
@@ -270,49 +316,80 @@ __global__ __launch_bounds__(RsShape<B16>::TPB) void k_restore_swap(RsArgs a) {
     float acc[C], sps[C];
 #pragma unroll
     for (int cc = 0; cc < C; ++cc) acc[cc] = sps[cc] = 0.0f;
+    // W = 4: this wave's pd of the tile (rows 16j + C*w + cc) read in pre(); wider waves (more
+    // classes each) read them in the body, as registers would not hold them
+    constexpr bool PRE = W == 4;
+    float pt[PRE ? 4 * C : 1];
+    auto pre = [&](int t) {
+      if constexpr (!PRE) return;
+      unsigned long long mw = 0;
+      if constexpr (MASKED) mw = mask[t];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int cc = 0; cc < C; cc += 4) {
+          const float4 p4 = *reinterpret_cast<const float4*>(PbL + 64 * t + 16 * j + C * w + cc);
+          pt[C * j + cc] = p4.x;
+          pt[C * j + cc + 1] = p4.y;
+          pt[C * j + cc + 2] = p4.z;
+          pt[C * j + cc + 3] = p4.w;
+        }
+        if constexpr (MASKED) {
+          // the drop bits of the wave's 16 rows of group j, in a uniform register
+          const uint32_t half = __builtin_amdgcn_readfirstlane(j < 2 ? (uint32_t)mw : (uint32_t)(mw >> 32));
+          const uint32_t bits = half >> (16 * (j & 1) + C * w);
+#pragma unroll
+          for (int cc = 0; cc < C; ++cc) pt[C * j + cc] = ((bits >> cc) & 1u) ? pt[C * j + cc] : 0.0f;
+        }
+      }
+    };
     auto body = [&](const float4* tile, int t) {
       const float* tf = reinterpret_cast<const float*>(tile);
       const uint32_t* tw = reinterpret_cast<const uint32_t*>(tile);
       unsigned long long mw = 0;
-      if constexpr (MASKED) mw = mask[t];
+      if constexpr (MASKED && !PRE) mw = mask[t];
       // with 8 or 16 classes per wave the four 16-row groups run as a loop: unrolled, their
       // loads would be paired across groups and all issued ahead of the arithmetic
 #pragma unroll(C > 4 ? 1 : 4)
       for (int j = 0; j < 4; ++j) {
         float pv[C], vv[C];
+        if constexpr (PRE) {
 #pragma unroll
-        for (int cc = 0; cc < C; cc += 4) {
-          const float4 p4 = *reinterpret_cast<const float4*>(PbL + 64 * t + 16 * j + C * w + cc);
-          pv[cc] = p4.x;
-          pv[cc + 1] = p4.y;
-          pv[cc + 2] = p4.z;
-          pv[cc + 3] = p4.w;
+          for (int cc = 0; cc < C; ++cc) pv[cc] = pt[(C * j + cc) % (PRE ? 4 * C : 1)];
+        } else {
+#pragma unroll
+          for (int cc = 0; cc < C; cc += 4) {
+            const float4 p4 = *reinterpret_cast<const float4*>(PbL + 64 * t + 16 * j + C * w + cc);
+            pv[cc] = p4.x;
+            pv[cc + 1] = p4.y;
+            pv[cc + 2] = p4.z;
+            pv[cc + 3] = p4.w;
+          }
+          if constexpr (MASKED) {
+            const uint32_t half = __builtin_amdgcn_readfirstlane(j < 2 ? (uint32_t)mw : (uint32_t)(mw >> 32));
+            const uint32_t bits = half >> (16 * (j & 1) + C * w);
+#pragma unroll
+            for (int cc = 0; cc < C; ++cc) pv[cc] = ((bits >> cc) & 1u) ? pv[cc] : 0.0f;
+          }
         }
 #pragma unroll
         for (int cc = 0; cc < C; ++cc) vv[cc] = B16 ? vdim(tw[voff[cc] + 512 * j]) : tf[voff[cc] + 1024 * j];
 #pragma unroll
         for (int cc = 0; cc < C; ++cc) {
-          float pd = pv[cc];
-          if constexpr (MASKED) pd = ((mw >> (16 * j + C * w + cc)) & 1ull) ? pd : 0.0f;
-          acc[cc] = fmaf(pd, vv[cc], acc[cc]);
-          sps[cc] = sps[cc] + pd;
+          acc[cc] = fmaf(pv[cc], vv[cc], acc[cc]);
+          sps[cc] = sps[cc] + pv[cc];
         }
       }
     };
-    rs_barrier();  // every wave is done with the tile buffers of the previous collective
-    tile_dma(tb0, 0);
-    auto step = [&](const float4* cur, float4* other, int t) {
-      rs_wait_vmcnt<0>();  // this wave's slices of tile t
-      rs_barrier();        // ... and every other wave's; tile t-1 (in `other`) is done
-      if (t + 1 < T) tile_dma(other, t + 1);
-      body(cur, t);
-    };
+    stream_begin(T);
     int t = 0;
-    for (; t + 2 <= T; t += 2) {
-      step(tb0, tb1, t);
-      step(tb1, tb0, t + 1);
+    for (; t + 3 <= T; t += 3) {
+      step3(T, t, tb0, tb2, pre, body);
+      step3(T, t + 1, tb1, tb0, pre, body);
+      step3(T, t + 2, tb2, tb1, pre, body);
     }
-    if (t < T) step(tb0, tb1, t);
+    if (t < T) step3(T, t, tb0, tb2, pre, body);
+    if (t + 1 < T) step3(T, t + 1, tb1, tb0, pre, body);
     // the wave's subtree of classes, then the W subtrees
     chain[w * 65 + lane] = rs_tree<C>(acc);
     if (lane == 0) chain[w * 65 + 64] = rs_tree<C>(sps);
@@ -334,70 +411,99 @@ __global__ __launch_bounds__(RsShape<B16>::TPB) void k_restore_swap(RsArgs a) {
   auto products = [&](const float* vec, float (&out)[NS]) {
 #pragma unroll
     for (int i = 0; i < NS; ++i) out[i] = 0.0f;
+    // W = 4: this wave's chunk of vec in registers (read before any DMA of the pass); wider
+    // waves read their chunks per tile
+    constexpr bool VREG = W == 4;
+    float vr[16];
+    if constexpr (VREG) {
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const float4 v4 = *reinterpret_cast<const float4*>(vec + 16 * w + 4 * q4);
+        vr[4 * q4] = v4.x;
+        vr[4 * q4 + 1] = v4.y;
+        vr[4 * q4 + 2] = v4.z;
+        vr[4 * q4 + 3] = v4.w;
+      }
+    }
     auto combine = [&](int t) -> float {
       float p[W];
 #pragma unroll
       for (int u = 0; u < W; ++u) p[u] = prod[((t & 1) * W + u) * 64 + lane];
       return rs_tree<W>(p);
     };
-    rs_barrier();
-    tile_dma(tb0, 0);
+    // the partial of tile t is held in a register, written to prod[t & 1] at step t+1 and
+    // combined by the owner wave (t % W) at step t+2
+    float held = 0.0f;
+    stream_begin(G);
 #pragma unroll
     for (int t = 0; t < NS * W; ++t) {
       if (t < G) {
-        const float4* cur = (t & 1) ? tb1 : tb0;
-        float4* other = (t & 1) ? tb0 : tb1;
-        rs_wait_vmcnt<0>();
-        rs_barrier();
-        if (t + 1 < G) tile_dma(other, t + 1);
-        if (t >= 1 && w == (t - 1) % W) out[(t - 1) / W] = combine(t - 1);
-        float part[CH];
+        const float4* cur = t % 3 == 0 ? tb0 : (t % 3 == 1 ? tb1 : tb2);
+        float4* ahead = t % 3 == 0 ? tb2 : (t % 3 == 1 ? tb0 : tb1);
+        auto pre = [&](int) {
+          if (t >= 1) prod[(((t - 1) & 1) * W + w) * 64 + lane] = held;
+          if (t >= 2 && w == (t - 2) % W) out[(t - 2) / W] = combine(t - 2);
+        };
+        auto body = [&](const float4* tile, int) {
+          float part[CH];
 #pragma unroll
-        for (int ch = 0; ch < CH; ++ch) {
-          const int c = CH * w + ch;  // dims 16c..16c+15 of candidate 64t + lane
-          float vc[16];  // vec[16c..16c+15], broadcast reads
+          for (int ch = 0; ch < CH; ++ch) {
+            const int c = CH * w + ch;  // dims 16c..16c+15 of candidate 64t + lane
+            float vc[16];
+            if constexpr (VREG) {
 #pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) {
-            const float4 v4 = *reinterpret_cast<const float4*>(vec + 16 * c + 4 * q4);
-            vc[4 * q4] = v4.x;
-            vc[4 * q4 + 1] = v4.y;
-            vc[4 * q4 + 2] = v4.z;
-            vc[4 * q4 + 3] = v4.w;
-          }
-          float s = 0.0f;
-          if constexpr (B16) {
-            uint4 q[2];
+              for (int u = 0; u < 16; ++u) vc[u] = vr[u];
+            } else {
 #pragma unroll
-            for (int e = 0; e < 2; ++e) q[e] = *reinterpret_cast<const uint4*>(cur + lane * 8 + ((2 * c + e) ^ (lane & 7)));
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-              float x[8];
-              unpack_bf16x8(q[e], x);
-#pragma unroll
-              for (int u = 0; u < 8; ++u) s = fmaf(x[u], vc[8 * e + u], s);
+              for (int q4 = 0; q4 < 4; ++q4) {
+                const float4 v4 = *reinterpret_cast<const float4*>(vec + 16 * c + 4 * q4);
+                vc[4 * q4] = v4.x;
+                vc[4 * q4 + 1] = v4.y;
+                vc[4 * q4 + 2] = v4.z;
+                vc[4 * q4 + 3] = v4.w;
+              }
             }
-          } else {
-            float4 q[4];
+            float sacc = 0.0f;
+            if constexpr (B16) {
+              uint4 q[2];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) q[e] = cur[lane * 16 + ((4 * c + e) ^ (lane & 15))];
+              for (int e = 0; e < 2; ++e)
+                q[e] = *reinterpret_cast<const uint4*>(tile + lane * 8 + ((2 * c + e) ^ (lane & 7)));
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              s = fmaf(q[e].x, vc[4 * e], s);
-              s = fmaf(q[e].y, vc[4 * e + 1], s);
-              s = fmaf(q[e].z, vc[4 * e + 2], s);
-              s = fmaf(q[e].w, vc[4 * e + 3], s);
+              for (int e = 0; e < 2; ++e) {
+                float x[8];
+                unpack_bf16x8(q[e], x);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) sacc = fmaf(x[u], vc[8 * e + u], sacc);
+              }
+            } else {
+              float4 q[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) q[e] = tile[lane * 16 + ((4 * c + e) ^ (lane & 15))];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                sacc = fmaf(q[e].x, vc[4 * e], sacc);
+                sacc = fmaf(q[e].y, vc[4 * e + 1], sacc);
+                sacc = fmaf(q[e].z, vc[4 * e + 2], sacc);
+                sacc = fmaf(q[e].w, vc[4 * e + 3], sacc);
+              }
             }
+            part[ch] = sacc;
+            if constexpr (CH > 1) __builtin_amdgcn_sched_barrier(0);
           }
-          part[ch] = s;
-          if constexpr (CH > 1) __builtin_amdgcn_sched_barrier(0);
-        }
-        prod[((t & 1) * W + w) * 64 + lane] = rs_tree<CH>(part);
+          held = rs_tree<CH>(part);
+        };
+        step3(G, t, cur, ahead, pre, body);
       }
     }
+    // the last tile's partial, then the last two tiles' combines
+#pragma unroll
+    for (int t = 0; t < NS * W; ++t)
+      if (t == G - 1) prod[((t & 1) * W + w) * 64 + lane] = held;
     rs_barrier();
 #pragma unroll
     for (int t = 0; t < NS * W; ++t)
-      if (t == G - 1 && w == t % W) out[t / W] = combine(t);
+      if (t >= G - 2 && t < G && w == t % W) out[t / W] = combine(t);
   };
 
   // ---- sum of a wave-uniform count over the row's W waves (counter slot `slot`); one barrier
@@ -515,22 +621,11 @@ __global__ __launch_bounds__(RsShape<B16>::TPB) void k_restore_swap(RsArgs a) {
   vqs[lane] = vq;
   __builtin_amdgcn_wave_barrier();
   // quadratic_deviation's query side: Mvq = big(Mb vq), term_q = big(sum big(Mvq*vq))
-  float mvq = 0.0f;
-#pragma unroll 8
-  for (int j = 0; j < 64; ++j) mvq = fmaf(rs_bf(M32T[j * 64 + lane], big), vqs[j], mvq);
-  mvq = rs_bf(mvq, big);
+  const float mvq = rs_bf(rs_dot_col<true>(M32T + lane, vqs, big), big);
   t0[lane] = mvq;
   t1[lane] = rs_bf(mvq * vq, big);
   __builtin_amdgcn_wave_barrier();
-  float tq = 0.0f;
-  for (int i = 0; i < 64; i += 4) {
-    const float4 x = *reinterpret_cast<const float4*>(t1 + i);
-    tq = tq + x.x;
-    tq = tq + x.y;
-    tq = tq + x.z;
-    tq = tq + x.w;
-  }
-  tq = rs_bf(tq, big);
+  const float tq = rs_bf(rs_sum64(t1), big);
   // s, s_cut, s^2 per candidate
   float ssq[NS];
   uint32_t key[NS];
@@ -579,20 +674,11 @@ __global__ __launch_bounds__(RsShape<B16>::TPB) void k_restore_swap(RsArgs a) {
     __builtin_amdgcn_wave_barrier();
     t1[lane] = g;
     __builtin_amdgcn_wave_barrier();
-    float mg = 0.0f;
-#pragma unroll 8
-    for (int j = 0; j < 64; ++j) mg = fmaf(M32T[j * 64 + lane], t1[j], mg);
+    const float mg = rs_dot_col<false>(M32T + lane, t1, big);
     t2[lane] = g * mg;  // products of ||g||^2_M
     t3[lane] = mg;
     __builtin_amdgcn_wave_barrier();
-    float n2 = 0.0f;
-    for (int i = 0; i < 64; i += 4) {
-      const float4 x = *reinterpret_cast<const float4*>(t2 + i);
-      n2 = n2 + x.x;
-      n2 = n2 + x.y;
-      n2 = n2 + x.z;
-      n2 = n2 + x.w;
-    }
+    const float n2 = rs_sum64(t2);
     float K = tm - sp;
     K = K < 1e-6f ? 1e-6f : K;
     gn = n2;
@@ -680,15 +766,7 @@ __global__ __launch_bounds__(RsShape<B16>::TPB) void k_restore_swap(RsArgs a) {
     t2[lane] = vq * t3[lane];
     t0[lane] = rs_bf(t3[lane], big);
     __builtin_amdgcn_wave_barrier();
-    float tqr = 0.0f;
-    for (int i = 0; i < 64; i += 4) {
-      const float4 x = *reinterpret_cast<const float4*>(t2 + i);
-      tqr = tqr + x.x;
-      tqr = tqr + x.y;
-      tqr = tqr + x.z;
-      tqr = tqr + x.w;
-    }
-    const float tqb = rs_bf(tqr, big);
+    const float tqb = rs_bf(rs_sum64(t2), big);
     float tk[NS];
     products(t0, tk);  // term_k = v_k . big(Mg)
     // restore quality of the dropped (higher is better), then the compensation quality of
@@ -981,17 +1059,6 @@ __global__ __launch_bounds__(64 * RSR_WAVES) void k_restore_swap_row(RsArgs a, i
       if (ng == 3) run(std::integral_constant<int, 12>{});
     }
   };
-  auto sum64 = [&](const float* vec) {
-    float acc = 0.0f;
-    for (int i = 0; i < 64; i += 4) {
-      const float4 x = *reinterpret_cast<const float4*>(vec + i);
-      acc = acc + x.x;
-      acc = acc + x.y;
-      acc = acc + x.z;
-      acc = acc + x.w;
-    }
-    return acc;
-  };
 
   const int q_begin = bgrp * rows_per_wg, q_end = min(a.q_blk, (bgrp + 1) * rows_per_wg);
   for (int q = q_begin + w; q < q_end; q += RSR_WAVES) {
@@ -1014,14 +1081,11 @@ __global__ __launch_bounds__(64 * RSR_WAVES) void k_restore_swap_row(RsArgs a, i
     }
     vqs[lane] = vq;
     __builtin_amdgcn_wave_barrier();
-    float mvq = 0.0f;
-#pragma unroll 8
-    for (int j = 0; j < 64; ++j) mvq = fmaf(rs_bf(M32T[j * 64 + lane], big), vqs[j], mvq);
-    mvq = rs_bf(mvq, big);
+    const float mvq = rs_bf(rs_dot_col<true>(M32T + lane, vqs, big), big);
     t0[lane] = mvq;
     t1[lane] = rs_bf(mvq * vq, big);
     __builtin_amdgcn_wave_barrier();
-    const float tq = rs_bf(sum64(t1), big);
+    const float tq = rs_bf(rs_sum64(t1), big);
     uint32_t key[NPL];
     {
       float cr[NPL];
@@ -1067,13 +1131,11 @@ __global__ __launch_bounds__(64 * RSR_WAVES) void k_restore_swap_row(RsArgs a, i
       __builtin_amdgcn_wave_barrier();
       t1[lane] = g;
       __builtin_amdgcn_wave_barrier();
-      float mg = 0.0f;
-#pragma unroll 8
-      for (int j = 0; j < 64; ++j) mg = fmaf(M32T[j * 64 + lane], t1[j], mg);
+      const float mg = rs_dot_col<false>(M32T + lane, t1, big);
       t2[lane] = g * mg;
       t3[lane] = mg;
       __builtin_amdgcn_wave_barrier();
-      const float n2 = sum64(t2);
+      const float n2 = rs_sum64(t2);
       float K = tm - sp;
       K = K < 1e-6f ? 1e-6f : K;
       gn = n2;
@@ -1096,7 +1158,7 @@ __global__ __launch_bounds__(64 * RSR_WAVES) void k_restore_swap_row(RsArgs a, i
       t2[lane] = vq * t3[lane];
       t0[lane] = rs_bf(t3[lane], big);
       __builtin_amdgcn_wave_barrier();
-      const float tqb = rs_bf(sum64(t2), big);
+      const float tqb = rs_bf(rs_sum64(t2), big);
       float tk[NPL];
       products(t0, tk);  // term_k = v_k . big(Mg)
       auto quality = [&](int i, bool restore_side) -> float {
