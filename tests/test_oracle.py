@@ -328,6 +328,27 @@ def test_hilbert_order_is_a_bijection_with_unit_steps():
     assert synth.gilbert_order(37, 37)[0] == (0, 0)
 
 
+def test_hilbert_order_matches_reference_vectors():
+    """The curve equals the reference's own (src/ress/models/hilbert.py gilbert2d and
+    make_hilbert_gather_idx), cell for cell, on the 37x37 patch grid and two odd rectangles:
+    vectors written by tests/golden/make_hilbert_orders.py. The gather table the kernels read
+    in place (patch_order: kernel patch j = storage patch perm[j]) is the reference's
+    forward gather, and its inverse is the reference's inverse gather."""
+    import json
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "hilbert_orders.json")
+    grids = json.load(open(path))["grids"]
+    assert [(g["width"], g["height"]) for g in grids] == [(37, 37), (13, 11), (23, 7)]
+    for g in grids:
+        w, h = g["width"], g["height"]
+        assert [list(c) for c in synth.gilbert_order(w, h)] == g["cells"]
+        perm = synth.hilbert_permutation(w, h)
+        assert perm.tolist() == g["gather"]
+        inv = np.empty_like(perm)
+        inv[perm] = np.arange(w * h)
+        assert inv.tolist() == g["gather_inverse"]
+
+
 def test_generator_is_deterministic_and_shaped():
     q1, k1, v1, m = synth.make_layer_qkv(2, H=2)
     q2, _, _, _ = synth.make_layer_qkv(2, H=2)

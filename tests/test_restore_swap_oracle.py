@@ -6,6 +6,9 @@
 * the bf16 rounding ladder against the same restatement run with the reference's bf16
   casts, on inputs whose dot products are exact in fp32 (so torch's summation order
   cannot matter and only the rounding points are compared);
+* the bf16 ladder against its float64 definition on the same bf16 inputs: the scores, the
+  cut key and J of the cut within per-term rounding bounds, and the cut's keep set equal to
+  the float64 top-nts wherever the margin at the threshold exceeds the bounds;
 * invariants: the kept count is min(nts, n_cand); track_best never returns a set with a
   larger J than the initial cut; the reported J is the float64 J of the returned set;
 * the identities the reference states, each computed from its definition in float64
@@ -215,3 +218,124 @@ def test_identity_metric_is_head_space_damage():
         vq = np.einsum("hqk,hkd->hqd", A64, V64)
         dmg = A64[..., :n] * np.linalg.norm(vq[:, :, None, :] - V64[:, None, :n, :], axis=-1)
         np.testing.assert_allclose(s, dmg, rtol=5e-5, atol=1e-7)
+
+
+# ---- the _bf16 ladder against its float64 definition -------------------------------------
+# The production recipe (restore_swap_iter5_bf16_trackbest) rounds the k-wide tensors to
+# bf16 at the reference's points (projected.py:763-783, 868-878). test_bf16_ladder_on_exact_sums
+# pins where the roundings sit; these pin how far they may move the result: every quantity
+# the cut and the objective rank by stays within a rounding bound of its float64 definition
+# on the same bf16 inputs (P, V and M rounded to bf16, as the recipe casts them), and the cut
+# keeps the float64 top-nts wherever the ranking margin at the threshold exceeds the bounds.
+_U = 2.0 ** -8  # bf16 unit roundoff (8 significand bits, round to nearest)
+
+
+def _bf(x):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(torch.bfloat16).double().numpy()
+
+
+def _ladder_bounds(A, V, M, n):
+    """float64 s (and the cut key) on the bf16 inputs, and per-candidate bounds. With
+    m = Mb vq, mk = Mb V_k and e = vq - V_k, the ladder's roundings move the expanded
+    quadratic form term_q - 2 cross + term_k by at most u times: 2 sum|vq_i (Mb e)_i|
+    (v_bar_query itself), 2 sum|m_i vq_i| + |term_q| (M vq, the products, their sum),
+    2 (sum|m_i V_ki| + |cross|) (M vq, the cross sum), 2 sum|mk_i V_ki| + |term_k| (the key
+    side), |term_q - 2 cross| + |quad| (the two additions); 1.25 of that covers the fp32 sums.
+    |sqrt a - sqrt b| <= min(sqrt |a - b|, |a - b| / sqrt b) carries it through the root, and
+    the last roundings (sqrt, P * sqrt, s / (1 - P)) add a few u relative."""
+    Pb, Vb, Mb = _bf(A), _bf(V), _bf(M)
+    vq = np.einsum("hqk,hkd->hqd", Pb, Vb)
+    Vn = Vb[:, :n]
+    m = np.einsum("hij,hqj->hqi", Mb, vq)
+    mk = np.einsum("hij,hkj->hki", Mb, Vn)
+    tq = np.einsum("hqi,hqi->hq", m, vq)[..., None]
+    cr = np.einsum("hqi,hki->hqk", m, Vn)
+    tk = np.einsum("hki,hki->hk", mk, Vn)[:, None, :]
+    quad_raw = tq - 2 * cr + tk
+    quad = np.maximum(quad_raw, 0.0)
+    me = m[:, :, None, :] - mk[:, None, :, :]                      # Mb e_k
+    d = (2 * np.einsum("hqi,hqki->hqk", np.abs(vq), np.abs(me))
+         + 2 * np.einsum("hqi,hqi->hq", np.abs(m), np.abs(vq))[..., None] + np.abs(tq)
+         + 2 * (np.einsum("hqi,hki->hqk", np.abs(m), np.abs(Vn)) + np.abs(cr))
+         + 2 * np.einsum("hki,hki->hk", np.abs(mk), np.abs(Vn))[:, None, :] + np.abs(tk)
+         + np.abs(tq - 2 * cr) + quad)
+    dq = 1.25 * _U * d
+    p = Pb[..., :n]
+    s64 = p * np.sqrt(quad)
+    tol_s = p * np.minimum(np.sqrt(dq), dq / np.maximum(np.sqrt(quad), 1e-300)) + 4 * _U * s64
+    om = np.maximum(1.0 - p, 1e-4)
+    return s64, tol_s, s64 / om, tol_s / om + 3 * _U * s64 / om
+
+
+def _flat_problem(seed, H=2, q_blk=4, kb_p=48):
+    """Softmax rows with logits of scale 0.3: v_bar_query is a broad average, well away from
+    every V_k, so the expanded form's terms do not cancel and the bounds are informative."""
+    rng = np.random.default_rng(seed)
+    logits = rng.normal(size=(H, q_blk, kb_p)) * 0.3
+    A = np.exp(logits)
+    A = (A / A.sum(-1, keepdims=True)).astype(np.float32)
+    V = rng.normal(size=(H, kb_p, 64)).astype(np.float32)
+    W = (rng.normal(size=(H, 64, 64)) / 8).astype(np.float32)
+    M = np.einsum("hji,hjk->hik", W, W).astype(np.float32)
+    return A, V, M, kb_p - 2
+
+
+def test_bf16_scores_within_rounding_bound_of_float64():
+    for seed in range(6):
+        for A, V, M, n in (_softmax_problem(700 + seed, H=2, q_blk=4, kb_p=48), _flat_problem(750 + seed)):
+            s, scut, _, _, _ = oracle.rs_probe(A, V, M, np.zeros(A.shape[:2] + (n,), bool), n, big_bf16=True)
+            s64, tol_s, c64, tol_c = _ladder_bounds(A, V, M, n)
+            assert (np.abs(s.astype(np.float64) - s64) <= tol_s).all(), seed
+            assert (np.abs(scut.astype(np.float64) - c64) <= tol_c).all(), seed
+        # on the flat rows the bound is informative: a few percent of s
+        assert np.median(tol_s / np.maximum(s64, 1e-30)) < 0.05
+
+
+def test_bf16_cut_keeps_float64_top_where_margin_exceeds_bound():
+    decided = 0
+    for seed in range(8):
+        A, V, M, n = _flat_problem(800 + seed, H=4, q_blk=8, kb_p=12)
+        H, Q = A.shape[:2]
+        rng = np.random.default_rng(seed)
+        nts = rng.integers(2, n, size=(H, Q)).astype(np.int32)
+        keep, _ = oracle.restore_swap(A, V, M, nts, n, n_iters=0, big_bf16=True, track_best=False)
+        _, _, c64, tol_c = _ladder_bounds(A, V, M, n)
+        for h in range(H):
+            for q in range(Q):
+                order = np.argsort(-c64[h, q], kind="stable")
+                m = int(nts[h, q])
+                lo, hi = order[m - 1], order[m]   # the last kept, the first dropped (float64)
+                if c64[h, q, lo] - tol_c[h, q, lo] > c64[h, q, hi] + tol_c[h, q, hi]:
+                    want = np.zeros(n, bool)
+                    want[order[:m]] = True
+                    assert np.array_equal(keep[h, q].astype(bool), want), (seed, h, q)
+                    decided += 1
+    assert decided >= 40  # most rows have a margin above the bound
+
+
+def test_bf16_objective_within_rounding_bound_of_float64():
+    """J = ||g||^2_M / K^2 of the cut's drop set, the _bf16 ladder (bf16 sum_Pd, Pd @ v_bar and
+    v_bar_query; fp32 M) against the float64 J on the same bf16 P and V. g = sum_Pd vq - Pd @ V
+    moves by |dg_i| <= u (2.5 sum_Pd |vq_i| + 1.25 |(Pd @ V)_i|) (the three roundings and the
+    fp32 sums), so g^T M g moves by at most 2 |dg|^T |M g| + |dg|^T |M| |dg|."""
+    for seed in range(6):
+        A, V, M, n = _flat_problem(900 + seed)
+        H, Q = A.shape[:2]
+        nts = np.full((H, Q), n // 2, np.int32)
+        keep, _ = oracle.restore_swap(A, V, M, nts, n, n_iters=0, big_bf16=True, track_best=False)
+        drop = ~keep.astype(bool)
+        _, _, J, _, _ = oracle.rs_probe(A, V, M, drop, n, big_bf16=True)
+        Pb, Vb = _bf(A), _bf(V)
+        M64 = M.astype(np.float64)
+        vq = np.einsum("hqk,hkd->hqd", Pb, Vb)
+        Pd = Pb[..., :n] * drop
+        g = Pd.sum(-1)[..., None] * vq - np.einsum("hqk,hkd->hqd", Pd, Vb[:, :n])
+        K = Pb.sum(-1) - Pd.sum(-1)
+        J64 = np.einsum("hqi,hij,hqj->hq", g, M64, g) / K ** 2
+        mv = np.einsum("hqk,hkd->hqd", Pd, Vb[:, :n])
+        gabs = _U * (2.5 * Pd.sum(-1)[..., None] * np.abs(vq) + 1.25 * np.abs(mv))
+        Mg = np.einsum("hij,hqj->hqi", M64, g)
+        dG = 2 * np.einsum("hqi,hqi->hq", gabs, np.abs(Mg)) + np.einsum("hqi,hij,hqj->hq", gabs, np.abs(M64), gabs)
+        tol = dG / K ** 2 + 4 * _U * J64 + 1e-30
+        assert (np.abs(J.astype(np.float64) - J64) <= tol).all(), seed
+        assert np.median(tol / np.maximum(J64, 1e-30)) < 0.2
