@@ -34,7 +34,9 @@ int ress_abi_version(void);
  *   q_i8 [BH][qb_p+qb_s][128][64] int8, q_scale [BH][qb_p+qb_s] f32,
  *   pooled_q [BH][qb_p][64] f32                 qb_p = ceil(T_p/128), qb_s = ceil(T_s/128)
  *   k_i8 [BH][kb_tot][64][64] int8, k_scale [BH][kb_tot] f32   kb_tot = ceil(frames*P/64)
- *   pooled_k, pooled_v [BH][kb_p][64] f32       kb_p = ceil(T_p/64) (patch keys only)
+ *   pooled_k, pooled_v [BH][kb_p][64] f32       kb_p = ceil(T_p/64) (patch keys only), or
+ *                  [BH][kb_tot][64] with pool_all = 1 (every key in kernel order: the
+ *                  sink-mass map, RESS_SINK_MASS, src/ress/models/attention.py:78, 451-452)
  *   v_pack [BH][kb_tot][4096] bf16, ksum [BH][kb_tot][64] f32, km [BH][64] f32
  *   q_lo / k_lo (optional, layouts of q_i8 / k_i8): split-INT8 residual codes, x ~
  *   scale*hi + scale/254*lo, used by ress_sparse_attn_fwd for a two-term INT8 QK^T.
@@ -51,7 +53,7 @@ int ress_prep_qkv(const void* q, const void* k, const void* v, int B, int H, int
                   const int* patch_order, long long sqB, long long sqH, long long sqT, long long skB, long long skH, long long skT,
                   long long svB, long long svH, long long svT, void* q_i8, void* q_lo, void* q_scale,
                   void* pooled_q, void* k_i8, void* k_lo, void* k_scale, void* pooled_k, void* pooled_v,
-                  void* v_pack, void* k_pack, void* ksum, void* km, hipStream_t stream);
+                  void* v_pack, void* k_pack, void* ksum, void* km, int pool_all, hipStream_t stream);
 
 /* Replaces SpargeAttn per_block_int8(q, k) (call site src/ress/models/attention.py:232,
  * patched Q scale spargeattn.patch:38-41). km [BH][64] optional (NULL = no smoothing).

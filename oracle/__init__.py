@@ -57,16 +57,17 @@ def expf(x):
     return np.float32(lib().oracle_expf(ctypes.c_float(float(x))))
 
 
-def prep_qkv(q, k, v, frames, P, S):
+def prep_qkv(q, k, v, frames, P, S, pool_all=False):
     """q,k,v: bf16 (B,H,frames*P,64) (torch tensors or uint16 arrays). Returns a dict of
-    the ress_prep_qkv outputs, shapes as in include/ress_hip.h."""
+    the ress_prep_qkv outputs, shapes as in include/ress_hip.h (pool_all: pooled K/V over
+    every key block, the sink-mass grid)."""
     qu, ku, vu = _u16(q), _u16(k), _u16(v)
     B, H, N, D = qu.shape
     assert D == 64 and N == frames * P
     BH = B * H
     T_p, T_s = frames * (P - S), frames * S
     qbp, qbs = -(-T_p // 128), -(-T_s // 128)
-    kbt, kbp = -(-N // 64), -(-T_p // 64)
+    kbt, kbp = -(-N // 64), -(-(N if pool_all else T_p) // 64)
     out = dict(
         q_i8=np.zeros((BH, qbp + qbs, 128, 64), np.int8),
         q_lo=np.zeros((BH, qbp + qbs, 128, 64), np.int8),
@@ -84,7 +85,7 @@ def prep_qkv(q, k, v, frames, P, S):
     )
     lib().oracle_prep_qkv(_p(qu), _p(ku), _p(vu), BH, frames, P, S, *[_p(out[n]) for n in (
         "q_i8", "q_lo", "q_scale", "pooled_q", "k_i8", "k_lo", "k_scale", "pooled_k", "pooled_v", "v_pack", "ksum",
-        "km", "k_norm")])
+        "km", "k_norm")], 1 if pool_all else 0)
     return out
 
 

@@ -122,11 +122,13 @@ static inline int8_t quant_lo(float x, float scale, int8_t hi) {
 void oracle_prep_qkv(const uint16_t* q, const uint16_t* k, const uint16_t* v, int BH, int frames, int P, int S,
                      int8_t* q_i8, int8_t* q_lo, float* q_scale, float* pooled_q, int8_t* k_i8, int8_t* k_lo,
                      float* k_scale, float* pooled_k, float* pooled_v, uint16_t* v_pack, float* ksum, float* km,
-                     float* k_norm) {
+                     float* k_norm, int pool_all) {
   tokmap m = mkmap(frames, P, S);
   const int N = frames * P, Tk = N;
   const int qbp = cdiv(m.T_p, 128), qbs = cdiv(m.T_s, 128), qbt = qbp + qbs;
-  const int kbt = cdiv(Tk, 64), kbp = cdiv(m.T_p, 64);
+  const int kbt = cdiv(Tk, 64);
+  /* the pooled grid: the patch keys, or every key in kernel order (pool_all) */
+  const int T_pool = pool_all ? Tk : m.T_p, kbp = cdiv(T_pool, 64);
 #pragma omp parallel for schedule(dynamic, 1)
   for (int bh = 0; bh < BH; ++bh) {
     int rows[128];
@@ -160,7 +162,7 @@ void oracle_prep_qkv(const uint16_t* q, const uint16_t* k, const uint16_t* v, in
     for (int kb = 0; kb < kbt; ++kb) {
       const int base = kb * 64;
       const int cnt = Tk - base < 64 ? Tk - base : 64;
-      int cnt_p = m.T_p - base < 64 ? m.T_p - base : 64;
+      int cnt_p = T_pool - base < 64 ? T_pool - base : 64;
       if (cnt_p < 0) cnt_p = 0;
       for (int t = 0; t < cnt; ++t) rows[t] = key_st(base + t, &m);
       for (int d = 0; d < 64; ++d) {

@@ -11,6 +11,7 @@ The hot path runs on hand-written HIP kernels for gfx950 (libress_hip.so, built 
 from ress_amd.api import apply_dense, apply_hess, apply_ress, apply_sparse_vggt, load_backbone
 from ress_amd.attention import check_layers
 from ress_amd.backbones import BACKBONES, get_backbone
+from ress_amd.qkv import declare_rope
 
 __all__ = [
     "BACKBONES",
@@ -19,6 +20,7 @@ __all__ = [
     "apply_ress",
     "apply_sparse_vggt",
     "check_layers",
+    "declare_rope",
     "get_backbone",
     "load_backbone",
 ]

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(_HERE, "libress_hip.so")
 
 # argument codes: p = pointer, i = int, l = long long, f = float, d = double, s = stream
 _SIGS = {
-    "ress_prep_qkv": "pppiiiii" + "p" + "lllllllll" + "ppppppppppppp" + "s",
+    "ress_prep_qkv": "pppiiiii" + "p" + "lllllllll" + "ppppppppppppp" + "i" + "s",
     "ress_per_block_int8": "pppiiii" + "llllll" + "ppppp" + "s",
     "ress_prep_kv_plain": "ppiii" + "llllll" + "ppppp" + "s",
     "ress_pooled_scores": "ppiiiifpp" + "s",

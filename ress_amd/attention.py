@@ -270,6 +270,9 @@ def sparse_global_attention(q, k, v, grid, *, num_to_select=None, budget_fn=None
         if sink_lead:  # forced blocks go on last, so the swap never trades one away
             final_map[..., :sink_lead] = True
         lut, nvalid = kernels.lut_from_map(final_map, grid)
+    if M is not None:  # after every step that can move the map, as the reference records it
+        from ress_amd import projected as _projected
+        _projected.record_layer_drift(M, attn_full, v_bar_full, final_map, grid.n_cand)
     o = kernels.sparse_attention(blocks, lut, nvalid, out=out, out_dtype=out_dtype)
     res = LayerResult(out=o, final_map=final_map, budget_iters=budget_iters, max_iters=max_iters,
                       attn_status=getattr(o, "ress_attn_status", None))
@@ -297,9 +300,14 @@ def ress_attention_forward(self, x, pos, num_to_select=None, budget_fn=None, per
                            joint_select_fn=None, block_criterion="probability", pool_mode="avg",
                            num_special_tokens=5, num_heads=16, shape=None, aux_store=None, aux_full=True,
                            dense=False, retain_output_grad=False, pooled_fallback=False, protect_own_frame=False,
-                           attention_sink=0, patch_order=None, eager_check=False):
+                           attention_sink=0, patch_order=None, eager_check=False, sink_mass=False,
+                           sink_protect=True):
     """Replacement forward of a global-attention block (reference attention.py:296-659),
     same arguments and return value: (B, N*P, dim) after the W_O projection.
+    sink_mass / sink_protect: the reference's RESS_SINK_MASS / RESS_SINK_PROTECT process
+    flags (attention.py:50-79) as per-call arguments with the same defaults: pool the map
+    over every key instead of the patch keys, and keep the block that straddles the patch
+    tail and the special keys out of the candidates (kernels.LayerGrid).
     attention_sink (not a reference argument; default 0 = the reference's behaviour):
     leading tokens whose key blocks every row keeps, as sparse_global_attention.
     patch_order (not a reference argument; the module attribute set by the aggregator's
@@ -318,7 +326,7 @@ def ress_attention_forward(self, x, pos, num_to_select=None, budget_fn=None, per
     B, N, P, hd, nh, S = shp["B"], shp["N"], shp["P"], shp["head_dim"], shp["num_heads"], shp["S"]
     if hd != 64:
         raise ValueError(f"head_dim {hd} unsupported (the kernels are written for 64)")
-    grid = LayerGrid(B=B, H=nh, frames=N, P=P, S=S)
+    grid = LayerGrid(B=B, H=nh, frames=N, P=P, S=S, sink_protect=bool(sink_protect), sink_mass=bool(sink_mass))
     res = None
     if dense:
         x_out = _dense_storage(q, k, v, shp).float()

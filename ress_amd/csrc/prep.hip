@@ -100,8 +100,10 @@ __global__ __launch_bounds__(64) void k_prep_q(const uint16_t* __restrict__ q, S
 //         exact in fp16 unless below 2^-14 in magnitude (the subnormal range) or above 65504
 //  k_norm [BH][kb_tot]  the block's largest key norm sqrt(sum_d k_d^2) (or null): per key
 //         an fmaf chain over each lane's 8 dims, the tree of the 8 lanes, sqrtf; then the max
-//  pooled_k [BH][kb_p][64]  patch-only K means (the scoring grid)
-//  pooled_v [BH][kb_p][64]  patch-only V means (ReSS's v_bar)
+//  pooled_k [BH][kb_pool][64]  K means of the scoring grid: the patch keys only (kb_pool =
+//                              kb_p), or every key in kernel order (kb_pool = kb_tot; the
+//                              sink-mass map, attention.py:78, 451-452)
+//  pooled_v [BH][kb_pool][64]  V means over the same grid (ReSS's v_bar)
 //  v_pack [BH][kb_tot][64 dims][64 keys]  bf16, keys permuted inside every group of
 //         16 as 0-3,8-11,4-7,12-15 so that one 16-byte read per lane is an MFMA
 //         operand; keys past the sequence end are zero.
@@ -111,12 +113,12 @@ __device__ __forceinline__ void prep_kv_block(int kb, int bh, const uint16_t* __
                                               float* __restrict__ ksum, float* __restrict__ pooled_k,
                                               float* __restrict__ pooled_v, uint16_t* __restrict__ v_pack,
                                               uint16_t* __restrict__ k_pack, float* __restrict__ k_norm,
-                                              uint16_t* __restrict__ vt) {
+                                              uint16_t* __restrict__ vt, int T_pool) {
   const int lane = threadIdx.x;
   const int j = lane >> 3, dg = lane & 7;
   const int base = kb * 64;
   const int cnt = min(64, Tk - base);
-  const int cnt_p = min(64, m.T_p - base);  // <= 0 past the patch keys
+  const int cnt_p = min(64, T_pool - base);  // <= 0 past the pooled keys
   const uint16_t* ksrc = k + bh_offset(bh, sk) + dg * 8;
   const uint16_t* vsrc = v + bh_offset(bh, sv) + dg * 8;
 
@@ -220,11 +222,12 @@ __global__ __launch_bounds__(64) void k_prep_kv(const uint16_t* __restrict__ k, 
                                                 uint16_t* __restrict__ k_pack, float* __restrict__ k_norm) {
   __shared__ uint16_t vt[64 * 64];
   prep_kv_block(blockIdx.x, blockIdx.y, k, v, sk, sv, m, Tk, kb_tot, kb_p, ksum, pooled_k, pooled_v, v_pack, k_pack,
-                k_norm, vt);
+                k_norm, vt, m.T_p);
 }
 
 // The layer's Q blocks and K/V blocks in one launch (they are independent): x < nqb is Q
-// block x, the rest K/V block x - nqb.
+// block x, the rest K/V block x - nqb. The K/V pools cover the first T_pool keys in kernel
+// order (T_p: the patch keys; Tk: every key) in kb_pool blocks.
 __global__ __launch_bounds__(64) void k_prep_qkv(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                  const uint16_t* __restrict__ v, Strides sq, Strides sk, Strides sv,
                                                  TokenMap m, int nqb, int q_blk_p, int q_blk_total, int Tk, int kb_tot,
@@ -232,13 +235,14 @@ __global__ __launch_bounds__(64) void k_prep_qkv(const uint16_t* __restrict__ q,
                                                  float* __restrict__ q_scale, float* __restrict__ pooled_q,
                                                  float* __restrict__ ksum, float* __restrict__ pooled_k,
                                                  float* __restrict__ pooled_v, uint16_t* __restrict__ v_pack,
-                                                 uint16_t* __restrict__ k_pack, float* __restrict__ k_norm) {
+                                                 uint16_t* __restrict__ k_pack, float* __restrict__ k_norm,
+                                                 int T_pool) {
   __shared__ uint16_t vt[64 * 64];
   if ((int)blockIdx.x < nqb)
     prep_q_block(blockIdx.x, blockIdx.y, q, sq, m, q_blk_p, q_blk_total, q_i8, q_lo, q_scale, pooled_q);
   else
     prep_kv_block(blockIdx.x - nqb, blockIdx.y, k, v, sk, sv, m, Tk, kb_tot, kb_p, ksum, pooled_k, pooled_v, v_pack,
-                  k_pack, k_norm, vt);
+                  k_pack, k_norm, vt, T_pool);
 }
 
 // key mean over all Tk keys: km[d] = SEQ-sum of the block sums / Tk. The loads are
@@ -326,13 +330,16 @@ static TokenMap make_map(int frames, int P, int S, const int* perm = nullptr) {
 // written whenever it is non-null. patch_order: null, or HW = P-S int32 in device memory,
 // the frame's patch tokens in the order blocks are formed (the Hilbert order of
 // hilbert_permute), read in place; the same table must go to the attention call.
+// pool_all: 0 pools K and V over the patch keys (kb_p blocks), 1 over every key in kernel
+// order (kb_tot blocks: the sink-mass map of attention.py:78, 451-452 and its v_bar).
 RESS_API int ress_prep_qkv(const void* q, const void* k, const void* v, int B, int H, int frames, int P, int S,
                            const int* patch_order, long long sqB, long long sqH, long long sqT, long long skB, long long skH, long long skT,
                            long long svB, long long svH, long long svT, void* q_i8, void* q_lo, void* q_scale,
                            void* pooled_q, void* k_i8, void* k_lo, void* k_scale, void* pooled_k, void* pooled_v,
-                           void* v_pack, void* k_pack, void* ksum, void* km, hipStream_t stream) {
+                           void* v_pack, void* k_pack, void* ksum, void* km, int pool_all, hipStream_t stream) {
   RESS_REQUIRE(B > 0 && H > 0 && frames > 0 && P > S && S >= 0, "ress_prep_qkv: bad geometry B=%d H=%d F=%d P=%d S=%d",
                B, H, frames, P, S);
+  RESS_REQUIRE(pool_all == 0 || pool_all == 1, "ress_prep_qkv: pool_all must be 0 or 1");
   RESS_REQUIRE(q && k && v && pooled_q && pooled_k && pooled_v && v_pack, "ress_prep_qkv: null pointer");
   const bool quant = q_i8 != nullptr;
   RESS_REQUIRE((q_i8 == nullptr) == (k_i8 == nullptr), "ress_prep_qkv: give both q_i8 and k_i8, or neither");
@@ -354,10 +361,11 @@ RESS_API int ress_prep_qkv(const void* q, const void* k, const void* v, int B, i
   // without codes only the patch blocks (the pooled ones) have Q work
   const int nqb = quant ? q_blk_p + q_blk_s : q_blk_p;
   hipLaunchKernelGGL(k_prep_qkv, dim3(nqb + kb_tot, BH), dim3(64), 0, stream, (const uint16_t*)q, (const uint16_t*)k,
-                     (const uint16_t*)v, sq, sk, sv, m, nqb, q_blk_p, q_blk_p + q_blk_s, Tk, kb_tot, kb_p,
+                     (const uint16_t*)v, sq, sk, sv, m, nqb, q_blk_p, q_blk_p + q_blk_s, Tk, kb_tot,
+                     pool_all ? kb_tot : kb_p,
                      (int8_t*)q_i8, (int8_t*)q_lo, (float*)q_scale, (float*)pooled_q,
                      (float*)(quant ? ksum : nullptr), (float*)pooled_k, (float*)pooled_v, (uint16_t*)v_pack,
-                     (uint16_t*)k_pack, (float*)(quant ? nullptr : k_scale));
+                     (uint16_t*)k_pack, (float*)(quant ? nullptr : k_scale), pool_all ? Tk : m.T_p);
   RESS_LAUNCHED("k_prep_qkv");
   if (!quant) return 0;
   hipLaunchKernelGGL(k_key_mean, dim3(BH), dim3(64), 0, stream, (const float*)ksum, kb_tot, Tk, (float*)km);

@@ -35,6 +35,9 @@ class LayerGrid:
     P: int
     S: int
     sink_protect: bool = True
+    # pool the map over every key (kernel order cat(patch, special)) instead of the patch
+    # keys alone: the reference's RESS_SINK_MASS (attention.py:78, 451-452), default off
+    sink_mass: bool = False
 
     @property
     def BH(self):
@@ -66,8 +69,9 @@ class LayerGrid:
 
     @property
     def kb_p(self):
-        """Width of the pooled map (patch keys only, ceil)."""
-        return _cdiv(self.T_p, KS_K)
+        """Width of the pooled map: the patch key blocks (ceil), or with sink_mass every key
+        block of the kernel grid."""
+        return self.kb_tot if self.sink_mass else _cdiv(self.T_p, KS_K)
 
     @property
     def kb_tot(self):
@@ -188,12 +192,13 @@ def prepare_blocks(q, k, v, grid, mode="f16", split=None, patch_order=None):
         "ress_prep_qkv", P(q), P(k), P(v), grid.B, grid.H, grid.frames, grid.P, grid.S, P(patch_order),
         *q.stride()[:3], *k.stride()[:3], *v.stride()[:3],
         P(b.q_i8), P(b.q_lo), P(b.q_scale), P(b.pooled_q), P(b.k_i8), P(b.k_lo), P(b.k_scale), P(b.pooled_k),
-        P(b.pooled_v), P(b.v_pack), P(b.k_pack), P(b.ksum), P(b.km), _lib.stream_handle(dev))
+        P(b.pooled_v), P(b.v_pack), P(b.k_pack), P(b.ksum), P(b.km), 1 if grid.sink_mass else 0,
+        _lib.stream_handle(dev))
     return b
 
 
 def pooled_scores(blocks):
-    """(attn_full, attn_cond): the pooled softmax over the kb_p patch key blocks and its
+    """(attn_full, attn_cond): the pooled softmax over the kb_p key blocks of the map and its
     renormalisation over the n_cand candidates, both (B,H,q_blk_p,*) fp32."""
     g = blocks.grid
     dev = blocks.pooled_q.device

@@ -5,6 +5,8 @@ M_h = (W_O^h)^T W_O^h is baked once per model; the per-candidate score is
 s_ij = P_ij * sqrt(d^T M_h d), d = v_bar_query_i - v_bar_j.
 """
 
+import contextlib
+
 import torch
 
 from ress_amd import _lib
@@ -62,6 +64,55 @@ def projected_score(attn_pooled, v_bar, M, n_cand=None, renormalize=True):
     if renormalize:
         score = score / (1.0 - P).clamp(min=1e-4)
     return score
+
+
+# The list record_realized_drift has active, or None: the forward appends to it only while
+# a recorder is open (reference projected.py:84-93).
+_realized_records = None
+
+
+@contextlib.contextmanager
+def record_realized_drift():
+    """While active, every block-sparse attention layer that has an M (bake_and_attach_M)
+    appends one float to the yielded list, in forward order: the mean over its (batch,
+    head, query-block) rows of J = ||g||^2_M / K^2 for the kept set the attention kernel
+    was handed, sinks included (reference projected.py:95-109, attention.py:199-214, 620-623).
+    Each recorded layer synchronises once; nothing changes while no recorder is open."""
+    global _realized_records
+    prev = _realized_records
+    records = []
+    _realized_records = records
+    try:
+        yield records
+    finally:
+        _realized_records = prev
+
+
+def realized_objective(attn_pooled, v_bar, M, keep_mask, n_cand=None, dtype=torch.float32):
+    """J = ||g||^2_M / K^2 per (..., nh, q_blk) for any kept set (reference
+    projected.py:112-129): g = (sum of the dropped P) * v_bar_query - (dropped P) @ V over
+    the candidates, K = total mass - dropped mass (floored at KEPT_MASS_EPS before squaring).
+    attn_pooled / v_bar: the pooled map and block means over the whole pooled grid
+    (candidates first); keep_mask (..., nh, q_blk, n_cand) bool over the candidates only.
+    The same J the restore-swap kernel reports for its own set, here in torch fp32 for a
+    set made by any criterion: a diagnostic, off the layer's hot path."""
+    P, V, vq, total = dense_reference(attn_pooled.to(dtype), v_bar.to(dtype), n_cand)
+    Pd = P * (~keep_mask.bool()).to(dtype)
+    sum_pd = Pd.sum(dim=-1)
+    g = sum_pd.unsqueeze(-1) * vq - torch.matmul(Pd, V)
+    Mg = torch.matmul(g, M.to(dtype).transpose(-1, -2))
+    obj = (g * Mg).sum(dim=-1)
+    return obj / (total - sum_pd).clamp(min=KEPT_MASS_EPS).pow(2)
+
+
+def record_layer_drift(M, attn_full, v_bar_full, final_map, n_cand):
+    """Append the layer's mean realized J to the open recorder; a no-op when none is open
+    or the layer has no M (reference attention.py:199-214)."""
+    if _realized_records is None or M is None:
+        return
+    with torch.no_grad():
+        J = realized_objective(attn_full, v_bar_full, M, final_map[..., :n_cand].bool(), n_cand=n_cand)
+    _realized_records.append(J.float().mean().item())
 
 
 def kept_mass_norm_quality(G, K, delta_G, u, eps=KEPT_MASS_EPS):

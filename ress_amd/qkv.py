@@ -29,17 +29,50 @@ def grid_shape(x, pos, num_special_tokens=5, num_heads=16, shape=None):
     return {"B": B, "N": N, "P": P, "head_dim": dim // num_heads, "num_heads": num_heads, "H": H, "W": W, "S": S}
 
 
+# The rotation the fused kernel implements: the head dim split in two halves, the first
+# rotated by the row position pos[..., 0] and the second by the column pos[..., 1]; in each
+# half of width d, element i < d/2 pairs with i + d/2 (rotate-half: x*cos + (-x2, x1)*sin)
+# at angle pos * base^(-2i/d), angles in fp32.
+ROPE_LAYOUT = "rotate_half_2d"
+
+
+def declare_rope(rope, base, layout=ROPE_LAYOUT):
+    """Declare a backbone's own RoPE module (the `self.rope` the reference forward calls,
+    src/ress/models/qkv.py:56-58) to be the rotation the fused q/k-norm + RoPE kernel
+    implements, with the given base frequency, so that its attention takes the fused path.
+    The declaration is the caller's statement about the module's arithmetic: the fused
+    kernel does not run the module. Returns the module."""
+    if layout != ROPE_LAYOUT:
+        raise ValueError(f"RoPE layout {layout!r} is not implemented by the fused kernel (only {ROPE_LAYOUT!r})")
+    base = float(base)
+    if not base > 1.0:
+        raise ValueError(f"RoPE base must be > 1, got {base}")
+    rope.ress_rope = (layout, base)
+    return rope
+
+
+def rope_base(rope):
+    """Base frequency of a rotation the fused kernel implements (this package's RoPE2D, or
+    a module passed to declare_rope), else None."""
+    from ress_amd.aggregator import RoPE2D
+    if isinstance(rope, RoPE2D):
+        return float(rope.base)
+    decl = getattr(rope, "ress_rope", None)
+    if isinstance(decl, tuple) and len(decl) == 2 and decl[0] == ROPE_LAYOUT:
+        return float(decl[1])
+    return None
+
+
 def _fusable(self, x, hd):
     """True when the module's q/k normalisation and rotary embedding are the ones the
-    fused kernel implements: bf16 on the GPU, LayerNorm(64) with affine weights, and this
-    package's RoPE2D (or no rotation)."""
-    from ress_amd.aggregator import RoPE2D
+    fused kernel implements: bf16 on the GPU, LayerNorm(64) with affine weights, and a
+    RoPE with a known base (rope_base) or no rotation."""
     rope = getattr(self, "rope", None)
     qn, kn = getattr(self, "q_norm", None), getattr(self, "k_norm", None)
     return (x.is_cuda and x.dtype == torch.bfloat16 and hd == 64
             and all(isinstance(n, torch.nn.LayerNorm) and n.normalized_shape == (64,) and n.weight is not None
                     and n.bias is not None and n.weight.dtype == torch.bfloat16 for n in (qn, kn))
-            and (rope is None or isinstance(rope, RoPE2D)))
+            and (rope is None or rope_base(rope) is not None))
 
 
 def fused_qk_norm_rope(self, qkv_out, pos, nh):
@@ -55,7 +88,7 @@ def fused_qk_norm_rope(self, qkv_out, pos, nh):
     qn, kn = self.q_norm, self.k_norm
     _lib.call("ress_qk_norm_rope", _lib.ptr(src), B, T, nh, _lib.ptr(qn.weight), _lib.ptr(qn.bias),
               _lib.ptr(kn.weight), _lib.ptr(kn.bias), float(qn.eps), _lib.ptr(p),
-              float(rope.base) if rope is not None else 0.0, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v),
+              rope_base(rope) if rope is not None else 0.0, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v),
               _lib.stream_handle(dev))
     return q, k, v
 
@@ -63,7 +96,8 @@ def fused_qk_norm_rope(self, qkv_out, pos, nh):
 def compute_qkv(self, x, pos, num_special_tokens=5, num_heads=16, shape=None):
     """(q, k, v, shape): each (B, nh, N*P, hd) in storage order, after q_norm/k_norm and
     RoPE -- reference qkv.py:60-68 without the split. Modules with LayerNorm q/k norms and
-    this package's RoPE2D take the fused kernel; others run the torch modules."""
+    a RoPE the fused kernel implements (rope_base: this package's RoPE2D or a declared one)
+    take the fused kernel; others run the torch modules."""
     shp = grid_shape(x, pos, num_special_tokens, num_heads, shape)
     B, NP, _ = x.shape
     nh, hd = shp["num_heads"], shp["head_dim"]

@@ -25,6 +25,8 @@ CALL_ATTRIBUTES = (
     ("attention_sink", 0),
     ("patch_order", None),
     ("eager_check", False),
+    ("sink_mass", False),
+    ("sink_protect", True),
 )
 
 

@@ -7,14 +7,14 @@ from ress_amd.kernels import LayerGrid
 
 
 def oracle_layer(q, k, v, frames, P, S, sparse_ratio=None, cdf_threshold=None, head_scores=None, B=1, H=16,
-                 sink_lead=0, criterion="probability", M=None, rank_key=None, max_iters=1000):
+                 sink_lead=0, criterion="probability", M=None, rank_key=None, max_iters=1000, sink_mass=False):
     """Returns a dict with prep outputs, attn_full/attn_cond, baseline, counts, map, lut, nvalid.
 
     criterion: "probability" ranks by attn_cond; "ress" by the restore_swap_iter5_bf16_trackbest
     keep set (M: (H, 64, 64)); "key" by the given rank_key (B*H, q_blk_p, n_cand). sink_lead:
-    leading key blocks forced on (the attention sink)."""
-    g = LayerGrid(B, H, frames, P, S)
-    o = oracle.prep_qkv(q, k, v, frames, P, S)
+    leading key blocks forced on (the attention sink). sink_mass: the map pooled over every key."""
+    g = LayerGrid(B, H, frames, P, S, sink_mass=sink_mass)
+    o = oracle.prep_qkv(q, k, v, frames, P, S, pool_all=sink_mass)
     full, cond = oracle.pooled_scores(o["pooled_q"], o["pooled_k"], g.n_cand)
     base = oracle.baseline_budget(cond, sparse_ratio, cdf_threshold).reshape(B, H, g.q_blk_p)
     if head_scores is not None:

@@ -9,6 +9,7 @@ weights, its global blocks wired to the block-sparse forward.
   global layer, keep about the requested fraction of blocks, and stay close to dense;
 * switching modes back to dense restores the dense output exactly (modes do not leak)."""
 
+import numpy as np
 import pytest
 import torch
 
@@ -88,6 +89,21 @@ def test_sparse_modes_run_every_layer(models, mode):
     assert _cos(got, want) >= 0.95
 
 
+def test_realized_drift_recorded_per_layer(models):
+    """record_realized_drift over a ReSS forward: one finite J >= 0 per global layer, in
+    forward order; nothing is recorded once the recorder is closed."""
+    from ress_amd import projected
+    model, images, _ = models
+    with torch.no_grad():
+        ress.apply_ress(model, 0.5, n_iters=5)
+        with projected.record_realized_drift() as rec:
+            model(images)
+        model(images)
+    torch.cuda.synchronize()
+    assert len(rec) == DEPTH, rec
+    assert all(np.isfinite(j) and j >= 0.0 for j in rec), rec
+
+
 @pytest.mark.parametrize("max_pos", [38, 5000], ids=["grid", "large_positions"])
 def test_fused_qk_norm_rope_matches_modules(max_pos, dev):
     """The fused q/k LayerNorm + 2D RoPE kernel against the torch modules it replaces:
@@ -116,6 +132,71 @@ def test_fused_qk_norm_rope_matches_modules(max_pos, dev):
         err = (got.float() - want.float()).abs()
         assert err.max().item() <= 2 ** -6 * want.float().abs().max().item()
         assert (err > 0).float().mean().item() < 0.02  # nearly all bit-identical
+
+
+class _RowColRotary(torch.nn.Module):
+    """A backbone-style 2D rotary module written apart from this package's RoPE2D: angle
+    tables per position built once per call, the halves taken with chunk, positions read
+    as (row, column). round_tables rounds cos/sin to the token dtype before use, as some
+    backbones cache them."""
+
+    def __init__(self, frequency=100.0, round_tables=False):
+        super().__init__()
+        self.frequency = frequency
+        self.round_tables = round_tables
+
+    def _one(self, x, p):
+        d = x.shape[-1]
+        inv = self.frequency ** (-torch.arange(0, d, 2, device=x.device, dtype=torch.float32) / d)
+        ang = torch.einsum("bt,f->btf", p.to(torch.float32), inv)
+        ang = torch.cat((ang, ang), dim=-1)[:, None]
+        cos, sin = ang.cos(), ang.sin()
+        if self.round_tables:
+            cos, sin = cos.to(x.dtype).float(), sin.to(x.dtype).float()
+        a, b = x.float().chunk(2, dim=-1)
+        return x.float() * cos + torch.cat((-b, a), dim=-1) * sin
+
+    def forward(self, tokens, positions):
+        rows, cols = tokens.chunk(2, dim=-1)
+        return torch.cat((self._one(rows, positions[..., 0]), self._one(cols, positions[..., 1])),
+                         dim=-1).to(tokens.dtype)
+
+
+@pytest.mark.parametrize("round_tables", [False, True], ids=["fp32_tables", "bf16_tables"])
+def test_fused_path_takes_a_declared_foreign_rope(round_tables, dev):
+    """A RoPE module that is not this package's, declared with declare_rope, takes the fused
+    kernel; its q and k against the module's own torch norms and rotation: with fp32
+    angle tables nearly all bit-identical, with tables rounded to bf16 within the bf16
+    rounding of cos/sin. An undeclared module keeps the torch path."""
+    from ress_amd.aggregator import Attention
+    from ress_amd.qkv import _fusable, declare_rope, fused_qk_norm_rope
+    torch.manual_seed(5)
+    rope = _RowColRotary(100.0, round_tables)
+    attn = Attention(256, 4, rope).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        for n in (attn.q_norm, attn.k_norm):
+            n.weight.uniform_(0.5, 1.5)
+            n.bias.uniform_(-0.2, 0.2)
+    B, T = 2, 300
+    x = torch.randn(B, T, 256, device=dev).to(torch.bfloat16)
+    pos = torch.randint(0, 38, (B, T, 2), device=dev)
+    assert not _fusable(attn, x, 64)
+    declare_rope(rope, base=rope.frequency)
+    assert _fusable(attn, x, 64)
+    with torch.no_grad():
+        qkv = attn.qkv(x)
+        q, k, v = fused_qk_norm_rope(attn, qkv, pos, 4)
+        rq, rk, rv = qkv.reshape(B, T, 3, 4, 64).permute(2, 0, 3, 1, 4).unbind(0)
+        rq, rk = rope(attn.q_norm(rq), pos), rope(attn.k_norm(rk), pos)
+    torch.cuda.synchronize()
+    assert torch.equal(v, rv.contiguous())
+    for got, want in ((q, rq), (k, rk)):
+        err = (got.float() - want.float()).abs()
+        scale = want.float().abs().max().item()
+        print(f"[declared rope {round_tables}] max-abs {err.max().item():.3e} of {scale:.3e}")
+        assert err.max().item() <= (2 ** -5 if round_tables else 2 ** -6) * scale
+        if not round_tables:
+            assert (err > 0).float().mean().item() < 0.02  # nearly all bit-identical
 
 
 def test_modes_do_not_leak(models):

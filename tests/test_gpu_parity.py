@@ -289,6 +289,67 @@ def test_layer_pipeline_matches_oracle(cfg, mode, dev):
     print(f"[{cfg} {mode}] attention max-abs {w:.3e} min-cos {c:.6f}")
 
 
+@pytest.mark.parametrize("criterion", ["probability", "ress"])
+def test_sink_mass_layer_matches_oracle(criterion, dev):
+    """sink_mass (the reference's RESS_SINK_MASS, attention.py:451-452, 481): the pools,
+    the map over every key block and the restore-swap keep sets bit-exact against the
+    oracle pipeline on the same grid; the budget reads the renormalised candidate map."""
+    frames, sr = 4, 0.7
+    q, k, v, meta = synth.make_layer_qkv(frames)
+    P, S = meta["P"], meta["S"]
+    g = LayerGrid(1, 16, frames, P, S, sink_mass=True)
+    assert g.kb_p == g.kb_tot > g.n_cand
+    W_O = synth.make_w_o()
+    M = torch.stack([W_O[:, h * 64:(h + 1) * 64].T @ W_O[:, h * 64:(h + 1) * 64] for h in range(16)])
+    bud = budget.UniformBudget()
+    crit = "restore_swap_iter5_bf16_trackbest" if criterion == "ress" else "probability"
+    print(f"[sink_mass {criterion}] frames={frames} kb_p={g.kb_p} n_cand={g.n_cand}", flush=True)
+    res = sparse_global_attention(q.to(dev), k.to(dev), v.to(dev), g,
+                                  budget_fn=lambda a: bud.num_to_select(0, a, sr, None, 1.0), block_criterion=crit,
+                                  M=M.to(dev), keep_intermediates=True)
+    torch.cuda.synchronize()
+    o = oracle_layer(q, k, v, frames, P, S, sparse_ratio=sr, criterion=criterion, M=M.numpy(), sink_mass=True)
+    assert _bits_equal(_np(res.blocks.pooled_k), o["pooled_k"])
+    assert _bits_equal(_np(res.blocks.pooled_v), o["pooled_v"])
+    assert _bits_equal(_np(res.attn_full).reshape(o["attn_full"].shape), o["attn_full"])
+    assert np.array_equal(_np(res.final_map).reshape(o["map"].shape), o["map"])
+    assert np.array_equal(_np(res.nvalid), o["nvalid"])
+    rows = row_sample(o["nvalid"], 8)
+    w, c = _check_attention(res.out, q, k, v, frames, P, S, o["lut"], o["nvalid"], rows)
+    print(f"[sink_mass {criterion}] sparsity {res.sparsity():.4f} max-abs {w:.3e} min-cos {c:.6f}")
+
+
+def test_realized_drift_is_recorded_for_the_kernels_keep_set(dev):
+    """record_realized_drift around one layer (fp32 restore-swap, track_best): one value, the
+    mean J of the keep set the attention kernel ran with, equal within fp32 reassociation to
+    the oracle's J of the oracle's keep set on the same pooled map (the two keep sets are
+    bit-exact; reference attention.py:199-214, projected.py:112-129)."""
+    from ress_amd import projected
+    frames, sr = 4, 0.6
+    q, k, v, meta = synth.make_layer_qkv(frames)
+    P, S = meta["P"], meta["S"]
+    g = LayerGrid(1, 16, frames, P, S)
+    W_O = synth.make_w_o()
+    M = torch.stack([W_O[:, h * 64:(h + 1) * 64].T @ W_O[:, h * 64:(h + 1) * 64] for h in range(16)])
+    bud = budget.UniformBudget()
+    print(f"[realized drift] frames={frames} n_cand={g.n_cand}", flush=True)
+    with projected.record_realized_drift() as rec:
+        res = sparse_global_attention(q.to(dev), k.to(dev), v.to(dev), g,
+                                      budget_fn=lambda a: bud.num_to_select(0, a, sr, None, 1.0),
+                                      block_criterion="restore_swap_iter5_trackbest", M=M.to(dev),
+                                      keep_intermediates=True)
+    torch.cuda.synchronize()
+    assert len(rec) == 1
+    o = oracle.prep_qkv(q, k, v, frames, P, S)
+    full, _ = oracle.pooled_scores(o["pooled_q"], o["pooled_k"], g.n_cand)
+    counts = np.maximum(_np(res.counts).reshape(16, g.q_blk_p), min(2, g.n_cand)).astype(np.int32)
+    keep, J = oracle.restore_swap(full.reshape(16, g.q_blk_p, g.kb_p), o["pooled_v"].reshape(16, g.kb_p, 64),
+                                  M.numpy(), counts, g.n_cand, n_iters=5, big_bf16=False, track_best=True)
+    assert np.array_equal(_np(res.final_map).reshape(16, g.q_blk_p, g.kb_tot)[..., :g.n_cand], keep)
+    np.testing.assert_allclose(rec[0], float(J.astype(np.float64).mean()), rtol=2e-4)
+    print(f"[realized drift] recorded {rec[0]:.6e} oracle {J.mean():.6e}")
+
+
 def test_layer_protect_own_frame(dev):
     """protect_own_frame inside the layer: the swapped map is the oracle map after the
     budget-neutral own-frame swap, the LUT is rebuilt from it, per-row kept counts are

@@ -409,3 +409,40 @@ def test_check_layers_raises_what_the_forwards_left():
                                                   max_iters=1000)
     with pytest.raises(RuntimeError, match="did not converge"):
         ress.check_layers(nn.ModuleList([ok, bad_hess]))
+
+
+def test_declare_rope_marks_a_foreign_rotation():
+    """A module that is not this package's RoPE2D is fused only once declared; the
+    declaration names the layout and base the fused kernel implements and rejects others."""
+    from ress_amd.aggregator import RoPE2D
+    from ress_amd.qkv import ROPE_LAYOUT, rope_base
+
+    class Foreign(nn.Module):
+        def forward(self, t, pos):
+            return t
+
+    r = Foreign()
+    assert rope_base(r) is None
+    assert rope_base(RoPE2D(50.0)) == 50.0
+    assert ress.declare_rope(r, base=100) is r and rope_base(r) == 100.0
+    assert r.ress_rope == (ROPE_LAYOUT, 100.0)
+    with pytest.raises(ValueError):
+        ress.declare_rope(Foreign(), base=100.0, layout="interleaved_2d")
+    with pytest.raises(ValueError):
+        ress.declare_rope(Foreign(), base=1.0)
+
+
+def test_sink_mass_and_protect_reach_the_forward_grid():
+    """The module attributes sink_mass / sink_protect (the reference's RESS_SINK_MASS /
+    RESS_SINK_PROTECT flags, attention.py:50-79) reach the layer grid: the pooled map's
+    width and the candidate count."""
+    assert [n for n, _ in wiring.CALL_ATTRIBUTES if n.startswith("sink")] == ["sink_mass", "sink_protect"]
+    g = LayerGrid(1, 16, 4, 1374, 5)
+    gm = LayerGrid(1, 16, 4, 1374, 5, sink_mass=True)
+    gp = LayerGrid(1, 16, 4, 1374, 5, sink_protect=False)
+    assert (g.kb_p, g.n_cand, g.kb_tot) == (86, 85, 86)
+    assert (gm.kb_p, gm.n_cand, gm.sink_blocks) == (86, 85, 1)
+    assert gp.n_cand == 86 and gp.sink_blocks == 0
+    big = LayerGrid(1, 16, 12, 1374, 5)  # 60 special keys: one whole special block past the straddler
+    bigm = LayerGrid(1, 16, 12, 1374, 5, sink_mass=True)
+    assert (big.kb_p, bigm.kb_p, big.kb_tot, big.n_cand) == (257, 258, 258, 256)

@@ -104,6 +104,30 @@ def test_pooling_matches_torch_avg_pool(small_layer):
         np.testing.assert_allclose(pooled[:, -1], last, rtol=0, atol=2e-6)
 
 
+
+def test_sink_mass_pooling_covers_every_key(small_layer):
+    """pool_all (the sink-mass grid, reference attention.py:451-452, 481): K and V pooled
+    over cat(patch, special) in kernel order, kb_tot blocks, the block straddling the patch
+    tail and the first special keys mixing both; the other outputs do not change."""
+    q, k, v, frames, P, S, o = small_layer
+    om = oracle.prep_qkv(q, k, v, frames, P, S, pool_all=True)
+    g = LayerGrid(1, 2, frames, P, S, sink_mass=True)
+    assert om["pooled_k"].shape == (2, g.kb_tot, 64) and g.kb_p == g.kb_tot
+    for x, pooled in ((k, om["pooled_k"]), (v, om["pooled_v"])):
+        xp, xs = ref.split_tokens(x.float(), frames, P, S)
+        key = torch.cat([xp, xs], dim=2)[0]
+        t = torch.nn.functional.avg_pool1d(key.transpose(-1, -2), 64, ceil_mode=True).transpose(-1, -2)
+        np.testing.assert_allclose(pooled, t.numpy(), rtol=0, atol=2e-6)
+        T_p = xp.shape[2]
+        b = T_p // 64  # the straddling block: patch tail and leading special keys together
+        mixed = key[:, b * 64:b * 64 + 64].double().mean(dim=1).numpy()
+        np.testing.assert_allclose(pooled[:, b], mixed, rtol=0, atol=2e-6)
+    for name in ("q_i8", "q_scale", "pooled_q", "k_i8", "k_scale", "v_pack", "ksum", "km"):
+        assert np.array_equal(om[name], o[name]), name
+    # the patch-only grid is the leading kb_p blocks where no block straddles
+    n_whole = (frames * (P - S)) // 64
+    np.testing.assert_array_equal(om["pooled_k"][:, :n_whole], o["pooled_k"][:, :n_whole])
+
 def _sage_quant(x, scale):
     """SageAttention per-block rule, vectorised numpy fp32."""
     x = x.astype(np.float32)
