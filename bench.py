@@ -166,11 +166,13 @@ def time_meansim(q, k, reps):
             torch.empty(B * H, nk * 64, 64, dtype=torch.int8, device=dev), torch.empty(B * H, nk, device=dev),
             torch.empty(B * H, nq, 64, device=dev), torch.empty(B * H, nk, 64, device=dev),
             torch.empty(B * H, nq, dtype=torch.uint8, device=dev), torch.empty(B * H, nk, dtype=torch.uint8, device=dev)]
+    ws_bytes = _lib.lib().ress_meansim_workspace_size(B, H, T, T)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
 
     def run():
         _lib.call("ress_meansim_block_map", _lib.ptr(q), _lib.ptr(k), _lib.ptr(km), B, H, T, T, *q.stride()[:3],
-                  *k.stride()[:3], _lib.ptr(th), _lib.ptr(cd), 1374, *(_lib.ptr(b) for b in bufs),
-                  _lib.stream_handle(dev))
+                  *k.stride()[:3], _lib.ptr(th), _lib.ptr(cd), 1374, *(_lib.ptr(b) for b in bufs), _lib.ptr(ws),
+                  ws_bytes, _lib.stream_handle(dev))
 
     run()
     torch.cuda.synchronize()

@@ -147,7 +147,13 @@ int ress_meansim_block_map(const void* q, const void* k, const void* km, int B, 
                            long long sqB, long long sqH, long long sqT, long long skB, long long skH, long long skT,
                            const void* simthreshd1, const void* cdfthreshd, int attention_sink, void* map, void* q_i8,
                            void* q_scale, void* k_i8, void* k_scale, void* pooled_q, void* pooled_k, void* sim_q,
-                           void* sim_k, hipStream_t stream);
+                           void* sim_k, void* workspace, long long workspace_bytes, hipStream_t stream);
+
+/* Bytes of ress_meansim_block_map's optional workspace (16-byte aligned): the fp32 scores
+ * of every row when rows are long (nk > 1024), computed by one matrix-core GEMM; 0 for
+ * shorter rows. With workspace = NULL long rows compute their own scores (slower; the same
+ * map). */
+long long ress_meansim_workspace_size(int B, int H, int Tq, int Tk);
 
 /* ---- ReSS restore-swap (ress_swap.hip) ------------------------------------ */
 

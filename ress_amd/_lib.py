@@ -29,7 +29,7 @@ _SIGS = {
     "ress_sparse_attn_fwd_f16_noalloc": "plllppppp" + "iiiii" + "pf" + "pi" + "lll" + "s",
     "ress_qattn_block_sparse_fwd": "pppipipppppiiiilllllliiifipls",
     "ress_restore_swap": "pppp" + "iiiiii" + "dd" + "i" + "ppp" + "pl" + "s",
-    "ress_meansim_block_map": "ppp" + "iiii" + "llllll" + "ppi" + "ppppppppp" + "s",
+    "ress_meansim_block_map": "ppp" + "iiii" + "llllll" + "ppi" + "ppppppppp" + "pl" + "s",
     "ress_qk_norm_rope": "piii" + "pppp" + "f" + "pf" + "ppp" + "s",
 }
 _CT = {
@@ -62,6 +62,8 @@ def lib():
         L.ress_attn_sched_bytes.argtypes = [ctypes.c_int] * 3
         L.ress_restore_swap_workspace_size.restype = ctypes.c_longlong
         L.ress_restore_swap_workspace_size.argtypes = [ctypes.c_int] * 3
+        L.ress_meansim_workspace_size.restype = ctypes.c_longlong
+        L.ress_meansim_workspace_size.argtypes = [ctypes.c_int] * 4
         L.ress_noalloc_scratch_bytes.restype = ctypes.c_longlong
         L.ress_noalloc_scratch_bytes.argtypes = []
         L.ress_noalloc_status_address.restype = ctypes.c_int
@@ -100,5 +102,6 @@ def last_error():
 
 def exported_symbols():
     return list(_SIGS) + ["ress_last_error", "ress_abi_version", "ress_qattn_workspace_size",
-                          "ress_attn_sched_bytes", "ress_restore_swap_workspace_size", "ress_noalloc_scratch_bytes",
+                          "ress_attn_sched_bytes", "ress_restore_swap_workspace_size", "ress_meansim_workspace_size",
+                          "ress_noalloc_scratch_bytes",
                           "ress_noalloc_status_address"]

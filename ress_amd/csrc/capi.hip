@@ -15,4 +15,4 @@ void ress_set_error(const char* fmt, ...) {
 
 RESS_API const char* ress_last_error(void) { return g_err; }
 
-RESS_API int ress_abi_version(void) { return 3; }
+RESS_API int ress_abi_version(void) { return 4; }

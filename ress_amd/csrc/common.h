@@ -13,6 +13,11 @@
 //              for l = 0..63, then a butterfly: at offsets 1,2,4,8,16,32 every
 //              partial becomes partial[l] + partial[l ^ off].
 //   DOT64      pooled dot products: acc = fmaf(a[d], b[d], acc), d = 0..63, from 0.
+//              On gfx950 v_mfma_f32_32x32x2_f32 adds its two k terms to the
+//              accumulator as fmaf(a1, b1, fmaf(a0, b0, c)), IEEE with subnormals
+//              kept (checked bit for bit against that chain on the GPU, random and
+//              subnormal operands), so 32 chained steps over k = (0,1), (2,3), ...
+//              are DOT64 exactly (scores_gemm).
 //   SEQ        sequential sums in index order (CDF prefix sums, HeSS head sums,
 //              the key mean over blocks).
 //
@@ -329,3 +334,9 @@ __device__ __forceinline__ float sum8_tree(float v) {
 }
 
 __host__ __device__ constexpr __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+// S[bh][r][c] = DOT64(a[bh][r], b[bh][c]) * scale for r_begin <= r < r_end (of na rows per
+// head), c < nb (rows of 64 fp32, 16-byte aligned) on the matrix cores, bit-exact with the
+// fmaf chain (scores.hip). Returns 0 or the RESS_LAUNCHED code.
+int scores_gemm(const float* a, const float* b, int BH, int na, int nb, int r_begin, int r_end, float scale,
+                float* S, hipStream_t stream);

@@ -34,7 +34,9 @@
 // lane butterflies, and only the 4 waves' partial sums go through LDS.
 // k_ms_map_wave (nk <= 1024): one wave per (q-block, batch*head) row, four rows per
 // workgroup; details at the kernel.
-// k_ms_map_long (nk > 1024): one 256-thread workgroup per row.
+// k_ms_map_long (nk > 1024): one 256-thread workgroup per row; with a workspace the
+// scores come from one matrix-core GEMM over all rows (scores_gemm, DOT64 exactly), else
+// each row computes its own.
 // Both find n without sorting: an MSB-first radix descent over the bits of p (8-bit
 // digits from the highest bit where the row's keys differ) with per-digit counts and
 // uint64 sums of q, and the tie rank by index.
@@ -346,21 +348,23 @@ __device__ __forceinline__ int ms_cdf_wave(const uint32_t (&key)[E], int nk, flo
 }
 
 // One 256-thread workgroup per (head, q-block) row for nk > 1024:
-//  scores  wave w scores columns c = 256i + 64w + lane, each lane reading its column's
-//          pooled K (64 floats) straight from L2 (DOT64 chain, pooled Q in registers).
+//  scores  PRE: read from S (the scores_gemm output, [BH][nq][nk], already * 0.125);
+//          otherwise wave w scores columns c = 256i + 64w + lane, each lane reading its
+//          column's pooled K through the wave's LDS chunk (DOT64 chain, pooled Q in registers).
 //  cut     the CDF radix descent over p in LDS (column order): a workgroup histogram per
 //          digit, scanned by wave 0 (ms_cdf_digit).
 //  select  contiguous column chunks per thread and a workgroup scan for the tie rank.
+template <bool PRE>
 __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ pooled_q,
                                                      const float* __restrict__ pooled_k,
                                                      const uint8_t* __restrict__ sim_q,
                                                      const uint8_t* __restrict__ sim_k, int H, int nq, int nk,
                                                      const float* __restrict__ cdfth, int n_sink,
-                                                     uint8_t* __restrict__ map) {
+                                                     const float* __restrict__ S, uint8_t* __restrict__ map) {
   extern __shared__ __align__(16) unsigned char ms_dyn[];
-  // front region (MS_LONG_FRONT_BYTES): the waves' score chunks
+  // front region (MS_LONG_FRONT_BYTES, without PRE): the waves' score chunks
   float* scw = reinterpret_cast<float*>(ms_dyn) + (threadIdx.x >> 6) * (64 * MS_CH_LD);  // [64][MS_CH_LD]
-  float* p = reinterpret_cast<float*>(ms_dyn + MS_LONG_FRONT_BYTES);  // [nk] scores -> p, column order
+  float* p = reinterpret_cast<float*>(ms_dyn + (PRE ? 0 : MS_LONG_FRONT_BYTES));  // [nk] scores -> p, column order
   __shared__ float red[4];
   __shared__ int ired[4];
   __shared__ int hc[256];
@@ -376,6 +380,18 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
     for (int c = tid; c < nk; c += 256) row[c] = 1;
     return;
   }
+  float mx = -__builtin_huge_valf();
+  if constexpr (PRE) {
+    const float* srow = S + ((long long)bh * nq + r) * nk;
+    for (int c = tid; c < nk; c += 256) {
+      float s = -__builtin_huge_valf();
+      if (sk[c]) {
+        s = srow[c];
+        mx = fmaxf(mx, s);
+      }
+      p[c] = s;
+    }
+  } else {
   float pq[64];
   {
     const float4* q4 = reinterpret_cast<const float4*>(pooled_q + ((long long)bh * nq + r) * 64);
@@ -389,7 +405,6 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
     }
   }
   const float* pkh = pooled_k + (long long)bh * nk * 64;
-  float mx = -__builtin_huge_valf();
   // wave w scores columns c0..c0+63 (c0 = 256i + 64w), lane = column: the columns' pooled
   // K goes through the wave's LDS chunk 16 dims at a time (coalesced loads, the next
   // chunk in flight while one is used), and the DOT64 chain runs over d = 0..63 in order
@@ -434,6 +449,7 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
       p[c] = s;
     }
   }
+  }  // PRE
   mx = wave_max(mx);
   if (lane == 0) red[w] = mx;
   __syncthreads();
@@ -733,13 +749,20 @@ __global__ __launch_bounds__(256) void k_ms_map_wave(const float* __restrict__ p
 
 }  // namespace
 
+// Bytes of the optional workspace of ress_meansim_block_map: the fp32 scores of every row
+// when rows are long (nk > 1024), else 0 (the short-row kernel keeps them on chip).
+RESS_API long long ress_meansim_workspace_size(int B, int H, int Tq, int Tk) {
+  const long long nq = cdiv(Tq, 128), nk = cdiv(Tk, 64);
+  return B > 0 && H > 0 && nk > 1024 ? (long long)B * H * nq * nk * 4 : 0;
+}
+
 // get_block_map_meansim_fuse_quant (patched SpargeAttn, external/patches/spargeattn.patch:50-67)
 RESS_API int ress_meansim_block_map(const void* q, const void* k, const void* km, int B, int H, int Tq, int Tk,
                                     long long sqB, long long sqH, long long sqT, long long skB, long long skH,
                                     long long skT, const void* simthreshd1, const void* cdfthreshd,
                                     int attention_sink, void* map, void* q_i8, void* q_scale, void* k_i8,
                                     void* k_scale, void* pooled_q, void* pooled_k, void* sim_q, void* sim_k,
-                                    hipStream_t stream) {
+                                    void* workspace, long long workspace_bytes, hipStream_t stream) {
   RESS_REQUIRE(B > 0 && H > 0 && Tq > 0 && Tk > 0, "ress_meansim_block_map: bad geometry B=%d H=%d Tq=%d Tk=%d", B,
                H, Tq, Tk);
   RESS_REQUIRE(attention_sink >= 0, "ress_meansim_block_map: attention_sink=%d < 0", attention_sink);
@@ -754,6 +777,10 @@ RESS_API int ress_meansim_block_map(const void* q, const void* k, const void* km
                "ress_meansim_block_map: pooled buffers must be 16-byte and code buffers 8-byte aligned");
   const int nq = cdiv(Tq, 128), nk = cdiv(Tk, 64), BH = B * H;
   RESS_REQUIRE(nk <= MS_MAX_NK, "ress_meansim_block_map: %d key blocks exceed %d", nk, MS_MAX_NK);
+  RESS_REQUIRE(!workspace || (workspace_bytes >= ress_meansim_workspace_size(B, H, Tq, Tk) &&
+                              ((uintptr_t)workspace & 15u) == 0),
+               "ress_meansim_block_map: workspace of %lld bytes is smaller than %lld or not 16-byte aligned",
+               workspace_bytes, ress_meansim_workspace_size(B, H, Tq, Tk));
   const Strides sq{sqB, sqH, sqT, H}, sk{skB, skH, skT, H};
   hipLaunchKernelGGL(k_ms_stats, dim3(nq + nk, BH), dim3(256), 0, stream, (const uint16_t*)q, sq, Tq,
                      (const uint16_t*)k, sk, Tk, (const float*)km, (const float*)simthreshd1, nq, nk, (int8_t*)q_i8,
@@ -778,8 +805,15 @@ RESS_API int ress_meansim_block_map(const void* q, const void* k, const void* km
   } else if (nk <= 1024) {
     hipLaunchKernelGGL(k_ms_map_wave<16>, wgrid, dim3(256), 0, stream, pq, pk, sq8, sk8, H, nq, nk, cd, n_sink, m8);
   } else {
-    hipLaunchKernelGGL(k_ms_map_long, dim3(nq, BH), dim3(256), MS_LONG_FRONT_BYTES + (size_t)nk * 4, stream, pq, pk, sq8,
-                       sk8, H, nq, nk, cd, n_sink, m8);
+    if (workspace) {
+      const int rc = scores_gemm(pq, pk, BH, nq, nk, 0, nq, 0.125f, (float*)workspace, stream);
+      if (rc) return rc;
+      hipLaunchKernelGGL(k_ms_map_long<true>, dim3(nq, BH), dim3(256), (size_t)nk * 4, stream, pq, pk, sq8, sk8, H,
+                         nq, nk, cd, n_sink, (const float*)workspace, m8);
+    } else {
+      hipLaunchKernelGGL(k_ms_map_long<false>, dim3(nq, BH), dim3(256), MS_LONG_FRONT_BYTES + (size_t)nk * 4, stream,
+                         pq, pk, sq8, sk8, H, nq, nk, cd, n_sink, (const float*)nullptr, m8);
+    }
   }
   RESS_LAUNCHED("k_ms_map");
   return 0;

@@ -192,6 +192,13 @@ def check_last_call():
         raise_for_status(_last_status.item())
 
 
+def _meansim_workspace(B, H, Tq, Tk, dev):
+    """(buffer or None, bytes): the scores workspace ress_meansim_block_map uses for long
+    rows (ress_meansim_workspace_size), allocated per call."""
+    n = _lib.lib().ress_meansim_workspace_size(B, H, Tq, Tk)
+    return (torch.empty(n, dtype=torch.uint8, device=dev) if n else None), n
+
+
 def get_block_map_meansim_fuse_quant(q, k, km=None, is_causal=False, BLKQ=BLKQ, BLKK=BLKK, simthreshd1=0.1,
                                      cdfthreshd=0.9, is_sparse=True, return_lut=False, attention_sink=0):
     """SpargeAttn's fused block map, as the reference patches it (spargeattn.patch:50-67):
@@ -242,10 +249,11 @@ def get_block_map_meansim_fuse_quant(q, k, km=None, is_causal=False, BLKQ=BLKQ, 
     pooled_k = torch.empty(B * H, nk, 64, device=dev)
     sim_q = torch.empty(B * H, nq, dtype=torch.uint8, device=dev)
     sim_k = torch.empty(B * H, nk, dtype=torch.uint8, device=dev)
+    ws, ws_bytes = _meansim_workspace(B, H, Tq, Tk, dev)
     _lib.call("ress_meansim_block_map", _lib.ptr(qb), _lib.ptr(kb), _lib.ptr(kmf), B, H, Tq, Tk, *qb.stride()[:3],
               *kb.stride()[:3], _lib.ptr(simth), _lib.ptr(cdfth), attention_sink, _lib.ptr(final_map),
               _lib.ptr(q_buf), _lib.ptr(q_scale), _lib.ptr(k_buf), _lib.ptr(k_scale), _lib.ptr(pooled_q),
-              _lib.ptr(pooled_k), _lib.ptr(sim_q), _lib.ptr(sim_k), _lib.stream_handle(dev))
+              _lib.ptr(pooled_k), _lib.ptr(sim_q), _lib.ptr(sim_k), _lib.ptr(ws), ws_bytes, _lib.stream_handle(dev))
     q_int8, k_int8 = q_buf[:, :, :Tq], k_buf[:, :, :Tk]
     if not return_lut:
         return final_map.bool(), q_int8, q_scale, k_int8, k_scale

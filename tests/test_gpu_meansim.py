@@ -111,6 +111,19 @@ def test_meansim_longest_rows(dev):
     _check(q, k, k.float().mean(2, keepdim=True), 0.2, 0.95, 1374, dev)
 
 
+@pytest.mark.parametrize("with_workspace", [True, False], ids=["gemm_scores", "row_scores"])
+def test_meansim_long_rows_both_score_paths(dev, with_workspace, monkeypatch):
+    """Rows past 1024 key blocks, with the workspace (the scores of every row by one
+    matrix-core GEMM, DOT64 exactly) and without it (each row's workgroup scores its own
+    columns): the same map and codes as the oracle either way; ragged row and column tiles
+    (q blocks not a multiple of 128, key blocks not a multiple of 128)."""
+    if not with_workspace:
+        monkeypatch.setattr(sparge, "_meansim_workspace", lambda *a: (None, 0))
+    q, k = _qk(21, 1, 2, 300 * 128 - 77, 1100 * 64 + 13, dup=True, zeros=True)
+    print(f"[meansim long rows workspace={with_workspace}] nq=300 nk=1101", flush=True)
+    _check(q, k, k.float().mean(2, keepdim=True), [0.1, 0.3], [0.9, 0.5], 200, dev)
+
+
 def test_meansim_no_km_scalar_thresholds(dev):
     q, k = _qk(7, 1, 3, 700, 900)
     _check(q, k, None, 0.1, 0.9, 0, dev)
