@@ -166,7 +166,7 @@ long long ress_meansim_workspace_size(int B, int H, int Tq, int Tk);
  * (optional) J of the returned set, s_out [BH][q_blk][n_cand] (optional) the scores
  * s = P*sqrt(d^T M d). flags: 1 bf16 k-wide tensors, 2 track_best, 4 maximize, 8
  * invert_cut, 16 renormalize off. kb_p <= 2048. */
-long long ress_restore_swap_workspace_size(int BH, int kb_p, int n_cand);
+long long ress_restore_swap_workspace_size(int BH, int q_blk, int kb_p, int n_cand);
 int ress_restore_swap(const void* A, const void* V, const void* M, const void* nts, int BH, int H, int q_blk, int kb_p,
                       int n_cand, int n_iters, double restore_frac, double decay, int flags, void* rank_key, void* obj,
                       void* s_out, void* workspace, long long workspace_bytes, hipStream_t stream);

@@ -438,19 +438,20 @@ void oracle_round_bf16_array(const float* x, float* y, long long n) {
  * reference stores in bf16 is rounded here (bf), at the same points (quadratic_deviation
  * projected.py:259-288, dense_reference :313-356, the round :903-947, fused_round.py
  * :176-226). The reference leaves GEMM / sum accumulation orders to torch-CUDA; this
- * restatement fixes them, in the same order as the GPU kernel:
- *  - SUMK, the sums over key blocks (P @ v_bar and sum P of the dense reference, Pd @ v_bar
- *    and sum_Pd of the objective): 16 interleaved classes k mod 16, each a sequential fp32
- *    chain over increasing k (fmaf for products), the class sums combined by the balanced
- *    pairwise tree over classes 0..15 (rs_tree16);
- *  - DOT4x16, the per-candidate products v_k . Mvq and v_k . big(Mg): four sequential
- *    fmaf chains over dims 16c..16c+15, combined as (c0 + c1) + (c2 + c3);
- *  - the objective's unrounded sum_Pd and Pd @ v_bar are formed by SUMK for the initial
- *    cut and then carried: each round adds its change, the restored (pd = -P) and
- *    compensated (pd = +P) candidates summed in four classes k mod 4 (a sequential chain
- *    over increasing k each, fmaf for the products), combined as (d0 + d1) + (d2 + d3);
+ * restatement fixes them, in the same order as the GPU kernels:
+ *  - SEQK, the sums over key blocks (P @ v_bar and sum P of the dense reference, Pd @ v_bar
+ *    and sum_Pd of a drop set): one sequential fp32 chain over increasing k of every key
+ *    block, fmaf(w_k, v_k[d], acc) with w_k = P_k, or 0 for a block outside the set (the
+ *    zero terms are part of the chain), and the weight sum as fmaf(w_k, 1, acc);
+ *  - DOT64, the per-candidate products v_k . Mvq and v_k . big(Mg): one sequential fmaf
+ *    chain over d = 0..63;
+ *  - the drop set's sum_Pd and Pd @ v_bar are formed afresh by SEQK for every objective
+ *    (the reference recomputes Pd @ v_bar each round, projected.py:903-907);
  *  - every other sum and 64-term product (M v_bar_query, M g, ||g||^2_M, term_q, term_k)
  *    is a sequential fp32 chain in index order.
+ * The GPU evaluates SEQK and DOT64 on the matrix cores (v_mfma_f32_16x16x4_f32 /
+ * v_mfma_f32_32x32x2_f32 add their k terms to the accumulator one fmaf at a time, in k
+ * order, on gfx950).
  *
  * A [H][q_blk][kb_p]  pooled map over the patch key blocks (attn_full), fp32
  * V [H][kb_p][64]     block-mean values (v_bar_full), fp32
@@ -499,70 +500,33 @@ static inline float rs_knorm(float G, float K, float dG, float u) {
   return (a * b / (K * K) - dG) / (Kn * Kn);
 }
 
-/* balanced pairwise tree over 16 values */
-static float rs_tree16(const float* a) {
-  float t8[8], t4[4];
-  for (int i = 0; i < 8; ++i) t8[i] = a[2 * i] + a[2 * i + 1];
-  for (int i = 0; i < 4; ++i) t4[i] = t8[2 * i] + t8[2 * i + 1];
-  return (t4[0] + t4[1]) + (t4[2] + t4[3]);
-}
-/* SUMK over k < n of the terms with use[k] != 0 (use NULL: all): dot[d] = sum P[k] V[k][d],
- * *sum = sum P[k] */
-static void rs_sumk(const float* P, const uint8_t* use, const float* Vb, int n, float* dot, float* sum) {
-  float acc[16][64], sps[16];
-  for (int c = 0; c < 16; ++c) {
-    sps[c] = 0.0f;
-    for (int d = 0; d < 64; ++d) acc[c][d] = 0.0f;
-  }
+/* SEQK over k < n (use NULL: every k; else w_k = 0 where use[k] == 0): dot[d] = the fmaf
+ * chain of w_k * V[k][d], *sum = the chain of w_k */
+static void rs_seqk(const float* P, const uint8_t* use, const float* Vb, int n, float* dot, float* sum) {
+  float acc[64], sp = 0.0f;
+  for (int d = 0; d < 64; ++d) acc[d] = 0.0f;
   for (int k = 0; k < n; ++k) {
-    if (use && !use[k]) continue;
-    const int c = k & 15;
-    sps[c] = sps[c] + P[k];
-    for (int d = 0; d < 64; ++d) acc[c][d] = fmaf(P[k], Vb[(long long)k * 64 + d], acc[c][d]);
+    const float w = (use && !use[k]) ? 0.0f : P[k];
+    sp = fmaf(w, 1.0f, sp);
+    for (int d = 0; d < 64; ++d) acc[d] = fmaf(w, Vb[(long long)k * 64 + d], acc[d]);
   }
-  for (int d = 0; d < 64; ++d) {
-    float col[16];
-    for (int c = 0; c < 16; ++c) col[c] = acc[c][d];
-    dot[d] = rs_tree16(col);
-  }
-  *sum = rs_tree16(sps);
+  for (int d = 0; d < 64; ++d) dot[d] = acc[d];
+  *sum = sp;
 }
-/* DOT4x16 of a and b (64 values each) */
-static float rs_dot4x16(const float* a, const float* b) {
-  float c[4];
-  for (int q = 0; q < 4; ++q) {
-    float s = 0.0f;
-    for (int d = 16 * q; d < 16 * q + 16; ++d) s = fmaf(a[d], b[d], s);
-    c[q] = s;
-  }
-  return (c[0] + c[1]) + (c[2] + c[3]);
+/* DOT64 of a and b (64 values each) */
+static float rs_dot64(const float* a, const float* b) {
+  float s = 0.0f;
+  for (int d = 0; d < 64; ++d) s = fmaf(a[d], b[d], s);
+  return s;
 }
 
-/* The carried objective state of a drop set: unrounded sum_Pd and Pd @ v_bar. */
+/* The objective state of a drop set: unrounded sum_Pd and Pd @ v_bar. */
 typedef struct {
   float sp;
   float mv[64];
 } rs_state;
-static void rs_state_init(rs_state* st, const float* Pb, const uint8_t* drop, const float* Vb, int n_cand) {
-  rs_sumk(Pb, drop, Vb, n_cand, st->mv, &st->sp);
-}
-/* a round's move: restored candidates leave the drop set, compensated ones join it */
-static void rs_state_carry(rs_state* st, const float* Pb, const uint8_t* restored, const uint8_t* comp,
-                           const float* Vb, int n_cand) {
-  float dm[4][64], ds[4];
-  for (int c = 0; c < 4; ++c) {
-    ds[c] = 0.0f;
-    for (int d = 0; d < 64; ++d) dm[c][d] = 0.0f;
-  }
-  for (int k = 0; k < n_cand; ++k) {
-    if (!restored[k] && !comp[k]) continue;
-    const int c = k & 3;
-    const float pd = comp[k] ? Pb[k] : -Pb[k];
-    ds[c] = ds[c] + pd;
-    for (int d = 0; d < 64; ++d) dm[c][d] = fmaf(pd, Vb[(long long)k * 64 + d], dm[c][d]);
-  }
-  for (int d = 0; d < 64; ++d) st->mv[d] = st->mv[d] + ((dm[0][d] + dm[1][d]) + (dm[2][d] + dm[3][d]));
-  st->sp = st->sp + ((ds[0] + ds[1]) + (ds[2] + ds[3]));
+static void rs_state_of(rs_state* st, const float* Pb, const uint8_t* drop, const float* Vb, int n_cand) {
+  rs_seqk(Pb, drop, Vb, n_cand, st->mv, &st->sp);
 }
 
 /* g, Mg, ||g||^2_M, K and J of a state (projected.py:859-868 / 903-918) */
@@ -611,7 +575,7 @@ static void rs_row_setup(const float* Arow, const float* Mb, const float* Vb, co
                          int big, int renorm, float* Pb, float* vq, float* tm_out, float* s, float* scut, float* ssq) {
   for (int k = 0; k < kb_p; ++k) Pb[k] = rs_bf(Arow[k], big);
   float tm;
-  rs_sumk(Pb, NULL, Vb, kb_p, vq, &tm);
+  rs_seqk(Pb, NULL, Vb, kb_p, vq, &tm);
   *tm_out = rs_bf(tm, big);
   for (int d = 0; d < 64; ++d) vq[d] = rs_bf(vq[d], big);
   float Mvq[64], tq = 0.0f;
@@ -623,7 +587,7 @@ static void rs_row_setup(const float* Arow, const float* Mb, const float* Vb, co
   for (int i = 0; i < 64; ++i) tq = tq + rs_bf(Mvq[i] * vq[i], big);
   tq = rs_bf(tq, big);
   for (int k = 0; k < n_cand; ++k) {
-    const float cr = rs_bf(rs_dot4x16(Mvq, Vb + (long long)k * 64), big);
+    const float cr = rs_bf(rs_dot64(Mvq, Vb + (long long)k * 64), big);
     float qd = rs_bf(rs_bf(tq - rs_bf(2.0f * cr, big), big) + termk[k], big);
     qd = qd < 0.0f ? 0.0f : qd;
     const float sq = rs_bf(sqrtf(qd), big);
@@ -650,7 +614,7 @@ static float rs_round_qualities(const float* Pb, const rs_state* st, const float
   const float tqb = rs_bf(tqr, big);
   for (int d = 0; d < 64; ++d) Mgb[d] = rs_bf(Mg[d], big);
   for (int k = 0; k < n_cand; ++k) {
-    const float tk = rs_bf(rs_dot4x16(Vb + (long long)k * 64, Mgb), big);
+    const float tk = rs_bf(rs_dot64(Vb + (long long)k * 64, Mgb), big);
     const float raw = rs_bf(Pb[k] * rs_bf(tk - tqb, big), big);
     rq[k] = rs_knorm(gn, K, 2.0f * raw + ssq[k], Pb[k]);
     cq[k] = rs_knorm(gn, K, ssq[k] - 2.0f * raw, -Pb[k]);
@@ -712,7 +676,7 @@ static void rs_row(const float* Arow, const float* Mb, const float* Vb, const fl
   for (int k = 0; k < n_cand; ++k) drop[k] = !sel[k];
   float g[64], Mg[64], gn, K, sp;
   rs_state st;
-  rs_state_init(&st, Pb, drop, Vb, n_cand);
+  rs_state_of(&st, Pb, drop, Vb, n_cand);
   float best_obj = 0.0f;
   if (track) {
     best_obj = rs_objective(&st, M32, vq, tm, big, g, Mg, &gn, &K, &sp);
@@ -756,7 +720,7 @@ static void rs_row(const float* Arow, const float* Mb, const float* Vb, const fl
     for (int k = 0; k < n_cand; ++k) valid[k] = !drop[k];
     rs_top_m(cq, valid, n_cand, cnt, sel2, w->keys, w->idx);
     for (int k = 0; k < n_cand; ++k) drop[k] = (uint8_t)((drop[k] && !sel[k]) || sel2[k]);
-    rs_state_carry(&st, Pb, sel, sel2, Vb, n_cand);
+    rs_state_of(&st, Pb, drop, Vb, n_cand);
   }
   float fin = 0.0f;
   if (track || obj) fin = rs_objective(&st, M32, vq, tm, big, g, Mg, &gn, &K, &sp);
@@ -822,7 +786,7 @@ int oracle_rs_probe(const float* A, const float* V, const float* M, const uint8_
       rs_row_setup(A + row * kb_p, Mb, Vb, termk, kb_p, n_cand, big, renorm, Pb, vq, &tm, s_out + row * n_cand,
                    scut_out + row * n_cand, ssq);
       rs_state st;
-      rs_state_init(&st, Pb, drop + row * n_cand, Vb, n_cand);
+      rs_state_of(&st, Pb, drop + row * n_cand, Vb, n_cand);
       J_out[row] = rs_round_qualities(Pb, &st, Vb, M32, vq, tm, ssq, n_cand, big, rq_out + row * n_cand,
                                       cq_out + row * n_cand);
     }

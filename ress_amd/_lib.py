@@ -61,7 +61,7 @@ def lib():
         L.ress_attn_sched_bytes.restype = ctypes.c_longlong
         L.ress_attn_sched_bytes.argtypes = [ctypes.c_int] * 3
         L.ress_restore_swap_workspace_size.restype = ctypes.c_longlong
-        L.ress_restore_swap_workspace_size.argtypes = [ctypes.c_int] * 3
+        L.ress_restore_swap_workspace_size.argtypes = [ctypes.c_int] * 4
         L.ress_meansim_workspace_size.restype = ctypes.c_longlong
         L.ress_meansim_workspace_size.argtypes = [ctypes.c_int] * 4
         L.ress_noalloc_scratch_bytes.restype = ctypes.c_longlong

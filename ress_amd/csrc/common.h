@@ -96,16 +96,16 @@ __device__ __forceinline__ void unpack_bf16x8(const uint4& r, float x[8]) {
   x[4] = bf16_lo(r.z); x[5] = bf16_hi(r.z);
   x[6] = bf16_lo(r.w); x[7] = bf16_hi(r.w);
 }
-// fp32 -> bf16, round to nearest even (NaN kept quiet)
 // two floats -> packed fp16 pair (round to nearest even), lo in bits 0..15
 __device__ __forceinline__ uint32_t f32x2_to_f16_bits(float lo, float hi) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
 }
+// fp32 -> bf16, round to nearest even, a NaN made quiet with its payload's high bits kept:
+// the bits of ((u + 0x7fff + ((u >> 16) & 1)) >> 16) for numbers and ((u >> 16) | 0x40) for
+// NaNs. gfx950's v_cvt_pk_bf16_f32 (the __bf16 conversion) gives exactly these bits for
+// every one of the 2^32 inputs (checked exhaustively on the device, subnormals included).
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
 }
 __device__ __forceinline__ float round_bf16(float f) {
   return __uint_as_float(f32_to_bf16_bits(f) << 16);

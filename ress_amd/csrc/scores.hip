@@ -13,11 +13,12 @@
 // workgroups, else one), scores in LDS; pooled K goes through LDS in coalesced 64-block
 // tiles that the rows share (tile t+1 is loaded into registers while tile t is used), and
 // lane l owns the columns kb = 64t + l, which is also the SUM64 partial order.
-// Longer rows: the scores as one matrix-core GEMM into attn_full (k_scores_gemm, DOT64
+// Longer rows: the scores as one matrix-core GEMM into attn_full (k_gemm64, DOT64
 // exactly), then k_pooled_softmax_rows; k_pooled_scores_rows beyond 64*PS_E_MAX blocks.
 #include <type_traits>
 
 #include "common.h"
+#include "mfma_gemm.h"
 
 namespace {
 constexpr int PS_TILED_MAX = 1024;
@@ -121,149 +122,6 @@ __global__ __launch_bounds__(256) void k_pooled_scores_tiled(const float* __rest
     for (int kb = lane; kb < n_cand; kb += 64) cond[kb] = (e[kb] / total) / rs;
   }
 }
-// ---- the score GEMM on the matrix cores ------------------------------------------------
-// A workgroup of 4 waves takes a 128-row tile of S and walks column tiles of 128 (tiles
-// blockIdx.x, blockIdx.x + gridDim.x, ...). Wave w holds rows 32w..32w+31 of the A operand
-// in registers for the whole walk and computes them against all 128 columns of each tile
-// (4 column sub-tiles of 32). Step s of v_mfma_f32_32x32x2_f32 takes dim 2s + l/32 of row
-// l%32 from lane l, so B tiles sit in LDS with each row's 64 dims split into the even dims
-// (floats 0..31) and the odd dims (32..63): a lane's 32 values are one contiguous run, read
-// as 8 float4s; the 68-float row stride puts 16 consecutive rows' float4 reads in distinct
-// banks. B tiles are double-buffered: the next tile's loads are in flight during the MFMAs.
-constexpr int SG_T = 128;
-constexpr int SG_LD = 68;
-constexpr int SG_WALK = 4;  // column tiles per workgroup (at most)
-typedef float sg_f16v __attribute__((ext_vector_type(16)));
-
-__global__ __launch_bounds__(256) void k_scores_gemm(const float* __restrict__ a, const float* __restrict__ b,
-                                                     int na, int nb, int r_begin, int r_end, float scale,
-                                                     float* __restrict__ S) {
-  __shared__ __align__(16) float bl[2][SG_T * SG_LD];
-  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r0 = r_begin + blockIdx.y * SG_T, bh = blockIdx.z, h = lane >> 5, rl = lane & 31;
-  const int ntile = cdiv(nb, SG_T);
-  const float* bhd = b + (long long)bh * nb * 64;
-  // B tile loads: 2048 float4 chunks, chunk f = row f/16, dims 4(f%16)..+3; rows past the
-  // matrix read its last row (zeroed when written to LDS; their outputs are not stored)
-  float4 ys[8];
-  auto load_b = [&](int t) {
-    const int c0 = t * SG_T;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int f = tid + 256 * i;
-      ys[i] = reinterpret_cast<const float4*>(bhd + (long long)min(c0 + (f >> 4), nb - 1) * 64)[f & 15];
-    }
-  };
-  auto store_b = [&](int t, float* dst) {
-    const int c0 = t * SG_T;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int f = tid + 256 * i, r = f >> 4, q = f & 15;
-      const float4 y = c0 + r < nb ? ys[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      // dims 4q and 4q+2 go to even positions 2q, 2q+1; dims 4q+1 and 4q+3 to the odd half
-      *reinterpret_cast<float2*>(dst + r * SG_LD + 2 * q) = make_float2(y.x, y.z);
-      *reinterpret_cast<float2*>(dst + r * SG_LD + 32 + 2 * q) = make_float2(y.y, y.w);
-    }
-  };
-  int t = blockIdx.x;
-  if (t >= ntile) return;  // workgroup-uniform
-  load_b(t);
-  // the wave's A operand: dim 2s + h of row r0 + 32w + rl for s = 0..31 (zero past the matrix)
-  float av[32];
-  {
-    const int ra = r0 + 32 * w + rl;
-    const float4* ap = reinterpret_cast<const float4*>(a + ((long long)bh * na + min(ra, r_end - 1)) * 64);
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const float4 x = ap[q];
-      av[2 * q] = ra < r_end ? (h ? x.y : x.x) : 0.0f;
-      av[2 * q + 1] = ra < r_end ? (h ? x.w : x.z) : 0.0f;
-    }
-  }
-  store_b(t, bl[0]);
-  __syncthreads();
-  const int lrow = 32 * w + 4 * h;
-  char* trow = reinterpret_cast<char*>(S + ((long long)bh * na + r0) * nb);  // the row tile's origin
-  constexpr int BCT = 32 * SG_LD / 4;            // float4s between column sub-tiles
-#pragma unroll 1
-  for (int it = 0;; ++it) {
-    const int tn = t + (int)gridDim.x;
-    const bool more = it + 1 < SG_WALK && tn < ntile;  // uniform
-    if (more) load_b(tn);
-    const float4* bp = reinterpret_cast<const float4*>(bl[it & 1] + rl * SG_LD + 32 * h);
-    sg_f16v acc[4];
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) acc[ct][j] = 0.0f;
-    // every accumulator takes steps s = 0..31 in order: DOT64 over d = 0..63. The B
-    // operands of steps 4(j+1).. are read from LDS before the MFMAs of steps 4j.. issue.
-    float4 bv[4], bn[4];
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) bv[ct] = bp[ct * BCT];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (j + 1 < 8) {
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) bn[ct] = bp[ct * BCT + j + 1];
-      }
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct)
-        acc[ct] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * j], bv[ct].x, acc[ct], 0, 0, 0);
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct)
-        acc[ct] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * j + 1], bv[ct].y, acc[ct], 0, 0, 0);
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct)
-        acc[ct] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * j + 2], bv[ct].z, acc[ct], 0, 0, 0);
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct)
-        acc[ct] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * j + 3], bv[ct].w, acc[ct], 0, 0, 0);
-      if (j + 1 < 8) {
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) bv[ct] = bn[ct];
-      }
-    }
-    // accumulator element j of lane l is row 8(j/4) + 4(l/32) + j%4, column l%32 of its
-    // sub-tile; offsets from the (uniform) tile origin fit 32 bits
-    const int c0 = t * SG_T;
-    char* tile = trow + 4ll * c0;
-    // byte offsets from the uniform tile origin (below 2^31: 128 rows of at most 2^21
-    // floats), unsigned so that the stores take the scalar-base + 32-bit offset form
-    if (r0 + SG_T <= r_end && c0 + SG_T <= nb) {  // whole tile (uniform): no per-store test
-      unsigned lofs = 4u * (unsigned)(lrow * nb + rl);
-      // kept opaque so the 64 store offsets are formed per tile, not hoisted out of the
-      // walk into 64 live registers
-      asm volatile("" : "+v"(lofs));
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-          *reinterpret_cast<float*>(tile + (lofs + 4u * (unsigned)((8 * (j >> 2) + (j & 3)) * nb + 32 * ct))) =
-              acc[ct][j] * scale;
-    } else {
-      // rows and columns this lane may still store (opaque for the same reason as above)
-      int rlim = r_end - r0 - lrow, clim = nb - c0 - rl;
-      unsigned lofs = 4u * (unsigned)(lrow * nb + rl);
-      asm volatile("" : "+v"(rlim), "+v"(clim), "+v"(lofs));
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int dr = 8 * (j >> 2) + (j & 3);
-          if (dr < rlim && 32 * ct < clim)
-            *reinterpret_cast<float*>(tile + (lofs + 4u * (unsigned)(dr * nb + 32 * ct))) = acc[ct][j] * scale;
-        }
-    }
-    if (!more) break;
-    // buffer (it+1)&1 was last read in the previous iteration, which every wave finished
-    // before the barrier that ended it
-    store_b(tn, bl[(it + 1) & 1]);
-    __syncthreads();
-    t = tn;
-  }
-}
-
 // The softmax of rows whose raw scores are already in attn_full, one wave per row (four
 // rows per workgroup): lane l holds columns kb = 64e + l (e < E) in registers, the SUM64
 // partial order; the same outputs as k_pooled_scores_tiled.
@@ -316,11 +174,10 @@ constexpr int PS_E_MAX = 128;  // k_pooled_softmax_rows: rows of up to 64*PS_E_M
 
 int scores_gemm(const float* a, const float* b, int BH, int na, int nb, int r_begin, int r_end, float scale,
                 float* S, hipStream_t stream) {
-  // column tiles t = x, x + gx, ... per workgroup, at most SG_WALK of them
-  const int gx = cdiv(cdiv(nb, SG_T), SG_WALK);
-  hipLaunchKernelGGL(k_scores_gemm, dim3(gx, cdiv(r_end - r_begin, SG_T), BH), dim3(256), 0, stream, a, b, na, nb,
-                     r_begin, r_end, scale, S);
-  RESS_LAUNCHED("k_scores_gemm");
+  hipLaunchKernelGGL(k_gemm64<G64Store<>>, g64_grid(BH, nb, r_begin, r_end, G64Store<>::kWalk), dim3(256), 0, stream,
+                     a, b, na, nb,
+                     64ll * nb, r_begin, r_end, G64Store<>{S, scale});
+  RESS_LAUNCHED("k_gemm64<G64Store<>>");
   return 0;
 }
 

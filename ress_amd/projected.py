@@ -147,7 +147,7 @@ def _restore_swap(attn_pooled, v_bar, M, num_to_select, restore_frac, n_iters, t
     flags = ((_RS_BF16 if big_dtype == torch.bfloat16 else 0) | (_RS_TRACK_BEST if track_best else 0)
              | (_RS_MAXIMIZE if maximize else 0) | (_RS_INVERT_CUT if invert_cut else 0)
              | (0 if (True if renormalize is None else renormalize) else _RS_NO_RENORM))
-    ws_bytes = _lib.lib().ress_restore_swap_workspace_size(BH, kb_p, n_cand)
+    ws_bytes = _lib.lib().ress_restore_swap_workspace_size(BH, q_blk, kb_p, n_cand)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     _lib.call("ress_restore_swap", _lib.ptr(A), _lib.ptr(V), _lib.ptr(Mf), _lib.ptr(nts), BH, nh, q_blk, kb_p, n_cand,
               int(n_iters), float(restore_frac), float(decay), flags, _lib.ptr(keep), None, _lib.ptr(s), _lib.ptr(ws),

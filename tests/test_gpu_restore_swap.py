@@ -1,8 +1,8 @@
 """GPU parity of the ReSS restore-swap kernel (ress_swap.hip) against the C oracle.
 
 Keep sets, the drift scores s and the objective J of the returned set are compared bit
-for bit, across row lengths that exercise every lane-width variant of the kernel and the
-modes the criterion grammar reaches; then the whole ReSS layer (HeSS budget +
+for bit, across row counts and lengths that exercise every tiling edge of the kernels and
+the modes the criterion grammar reaches; then the whole ReSS layer (HeSS budget +
 restore_swap_iter5_bf16_trackbest + selection + attention) against the oracle pipeline."""
 
 import numpy as np
@@ -38,7 +38,7 @@ def _gpu_restore_swap(A, V, M, nts, n_cand, n_iters, restore_frac, decay, flags,
     key = torch.empty(H, q_blk, n_cand, device=dev)
     s = torch.empty(H, q_blk, n_cand, device=dev)
     obj = torch.empty(H, q_blk, device=dev)
-    ws_bytes = _lib.lib().ress_restore_swap_workspace_size(H, kb_p, n_cand)
+    ws_bytes = _lib.lib().ress_restore_swap_workspace_size(H, q_blk, kb_p, n_cand)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     Ad, Vd, Md, nd = t(A), t(V), t(M), t(nts)
     _lib.call("ress_restore_swap", _lib.ptr(Ad), _lib.ptr(Vd), _lib.ptr(Md), _lib.ptr(nd), H, H, q_blk, kb_p,
@@ -48,10 +48,12 @@ def _gpu_restore_swap(A, V, M, nts, n_cand, n_iters, restore_frac, decay, flags,
     return key.cpu().numpy(), s.cpu().numpy(), obj.cpu().numpy()
 
 
-# row lengths: every lane-width variant, LDS-resident V (bf16 up to ~730 blocks), and streamed
-# V through four tile buffers (up to ~1700 blocks) or two (1800)
-SHAPES = [(2, 7, 40, 39), (3, 9, 130, 129), (2, 5, 400, 399), (2, 5, 685, 684), (1, 3, 900, 899),
-          (1, 3, 1100, 1100), (1, 2, 1369, 1368), (1, 2, 1800, 1799)]
+# (heads, rows, key blocks, candidates): row lengths across every selection width (candidate
+# slots per lane 4..32), key-block chunks of the P @ v_bar sums (partial last chunk),
+# candidate tiles of the product GEMM (partial last tile), row groups of the sums (16 rows,
+# ragged last group) and row tiles of the GEMM (128 rows, ragged last tile)
+SHAPES = [(2, 7, 40, 39), (3, 9, 130, 129), (2, 37, 300, 299), (2, 5, 685, 684), (1, 3, 900, 899),
+          (1, 150, 700, 700), (1, 3, 1100, 1100), (1, 2, 1369, 1368), (1, 2, 1800, 1799)]
 MODES = {
     "ress_recipe": (5, 0.5, 0.5, 1 | 2),
     "fp32": (5, 0.5, 0.5, 2),
@@ -60,6 +62,7 @@ MODES = {
     "antiswap": (5, 0.5, 0.5, 1 | 2 | 4),
     "anti": (5, 0.5, 0.5, 1 | 2 | 4 | 8),
     "no_renorm": (3, 0.5, 0.5, 1 | 2 | 16),
+    "cut_only": (0, 0.5, 0.5, 1 | 2),
 }
 
 
