@@ -44,7 +44,7 @@
 
 namespace {
 
-constexpr int MS_MAX_NK = 6144;    // key blocks per row of the map kernels (24 KiB of p in LDS)
+constexpr int MS_MAX_NK = 6144;    // key blocks per row of the map kernels (24 KiB of p, 6 KiB of flags in LDS)
 constexpr int MS_CH_LD = 17;       // k_ms_map_long score chunks: 64 columns x 16 dims, odd row stride
 constexpr float MS_Q_SCALE = 1125899906842624.0f;  // 2^50: q(p) = floor(p * 2^50)
 // front LDS region of k_ms_map_long: the four waves' score chunks
@@ -365,6 +365,7 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
   // front region (MS_LONG_FRONT_BYTES, without PRE): the waves' score chunks
   float* scw = reinterpret_cast<float*>(ms_dyn) + (threadIdx.x >> 6) * (64 * MS_CH_LD);  // [64][MS_CH_LD]
   float* p = reinterpret_cast<float*>(ms_dyn + (PRE ? 0 : MS_LONG_FRONT_BYTES));  // [nk] scores -> p, column order
+  uint8_t* skl = reinterpret_cast<uint8_t*>(p + nk);  // [nk] the columns' similarity flags, then the map row
   __shared__ float red[4];
   __shared__ int ired[4];
   __shared__ int hc[256];
@@ -382,14 +383,27 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
   }
   float mx = -__builtin_huge_valf();
   if constexpr (PRE) {
+    // every load of a batch of eight columns per thread is issued before any is used
+    // (columns past nk read column nk - 1 and are dropped)
     const float* srow = S + ((long long)bh * nq + r) * nk;
-    for (int c = tid; c < nk; c += 256) {
-      float s = -__builtin_huge_valf();
-      if (sk[c]) {
-        s = srow[c];
-        mx = fmaxf(mx, s);
+    for (int cb = 0; cb < nk; cb += 256 * 8) {
+      float sv[8];
+      uint8_t kv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int c = min(cb + 256 * u + tid, nk - 1);
+        sv[u] = srow[c];
+        kv[u] = sk[c];
       }
-      p[c] = s;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int c = cb + 256 * u + tid;
+        if (c < nk) {
+          if (kv[u]) mx = fmaxf(mx, sv[u]);
+          p[c] = kv[u] ? sv[u] : -__builtin_huge_valf();
+          skl[c] = kv[u];
+        }
+      }
     }
   } else {
   float pq[64];
@@ -447,6 +461,7 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
         mx = fmaxf(mx, s);
       }
       p[c] = s;
+      skl[c] = live ? 1 : 0;
     }
   }
   }  // PRE
@@ -458,7 +473,7 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
     for (int c = tid; c < nk; c += 256) row[c] = 1;
     return;
   }
-  for (int c = tid; c < nk; c += 256) p[c] = sk[c] ? ress_expf(p[c] - mx) : 0.0f;
+  for (int c = tid; c < nk; c += 256) p[c] = skl[c] ? ress_expf(p[c] - mx) : 0.0f;
   __syncthreads();
   if (w == 0) {
     float a = 0.0f;
@@ -589,8 +604,10 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
         ++rank_eq;
       }
     }
-    row[c] = (sel || !sk[c] || c < n_sink) ? 1 : 0;
+    skl[c] = (sel || !skl[c] || c < n_sink) ? 1 : 0;  // column c is this thread's alone
   }
+  __syncthreads();
+  for (int c = tid; c < nk; c += 256) row[c] = skl[c];  // coalesced
 }
 
 // One wave per (head, q-block) row, E = 64-key-block columns per lane (nk <= 64E), four
@@ -808,10 +825,10 @@ RESS_API int ress_meansim_block_map(const void* q, const void* k, const void* km
     if (workspace) {
       const int rc = scores_gemm(pq, pk, BH, nq, nk, 0, nq, 0.125f, (float*)workspace, stream);
       if (rc) return rc;
-      hipLaunchKernelGGL(k_ms_map_long<true>, dim3(nq, BH), dim3(256), (size_t)nk * 4, stream, pq, pk, sq8, sk8, H,
+      hipLaunchKernelGGL(k_ms_map_long<true>, dim3(nq, BH), dim3(256), (size_t)nk * 5, stream, pq, pk, sq8, sk8, H,
                          nq, nk, cd, n_sink, (const float*)workspace, m8);
     } else {
-      hipLaunchKernelGGL(k_ms_map_long<false>, dim3(nq, BH), dim3(256), MS_LONG_FRONT_BYTES + (size_t)nk * 4, stream,
+      hipLaunchKernelGGL(k_ms_map_long<false>, dim3(nq, BH), dim3(256), MS_LONG_FRONT_BYTES + (size_t)nk * 5, stream,
                          pq, pk, sq8, sk8, H, nq, nk, cd, n_sink, (const float*)nullptr, m8);
     }
   }
