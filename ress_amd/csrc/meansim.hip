@@ -47,6 +47,11 @@ namespace {
 constexpr int MS_MAX_NK = 6144;    // key blocks per row of the map kernels (24 KiB of p, 6 KiB of flags in LDS)
 constexpr int MS_CH_LD = 17;       // k_ms_map_long score chunks: 64 columns x 16 dims, odd row stride
 constexpr float MS_Q_SCALE = 1125899906842624.0f;  // 2^50: q(p) = floor(p * 2^50)
+// One 64-bit histogram word per bin: count << 51 | sum of q. A row's p sum to 1 within
+// nk rounding errors (< 1.001 for nk <= MS_MAX_NK), so any bin's q sum stays below 2^51,
+// and its count (<= MS_MAX_NK) fits the 13 bits above.
+constexpr int MS_PACK_SHIFT = 51;
+static_assert(MS_MAX_NK < (1 << (64 - MS_PACK_SHIFT)), "a bin's count fits above its q sum");
 // front LDS region of k_ms_map_long: the four waves' score chunks
 constexpr size_t MS_LONG_FRONT_BYTES = 4 * 64 * MS_CH_LD * 4;
 
@@ -217,6 +222,8 @@ __global__ __launch_bounds__(256) void k_ms_stats(const uint16_t* __restrict__ q
 // the running total stays <= T. Returns false if every bin fits (above, n_above then
 // include them all); otherwise the crossing bin with its count and sum, and above /
 // n_above advanced over the bins before it. Every lane gets the same results.
+// PACKED: hs[bin] holds count << MS_PACK_SHIFT | sum of q (hc unused).
+template <bool PACKED = false>
 __device__ __forceinline__ bool ms_cdf_digit(const int* hc, const unsigned long long* hs, unsigned long long T,
                                              unsigned long long& above, int& n_above, int lane, int& bin,
                                              int& bcnt, unsigned long long& bsum) {
@@ -225,8 +232,14 @@ __device__ __forceinline__ bool ms_cdf_digit(const int* hc, const unsigned long 
   int lc = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {  // lane l: bins 255-4l down to 252-4l
-    c4[j] = hc[255 - 4 * lane - j];
-    s4[j] = hs[255 - 4 * lane - j];
+    if constexpr (PACKED) {
+      const unsigned long long v = hs[255 - 4 * lane - j];
+      c4[j] = (int)(v >> MS_PACK_SHIFT);
+      s4[j] = v & ((1ull << MS_PACK_SHIFT) - 1ull);
+    } else {
+      c4[j] = hc[255 - 4 * lane - j];
+      s4[j] = hs[255 - 4 * lane - j];
+    }
     ls += s4[j];
     lc += c4[j];
   }
@@ -368,8 +381,7 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
   uint8_t* skl = reinterpret_cast<uint8_t*>(p + nk);  // [nk] the columns' similarity flags, then the map row
   __shared__ float red[4];
   __shared__ int ired[4];
-  __shared__ int hc[256];
-  __shared__ unsigned long long hs[256];
+  __shared__ unsigned long long hs[256];  // packed histogram (MS_PACK_SHIFT)
   __shared__ unsigned long long cut_l[2];  // the digit's result: above, then bsum
   __shared__ int cut_i[4];                 // crossed, bin, n_above, bcnt
   __shared__ uint32_t vmin_l;
@@ -475,9 +487,17 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
   }
   for (int c = tid; c < nk; c += 256) p[c] = skl[c] ? ress_expf(p[c] - mx) : 0.0f;
   __syncthreads();
-  if (w == 0) {
+  if (w == 0) {  // lane l adds columns l, l + 64, ... in order; eight reads in flight
     float a = 0.0f;
-    for (int i = lane; i < nk; i += 64) a = a + p[i];
+    int i = lane;
+    for (; i + 448 < nk; i += 512) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = p[i + 64 * u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) a = a + v[u];
+    }
+    for (; i < nk; i += 64) a = a + p[i];
     a = sum64_tree(a);
     if (lane == 0) red[0] = a;
   }
@@ -518,20 +538,18 @@ __global__ __launch_bounds__(256) void k_ms_map_long(const float* __restrict__ p
     while (hi >= 0) {
       const int shift = max(hi - 7, 0);
       const uint32_t dmask = (2u << (hi - shift)) - 1u;
-      hc[tid] = 0;
       hs[tid] = 0ull;
       __syncthreads();
       for (int c = tid; c < nk; c += 256) {
         const uint32_t b = __float_as_uint(p[c]);
-        if ((b & pmask) == prefix) {
-          atomicAdd(&hc[(b >> shift) & dmask], 1);
-          atomicAdd(&hs[(b >> shift) & dmask], (unsigned long long)(p[c] * MS_Q_SCALE));
-        }
+        if ((b & pmask) == prefix)
+          atomicAdd(&hs[(b >> shift) & dmask],
+                    (1ull << MS_PACK_SHIFT) | (unsigned long long)(__uint_as_float(b) * MS_Q_SCALE));
       }
       __syncthreads();
       if (w == 0) {
         int bin = 0;
-        const bool x = ms_cdf_digit(hc, hs, T, above, n_above, lane, bin, bcnt, bsum);
+        const bool x = ms_cdf_digit<true>(nullptr, hs, T, above, n_above, lane, bin, bcnt, bsum);
         if (lane == 0) {
           cut_i[0] = x;
           cut_i[1] = bin;
