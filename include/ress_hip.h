@@ -20,6 +20,15 @@ extern "C" {
 /* ---- library ------------------------------------------------------------- */
 const char* ress_last_error(void);
 int ress_abi_version(void);
+/* Self-check of the device's bf16 rounding (no counterpart in the reference; for tests and
+ * for callers that want to confirm a device before trusting bit-exact bf16 results). Every
+ * kernel here rounds fp32 to bf16 with the device's conversion instruction, which stands
+ * for round-to-nearest-even with NaNs made quiet ((u >> 16) | 0x40) -- the rounding of
+ * torch's .to(bfloat16) for numbers. For the fp32 bit patterns first .. first+count-1
+ * (count <= 2^32), adds the number of patterns whose conversion differs to out[0] and
+ * lowers out[1] to the lowest such pattern: out is two uint64 in device memory, which the
+ * caller sets to {0, ~0} first. */
+int ress_bf16_selfcheck(unsigned int first, unsigned long long count, void* out, hipStream_t stream);
 
 /* ---- block preparation (prep.hip) ---------------------------------------- */
 

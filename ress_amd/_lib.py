@@ -31,6 +31,7 @@ _SIGS = {
     "ress_restore_swap": "pppp" + "iiiiii" + "dd" + "i" + "ppp" + "pl" + "s",
     "ress_meansim_block_map": "ppp" + "iiii" + "llllll" + "ppi" + "ppppppppp" + "pl" + "s",
     "ress_qk_norm_rope": "piii" + "pppp" + "f" + "pf" + "ppp" + "s",
+    "ress_bf16_selfcheck": "Il" + "p" + "s",
 }
 _CT = {
     "p": ctypes.c_void_p,

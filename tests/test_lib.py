@@ -52,7 +52,7 @@ def test_binding_argument_counts_match_header(library):
 
 
 def test_abi_version_and_error_string(library):
-    assert library.ress_abi_version() == 4
+    assert library.ress_abi_version() == 5
     assert isinstance(library.ress_last_error(), bytes)
 
 
