@@ -75,9 +75,10 @@ __host__ __device__ __forceinline__ int rs_dstride(int n_cand) { return (n_cand 
 // after the final objective, 1 when the best round's set is returned.
 enum { RSV_TM = 0, RSV_TQ, RSV_TQB, RSV_GN, RSV_K, RSV_J, RSV_BEST, RSV_FLAG, RS_NSCAL = 8 };
 
-// Per-head preparation, 64 key blocks per workgroup: Vb = big(V) [kb64][64] fp32 (rows
-// past kb_p zero), the same values per 64-block chunk in the sums' operand order Vt (see
-// pv_kpos) and the key side of quadratic_deviation, termk[k] =
+// Per-head preparation, 64 key blocks per workgroup: Vb = big(V) [kb64][64] fp32 with each
+// row's even dims first, then its odd dims (the products' B operand; rows past kb_p zero),
+// the same values per 64-block chunk in the sums' operand order Vt (key 4s + j at position
+// 16j + s) and the key side of quadratic_deviation, termk[k] =
 // big(sum_i big(big(Mb v_k)_i * v_ki)) with the product and the sum sequential in index
 // order (the block goes through an LDS tile).
 __global__ __launch_bounds__(256) void k_rs_head(const float* __restrict__ V, const float* __restrict__ M, int H,
@@ -92,7 +93,7 @@ __global__ __launch_bounds__(256) void k_rs_head(const float* __restrict__ V, co
   for (int r = w; r < 64; r += 4) {  // rows of V: lane = dim; the grid covers kb64 rows exactly
     const int k = k0 + r;
     const float x = k < kb_p ? rs_bf(V[((long long)bh * kb_p + k) * 64 + lane], big) : 0.0f;
-    Vb[((long long)bh * kb64 + k) * 64 + lane] = x;
+    Vb[((long long)bh * kb64 + k) * 64 + (lane >> 1) + 32 * (lane & 1)] = x;  // evens, then odds
     tile[r][lane] = x;
   }
   __syncthreads();
@@ -121,10 +122,11 @@ struct RsPvArgs {
   const float* A;   // [BH][q_blk][kb_p] pooled map
   const float* M;   // [H][64][64]
   const float* Vt;  // [BH][kb64/64][64 dims][64] big(V) per chunk in operand order, zero past kb_p
+  const float* Vb;  // [BH][kb64][64] big(V), zero rows past kb_p; each row's even dims, then its odd dims
   uint8_t* drop;    // [BH][q_blk][n_cand] 1 = dropped
   uint8_t* best;    // [BH][q_blk][n_cand] the track-best set
   float* vq;        // [BH][q_blk][64] big(v_bar_query)
-  float* X;         // [BH][q_blk][64] setup: big(Mb vq); rounds: big(M g)
+  float* T;         // [BH][q_blk][n_cand] setup: v_k . big(Mb vq); rounds: v_k . big(M g)
   float* rsv;       // [BH][q_blk][RS_NSCAL]
   float* rank_key;  // [BH][q_blk][n_cand] final: 1 kept, 0 dropped
   float* obj;       // [BH][q_blk] final (optional): J of the returned set
@@ -146,6 +148,63 @@ constexpr int PV_NBUF = 2;   // chunk buffers (double-buffered LDS)
 
 // float offset of V chunk float4 f (dim f/16, positions 4(f%16)..+3)
 __device__ __forceinline__ int pv_vofs(int f) { return (f >> 4) * PV_LDV + 4 * (f & 15); }
+
+// The products of a workgroup's rows, T[r][k] = X_r . big(V_k) for k < n_cand (DOT64 on the
+// matrix cores, the chain k_gemm64 runs: v_mfma_f32_32x32x2_f32 steps over d = (0,1), (2,3),
+// ...), with X_r row r of Cl (rounded to big here when ROUND: the rounds' M g). The
+// candidates are taken in blocks of 32, block b by wave b % 4 (waves 0..3, one per SIMD; a
+// fifth wave would share SIMD 0's matrix core), each wave on its own (no barrier): lane l
+// supplies A = X[l%32][2s + l/32] and B = V[32b + l%32][2s + l/32], which is
+// one contiguous run of 32 floats of Vbe (a row's even dims, then its odd dims), loaded as
+// eight 16-byte loads a block ahead. Candidate rows past kb64 read row kb64 - 1 (their
+// products are not stored).
+template <bool ROUND>
+__device__ __forceinline__ void rs_pv_products(const float* Cl, const float* __restrict__ Vbe, int kb64, int n_cand,
+                                               int nrow, float* __restrict__ Tg, bool big, int w, int lane) {
+  const int rl = lane & 31, h = lane >> 5;
+  float av[32];
+#pragma unroll
+  for (int s = 0; s < 32; ++s) {
+    const float x = Cl[rl * PV_LDC + 2 * s + h];
+    av[s] = ROUND ? rs_bf(x, big) : x;
+  }
+  const int nblk = cdiv(n_cand, 32);
+  auto load = [&](int blk, float4 (&y)[8]) {
+    const float4* src =
+        reinterpret_cast<const float4*>(Vbe + (long long)min(32 * blk + rl, kb64 - 1) * 64 + 32 * h);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = src[i];
+  };
+  float4 cur[8], nxt[8];
+  int blk = w;
+  if (w >= 4) return;  // wave-uniform; no barrier follows
+  if (blk < nblk) load(blk, cur);
+#pragma unroll 1
+  for (; blk < nblk; blk += 4) {
+    if (blk + 4 < nblk) load(blk + 4, nxt);
+    g64_f16v acc;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * i], cur[i].x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * i + 1], cur[i].y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * i + 2], cur[i].z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * i + 3], cur[i].w, acc, 0, 0, 0);
+    }
+    // element j: row 8(j/4) + 4h + j%4, column 32 blk + l%32
+    const int col = 32 * blk + rl;
+    if (col < n_cand) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int r = 8 * (j >> 2) + 4 * h + (j & 3);
+        if (r < nrow) Tg[(long long)r * n_cand + col] = acc[j];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
+  }
+}
 
 // Sums over key blocks for 32 rows of one head (one row group of one head per workgroup),
 // then the per-row vector math. Waves 0..3 accumulate dims 16c..16c+15 of w @ v_bar as
@@ -361,7 +420,6 @@ __global__ __launch_bounds__(320) void k_rs_pv(RsPvArgs a) {
 #pragma unroll 8
         for (int j = 0; j < 64; ++j) s = fmaf(Ml[(i0 + u) * PV_LDM + j], Gl[m * PV_LDC + j], s);
         o[u] = rs_bf(s, big);
-        a.X[R * 64 + i0 + u] = o[u];
       }
     }
     __syncthreads();  // every read of Cl's sums is done
@@ -399,10 +457,6 @@ __global__ __launch_bounds__(320) void k_rs_pv(RsPvArgs a) {
 #pragma unroll
       for (int u = 0; u < PU; ++u) Cl[m * PV_LDC + i0 + u] = o[u];
     __syncthreads();
-    if constexpr (MODE == RS_PV_OBJ)
-      if (live)
-#pragma unroll
-        for (int u = 0; u < PU; ++u) a.X[R * 64 + i0 + u] = rs_bf(Cl[m * PV_LDC + i0 + u], big);
     if (lead) {
       const float* g = &Gl[m * PV_LDC];
       const float* Mg = &Cl[m * PV_LDC];
@@ -439,6 +493,11 @@ __global__ __launch_bounds__(320) void k_rs_pv(RsPvArgs a) {
       }
       sc[RSV_FLAG] = (float)f;
     }
+  }
+  if constexpr (MODE != RS_PV_FINAL) {
+    __syncthreads();  // Cl holds every row's X
+    rs_pv_products<MODE == RS_PV_OBJ>(Cl, a.Vb + (long long)bh * a.kb64 * 64, a.kb64, a.n_cand,
+                                      min(PV_ROWS, a.q_blk - g0), a.T + (rowbase + g0) * a.n_cand, big, w, lane);
   }
 }
 
@@ -526,7 +585,7 @@ __device__ __forceinline__ void rs_top_m_pair(const uint32_t (&key)[NPL], uint32
 }
 
 struct RsSelArgs {
-  const float* T;      // [BH][q_blk][n_cand] raw candidate products v_k . X (k_gemm64)
+  const float* T;      // [BH][q_blk][n_cand] raw candidate products v_k . X (k_rs_pv)
   const float* A;      // [BH][q_blk][kb_p] pooled map
   const float* termk;  // [BH][n_cand]
   const float* rsv;    // [BH][q_blk][RS_NSCAL]
@@ -669,7 +728,7 @@ __global__ __launch_bounds__(256) void k_rs_keep(const uint8_t* __restrict__ dro
 
 // ---- workspace -------------------------------------------------------------------------
 struct RsWs {
-  float *Vb, *Vt, *termk, *vq, *X, *rsv, *ssq, *T;
+  float *Vb, *Vt, *termk, *vq, *rsv, *ssq, *T;
   uint8_t *drop, *best;
   long long bytes;
 };
@@ -688,7 +747,6 @@ inline RsWs rs_ws(void* base, int BH, int q_blk, int kb_p, int n_cand) {
   w.Vt = reinterpret_cast<float*>(take((long long)BH * kb64 * 64 * 4));
   w.termk = reinterpret_cast<float*>(take((long long)BH * n_cand * 4));
   w.vq = reinterpret_cast<float*>(take(R * 64 * 4));
-  w.X = reinterpret_cast<float*>(take(R * 64 * 4));
   w.rsv = reinterpret_cast<float*>(take(R * RS_NSCAL * 4));
   w.ssq = reinterpret_cast<float*>(take(R * n_cand * 4));
   w.T = reinterpret_cast<float*>(take(R * n_cand * 4));
@@ -719,18 +777,6 @@ template <int MODE>
 int rs_pv(int BH, const RsPvArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL(k_rs_pv<MODE>, dim3(cdiv(a.q_blk, PV_ROWS) * BH), dim3(320), 0, stream, a);
   RESS_LAUNCHED("k_rs_pv");
-  return 0;
-}
-
-#ifndef RS_PROD_WALK
-#define RS_PROD_WALK 1
-#endif
-// T[bh][r][k] = X[bh][r] . Vb[bh][k] (DOT64) for k < n_cand
-int rs_products(int BH, const float* X, const float* Vb, int q_blk, int kb64, int n_cand, float* T,
-                hipStream_t stream) {
-  hipLaunchKernelGGL(k_gemm64<G64Store<RS_PROD_WALK>>, g64_grid(BH, n_cand, 0, q_blk, RS_PROD_WALK), dim3(256), 0,
-                     stream, X, Vb, q_blk, n_cand, 64ll * kb64, 0, q_blk, G64Store<RS_PROD_WALK>{T, 1.0f});
-  RESS_LAUNCHED("k_gemm64 (restore-swap products)");
   return 0;
 }
 
@@ -785,7 +831,8 @@ RESS_API int ress_restore_swap(const void* A, const void* V, const void* M, cons
   pa.drop = ws.drop;
   pa.best = ws.best;
   pa.vq = ws.vq;
-  pa.X = ws.X;
+  pa.Vb = ws.Vb;
+  pa.T = ws.T;
   pa.rsv = ws.rsv;
   pa.rank_key = (float*)rank_key;
   pa.obj = (float*)obj;
@@ -798,7 +845,6 @@ RESS_API int ress_restore_swap(const void* A, const void* V, const void* M, cons
   pa.first = 1;
   int rc = rs_pv<RS_PV_SETUP>(BH, pa, stream);
   if (rc) return rc;
-  if ((rc = rs_products(BH, ws.X, ws.Vb, q_blk, kb64, n_cand, ws.T, stream))) return rc;
   RsSelArgs sa{ws.T, (const float*)A, ws.termk, ws.rsv, ws.ssq, (float*)s_out, ws.drop, ws.best, (const int*)nts,
                q_blk, kb_p, n_cand, flags, 0.0f};
   if ((rc = rs_select<true>(BH, sa, stream))) return rc;
@@ -808,7 +854,6 @@ RESS_API int ress_restore_swap(const void* A, const void* V, const void* M, cons
     remaining -= frac;
     pa.first = it == 0;
     if ((rc = rs_pv<RS_PV_OBJ>(BH, pa, stream))) return rc;
-    if ((rc = rs_products(BH, ws.X, ws.Vb, q_blk, kb64, n_cand, ws.T, stream))) return rc;
     sa.frac = (float)frac;
     if ((rc = rs_select<false>(BH, sa, stream))) return rc;
   }
