@@ -505,7 +505,7 @@ __global__ __launch_bounds__(320) void k_rs_pv(RsPvArgs a) {
 // (slot i of a lane is in set (setb >> i) & 1 when valid): for each set the m[s] largest
 // order keys, ties at the threshold taken in candidate-index order (slot-major, then lane).
 // MSB-first radix select over four 8-bit digits; one pass over the slots per digit feeds
-// both sets' 256-bin histograms (hist: 512 ints of the wave's LDS). A set whose threshold
+// both sets' 256-bin histograms (hist: 576 ints of the wave's LDS, the last 64 spare). A set whose threshold
 // bin is taken whole stops descending (the same set as the full descent); a set with m <= 0
 // selects nothing, one with no more than m valid elements selects them all.
 template <int NPL>
@@ -530,11 +530,15 @@ __device__ __forceinline__ void rs_top_m_pair(const uint32_t (&key)[NPL], uint32
 #pragma unroll
     for (int j = 0; j < 8; ++j) hist[lane + 64 * j] = 0;
     __builtin_amdgcn_wave_barrier();
+    // every lane adds once per slot: an element outside the descent counts into the lane's
+    // own spare bin 512 + lane (no branch; distinct spare addresses do not collide)
+    const uint32_t a0 = act0 ? 1u : 0u, a1 = act1 ? 1u : 0u;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
-      const bool s1 = (setb >> i) & 1u;
-      const bool in = ((valid >> i) & 1u) && (s1 ? act1 && (key[i] & pm1) == thr1 : act0 && (key[i] & pm0) == thr0);
-      if (in) atomicAdd(&hist[(s1 ? 256 : 0) + ((key[i] >> shift) & 255u)], 1);
+      const uint32_t s1 = (setb >> i) & 1u;
+      const uint32_t pm = s1 ? pm1 : pm0, th = s1 ? thr1 : thr0;
+      const uint32_t in = ((valid >> i) & 1u) & (s1 ? a1 : a0) & ((key[i] & pm) == th ? 1u : 0u);
+      atomicAdd(&hist[in ? (s1 << 8) + ((key[i] >> shift) & 255u) : 512u + lane], 1);
     }
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -564,24 +568,29 @@ __device__ __forceinline__ void rs_top_m_pair(const uint32_t (&key)[NPL], uint32
     }
     __builtin_amdgcn_wave_barrier();
   }
-  sel0 = sel1 = 0u;
+  // keys above a set's threshold are taken; of its ties the first ones in index order, up to
+  // need (ties are rare: the rank work runs only for slots that hold one)
+  uint32_t take = 0u;
   int before0 = 0, before1 = 0;
   const unsigned long long lower = lane ? (~0ull >> (64 - lane)) : 0ull;
 #pragma unroll
   for (int i = 0; i < NPL; ++i) {
-    const bool v = (valid >> i) & 1u, s1 = (setb >> i) & 1u;
+    const uint32_t v = (valid >> i) & 1u, s1 = (setb >> i) & 1u;
     const uint32_t thr = s1 ? thr1 : thr0;
+    uint32_t t = v & (key[i] > thr ? 1u : 0u);
     const bool eq = v && key[i] == thr;
-    const unsigned long long b0 = __ballot(eq && !s1), b1 = __ballot(eq && s1);
-    const int rank = s1 ? before1 + __popcll(b1 & lower) : before0 + __popcll(b0 & lower);
-    const bool take = v && (key[i] > thr || (eq && rank < (s1 ? need1 : need0)));
-    if (take) {
-      if (s1) sel1 |= 1u << i;
-      else sel0 |= 1u << i;
+    const unsigned long long be = __ballot(eq);
+    if (be) {  // uniform
+      const unsigned long long b1 = be & __ballot(s1 != 0u), b0 = be & ~b1;
+      const int rank = s1 ? before1 + __popcll(b1 & lower) : before0 + __popcll(b0 & lower);
+      t |= (eq && rank < (s1 ? need1 : need0)) ? 1u : 0u;
+      before0 += __popcll(b0);
+      before1 += __popcll(b1);
     }
-    before0 += __popcll(b0);
-    before1 += __popcll(b1);
+    take |= t << i;
   }
+  sel1 = take & setb;
+  sel0 = take & ~setb;
 }
 
 struct RsSelArgs {
@@ -613,7 +622,7 @@ struct RsSelArgs {
 //         fused_round.py:126-226).
 template <int NPL, bool INIT>
 __global__ __launch_bounds__(256) void k_rs_select(RsSelArgs a) {
-  __shared__ int hist[4][512];
+  __shared__ int hist[4][576];  // per wave: two 256-bin histograms, then one spare bin per lane
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = blockIdx.x * 4 + w;
   if (r >= a.q_blk) return;  // wave-uniform; no workgroup barrier below
@@ -699,18 +708,16 @@ __global__ __launch_bounds__(256) void k_rs_select(RsSelArgs a) {
     if ((a.flags & RS_TRACK_BEST) && sc[RSV_FLAG] != 0.0f) {  // record the set this round starts from
       uint8_t* br = a.best + R * rs_dstride(n);
 #pragma unroll
-      for (int i = 0; i < NPL; ++i)
-        if (lane + 64 * i < n) br[lane + 64 * i] = (uint8_t)((dropb >> i) & 1u);
+      for (int i = 0; i < NPL; ++i)  // the row's padding past n (to its 64-byte stride) is never read
+        if (64 * i < rs_dstride(n)) br[lane + 64 * i] = (uint8_t)((dropb >> i) & 1u);
     }
     // set 0: the dropped candidates (restore the top cnt), set 1: the kept (drop the top cnt)
     rs_top_m_pair<NPL>(key, cand, cand & ~dropb, cnt, cnt, lane, hist[w], sel0, sel1);
     nd = (dropb & ~sel0) | sel1;
   }
 #pragma unroll
-  for (int i = 0; i < NPL; ++i) {
-    const int k = lane + 64 * i;
-    if (k < n) dr[k] = (uint8_t)((nd >> i) & 1u);
-  }
+  for (int i = 0; i < NPL; ++i)  // uniform bound: the row's padding past n is never read
+    if (64 * i < rs_dstride(n)) dr[lane + 64 * i] = (uint8_t)((nd >> i) & 1u);
 }
 
 // The keep set of each row, one wave per row: the final set, or under track-best the best
