@@ -169,40 +169,53 @@ __device__ __forceinline__ void rs_pv_products(const float* Cl, const float* __r
     av[s] = ROUND ? rs_bf(x, big) : x;
   }
   const int nblk = cdiv(n_cand, 32);
+  if (w >= 4) return;  // wave-uniform; no barrier follows
+  // block loads into two register sets used in turn (no copies between them); every load
+  // is issued (past the last block it repeats the last block), so each compute step waits
+  // only for its own set
   auto load = [&](int blk, float4 (&y)[8]) {
-    const float4* src =
-        reinterpret_cast<const float4*>(Vbe + (long long)min(32 * blk + rl, kb64 - 1) * 64 + 32 * h);
+    const float4* src = reinterpret_cast<const float4*>(
+        Vbe + (long long)min(32 * min(blk, nblk - 1) + rl, kb64 - 1) * 64 + 32 * h);
 #pragma unroll
     for (int i = 0; i < 8; ++i) y[i] = src[i];
   };
-  float4 cur[8], nxt[8];
-  int blk = w;
-  if (w >= 4) return;  // wave-uniform; no barrier follows
-  if (blk < nblk) load(blk, cur);
-#pragma unroll 1
-  for (; blk < nblk; blk += 4) {
-    if (blk + 4 < nblk) load(blk + 4, nxt);
+  auto compute = [&](int blk, const float4 (&y)[8]) {
     g64_f16v acc;
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * i], cur[i].x, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * i + 1], cur[i].y, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * i + 2], cur[i].z, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * i + 3], cur[i].w, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * i], y[i].x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * i + 1], y[i].y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * i + 2], y[i].z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * i + 3], y[i].w, acc, 0, 0, 0);
     }
     // element j: row 8(j/4) + 4h + j%4, column 32 blk + l%32
     const int col = 32 * blk + rl;
-    if (col < n_cand) {
+    float* dst = Tg + col;
+    if (nrow == PV_ROWS && 32 * blk + 32 <= n_cand) {  // uniform: the whole block is stored
+#pragma unroll
+      for (int j = 0; j < 16; ++j) dst[(long long)(8 * (j >> 2) + 4 * h + (j & 3)) * n_cand] = acc[j];
+    } else if (col < n_cand) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const int r = 8 * (j >> 2) + 4 * h + (j & 3);
-        if (r < nrow) Tg[(long long)r * n_cand + col] = acc[j];
+        if (r < nrow) dst[(long long)r * n_cand] = acc[j];
       }
     }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
+  };
+  float4 y0[8], y1[8];
+  int blk = w;
+  load(blk, y0);
+#pragma unroll 1
+  for (; blk < nblk; blk += 8) {
+    load(blk + 4, y1);
+    __builtin_amdgcn_sched_barrier(0);  // the loads issue before the block's MFMAs
+    compute(blk, y0);
+    if (blk + 4 >= nblk) break;  // uniform
+    load(blk + 8, y0);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(blk + 4, y1);
   }
 }
 
