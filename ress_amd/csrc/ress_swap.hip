@@ -5,15 +5,14 @@
 // J = ||g||^2_M / K^2, drift compensate, geometric schedule, >=1 floor on beneficial
 // rows, track-best) and fused_topm's exact top-m (ties to the lowest index). Every
 // (batch*head, query-block) row is independent; the rows advance together, round by
-// round, as the reference's batched tensors do, and each round is three kernels:
+// round, as the reference's batched tensors do, and each round is two kernels:
 //   k_rs_pv      the drop set's sum_Pd and Pd @ v_bar for 32 rows per workgroup (the
 //                matrix cores for Pd @ v_bar, one wave's VALU for sum_Pd), then per row g,
-//                M g, ||g||^2_M, K and J (and track-best);
-//   k_gemm64     v_k . big(M g) for every (row, candidate) on the matrix cores (raw
-//                products, mfma_gemm.h);
+//                M g, ||g||^2_M, K and J (and track-best), then the candidate products
+//                v_k . big(M g) of its rows on the matrix cores (rs_pv_products);
 //   k_rs_select  one wave per row: the restore / compensate qualities from the products,
 //                the round's counts and the two exact top-m selections in one radix pass.
-// The setup is the same three with the dense reference (P @ v_bar, M v_bar_query, the cut
+// The setup is the same pair with the dense reference (P @ v_bar, M v_bar_query, the cut
 // key s/(1-P)) and the initial cut; the last k_rs_pv applies track-best, k_rs_keep writes
 // the keep set.
 //
@@ -30,7 +29,7 @@
 //    sum is a chain of adds. An accumulator that starts at +0 never holds -0, so the zero
 //    terms (masked and padding blocks) leave it bit for bit unchanged.
 //  * DOT64 (v_k . Mvq and v_k . big(Mg)): one sequential fmaf chain over d = 0..63
-//    (k_gemm64, mfma_gemm.h).
+//    (v_mfma_f32_32x32x2_f32 steps over d = (0,1), (2,3), ..., as in mfma_gemm.h).
 //  * The drop set's sums are formed afresh for every objective, as the reference
 //    recomputes Pd @ v_bar each round (projected.py:903-907).
 //  * The 64-term products and sums of M (M v_bar_query, M g, ||g||^2_M, the term_q sums,
