@@ -6,14 +6,15 @@
 // rows, track-best) and fused_topm's exact top-m (ties to the lowest index). Every
 // (batch*head, query-block) row is independent; the rows advance together, round by
 // round, as the reference's batched tensors do, and each round is two kernels:
-//   k_rs_pv      the drop set's sum_Pd and Pd @ v_bar for 32 rows per workgroup (the
-//                matrix cores for Pd @ v_bar, one wave's VALU for sum_Pd), then per row g,
-//                M g, ||g||^2_M, K and J (and track-best), then the candidate products
-//                v_k . big(M g) of its rows on the matrix cores (rs_pv_products);
+//   k_rs_pw      for 16 rows per workgroup (four waves), the drop set's sum_Pd and
+//                Pd @ v_bar on the matrix cores with every operand loaded from global
+//                memory in operand order (no barrier in the chunk loop), then per row g,
+//                M g (matrix cores), ||g||^2_M, K and J (and track-best), then the
+//                candidate products v_k . big(M g) of its rows on the matrix cores;
 //   k_rs_select  one wave per row: the restore / compensate qualities from the products,
 //                the round's counts and the two exact top-m selections in one radix pass.
 // The setup is the same pair with the dense reference (P @ v_bar, M v_bar_query, the cut
-// key s/(1-P)) and the initial cut; the last k_rs_pv applies track-best, k_rs_keep writes
+// key s/(1-P)) and the initial cut; the last k_rs_pw applies track-best, k_rs_keep writes
 // the keep set.
 //
 // Numerics (the same operation order as oracle/ress_oracle.c):
@@ -68,31 +69,45 @@ __device__ __forceinline__ float rs_knorm(float G, float K, float dG, float u) {
 // Drop and best sets: one byte per candidate, rows of rs_dstride(n_cand) bytes (a multiple
 // of 64, so a thread's 8 bytes of a 64-block chunk are one aligned 8-byte load).
 __host__ __device__ __forceinline__ int rs_dstride(int n_cand) { return (n_cand + 63) & ~63; }
+// Operand order of a 64-block chunk (drop / best rows, Vt): key 4s + j of the chunk at
+// position 16j + s, so that lane 16j + r of a v_mfma_f32_16x16x4_f32 step s finds its key's
+// byte (or value) among 16 consecutive ones.
+__host__ __device__ __forceinline__ int rs_dpos(int k) { return (k & ~63) | ((k & 3) << 4) | ((k >> 2) & 15); }
 
 // Per-row scalars of the workspace (RS_NSCAL floats per row).
 // RSV_FLAG: after a round's objective, 1 when the round's set becomes the best so far;
 // after the final objective, 1 when the best round's set is returned.
 enum { RSV_TM = 0, RSV_TQ, RSV_TQB, RSV_GN, RSV_K, RSV_J, RSV_BEST, RSV_FLAG, RS_NSCAL = 8 };
 
-// Per-head preparation, 64 key blocks per workgroup: Vb = big(V) [kb64][64] fp32 with each
-// row's even dims first, then its odd dims (the products' B operand; rows past kb_p zero),
-// the same values per 64-block chunk in the sums' operand order Vt (key 4s + j at position
-// 16j + s) and the key side of quadratic_deviation, termk[k] =
+// Per-head preparation, 64 key blocks per workgroup: Vb = big(V) [kb64][64] fp32 with dim d
+// of a row at (d % 4) * 16 + d / 4 (the products' B operand; rows past kb_p zero), the same
+// values per 64-block chunk in the sums' operand order Vt (key 4s + j at position 16j + s),
+// the head's M and big(M) in operand order (workgroup 0: the matvecs' B operand) and the key
+// side of quadratic_deviation, termk[k] =
 // big(sum_i big(big(Mb v_k)_i * v_ki)) with the product and the sum sequential in index
 // order (the block goes through an LDS tile).
 __global__ __launch_bounds__(256) void k_rs_head(const float* __restrict__ V, const float* __restrict__ M, int H,
                                                  int kb_p, int kb64, int n_cand, int big, float* __restrict__ Vb,
-                                                 float* __restrict__ Vt, float* __restrict__ termk) {
+                                                 float* __restrict__ Vt, float* __restrict__ Mop,
+                                                 float* __restrict__ termk) {
   __shared__ float MbT[64 * 64];  // MbT[j*64 + i] = big(M[i][j])
   __shared__ float tile[64][65];  // [key][dim], padded
   __shared__ float prod[4][64];   // one key's rounded products per wave
   const int k0 = blockIdx.x * 64, bh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const float* Mh = M + (long long)(bh % H) * 4096;
   for (int e = tid; e < 4096; e += 256) MbT[(e & 63) * 64 + (e >> 6)] = rs_bf(Mh[e], big);
+  if (blockIdx.x == 0) {  // this head's M in operand order, rounded and not
+    float* mo = Mop + (long long)bh * 8192;
+    for (int e = tid; e < 4096; e += 256) {
+      const int o = (e & ~63) | ((e & 3) << 4) | ((e >> 2) & 15);
+      mo[o] = rs_bf(Mh[e], big);
+      mo[4096 + o] = Mh[e];
+    }
+  }
   for (int r = w; r < 64; r += 4) {  // rows of V: lane = dim; the grid covers kb64 rows exactly
     const int k = k0 + r;
     const float x = k < kb_p ? rs_bf(V[((long long)bh * kb_p + k) * 64 + lane], big) : 0.0f;
-    Vb[((long long)bh * kb64 + k) * 64 + (lane >> 1) + 32 * (lane & 1)] = x;  // evens, then odds
+    Vb[((long long)bh * kb64 + k) * 64 + ((lane & 3) << 4) + (lane >> 2)] = x;  // dim d at (d % 4) * 16 + d / 4
     tile[r][lane] = x;
   }
   __syncthreads();
@@ -119,11 +134,11 @@ __global__ __launch_bounds__(256) void k_rs_head(const float* __restrict__ V, co
 
 struct RsPvArgs {
   const float* A;   // [BH][q_blk][kb_p] pooled map
-  const float* M;   // [H][64][64]
   const float* Vt;  // [BH][kb64/64][64 dims][64] big(V) per chunk in operand order, zero past kb_p
-  const float* Vb;  // [BH][kb64][64] big(V), zero rows past kb_p; each row's even dims, then its odd dims
-  uint8_t* drop;    // [BH][q_blk][n_cand] 1 = dropped
-  uint8_t* best;    // [BH][q_blk][n_cand] the track-best set
+  const float* Vb;  // [BH][kb64][64] big(V), zero rows past kb_p; dim d of a row at (d % 4) * 16 + d / 4
+  const float* Mop;  // [BH][2][64][64]: big(M), then M, element j of row i at (j % 4) * 16 + j / 4
+  uint8_t* drop;    // [BH][q_blk][rs_dstride] 1 = dropped, candidates at rs_dpos
+  uint8_t* best;    // [BH][q_blk][rs_dstride] the track-best set, the same order
   float* vq;        // [BH][q_blk][64] big(v_bar_query)
   float* T;         // [BH][q_blk][n_cand] setup: v_k . big(Mb vq); rounds: v_k . big(M g)
   float* rsv;       // [BH][q_blk][RS_NSCAL]
@@ -133,383 +148,289 @@ struct RsPvArgs {
 };
 
 enum { RS_PV_SETUP = 0, RS_PV_OBJ = 1, RS_PV_FINAL = 2 };
-constexpr int PV_ROWS = 32;  // rows per workgroup: two 16-row MFMA tiles per wave
-constexpr int PV_KC = 64;    // key blocks per chunk
-// Operand order of a chunk: key 4s + j (s < 16, j < 4) at position 16j + s, so the lane
-// that supplies key 4s + j to MFMA step s (j = lane / 16) reads its 16 steps' values as
-// four 16-byte LDS reads.
-constexpr int PV_LDA = 68;   // A chunk row stride (rows of 64 positions; 16-lane groups of
-                             // 16-byte reads at this stride hit 64 distinct banks)
-constexpr int PV_LDV = 68;   // V chunk stride per dim (64 positions each)
-constexpr int PV_LDM = 65;   // M row stride
-constexpr int PV_LDC = 68;
-constexpr int PV_NBUF = 2;   // chunk buffers (double-buffered LDS)
+// ---- k_rs_pw: two waves per 16 rows --------------------------------------------------
+// The drop-set sums of 16 rows of one head per workgroup with no LDS staging: every
+// v_mfma_f32_16x16x4_f32 operand comes from global memory in operand order, and each wave
+// runs its own chain over the chunks (no barrier in the loop). Lane l = 16j + r supplies,
+// at step s of a 64-block chunk, A = w[row r][key 4s + j] (the pooled map, masked and
+// rounded at load) and, for dims tile t, B = big(V)[key 4s + j][dim 16t + r], which Vt
+// keeps at position 16j + s of dim 16t + r (four 16-byte loads per tile and chunk). Wave
+// h takes tiles 2h and 2h + 1; wave 0 also the weight sum (B = 1 in column 0). Every
+// accumulator takes its k terms in order (SEQK); lane l ends with rows 4j + i of column r
+// of each tile. Chunks are loaded one ahead into two register sets used in turn.
+// After the sums the row vectors go through LDS as 16 x 64 row-major tiles: wave h
+// computes columns 32h.. of the matvecs M g (or big(M) vq) on the matrix cores (A =
+// g[r][4s + j] from LDS, B = M[16t + r][4s + j] from Mop), wave 0's row lanes the scalar
+// chains (||g||^2_M, tq, tqb), and both waves the candidate products in blocks of 16 (A =
+// X[r][4s + j], B = big(V)[16b + r][4s + j], contiguous in Vb's layout).
+constexpr int PW_ROWS = 16;
+constexpr int PW_LD = 68;  // LDS tile row stride
+#ifndef RS_PW_NW
+#define RS_PW_NW 4
+#endif
+constexpr int PW_NW = RS_PW_NW;    // waves per 16 rows
+constexpr int PW_NT = 4 / PW_NW;   // dims tiles per wave
 
-// float offset of V chunk float4 f (dim f/16, positions 4(f%16)..+3)
-__device__ __forceinline__ int pv_vofs(int f) { return (f >> 4) * PV_LDV + 4 * (f & 15); }
+struct PwSet {
+  float x[16];  // the chunk of the 16 rows' map: row e, key k0 + lane at [e]
+  uint4 dm;
+  float4 v[4 * PW_NT];  // tile PW_NT h + c, step group q at [4c + q]
+};
 
-// The products of a workgroup's rows, T[r][k] = X_r . big(V_k) for k < n_cand (DOT64 on the
-// matrix cores, the chain k_gemm64 runs: v_mfma_f32_32x32x2_f32 steps over d = (0,1), (2,3),
-// ...), with X_r row r of Cl (rounded to big here when ROUND: the rounds' M g). The
-// candidates are taken in blocks of 32, block b by wave b % 4 (waves 0..3, one per SIMD; a
-// fifth wave would share SIMD 0's matrix core), each wave on its own (no barrier): lane l
-// supplies A = X[l%32][2s + l/32] and B = V[32b + l%32][2s + l/32], which is
-// one contiguous run of 32 floats of Vbe (a row's even dims, then its odd dims), loaded as
-// eight 16-byte loads a block ahead. Candidate rows past kb64 read row kb64 - 1 (their
-// products are not stored).
-template <bool ROUND>
-__device__ __forceinline__ void rs_pv_products(const float* Cl, const float* __restrict__ Vbe, int kb64, int n_cand,
-                                               int nrow, float* __restrict__ Tg, bool big, int w, int lane) {
-  const int rl = lane & 31, h = lane >> 5;
-  float av[32];
-#pragma unroll
-  for (int s = 0; s < 32; ++s) {
-    const float x = Cl[rl * PV_LDC + 2 * s + h];
-    av[s] = ROUND ? rs_bf(x, big) : x;
-  }
-  const int nblk = cdiv(n_cand, 32);
-  if (w >= 4) return;  // wave-uniform; no barrier follows
-  // block loads into two register sets used in turn (no copies between them); every load
-  // is issued (past the last block it repeats the last block), so each compute step waits
-  // only for its own set
-  auto load = [&](int blk, float4 (&y)[8]) {
-    const float4* src = reinterpret_cast<const float4*>(
-        Vbe + (long long)min(32 * min(blk, nblk - 1) + rl, kb64 - 1) * 64 + 32 * h);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = src[i];
-  };
-  auto compute = [&](int blk, const float4 (&y)[8]) {
-    g64_f16v acc;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * i], y[i].x, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * i + 1], y[i].y, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * i + 2], y[i].z, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[4 * i + 3], y[i].w, acc, 0, 0, 0);
-    }
-    // element j: row 8(j/4) + 4h + j%4, column 32 blk + l%32
-    const int col = 32 * blk + rl;
-    float* dst = Tg + col;
-    if (nrow == PV_ROWS && 32 * blk + 32 <= n_cand) {  // uniform: the whole block is stored
-#pragma unroll
-      for (int j = 0; j < 16; ++j) dst[(long long)(8 * (j >> 2) + 4 * h + (j & 3)) * n_cand] = acc[j];
-    } else if (col < n_cand) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int r = 8 * (j >> 2) + 4 * h + (j & 3);
-        if (r < nrow) dst[(long long)r * n_cand] = acc[j];
-      }
-    }
-  };
-  float4 y0[8], y1[8];
-  int blk = w;
-  load(blk, y0);
-#pragma unroll 1
-  for (; blk < nblk; blk += 8) {
-    load(blk + 4, y1);
-    __builtin_amdgcn_sched_barrier(0);  // the loads issue before the block's MFMAs
-    compute(blk, y0);
-    if (blk + 4 >= nblk) break;  // uniform
-    load(blk + 8, y0);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(blk + 4, y1);
-  }
-}
-
-// Sums over key blocks for 32 rows of one head (one row group of one head per workgroup),
-// then the per-row vector math. Waves 0..3 accumulate dims 16c..16c+15 of w @ v_bar as
-// two v_mfma_f32_16x16x4_f32 chains over k (rows 0..15 and 16..31; lane l supplies
-// A[row l%16][k 4s + l/16] and B[k 4s + l/16][column l%16]); in wave 4, lane r < 32 adds
-// row r's weights one at a time in k order (fmaf(w, 1, acc) is the rounded sum acc + w).
-// A and V go through LDS in chunks of 64 key blocks, two chunks' loads in flight.
-//  SETUP: w = big(P) over k < kb_p; vq = big(w @ V), tm = big(sum w), X = Mvq =
-//         big(Mb vq), tq = big(sum big(Mvq_i vq_i)).
-//  OBJ:   w = big(P) on the drop set of k < n_cand; g = big(sum_Pd) vq - big(Pd @ V),
-//         Mg = M g, ||g||^2_M, K = max(tm - big(sum_Pd), 1e-6), J; X = big(Mg),
-//         tqb = big(vq . Mg); track-best (the first round records J and the set).
-//  FINAL: J of the final set; track-best keeps the better of it and the best round's;
-//         rank_key and obj of the result.
 template <int MODE>
-__global__ __launch_bounds__(320) void k_rs_pv(RsPvArgs a) {
-  // two chunk buffers (the operands w and V); after the sums the same LDS holds M, the
-  // sums and the per-row vectors
-  __shared__ __align__(16) float Al[PV_NBUF][PV_ROWS * PV_LDA];
-  __shared__ __align__(16) float Vl[PV_NBUF][PV_KC * PV_LDV];
-  static_assert(64 * PV_LDM <= PV_NBUF * PV_KC * PV_LDV, "M fits the V buffers");
-  static_assert(2 * PV_ROWS * PV_LDC <= PV_NBUF * PV_ROWS * PV_LDA, "C and G fit the A buffers");
-  float* Cl = &Al[0][0];                     // after the sums: w @ V | sum w, then M vq / M g
-  float* Gl = &Al[0][0] + PV_ROWS * PV_LDC;  // vq (setup) / g (objective)
-  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+__global__ __launch_bounds__(64 * PW_NW) void k_rs_pw(RsPvArgs a) {
+  __shared__ __align__(16) float T0[PW_ROWS * PW_LD];  // sums C, then g (or vq in the setup)
+  __shared__ __align__(16) float T1[PW_ROWS * PW_LD];  // M g (or X in the setup)
+  __shared__ __align__(16) float T2[PW_ROWS * PW_LD];  // vq (rounds)
+  __shared__ float spl[PW_ROWS];
+  __shared__ __align__(16) float Aw[PW_NW][PW_ROWS * PW_LD];  // each wave's copy of the chunk's map rows
+  const int tid = threadIdx.x, lane = tid & 63, am = lane & 15, aq = lane >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   // XCD-aware order (workgroup L runs on XCD L % 8): with a multiple of 8 heads, XCD x takes
   // heads x, x + 8, ... whole, so each XCD's L2 holds the V of only its own heads
-  const int G = cdiv(a.q_blk, PV_ROWS), BH = gridDim.x / G, L = blockIdx.x;
+  const int G = cdiv(a.q_blk, PW_ROWS), BH = gridDim.x / G, L = blockIdx.x;
   int bh, grp;
   if ((BH & 7) == 0) {
-    const int j = L >> 3;
-    bh = (L & 7) + 8 * (j / G);
-    grp = j % G;
+    const int jj = L >> 3;
+    bh = (L & 7) + 8 * (jj / G);
+    grp = jj % G;
   } else {
     bh = L / G;
     grp = L % G;
   }
-  const int g0 = grp * PV_ROWS;
+  const int g0 = grp * PW_ROWS, nrow = min(PW_ROWS, a.q_blk - g0);
   const bool big = a.flags & RS_BF16;
   const int kend = MODE == RS_PV_SETUP ? a.kb_p : a.n_cand;
-  const long long rowbase = (long long)bh * a.q_blk;
-  const float* Vh = a.Vt + (long long)bh * a.kb64 * 64;
-  // Chunk loads: thread t takes row (t % 256)/8 of the group, key blocks 8(t%8)..+7 of the
-  // chunk (zero past kend, outside the drop set, and for rows past q_blk; stored in operand
-  // order as four pairs), and V float4s t, t + 320, t + 640 and min(t + 960, 1023) of the
-  // chunk's 64 dims of 16 float4s (already in operand order in Vt); threads
-  // 256.. repeat what threads 0.. load and store (the same values to the same places). The
-  // loads of chunk c are issued two chunks ahead into register set c & 1 and waited for
-  // only when the chunk is stored to LDS, after the MFMAs of chunk c - 1; rounding and
-  // masking happen at the store. Every load and store is unconditional (past the last
-  // chunk they repeat it), so the waits the compiler places are the ones per chunk.
-  // Addresses are uniform bases plus 32-bit lane offsets.
-  const int lm = (tid & 255) >> 3, lk = 8 * (tid & 7);
-  const bool lrow_ok = g0 + lm < a.q_blk;
-  const int lmc = min(lm, a.q_blk - 1 - g0);  // clamped row: every load stays in the matrix
-  const char* Ag = reinterpret_cast<const char*>(a.A + (rowbase + g0) * a.kb_p);
+  const long long rowbase = (long long)bh * a.q_blk + g0;
   const int dstr = rs_dstride(a.n_cand);
-  const char* Dg = reinterpret_cast<const char*>(a.drop + (rowbase + g0) * dstr);
-  const unsigned a_row = 4u * (unsigned)(lmc * a.kb_p), d_row = (unsigned)(lmc * dstr);
-  const char* Vg = reinterpret_cast<const char*>(Vh);
-  float x0_0 = 0.0f, x1_0 = 0.0f, x2_0 = 0.0f, x3_0 = 0.0f, x4_0 = 0.0f, x5_0 = 0.0f, x6_0 = 0.0f, x7_0 = 0.0f;
-  float x0_1 = 0.0f, x1_1 = 0.0f, x2_1 = 0.0f, x3_1 = 0.0f, x4_1 = 0.0f, x5_1 = 0.0f, x6_1 = 0.0f, x7_1 = 0.0f;
-  uint2 dm_0 = make_uint2(0u, 0u), dm_1 = dm_0;
-  int k0_0 = 0, k0_1 = 0;
-  const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  float4 v0_0 = z4, v1_0 = z4, v2_0 = z4, v3_0 = z4, v0_1 = z4, v1_1 = z4, v2_1 = z4, v3_1 = z4;
-#define RS_PV_X(S, u)                                                                              \
-  x##u##_##S = *reinterpret_cast<const float*>(Ag + (a_row + 4u * (unsigned)min(k0_##S + lk + (u), kend - 1)))
-#define RS_PV_LOAD(ch, S)                                                                          \
-  do {                                                                                             \
-    k0_##S = min((ch), nch - 1) * PV_KC;                                                           \
-    RS_PV_X(S, 0); RS_PV_X(S, 1); RS_PV_X(S, 2); RS_PV_X(S, 3);                                    \
-    RS_PV_X(S, 4); RS_PV_X(S, 5); RS_PV_X(S, 6); RS_PV_X(S, 7);                                    \
-    /* k0 + lk + 8 <= nch * 64 <= the row stride: in the row */                                    \
-    if (MODE != RS_PV_SETUP)                                                                       \
-      dm_##S = *reinterpret_cast<const uint2*>(Dg + (d_row + (unsigned)(k0_##S + lk)));            \
-    const char* vb_ = Vg + 256u * (unsigned)k0_##S;                                                \
-    v0_##S = *reinterpret_cast<const float4*>(vb_ + 16u * (unsigned)tid);                          \
-    v1_##S = *reinterpret_cast<const float4*>(vb_ + 16u * (unsigned)(tid + 320));                  \
-    v2_##S = *reinterpret_cast<const float4*>(vb_ + 16u * (unsigned)(tid + 640));                  \
-    v3_##S = *reinterpret_cast<const float4*>(vb_ + 16u * (unsigned)min(tid + 960, 1023));         \
-  } while (0)
-#define RS_PV_W(S, u)                                                                              \
-  ((lrow_ok & (k0_##S + lk + (u) < kend) &                                                         \
-    (MODE == RS_PV_SETUP || ((((u) < 4 ? dm_##S.x : dm_##S.y) >> (8 * ((u) & 3))) & 0xffu)))       \
-       ? rs_bf(x##u##_##S, big)                                                                    \
-       : 0.0f)
-#define RS_PV_STORE(S)                                                                             \
-  do {                                                                                             \
-    /* keys lk + j and lk + 4 + j sit at positions 16j + lk/4 and 16j + lk/4 + 1 */               \
-    float* al_ = &Al[S][lm * PV_LDA + (lk >> 2)];                                                  \
-    *reinterpret_cast<float2*>(al_) = make_float2(RS_PV_W(S, 0), RS_PV_W(S, 4));                   \
-    *reinterpret_cast<float2*>(al_ + 16) = make_float2(RS_PV_W(S, 1), RS_PV_W(S, 5));              \
-    *reinterpret_cast<float2*>(al_ + 32) = make_float2(RS_PV_W(S, 2), RS_PV_W(S, 6));              \
-    *reinterpret_cast<float2*>(al_ + 48) = make_float2(RS_PV_W(S, 3), RS_PV_W(S, 7));              \
-    float* vl_ = &Vl[S][0];                                                                        \
-    *reinterpret_cast<float4*>(vl_ + pv_vofs(tid)) = v0_##S;                                       \
-    *reinterpret_cast<float4*>(vl_ + pv_vofs(tid + 320)) = v1_##S;                                 \
-    *reinterpret_cast<float4*>(vl_ + pv_vofs(tid + 640)) = v2_##S;                                 \
-    *reinterpret_cast<float4*>(vl_ + pv_vofs(min(tid + 960, 1023))) = v3_##S;                      \
-  } while (0)
-  rs_f4v acc = {0.0f, 0.0f, 0.0f, 0.0f}, acc2 = acc;  // rows 0..15 and 16..31
-  const int am = lane & 15, aq = lane >> 4;
-  float wsum = 0.0f;  // wave 4, lane r < 32: row r's weight sum
-#define RS_PV_STEP(x, x2, y)                                          \
-  do {                                                                \
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, acc, 0, 0, 0);   \
-    acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(x2, y, acc2, 0, 0, 0); \
-  } while (0)
-#define RS_PV_ADD4(a0, a1, a2, a3) \
-  do {                             \
-    wsum = wsum + (a0);            \
-    wsum = wsum + (a1);            \
-    wsum = wsum + (a2);            \
-    wsum = wsum + (a3);            \
-  } while (0)
-#define RS_PV_MFMA(S)                                                                              \
-  do {                                                                                             \
-    if (w < 4) {                                                                                   \
-      const float4* Ab = reinterpret_cast<const float4*>(&Al[S][am * PV_LDA + 16 * aq]);           \
-      const float4* Ab2 = reinterpret_cast<const float4*>(&Al[S][(am + 16) * PV_LDA + 16 * aq]);   \
-      const float4* Vc = reinterpret_cast<const float4*>(&Vl[S][(16 * w + am) * PV_LDV + 16 * aq]); \
-      _Pragma("unroll") for (int q_ = 0; q_ < 4; ++q_) {                                           \
-        const float4 x_ = Ab[q_], x2_ = Ab2[q_], y_ = Vc[q_];                                      \
-        RS_PV_STEP(x_.x, x2_.x, y_.x);                                                             \
-        RS_PV_STEP(x_.y, x2_.y, y_.y);                                                             \
-        RS_PV_STEP(x_.z, x2_.z, y_.z);                                                             \
-        RS_PV_STEP(x_.w, x2_.w, y_.w);                                                             \
-      }                                                                                            \
-    } else { /* keys 4s + j in order: positions 16j + s */                                         \
-      const float* Ar = &Al[S][(lane & 31) * PV_LDA];                                              \
-      _Pragma("unroll") for (int q_ = 0; q_ < 4; ++q_) {                                           \
-        const float4 t0_ = *reinterpret_cast<const float4*>(Ar + 4 * q_);                          \
-        const float4 t1_ = *reinterpret_cast<const float4*>(Ar + 16 + 4 * q_);                     \
-        const float4 t2_ = *reinterpret_cast<const float4*>(Ar + 32 + 4 * q_);                     \
-        const float4 t3_ = *reinterpret_cast<const float4*>(Ar + 48 + 4 * q_);                     \
-        RS_PV_ADD4(t0_.x, t1_.x, t2_.x, t3_.x);                                                    \
-        RS_PV_ADD4(t0_.y, t1_.y, t2_.y, t3_.y);                                                    \
-        RS_PV_ADD4(t0_.z, t1_.z, t2_.z, t3_.z);                                                    \
-        RS_PV_ADD4(t0_.w, t1_.w, t2_.w, t3_.w);                                                    \
-      }                                                                                            \
-    }                                                                                              \
-  } while (0)
-  // chunk c lives in LDS buffer c & 1 and register set c & 1; a buffer is rewritten only
-  // after the barrier that ends the step which last read it. kend >= 1, and chunk rows
-  // stay below kb64 (nch * 64 <= kb64).
-  const int nch = cdiv(kend, PV_KC);
-  RS_PV_LOAD(0, 0);
-  RS_PV_LOAD(1, 1);
-  RS_PV_STORE(0);
-  __syncthreads();
-  for (int ch = 0; ch < nch; ch += 2) {
-    RS_PV_LOAD(ch + 2, 0);
-    RS_PV_MFMA(0);
-    RS_PV_STORE(1);
-    __syncthreads();
-    if (ch + 1 >= nch) break;  // uniform
-    RS_PV_LOAD(ch + 3, 1);
-    RS_PV_MFMA(1);
-    RS_PV_STORE(0);
-    __syncthreads();
-  }
-#undef RS_PV_X
-#undef RS_PV_LOAD
-#undef RS_PV_W
-#undef RS_PV_STORE
-#undef RS_PV_MFMA
-#undef RS_PV_STEP
-#undef RS_PV_ADD4
-  // M into the V buffers (free after the last barrier of the sums), rounded in the setup
-  float* Ml = &Vl[0][0];
+  const bool rok = am < nrow;
+  const int ra = min(am, nrow - 1);  // clamped row: every load stays in the matrix
+  const uint8_t* Dr = a.drop + (rowbase + ra) * dstr;
+  // the map's chunk is loaded a row per instruction (lane = key: one contiguous 256-byte
+  // run; rows past nrow read row nrow - 1, keys past kend key kend - 1, both masked later)
+  const float* A0 = a.A + rowbase * a.kb_p;
+  float* aw = Aw[wv];
+  // this lane's V: dims 16(PW_NT h + c) + am, positions 16aq.. of each chunk
+  const float4* Vh = reinterpret_cast<const float4*>(a.Vt + (long long)bh * a.kb64 * 64) +
+                     (16 * PW_NT * wv + am) * 16 + aq * 4;
+  const int nch = cdiv(kend, 64);
+  auto load = [&](PwSet& S, int ch) {
+    ch = min(ch, nch - 1);
+    const int k0 = ch * 64;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) S.x[e] = A0[(long long)min(e, nrow - 1) * a.kb_p + min(k0 + lane, kend - 1)];
+    if (MODE != RS_PV_SETUP) S.dm = *reinterpret_cast<const uint4*>(Dr + k0 + 16 * aq);
+#pragma unroll
+    for (int c = 0; c < PW_NT; ++c)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) S.v[4 * c + q] = Vh[(long long)ch * 1024 + c * 256 + q];
+  };
+  rs_f4v acc[PW_NT + 1];  // [PW_NT]: the weight sum (wave 0)
+#pragma unroll
+  for (int t = 0; t <= PW_NT; ++t) acc[t] = rs_f4v{0.0f, 0.0f, 0.0f, 0.0f};
+  const float one = am == 0 ? 1.0f : 0.0f;
+  auto compute = [&](const PwSet& S, int ch) {
+    const int k0 = ch * 64;
+    const uint32_t dw[4] = {S.dm.x, S.dm.y, S.dm.z, S.dm.w};
+    // through the wave's LDS tile into operand order: lane 16j + r reads keys 4s + j of row r
+    // (bank (4r + 4s + j) mod 64: the 64 lanes of a step hit 64 banks)
+    __builtin_amdgcn_wave_barrier();  // the previous chunk's reads are done
+#pragma unroll
+    for (int e = 0; e < 16; ++e) aw[e * PW_LD + lane] = S.x[e];
+    __builtin_amdgcn_wave_barrier();
+    float xs[16];
+#pragma unroll
+    for (int st = 0; st < 16; ++st) xs[st] = aw[am * PW_LD + 4 * st + aq];
+#pragma unroll
+    for (int st = 0; st < 16; ++st) {
+      const bool in = rok && k0 + 4 * st + aq < kend &&
+                      (MODE == RS_PV_SETUP || ((dw[st >> 2] >> (8 * (st & 3))) & 0xffu));
+      const float x = in ? rs_bf(xs[st], big) : 0.0f;
+#pragma unroll
+      for (int c = 0; c < PW_NT; ++c) {
+        const float4 v4 = S.v[4 * c + (st >> 2)];
+        const float y = (st & 3) == 0 ? v4.x : (st & 3) == 1 ? v4.y : (st & 3) == 2 ? v4.z : v4.w;
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, acc[c], 0, 0, 0);
+      }
+      if (wv == 0) acc[PW_NT] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, one, acc[PW_NT], 0, 0, 0);  // uniform
+    }
+  };
   {
-    const float* Mh = a.M + (long long)(bh % a.H) * 4096;
-    for (int e = tid; e < 4096; e += 320) {
-      const float mv = Mh[e];
-      Ml[(e >> 6) * PV_LDM + (e & 63)] = MODE == RS_PV_SETUP ? rs_bf(mv, big) : mv;
+    PwSet s0, s1;
+    load(s0, 0);
+#pragma unroll 1
+    for (int ch = 0; ch < nch; ch += 2) {
+      load(s1, ch + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(s0, ch);
+      if (ch + 1 >= nch) break;  // uniform
+      load(s0, ch + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(s1, ch + 1);
     }
   }
-  // lane l holds rows 4(l/16) + i (+16 in acc2), column l%16 of its wave's 16 columns
+  // ---- per-row vector math ----------------------------------------------------------
+  // lane l of wave h holds rows 4(l/16) + i, columns 16(PW_NT h + c) + l%16 (and, wave 0,
+  // the sums)
+  const int cb = 16 * PW_NT * wv + am;  // this lane's first column
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 4 * aq + i;
-    if (w < 4) {
-      Cl[r * PV_LDC + 16 * w + am] = acc[i];
-      Cl[(r + 16) * PV_LDC + 16 * w + am] = acc2[i];
-    }
-  }
-  if (w == 4 && lane < PV_ROWS) Cl[lane * PV_LDC + 64] = wsum;
+  for (int c = 0; c < PW_NT; ++c)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) T0[(4 * aq + i) * PW_LD + cb + 16 * c] = acc[c][i];
+  if (wv == 0 && am == 0)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) spl[4 * aq + i] = acc[PW_NT][i];
   __syncthreads();
-  // ---- per-row vector math: thread t < 256 is row t/8, outputs 8(t%8)..+7 ----------------
-  constexpr int PU = 64 * PV_ROWS / 256;  // outputs per thread
-  const int m = tid / (256 / PV_ROWS), r = g0 + m, i0 = PU * (tid % (256 / PV_ROWS));
-  const bool live = tid < 256 && r < a.q_blk;
-  const bool lead = live && i0 == 0;  // the row's scalar work
-  const long long R = rowbase + r;
-  float* sc = a.rsv + R * RS_NSCAL;
+  const float* Mo = a.Mop + (long long)bh * 8192 + (MODE == RS_PV_SETUP ? 0 : 4096);
+  float* scr = a.rsv + (rowbase + am) * RS_NSCAL;  // lane r < nrow: row r's scalars
+  // this wave's columns of the 16 x 64 tile in T0 times M^T on the matrix cores,
+  // out[r][i] = sum_j in order M[i][j] * T0[r][j]
+  auto matvec = [&](rs_f4v (&o)[PW_NT]) {
+#pragma unroll
+    for (int c = 0; c < PW_NT; ++c) o[c] = rs_f4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float4 m4[PW_NT];
+#pragma unroll
+      for (int c = 0; c < PW_NT; ++c)
+        m4[c] = reinterpret_cast<const float4*>(Mo + (cb + 16 * c) * 64 + 16 * aq)[q];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float xa = T0[am * PW_LD + 4 * (4 * q + u) + aq];
+#pragma unroll
+        for (int c = 0; c < PW_NT; ++c)
+          o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+              xa, u == 0 ? m4[c].x : u == 1 ? m4[c].y : u == 2 ? m4[c].z : m4[c].w, o[c], 0, 0, 0);
+      }
+    }
+  };
+  rs_f4v mo[PW_NT];
   if constexpr (MODE == RS_PV_SETUP) {
-    if (live) {
+    // vq = big(C) (T0 and the workspace), tm = big(sum w)
 #pragma unroll
-      for (int u = 0; u < PU; ++u) {
-        const float v = rs_bf(Cl[m * PV_LDC + i0 + u], big);
-        Gl[m * PV_LDC + i0 + u] = v;
-        a.vq[R * 64 + i0 + u] = v;
+    for (int c = 0; c < PW_NT; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * aq + i, d = cb + 16 * c;
+        const float v = rs_bf(acc[c][i], big);
+        T0[r * PW_LD + d] = v;
+        if (r < nrow) a.vq[(rowbase + r) * 64 + d] = v;
       }
-      if (lead) sc[RSV_TM] = rs_bf(Cl[m * PV_LDC + 64], big);
-    }
+    if (wv == 0 && lane < nrow) scr[RSV_TM] = rs_bf(spl[lane], big);
     __syncthreads();
-    float o[PU];
-    if (live) {
+    matvec(mo);  // big(M) vq
 #pragma unroll
-      for (int u = 0; u < PU; ++u) {
-        float s = 0.0f;
-#pragma unroll 8
-        for (int j = 0; j < 64; ++j) s = fmaf(Ml[(i0 + u) * PV_LDM + j], Gl[m * PV_LDC + j], s);
-        o[u] = rs_bf(s, big);
-      }
-    }
-    __syncthreads();  // every read of Cl's sums is done
-    if (live)
+    for (int c = 0; c < PW_NT; ++c)
 #pragma unroll
-      for (int u = 0; u < PU; ++u) Cl[m * PV_LDC + i0 + u] = o[u];
+      for (int i = 0; i < 4; ++i) T1[(4 * aq + i) * PW_LD + cb + 16 * c] = rs_bf(mo[c][i], big);  // X
     __syncthreads();
-    if (lead) {
+    if (wv == 0 && lane < nrow) {
       float tq = 0.0f;
-      for (int i = 0; i < 64; ++i) tq = tq + rs_bf(Cl[m * PV_LDC + i] * Gl[m * PV_LDC + i], big);
-      sc[RSV_TQ] = rs_bf(tq, big);
+      for (int i = 0; i < 64; ++i) tq = tq + rs_bf(T1[lane * PW_LD + i] * T0[lane * PW_LD + i], big);
+      scr[RSV_TQ] = rs_bf(tq, big);
     }
   } else {
     const bool track = a.flags & RS_TRACK_BEST, maxim = a.flags & RS_MAXIMIZE;
-    float sp = 0.0f;
-    if (live) {
-      sp = rs_bf(Cl[m * PV_LDC + 64], big);
+    // g = big(sum w) vq - big(C)
 #pragma unroll
-      for (int u = 0; u < PU; ++u)
-        Gl[m * PV_LDC + i0 + u] = sp * a.vq[R * 64 + i0 + u] - rs_bf(Cl[m * PV_LDC + i0 + u], big);
-    }
-    __syncthreads();
-    float o[PU];
-    if (live) {
+    for (int c = 0; c < PW_NT; ++c)
 #pragma unroll
-      for (int u = 0; u < PU; ++u) {
-        float s = 0.0f;
-#pragma unroll 8
-        for (int j = 0; j < 64; ++j) s = fmaf(Ml[(i0 + u) * PV_LDM + j], Gl[m * PV_LDC + j], s);
-        o[u] = s;
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * aq + i, d = cb + 16 * c;
+        const float vq = a.vq[(rowbase + min(r, nrow - 1)) * 64 + d];
+        T2[r * PW_LD + d] = vq;
+        T0[r * PW_LD + d] = rs_bf(spl[r], big) * vq - rs_bf(acc[c][i], big);
       }
-    }
-    __syncthreads();  // every read of Cl's sums is done
-    if (live)
-#pragma unroll
-      for (int u = 0; u < PU; ++u) Cl[m * PV_LDC + i0 + u] = o[u];
     __syncthreads();
-    if (lead) {
-      const float* g = &Gl[m * PV_LDC];
-      const float* Mg = &Cl[m * PV_LDC];
-      const float* vq = a.vq + R * 64;
+    matvec(mo);  // M g
+#pragma unroll
+    for (int c = 0; c < PW_NT; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) T1[(4 * aq + i) * PW_LD + cb + 16 * c] = mo[c][i];
+    __syncthreads();
+    if (wv == 0 && lane < nrow) {
+      const float* g = &T0[lane * PW_LD];
+      const float* Mg = &T1[lane * PW_LD];
+      const float sp = rs_bf(spl[lane], big);
       float gn = 0.0f;
       for (int d = 0; d < 64; ++d) gn = gn + g[d] * Mg[d];
-      float K = sc[RSV_TM] - sp;
+      float K = scr[RSV_TM] - sp;
       K = K < 1e-6f ? 1e-6f : K;
       const float J = gn / (K * K);
       int f = 0;
       if constexpr (MODE == RS_PV_OBJ) {
+        const float* vq = &T2[lane * PW_LD];
         float tqr = 0.0f;
-#pragma unroll 4
         for (int d = 0; d < 64; ++d) tqr = tqr + vq[d] * Mg[d];
-        sc[RSV_TQB] = rs_bf(tqr, big);
-        sc[RSV_GN] = gn;
-        sc[RSV_K] = K;
-        sc[RSV_J] = J;
+        scr[RSV_TQB] = rs_bf(tqr, big);
+        scr[RSV_GN] = gn;
+        scr[RSV_K] = K;
+        scr[RSV_J] = J;
         if (track) {  // this round's set becomes the best when it beats the best so far
-          const float b = sc[RSV_BEST];
+          const float b = scr[RSV_BEST];
           f = a.first || (maxim ? J > b : J < b);
-          if (f) sc[RSV_BEST] = J;
+          if (f) scr[RSV_BEST] = J;
         }
       } else {
         float fin = J;
         if (track && !a.first) {
-          const float b = sc[RSV_BEST];
+          const float b = scr[RSV_BEST];
           if (!(maxim ? J > b : J < b)) {  // the final set is not better: return the best one
             f = 1;
             fin = b;
           }
         }
-        if (a.obj) a.obj[R] = fin;
+        if (a.obj) a.obj[rowbase + lane] = fin;
       }
-      sc[RSV_FLAG] = (float)f;
+      scr[RSV_FLAG] = (float)f;
     }
   }
   if constexpr (MODE != RS_PV_FINAL) {
-    __syncthreads();  // Cl holds every row's X
-    rs_pv_products<MODE == RS_PV_OBJ>(Cl, a.Vb + (long long)bh * a.kb64 * 64, a.kb64, a.n_cand,
-                                      min(PV_ROWS, a.q_blk - g0), a.T + (rowbase + g0) * a.n_cand, big, w, lane);
+    // ---- candidate products: T[r][k] = X[r] . big(V_k), blocks of 16, block b by wave b % PW_NW
+    float xa[16];
+#pragma unroll
+    for (int st = 0; st < 16; ++st) {
+      const float x = T1[am * PW_LD + 4 * st + aq];
+      xa[st] = MODE == RS_PV_OBJ ? rs_bf(x, big) : x;  // the setup's X is rounded already
+    }
+    const int nb = cdiv(a.n_cand, 16);
+    const float* Vbh = a.Vb + (long long)bh * a.kb64 * 64;
+    float* Tg = a.T + rowbase * a.n_cand;
+    auto loadb = [&](float4 (&y)[4], int b) {
+      const float4* src =
+          reinterpret_cast<const float4*>(Vbh + (long long)min(16 * min(b, nb - 1) + am, a.kb64 - 1) * 64 + 16 * aq);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) y[q] = src[q];
+    };
+    auto block = [&](const float4 (&y)[4], int b) {
+      rs_f4v o = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int st = 0; st < 16; ++st) {
+        const float4 y4 = y[st >> 2];
+        const float yv = (st & 3) == 0 ? y4.x : (st & 3) == 1 ? y4.y : (st & 3) == 2 ? y4.z : y4.w;
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[st], yv, o, 0, 0, 0);
+      }
+      const int col = 16 * b + am;
+      if (col < a.n_cand)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (4 * aq + i < nrow) Tg[(long long)(4 * aq + i) * a.n_cand + col] = o[i];
+    };
+    float4 y0[4], y1[4];
+    int b = wv;
+    if (b < nb) {  // uniform
+      loadb(y0, b);
+#pragma unroll 1
+      for (; b < nb; b += 2 * PW_NW) {
+        loadb(y1, b + PW_NW);
+        __builtin_amdgcn_sched_barrier(0);
+        block(y0, b);
+        if (b + PW_NW >= nb) break;  // uniform
+        loadb(y0, b + 2 * PW_NW);
+        __builtin_amdgcn_sched_barrier(0);
+        block(y1, b + PW_NW);
+      }
+    }
   }
 }
 
@@ -606,14 +527,14 @@ __device__ __forceinline__ void rs_top_m_pair(const uint32_t (&key)[NPL], uint32
 }
 
 struct RsSelArgs {
-  const float* T;      // [BH][q_blk][n_cand] raw candidate products v_k . X (k_rs_pv)
+  const float* T;      // [BH][q_blk][n_cand] raw candidate products v_k . X (k_rs_pw)
   const float* A;      // [BH][q_blk][kb_p] pooled map
   const float* termk;  // [BH][n_cand]
   const float* rsv;    // [BH][q_blk][RS_NSCAL]
   float* ssq;          // [BH][q_blk][n_cand] s^2 (written by INIT, read by the rounds)
   float* s_out;        // [BH][q_blk][n_cand] or null: s (INIT)
-  uint8_t* drop;       // [BH][q_blk][n_cand]
-  uint8_t* best;       // [BH][q_blk][n_cand] the track-best set
+  uint8_t* drop;       // [BH][q_blk][rs_dstride] candidates at rs_dpos
+  uint8_t* best;       // [BH][q_blk][rs_dstride] the track-best set, the same order
   const int* nts;      // [BH][q_blk]
   int q_blk, kb_p, n_cand, flags;
   float frac;  // the round's fraction of nts (rounds only)
@@ -662,7 +583,7 @@ __global__ __launch_bounds__(256) void k_rs_select(RsSelArgs a) {
   if constexpr (!INIT) {
 #pragma unroll
     for (int i = 0; i < NPL; ++i)
-      if (dr[min(lane + 64 * i, n - 1)]) dropb |= 1u << i;
+      if (dr[rs_dpos(min(lane + 64 * i, n - 1))]) dropb |= 1u << i;
     dropb &= cand;
   }
   uint32_t key[NPL];
@@ -721,7 +642,7 @@ __global__ __launch_bounds__(256) void k_rs_select(RsSelArgs a) {
       uint8_t* br = a.best + R * rs_dstride(n);
 #pragma unroll
       for (int i = 0; i < NPL; ++i)  // the row's padding past n (to its 64-byte stride) is never read
-        if (64 * i < rs_dstride(n)) br[lane + 64 * i] = (uint8_t)((dropb >> i) & 1u);
+        if (64 * i < rs_dstride(n)) br[rs_dpos(lane + 64 * i)] = (uint8_t)((dropb >> i) & 1u);
     }
     // set 0: the dropped candidates (restore the top cnt), set 1: the kept (drop the top cnt)
     rs_top_m_pair<NPL>(key, cand, cand & ~dropb, cnt, cnt, lane, hist[w], sel0, sel1);
@@ -729,7 +650,7 @@ __global__ __launch_bounds__(256) void k_rs_select(RsSelArgs a) {
   }
 #pragma unroll
   for (int i = 0; i < NPL; ++i)  // uniform bound: the row's padding past n is never read
-    if (64 * i < rs_dstride(n)) dr[lane + 64 * i] = (uint8_t)((nd >> i) & 1u);
+    if (64 * i < rs_dstride(n)) dr[rs_dpos(lane + 64 * i)] = (uint8_t)((nd >> i) & 1u);
 }
 
 // The keep set of each row, one wave per row: the final set, or under track-best the best
@@ -742,12 +663,12 @@ __global__ __launch_bounds__(256) void k_rs_keep(const uint8_t* __restrict__ dro
   const long long R = (long long)blockIdx.y * q_blk + r;
   const uint8_t* src = (rsv[R * RS_NSCAL + RSV_FLAG] != 0.0f ? best : drop) + R * rs_dstride(n_cand);
   float* dst = rank_key + R * n_cand;
-  for (int k = lane; k < n_cand; k += 64) dst[k] = src[k] ? 0.0f : 1.0f;
+  for (int k = lane; k < n_cand; k += 64) dst[k] = src[rs_dpos(k)] ? 0.0f : 1.0f;
 }
 
 // ---- workspace -------------------------------------------------------------------------
 struct RsWs {
-  float *Vb, *Vt, *termk, *vq, *rsv, *ssq, *T;
+  float *Vb, *Vt, *Mop, *termk, *vq, *rsv, *ssq, *T;
   uint8_t *drop, *best;
   long long bytes;
 };
@@ -764,6 +685,7 @@ inline RsWs rs_ws(void* base, int BH, int q_blk, int kb_p, int n_cand) {
   };
   w.Vb = reinterpret_cast<float*>(take((long long)BH * kb64 * 64 * 4));
   w.Vt = reinterpret_cast<float*>(take((long long)BH * kb64 * 64 * 4));
+  w.Mop = reinterpret_cast<float*>(take((long long)BH * 8192 * 4));
   w.termk = reinterpret_cast<float*>(take((long long)BH * n_cand * 4));
   w.vq = reinterpret_cast<float*>(take(R * 64 * 4));
   w.rsv = reinterpret_cast<float*>(take(R * RS_NSCAL * 4));
@@ -794,8 +716,8 @@ int rs_select(int BH, const RsSelArgs& s, hipStream_t stream) {
 
 template <int MODE>
 int rs_pv(int BH, const RsPvArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL(k_rs_pv<MODE>, dim3(cdiv(a.q_blk, PV_ROWS) * BH), dim3(320), 0, stream, a);
-  RESS_LAUNCHED("k_rs_pv");
+  hipLaunchKernelGGL(k_rs_pw<MODE>, dim3(cdiv(a.q_blk, PW_ROWS) * BH), dim3(64 * PW_NW), 0, stream, a);
+  RESS_LAUNCHED("k_rs_pw");
   return 0;
 }
 
@@ -841,16 +763,16 @@ RESS_API int ress_restore_swap(const void* A, const void* V, const void* M, cons
   const int kb64 = cdiv(kb_p, 64) * 64;
   const int big = (flags & RS_BF16) ? 1 : 0;
   hipLaunchKernelGGL(k_rs_head, dim3(kb64 / 64, BH), dim3(256), 0, stream, (const float*)V, (const float*)M, H, kb_p,
-                     kb64, n_cand, big, ws.Vb, ws.Vt, ws.termk);
+                     kb64, n_cand, big, ws.Vb, ws.Vt, ws.Mop, ws.termk);
   RESS_LAUNCHED("k_rs_head");
   RsPvArgs pa;
   pa.A = (const float*)A;
-  pa.M = (const float*)M;
   pa.Vt = ws.Vt;
   pa.drop = ws.drop;
   pa.best = ws.best;
   pa.vq = ws.vq;
   pa.Vb = ws.Vb;
+  pa.Mop = ws.Mop;
   pa.T = ws.T;
   pa.rsv = ws.rsv;
   pa.rank_key = (float*)rank_key;
