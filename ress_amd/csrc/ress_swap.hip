@@ -92,7 +92,7 @@ __global__ __launch_bounds__(256) void k_rs_head(const float* __restrict__ V, co
                                                  float* __restrict__ termk) {
   __shared__ float MbT[64 * 64];  // MbT[j*64 + i] = big(M[i][j])
   __shared__ float tile[64][65];  // [key][dim], padded
-  __shared__ float prod[4][64];   // one key's rounded products per wave
+  __shared__ float pt[64][65];    // [key][dim]: big(big(Mb v_k)_i * v_ki)
   const int k0 = blockIdx.x * 64, bh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const float* Mh = M + (long long)(bh % H) * 4096;
   for (int e = tid; e < 4096; e += 256) MbT[(e & 63) * 64 + (e >> 6)] = rs_bf(Mh[e], big);
@@ -118,17 +118,36 @@ __global__ __launch_bounds__(256) void k_rs_head(const float* __restrict__ V, co
       dst[e] = tile[4 * (pos & 15) + (pos >> 4)][e >> 6];
     }
   }
-  for (int r = w; r < 64; r += 4) {  // termk: wave per key, lane = output dim i
-    const int k = k0 + r;
-    if (k >= n_cand) break;
-    float acc = 0.0f;
-    for (int j = 0; j < 64; ++j) acc = fmaf(MbT[j * 64 + lane], tile[r][j], acc);
-    prod[w][lane] = rs_bf(rs_bf(acc, big) * tile[r][lane], big);
-    __builtin_amdgcn_wave_barrier();
-    float t = 0.0f;
-    for (int i = 0; i < 64; ++i) t = t + prod[w][i];
-    if (lane == 0) termk[(long long)bh * n_cand + k] = rs_bf(t, big);
-    __builtin_amdgcn_wave_barrier();
+  // termk: Mb v_k for the block's 64 keys on the matrix cores, the sum over j in order
+  // (wave w: keys 16w.., lane 16q + r supplies A = v[16w + r][4s + q] and, for dims tile c,
+  // B = Mb[16c + r][4s + q]; lane l gets keys 16w + 4(l/16) + i, dim 16c + l%16), then
+  // big(big(.) * v_ki) per (key, dim) and each key's sum over the dims in order (lanes < 16)
+  {
+    const int am = lane & 15, aq = lane >> 4;
+    rs_f4v o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = rs_f4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int st = 0; st < 16; ++st) {
+      const float xa = tile[16 * w + am][4 * st + aq];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, MbT[(4 * st + aq) * 64 + 16 * c + am], o[c], 0, 0, 0);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * w + 4 * aq + i, d = 16 * c + am;
+        pt[r][d] = rs_bf(rs_bf(o[c][i], big) * tile[r][d], big);
+      }
+    __builtin_amdgcn_wave_barrier();  // each wave reads back only its own keys
+    const int k = k0 + 16 * w + lane;
+    if (lane < 16 && k < n_cand) {
+      float t = 0.0f;
+      for (int i = 0; i < 64; ++i) t = t + pt[16 * w + lane][i];
+      termk[(long long)bh * n_cand + k] = rs_bf(t, big);
+    }
   }
 }
 
@@ -386,7 +405,7 @@ __global__ __launch_bounds__(64 * PW_NW) void k_rs_pw(RsPvArgs a) {
     }
   }
   if constexpr (MODE != RS_PV_FINAL) {
-    // ---- candidate products: T[r][k] = X[r] . big(V_k), blocks of 16, block b by wave b % PW_NW
+    // ---- candidate products: T[r][k] = X[r] . big(V_k), blocks of 16
     float xa[16];
 #pragma unroll
     for (int st = 0; st < 16; ++st) {
@@ -416,19 +435,22 @@ __global__ __launch_bounds__(64 * PW_NW) void k_rs_pw(RsPvArgs a) {
         for (int i = 0; i < 4; ++i)
           if (4 * aq + i < nrow) Tg[(long long)(4 * aq + i) * a.n_cand + col] = o[i];
     };
+    // wave 0 ran the weight-sum tile besides its dims tile, so the other waves take the
+    // blocks (with a single wave, it takes them all)
+    constexpr int P0 = PW_NW > 1 ? 1 : 0, PS = PW_NW - P0;
     float4 y0[4], y1[4];
-    int b = wv;
-    if (b < nb) {  // uniform
+    int b = wv - P0;
+    if (b >= 0 && b < nb) {  // uniform
       loadb(y0, b);
 #pragma unroll 1
-      for (; b < nb; b += 2 * PW_NW) {
-        loadb(y1, b + PW_NW);
+      for (; b < nb; b += 2 * PS) {
+        loadb(y1, b + PS);
         __builtin_amdgcn_sched_barrier(0);
         block(y0, b);
-        if (b + PW_NW >= nb) break;  // uniform
-        loadb(y0, b + 2 * PW_NW);
+        if (b + PS >= nb) break;  // uniform
+        loadb(y0, b + 2 * PS);
         __builtin_amdgcn_sched_barrier(0);
-        block(y1, b + PW_NW);
+        block(y1, b + PS);
       }
     }
   }
