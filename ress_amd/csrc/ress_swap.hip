@@ -191,7 +191,7 @@ constexpr int PW_NW = RS_PW_NW;    // waves per 16 rows
 constexpr int PW_NT = 4 / PW_NW;   // dims tiles per wave
 
 struct PwSet {
-  float x[16];  // the chunk of the 16 rows' map: row e, key k0 + lane at [e]
+  float x[PW_ROWS / PW_NW];  // the chunk of the map rows this wave loads: row (16/NW) h + e, key k0 + lane
   uint4 dm;
   float4 v[4 * PW_NT];  // tile PW_NT h + c, step group q at [4c + q]
 };
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(64 * PW_NW) void k_rs_pw(RsPvArgs a) {
   __shared__ __align__(16) float T1[PW_ROWS * PW_LD];  // M g (or X in the setup)
   __shared__ __align__(16) float T2[PW_ROWS * PW_LD];  // vq (rounds)
   __shared__ float spl[PW_ROWS];
-  __shared__ __align__(16) float Aw[PW_NW][PW_ROWS * PW_LD];  // each wave's copy of the chunk's map rows
+  __shared__ __align__(16) float Aw[2][PW_ROWS * PW_LD];  // the chunk's map rows, two buffers in turn
   const int tid = threadIdx.x, lane = tid & 63, am = lane & 15, aq = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   // XCD-aware order (workgroup L runs on XCD L % 8): with a multiple of 8 heads, XCD x takes
@@ -228,7 +228,6 @@ __global__ __launch_bounds__(64 * PW_NW) void k_rs_pw(RsPvArgs a) {
   // the map's chunk is loaded a row per instruction (lane = key: one contiguous 256-byte
   // run; rows past nrow read row nrow - 1, keys past kend key kend - 1, both masked later)
   const float* A0 = a.A + rowbase * a.kb_p;
-  float* aw = Aw[wv];
   // this lane's V: dims 16(PW_NT h + c) + am, positions 16aq.. of each chunk
   const float4* Vh = reinterpret_cast<const float4*>(a.Vt + (long long)bh * a.kb64 * 64) +
                      (16 * PW_NT * wv + am) * 16 + aq * 4;
@@ -237,7 +236,8 @@ __global__ __launch_bounds__(64 * PW_NW) void k_rs_pw(RsPvArgs a) {
     ch = min(ch, nch - 1);
     const int k0 = ch * 64;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) S.x[e] = A0[(long long)min(e, nrow - 1) * a.kb_p + min(k0 + lane, kend - 1)];
+    for (int e = 0; e < PW_ROWS / PW_NW; ++e)
+      S.x[e] = A0[(long long)min((PW_ROWS / PW_NW) * wv + e, nrow - 1) * a.kb_p + min(k0 + lane, kend - 1)];
     if (MODE != RS_PV_SETUP) S.dm = *reinterpret_cast<const uint4*>(Dr + k0 + 16 * aq);
 #pragma unroll
     for (int c = 0; c < PW_NT; ++c)
@@ -251,12 +251,14 @@ __global__ __launch_bounds__(64 * PW_NW) void k_rs_pw(RsPvArgs a) {
   auto compute = [&](const PwSet& S, int ch) {
     const int k0 = ch * 64;
     const uint32_t dw[4] = {S.dm.x, S.dm.y, S.dm.z, S.dm.w};
-    // through the wave's LDS tile into operand order: lane 16j + r reads keys 4s + j of row r
-    // (bank (4r + 4s + j) mod 64: the 64 lanes of a step hit 64 banks)
-    __builtin_amdgcn_wave_barrier();  // the previous chunk's reads are done
+    // each wave's rows into the chunk's LDS tile, then every wave reads it in operand order:
+    // lane 16j + r reads keys 4s + j of row r (bank (4r + 4s + j) mod 64: the 64 lanes of a
+    // step hit 64 banks). Buffer ch % 2: a wave writes chunk ch + 1's only after this
+    // chunk's barrier, which every wave passes after reading chunk ch - 1's.
+    float* aw = Aw[ch & 1];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) aw[e * PW_LD + lane] = S.x[e];
-    __builtin_amdgcn_wave_barrier();
+    for (int e = 0; e < PW_ROWS / PW_NW; ++e) aw[((PW_ROWS / PW_NW) * wv + e) * PW_LD + lane] = S.x[e];
+    __syncthreads();
     float xs[16];
 #pragma unroll
     for (int st = 0; st < 16; ++st) xs[st] = aw[am * PW_LD + 4 * st + aq];
