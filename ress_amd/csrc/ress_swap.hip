@@ -7,8 +7,8 @@
 // (batch*head, query-block) row is independent; the rows advance together, round by
 // round, as the reference's batched tensors do, and each round is two kernels:
 //   k_rs_pw      for 16 rows per workgroup (four waves), the drop set's sum_Pd and
-//                Pd @ v_bar on the matrix cores with every operand loaded from global
-//                memory in operand order (no barrier in the chunk loop), then per row g,
+//                Pd @ v_bar on the matrix cores with the operands loaded in operand
+//                order (V straight from global memory, the map through LDS), then per row g,
 //                M g (matrix cores), ||g||^2_M, K and J (and track-best), then the
 //                candidate products v_k . big(M g) of its rows on the matrix cores;
 //   k_rs_select  one wave per row: the restore / compensate qualities from the products,
@@ -167,21 +167,23 @@ struct RsPvArgs {
 };
 
 enum { RS_PV_SETUP = 0, RS_PV_OBJ = 1, RS_PV_FINAL = 2 };
-// ---- k_rs_pw: two waves per 16 rows --------------------------------------------------
-// The drop-set sums of 16 rows of one head per workgroup with no LDS staging: every
-// v_mfma_f32_16x16x4_f32 operand comes from global memory in operand order, and each wave
-// runs its own chain over the chunks (no barrier in the loop). Lane l = 16j + r supplies,
-// at step s of a 64-block chunk, A = w[row r][key 4s + j] (the pooled map, masked and
-// rounded at load) and, for dims tile t, B = big(V)[key 4s + j][dim 16t + r], which Vt
-// keeps at position 16j + s of dim 16t + r (four 16-byte loads per tile and chunk). Wave
-// h takes tiles 2h and 2h + 1; wave 0 also the weight sum (B = 1 in column 0). Every
-// accumulator takes its k terms in order (SEQK); lane l ends with rows 4j + i of column r
-// of each tile. Chunks are loaded one ahead into two register sets used in turn.
-// After the sums the row vectors go through LDS as 16 x 64 row-major tiles: wave h
-// computes columns 32h.. of the matvecs M g (or big(M) vq) on the matrix cores (A =
-// g[r][4s + j] from LDS, B = M[16t + r][4s + j] from Mop), wave 0's row lanes the scalar
-// chains (||g||^2_M, tq, tqb), and both waves the candidate products in blocks of 16 (A =
-// X[r][4s + j], B = big(V)[16b + r][4s + j], contiguous in Vb's layout).
+// ---- k_rs_pw: four waves per 16 rows -------------------------------------------------
+// The drop-set sums of 16 rows of one head per workgroup on the matrix cores
+// (v_mfma_f32_16x16x4_f32). Lane l = 16j + r supplies, at step s of a 64-block chunk, A =
+// w[row r][key 4s + j] (the pooled map, masked by the drop bytes and rounded as it is read)
+// and, for dims tile t, B = big(V)[key 4s + j][dim 16t + r], which Vt keeps at position
+// 16j + s of dim 16t + r: four 16-byte global loads per tile and chunk, no LDS. The map's
+// chunk is loaded a row per instruction (each wave four of the 16 rows) into an LDS tile
+// that all waves then read in operand order (two buffers, one barrier per chunk); the drop
+// bytes of a lane's 16 keys are one 16-byte load. Wave h takes dims tile h; wave 0 also the
+// weight sum (B = 1 in column 0). Every accumulator takes its k terms in order (SEQK);
+// lane l ends with rows 4j + i of column r of each tile. Chunks are loaded one ahead into
+// two register sets used in turn.
+// After the sums the row vectors go through LDS as 16 x 64 row-major tiles: wave h computes
+// columns 16h.. of the matvecs M g (or big(M) vq) on the matrix cores (A = g[r][4s + j] from
+// LDS, B = M[16h + r][4s + j] from Mop), wave 0's row lanes the scalar chains (||g||^2_M, tq,
+// tqb), and waves 1..3 the candidate products in blocks of 16 (A = X[r][4s + j], B =
+// big(V)[16b + r][4s + j], contiguous in Vb's layout).
 constexpr int PW_ROWS = 16;
 constexpr int PW_LD = 68;  // LDS tile row stride
 #ifndef RS_PW_NW
