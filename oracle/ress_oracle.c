@@ -439,17 +439,19 @@ void oracle_round_bf16_array(const float* x, float* y, long long n) {
  * projected.py:259-288, dense_reference :313-356, the round :903-947, fused_round.py
  * :176-226). The reference leaves GEMM / sum accumulation orders to torch-CUDA; this
  * restatement fixes them, in the same order as the GPU kernels:
- *  - SEQK, the sums over key blocks (P @ v_bar and sum P of the dense reference, Pd @ v_bar
- *    and sum_Pd of a drop set): one sequential fp32 chain over increasing k of every key
- *    block, fmaf(w_k, v_k[d], acc) with w_k = P_k, or 0 for a block outside the set (the
- *    zero terms are part of the chain), and the weight sum as fmaf(w_k, 1, acc);
+ *  - SEQK4, the sums over key blocks (P @ v_bar and sum P of the dense reference, Pd @ v_bar
+ *    and sum_Pd of a drop set): four fp32 chains, chain c over the key blocks of the
+ *    64-block chunks c, c + 4, c + 8, ... (k / 64 = c mod 4) in increasing k,
+ *    fmaf(w_k, v_k[d], acc) with w_k = P_k, or 0 for a block outside the set (the zero
+ *    terms are part of the chain), and the weight sum as fmaf(w_k, 1, acc); the result is
+ *    (chain 0 + chain 1) + (chain 2 + chain 3);
  *  - DOT64, the per-candidate products v_k . Mvq and v_k . big(Mg): one sequential fmaf
  *    chain over d = 0..63;
- *  - the drop set's sum_Pd and Pd @ v_bar are formed afresh by SEQK for every objective
+ *  - the drop set's sum_Pd and Pd @ v_bar are formed afresh by SEQK4 for every objective
  *    (the reference recomputes Pd @ v_bar each round, projected.py:903-907);
  *  - every other sum and 64-term product (M v_bar_query, M g, ||g||^2_M, term_q, term_k)
  *    is a sequential fp32 chain in index order.
- * The GPU evaluates SEQK and DOT64 on the matrix cores (v_mfma_f32_16x16x4_f32 /
+ * The GPU evaluates SEQK4 (one chain per wave) and DOT64 on the matrix cores (v_mfma_f32_16x16x4_f32 /
  * v_mfma_f32_32x32x2_f32 add their k terms to the accumulator one fmaf at a time, in k
  * order, on gfx950).
  *
@@ -500,18 +502,21 @@ static inline float rs_knorm(float G, float K, float dG, float u) {
   return (a * b / (K * K) - dG) / (Kn * Kn);
 }
 
-/* SEQK over k < n (use NULL: every k; else w_k = 0 where use[k] == 0): dot[d] = the fmaf
- * chain of w_k * V[k][d], *sum = the chain of w_k */
+/* SEQK4 over k < n (use NULL: every k; else w_k = 0 where use[k] == 0): chain c = (k / 64)
+ * mod 4 takes the fmaf terms w_k * V[k][d] (and w_k for the weight sum) in increasing k;
+ * dot[d] = (chain 0 + chain 1) + (chain 2 + chain 3), *sum likewise */
 static void rs_seqk(const float* P, const uint8_t* use, const float* Vb, int n, float* dot, float* sum) {
-  float acc[64], sp = 0.0f;
-  for (int d = 0; d < 64; ++d) acc[d] = 0.0f;
+  float acc[4][64], sp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c = 0; c < 4; ++c)
+    for (int d = 0; d < 64; ++d) acc[c][d] = 0.0f;
   for (int k = 0; k < n; ++k) {
+    const int c = (k >> 6) & 3;
     const float w = (use && !use[k]) ? 0.0f : P[k];
-    sp = fmaf(w, 1.0f, sp);
-    for (int d = 0; d < 64; ++d) acc[d] = fmaf(w, Vb[(long long)k * 64 + d], acc[d]);
+    sp[c] = fmaf(w, 1.0f, sp[c]);
+    for (int d = 0; d < 64; ++d) acc[c][d] = fmaf(w, Vb[(long long)k * 64 + d], acc[c][d]);
   }
-  for (int d = 0; d < 64; ++d) dot[d] = acc[d];
-  *sum = sp;
+  for (int d = 0; d < 64; ++d) dot[d] = (acc[0][d] + acc[1][d]) + (acc[2][d] + acc[3][d]);
+  *sum = (sp[0] + sp[1]) + (sp[2] + sp[3]);
 }
 /* DOT64 of a and b (64 values each) */
 static float rs_dot64(const float* a, const float* b) {

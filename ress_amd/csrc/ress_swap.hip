@@ -6,9 +6,10 @@
 // rows, track-best) and fused_topm's exact top-m (ties to the lowest index). Every
 // (batch*head, query-block) row is independent; the rows advance together, round by
 // round, as the reference's batched tensors do, and each round is two kernels:
-//   k_rs_pw      for 16 rows per workgroup (four waves), the drop set's sum_Pd and
-//                Pd @ v_bar on the matrix cores with the operands loaded in operand
-//                order (V straight from global memory, the map through LDS), then per row g,
+//   k_rs_pw      for 16 rows per workgroup (four waves, one chain of the sums each), the
+//                drop set's sum_Pd and Pd @ v_bar on the matrix cores with the operands
+//                loaded in operand order (V straight from global memory, the map through
+//                LDS), then per row g,
 //                M g (matrix cores), ||g||^2_M, K and J (and track-best), then the
 //                candidate products v_k . big(M g) of its rows on the matrix cores;
 //   k_rs_select  one wave per row: the restore / compensate qualities from the products,
@@ -21,14 +22,16 @@
 //  * With `big` (the recipe's _bf16) every value the reference keeps in bf16 is rounded
 //    at the reference's points (quadratic_deviation projected.py:259-288,
 //    dense_reference :313-356, the round :903-947, fused_round.py:176-226).
-//  * SEQK (P @ v_bar and sum P of the dense reference, Pd @ v_bar and sum_Pd of a drop
-//    set): one sequential fp32 chain over increasing k, fmaf(w_k, v_k[d], acc) with
-//    w_k = big(P_k), or 0 outside the drop set, and the weight sum as fmaf(w_k, 1, acc).
-//    v_mfma_f32_16x16x4_f32 adds its four k terms to the accumulator one fmaf at a time,
-//    in k order, on gfx950 (IEEE, subnormals kept), so chained steps over k = 0..3,
-//    4..7, ... are the chain; fmaf(w, 1, acc) is the rounded sum acc + w, so the weight
-//    sum is a chain of adds. An accumulator that starts at +0 never holds -0, so the zero
-//    terms (masked and padding blocks) leave it bit for bit unchanged.
+//  * SEQK4 (P @ v_bar and sum P of the dense reference, Pd @ v_bar and sum_Pd of a drop
+//    set): four fp32 chains, chain c over the keys of the 64-block chunks c, c + 4,
+//    c + 8, ... in increasing k, fmaf(w_k, v_k[d], acc) with w_k = big(P_k), or 0 outside
+//    the drop set, and the weight sum as fmaf(w_k, 1, acc); the result is
+//    (chain 0 + chain 1) + (chain 2 + chain 3). v_mfma_f32_16x16x4_f32 adds its four k
+//    terms to the accumulator one fmaf at a time, in k order, on gfx950 (IEEE, subnormals
+//    kept), so chained steps over k = 0..3, 4..7, ... of a chain's chunks are the chain;
+//    fmaf(w, 1, acc) is the rounded sum acc + w, so the weight sum is a chain of adds. An
+//    accumulator that starts at +0 never holds -0, so the zero terms (masked and padding
+//    blocks) leave it bit for bit unchanged, and a chain with no chunk is +0.
 //  * DOT64 (v_k . Mvq and v_k . big(Mg)): one sequential fmaf chain over d = 0..63
 //    (v_mfma_f32_32x32x2_f32 steps over d = (0,1), (2,3), ..., as in mfma_gemm.h).
 //  * The drop set's sums are formed afresh for every objective, as the reference
@@ -169,42 +172,40 @@ struct RsPvArgs {
 enum { RS_PV_SETUP = 0, RS_PV_OBJ = 1, RS_PV_FINAL = 2 };
 // ---- k_rs_pw: four waves per 16 rows -------------------------------------------------
 // The drop-set sums of 16 rows of one head per workgroup on the matrix cores
-// (v_mfma_f32_16x16x4_f32). Lane l = 16j + r supplies, at step s of a 64-block chunk, A =
-// w[row r][key 4s + j] (the pooled map, masked by the drop bytes and rounded as it is read)
-// and, for dims tile t, B = big(V)[key 4s + j][dim 16t + r], which Vt keeps at position
-// 16j + s of dim 16t + r: four 16-byte global loads per tile and chunk, no LDS. The map's
-// chunk is loaded a row per instruction (each wave four of the 16 rows) into an LDS tile
-// that all waves then read in operand order (two buffers, one barrier per chunk); the drop
-// bytes of a lane's 16 keys are one 16-byte load. Wave h takes dims tile h; wave 0 also the
-// weight sum (B = 1 in column 0). Every accumulator takes its k terms in order (SEQK);
-// lane l ends with rows 4j + i of column r of each tile. Chunks are loaded one ahead into
-// two register sets used in turn.
-// After the sums the row vectors go through LDS as 16 x 64 row-major tiles: wave h computes
-// columns 16h.. of the matvecs M g (or big(M) vq) on the matrix cores (A = g[r][4s + j] from
-// LDS, B = M[16h + r][4s + j] from Mop), wave 0's row lanes the scalar chains (||g||^2_M, tq,
-// tqb), and waves 1..3 the candidate products in blocks of 16 (A = X[r][4s + j], B =
-// big(V)[16b + r][4s + j], contiguous in Vb's layout).
+// (v_mfma_f32_16x16x4_f32), in the SEQK4 order: wave c runs chain c, the 64-block chunks
+// c, c + 4, ... of the row, and the four chains are added as (c0 + c1) + (c2 + c3). Lane
+// l = 16j + r supplies, at step s of a chunk, A = w[row r][key 4s + j] (the pooled map,
+// masked by the drop bytes and rounded as it is read) and, for dims tile t, B =
+// big(V)[key 4s + j][dim 16t + r], which Vt keeps at position 16j + s of dim 16t + r: four
+// 16-byte global loads per tile and chunk, no LDS. The map's chunk is loaded a row per
+// instruction (lane = key) into the wave's LDS tile and read back in operand order; the
+// drop bytes of a lane's 16 keys are one 16-byte load. Each wave accumulates all four dims
+// tiles and the weight sum (B = 1 in column 0); every accumulator takes its chain's k terms
+// in order, and lane l ends with rows 4j + i of column r of each tile. A wave's chunks are
+// loaded one ahead into two register sets used in turn; the waves never wait for each
+// other until their chains end.
+// After the sums the row vectors go through LDS as 16 x 64 row-major tiles: wave h adds
+// the chains of, and computes, columns 16h.. of the matvecs M g (or big(M) vq) on the
+// matrix cores (A = g[r][4s + j] from LDS, B = M[16h + r][4s + j] from Mop), wave 0's row
+// lanes the scalar chains (||g||^2_M, tq, tqb), and waves 1..3 the candidate products in
+// blocks of 16 (A = X[r][4s + j], B = big(V)[16b + r][4s + j], contiguous in Vb's layout).
 constexpr int PW_ROWS = 16;
 constexpr int PW_LD = 68;  // LDS tile row stride
-#ifndef RS_PW_NW
-#define RS_PW_NW 4
-#endif
-constexpr int PW_NW = RS_PW_NW;    // waves per 16 rows
-constexpr int PW_NT = 4 / PW_NW;   // dims tiles per wave
+constexpr int PW_NW = 4;   // waves per 16 rows = SEQK4 chains
 
 struct PwSet {
-  float x[PW_ROWS / PW_NW];  // the chunk of the map rows this wave loads: row (16/NW) h + e, key k0 + lane
+  float x[PW_ROWS];  // the chunk of the map rows: row e, key k0 + lane
   uint4 dm;
-  float4 v[4 * PW_NT];  // tile PW_NT h + c, step group q at [4c + q]
+  float4 v[16];  // tile c, step group q at [4c + q]
 };
 
 template <int MODE>
-__global__ __launch_bounds__(64 * PW_NW) void k_rs_pw(RsPvArgs a) {
-  __shared__ __align__(16) float T0[PW_ROWS * PW_LD];  // sums C, then g (or vq in the setup)
+__global__ __launch_bounds__(64 * PW_NW, 2) void k_rs_pw(RsPvArgs a) {
+  __shared__ __align__(16) float T0[PW_ROWS * PW_LD];  // g (or vq in the setup)
   __shared__ __align__(16) float T1[PW_ROWS * PW_LD];  // M g (or X in the setup)
   __shared__ __align__(16) float T2[PW_ROWS * PW_LD];  // vq (rounds)
-  __shared__ float spl[PW_ROWS];
-  __shared__ __align__(16) float Aw[2][PW_ROWS * PW_LD];  // the chunk's map rows, two buffers in turn
+  __shared__ float spw[PW_NW][PW_ROWS];                // the chains' weight sums
+  __shared__ __align__(16) float Aw[PW_NW][PW_ROWS * PW_LD];  // per wave: its chunk's map rows, then its chains
   const int tid = threadIdx.x, lane = tid & 63, am = lane & 15, aq = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   // XCD-aware order (workgroup L runs on XCD L % 8): with a multiple of 8 heads, XCD x takes
@@ -230,37 +231,35 @@ __global__ __launch_bounds__(64 * PW_NW) void k_rs_pw(RsPvArgs a) {
   // the map's chunk is loaded a row per instruction (lane = key: one contiguous 256-byte
   // run; rows past nrow read row nrow - 1, keys past kend key kend - 1, both masked later)
   const float* A0 = a.A + rowbase * a.kb_p;
-  // this lane's V: dims 16(PW_NT h + c) + am, positions 16aq.. of each chunk
-  const float4* Vh = reinterpret_cast<const float4*>(a.Vt + (long long)bh * a.kb64 * 64) +
-                     (16 * PW_NT * wv + am) * 16 + aq * 4;
+  // this lane's V: dims 16c + am, positions 16aq.. of each chunk
+  const float4* Vh = reinterpret_cast<const float4*>(a.Vt + (long long)bh * a.kb64 * 64) + am * 16 + aq * 4;
   const int nch = cdiv(kend, 64);
+  float* aw = Aw[wv];
   auto load = [&](PwSet& S, int ch) {
-    ch = min(ch, nch - 1);
+    ch = min(ch, nch - 1);  // past the chain's end: a chunk in range, not used
     const int k0 = ch * 64;
 #pragma unroll
-    for (int e = 0; e < PW_ROWS / PW_NW; ++e)
-      S.x[e] = A0[(long long)min((PW_ROWS / PW_NW) * wv + e, nrow - 1) * a.kb_p + min(k0 + lane, kend - 1)];
+    for (int e = 0; e < PW_ROWS; ++e) S.x[e] = A0[(long long)min(e, nrow - 1) * a.kb_p + min(k0 + lane, kend - 1)];
     if (MODE != RS_PV_SETUP) S.dm = *reinterpret_cast<const uint4*>(Dr + k0 + 16 * aq);
 #pragma unroll
-    for (int c = 0; c < PW_NT; ++c)
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
       for (int q = 0; q < 4; ++q) S.v[4 * c + q] = Vh[(long long)ch * 1024 + c * 256 + q];
   };
-  rs_f4v acc[PW_NT + 1];  // [PW_NT]: the weight sum (wave 0)
+  rs_f4v acc[5];  // [4]: the weight sum
 #pragma unroll
-  for (int t = 0; t <= PW_NT; ++t) acc[t] = rs_f4v{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int t = 0; t < 5; ++t) acc[t] = rs_f4v{0.0f, 0.0f, 0.0f, 0.0f};
   const float one = am == 0 ? 1.0f : 0.0f;
   auto compute = [&](const PwSet& S, int ch) {
     const int k0 = ch * 64;
     const uint32_t dw[4] = {S.dm.x, S.dm.y, S.dm.z, S.dm.w};
-    // each wave's rows into the chunk's LDS tile, then every wave reads it in operand order:
-    // lane 16j + r reads keys 4s + j of row r (bank (4r + 4s + j) mod 64: the 64 lanes of a
-    // step hit 64 banks). Buffer ch % 2: a wave writes chunk ch + 1's only after this
-    // chunk's barrier, which every wave passes after reading chunk ch - 1's.
-    float* aw = Aw[ch & 1];
+    // through the wave's LDS tile into operand order: lane 16j + r reads keys 4s + j of row r
+    // (bank (4r + 4s + j) mod 64: the 64 lanes of a step hit 64 banks). A wave's LDS accesses
+    // complete in issue order, so the tile is rewritten only after the previous reads.
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int e = 0; e < PW_ROWS / PW_NW; ++e) aw[((PW_ROWS / PW_NW) * wv + e) * PW_LD + lane] = S.x[e];
-    __syncthreads();
+    for (int e = 0; e < PW_ROWS; ++e) aw[e * PW_LD + lane] = S.x[e];
+    __builtin_amdgcn_wave_barrier();
     float xs[16];
 #pragma unroll
     for (int st = 0; st < 16; ++st) xs[st] = aw[am * PW_LD + 4 * st + aq];
@@ -270,82 +269,80 @@ __global__ __launch_bounds__(64 * PW_NW) void k_rs_pw(RsPvArgs a) {
                       (MODE == RS_PV_SETUP || ((dw[st >> 2] >> (8 * (st & 3))) & 0xffu));
       const float x = in ? rs_bf(xs[st], big) : 0.0f;
 #pragma unroll
-      for (int c = 0; c < PW_NT; ++c) {
+      for (int c = 0; c < 4; ++c) {
         const float4 v4 = S.v[4 * c + (st >> 2)];
         const float y = (st & 3) == 0 ? v4.x : (st & 3) == 1 ? v4.y : (st & 3) == 2 ? v4.z : v4.w;
         acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, acc[c], 0, 0, 0);
       }
-      if (wv == 0) acc[PW_NT] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, one, acc[PW_NT], 0, 0, 0);  // uniform
+      acc[4] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, one, acc[4], 0, 0, 0);
     }
   };
-  {
+  if (wv < nch) {  // uniform per wave: chain wv
     PwSet s0, s1;
-    load(s0, 0);
+    load(s0, wv);
 #pragma unroll 1
-    for (int ch = 0; ch < nch; ch += 2) {
-      load(s1, ch + 1);
+    for (int ch = wv; ch < nch; ch += 2 * PW_NW) {
+      load(s1, ch + PW_NW);
       __builtin_amdgcn_sched_barrier(0);
       compute(s0, ch);
-      if (ch + 1 >= nch) break;  // uniform
-      load(s0, ch + 2);
+      if (ch + PW_NW >= nch) break;  // uniform per wave
+      load(s0, ch + 2 * PW_NW);
       __builtin_amdgcn_sched_barrier(0);
-      compute(s1, ch + 1);
+      compute(s1, ch + PW_NW);
     }
   }
   // ---- per-row vector math ----------------------------------------------------------
-  // lane l of wave h holds rows 4(l/16) + i, columns 16(PW_NT h + c) + l%16 (and, wave 0,
-  // the sums)
-  const int cb = 16 * PW_NT * wv + am;  // this lane's first column
+  // the chains into the waves' tiles (each wave's own reads of its tile are done), then
+  // lane l of wave h adds them for rows 4(l/16) + i, column 16h + l%16
+  __builtin_amdgcn_wave_barrier();
 #pragma unroll
-  for (int c = 0; c < PW_NT; ++c)
+  for (int c = 0; c < 4; ++c)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) T0[(4 * aq + i) * PW_LD + cb + 16 * c] = acc[c][i];
-  if (wv == 0 && am == 0)
+    for (int i = 0; i < 4; ++i) aw[(4 * aq + i) * PW_LD + 16 * c + am] = acc[c][i];
+  if (am == 0)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) spl[4 * aq + i] = acc[PW_NT][i];
+    for (int i = 0; i < 4; ++i) spw[wv][4 * aq + i] = acc[4][i];
   __syncthreads();
+  const int cb = 16 * wv + am;  // this lane's column
+  float cs[4];                  // the SEQK4 sums of rows 4aq + i, column cb
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int o = (4 * aq + i) * PW_LD + cb;
+    cs[i] = (Aw[0][o] + Aw[1][o]) + (Aw[2][o] + Aw[3][o]);
+  }
+  auto wsum = [&](int r) { return (spw[0][r] + spw[1][r]) + (spw[2][r] + spw[3][r]); };
   const float* Mo = a.Mop + (long long)bh * 8192 + (MODE == RS_PV_SETUP ? 0 : 4096);
   float* scr = a.rsv + (rowbase + am) * RS_NSCAL;  // lane r < nrow: row r's scalars
   // this wave's columns of the 16 x 64 tile in T0 times M^T on the matrix cores,
   // out[r][i] = sum_j in order M[i][j] * T0[r][j]
-  auto matvec = [&](rs_f4v (&o)[PW_NT]) {
-#pragma unroll
-    for (int c = 0; c < PW_NT; ++c) o[c] = rs_f4v{0.0f, 0.0f, 0.0f, 0.0f};
+  auto matvec = [&]() {
+    rs_f4v o = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      float4 m4[PW_NT];
-#pragma unroll
-      for (int c = 0; c < PW_NT; ++c)
-        m4[c] = reinterpret_cast<const float4*>(Mo + (cb + 16 * c) * 64 + 16 * aq)[q];
+      const float4 m4 = reinterpret_cast<const float4*>(Mo + cb * 64 + 16 * aq)[q];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const float xa = T0[am * PW_LD + 4 * (4 * q + u) + aq];
-#pragma unroll
-        for (int c = 0; c < PW_NT; ++c)
-          o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-              xa, u == 0 ? m4[c].x : u == 1 ? m4[c].y : u == 2 ? m4[c].z : m4[c].w, o[c], 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, u == 0 ? m4.x : u == 1 ? m4.y : u == 2 ? m4.z : m4.w, o, 0, 0,
+                                                  0);
       }
     }
+    return o;
   };
-  rs_f4v mo[PW_NT];
   if constexpr (MODE == RS_PV_SETUP) {
     // vq = big(C) (T0 and the workspace), tm = big(sum w)
 #pragma unroll
-    for (int c = 0; c < PW_NT; ++c)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * aq + i, d = cb + 16 * c;
-        const float v = rs_bf(acc[c][i], big);
-        T0[r * PW_LD + d] = v;
-        if (r < nrow) a.vq[(rowbase + r) * 64 + d] = v;
-      }
-    if (wv == 0 && lane < nrow) scr[RSV_TM] = rs_bf(spl[lane], big);
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * aq + i;
+      const float v = rs_bf(cs[i], big);
+      T0[r * PW_LD + cb] = v;
+      if (r < nrow) a.vq[(rowbase + r) * 64 + cb] = v;
+    }
+    if (wv == 0 && lane < nrow) scr[RSV_TM] = rs_bf(wsum(lane), big);
     __syncthreads();
-    matvec(mo);  // big(M) vq
+    const rs_f4v mo = matvec();  // big(M) vq
 #pragma unroll
-    for (int c = 0; c < PW_NT; ++c)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) T1[(4 * aq + i) * PW_LD + cb + 16 * c] = rs_bf(mo[c][i], big);  // X
+    for (int i = 0; i < 4; ++i) T1[(4 * aq + i) * PW_LD + cb] = rs_bf(mo[i], big);  // X
     __syncthreads();
     if (wv == 0 && lane < nrow) {
       float tq = 0.0f;
@@ -356,25 +353,21 @@ __global__ __launch_bounds__(64 * PW_NW) void k_rs_pw(RsPvArgs a) {
     const bool track = a.flags & RS_TRACK_BEST, maxim = a.flags & RS_MAXIMIZE;
     // g = big(sum w) vq - big(C)
 #pragma unroll
-    for (int c = 0; c < PW_NT; ++c)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * aq + i, d = cb + 16 * c;
-        const float vq = a.vq[(rowbase + min(r, nrow - 1)) * 64 + d];
-        T2[r * PW_LD + d] = vq;
-        T0[r * PW_LD + d] = rs_bf(spl[r], big) * vq - rs_bf(acc[c][i], big);
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * aq + i;
+      const float vq = a.vq[(rowbase + min(r, nrow - 1)) * 64 + cb];
+      T2[r * PW_LD + cb] = vq;
+      T0[r * PW_LD + cb] = rs_bf(wsum(r), big) * vq - rs_bf(cs[i], big);
+    }
     __syncthreads();
-    matvec(mo);  // M g
+    const rs_f4v mo = matvec();  // M g
 #pragma unroll
-    for (int c = 0; c < PW_NT; ++c)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) T1[(4 * aq + i) * PW_LD + cb + 16 * c] = mo[c][i];
+    for (int i = 0; i < 4; ++i) T1[(4 * aq + i) * PW_LD + cb] = mo[i];
     __syncthreads();
     if (wv == 0 && lane < nrow) {
       const float* g = &T0[lane * PW_LD];
       const float* Mg = &T1[lane * PW_LD];
-      const float sp = rs_bf(spl[lane], big);
+      const float sp = rs_bf(wsum(lane), big);
       float gn = 0.0f;
       for (int d = 0; d < 64; ++d) gn = gn + g[d] * Mg[d];
       float K = scr[RSV_TM] - sp;
@@ -439,9 +432,8 @@ __global__ __launch_bounds__(64 * PW_NW) void k_rs_pw(RsPvArgs a) {
         for (int i = 0; i < 4; ++i)
           if (4 * aq + i < nrow) Tg[(long long)(4 * aq + i) * a.n_cand + col] = o[i];
     };
-    // wave 0 ran the weight-sum tile besides its dims tile, so the other waves take the
-    // blocks (with a single wave, it takes them all)
-    constexpr int P0 = PW_NW > 1 ? 1 : 0, PS = PW_NW - P0;
+    // wave 0's row lanes ran the scalar chains, so the other waves take the blocks
+    constexpr int P0 = 1, PS = PW_NW - P0;
     float4 y0[4], y1[4];
     int b = wv - P0;
     if (b >= 0 && b < nb) {  // uniform
