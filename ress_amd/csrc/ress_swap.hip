@@ -82,9 +82,11 @@ __host__ __device__ __forceinline__ int rs_dpos(int k) { return (k & ~63) | ((k 
 // after the final objective, 1 when the best round's set is returned.
 enum { RSV_TM = 0, RSV_TQ, RSV_TQB, RSV_GN, RSV_K, RSV_J, RSV_BEST, RSV_FLAG, RS_NSCAL = 8 };
 
-// Per-head preparation, 64 key blocks per workgroup: Vb = big(V) [kb64][64] fp32 with dim d
-// of a row at (d % 4) * 16 + d / 4 (the products' B operand; rows past kb_p zero), the same
+// Per-head preparation, 64 key blocks per workgroup: Vb = big(V) [kb64][64] with dim d of a
+// row at (d % 4) * 16 + d / 4 (the products' B operand; rows past kb_p zero), the same
 // values per 64-block chunk in the sums' operand order Vt (key 4s + j at position 16j + s),
+// both as fp32, or with `big` as the bf16 bits of the (bf16-valued) big(V): the same values
+// in half the bytes;
 // the head's M and big(M) in operand order (workgroup 0: the matvecs' B operand) and the key
 // side of quadratic_deviation, termk[k] =
 // big(sum_i big(big(Mb v_k)_i * v_ki)) with the product and the sum sequential in index
@@ -110,15 +112,23 @@ __global__ __launch_bounds__(256) void k_rs_head(const float* __restrict__ V, co
   for (int r = w; r < 64; r += 4) {  // rows of V: lane = dim; the grid covers kb64 rows exactly
     const int k = k0 + r;
     const float x = k < kb_p ? rs_bf(V[((long long)bh * kb_p + k) * 64 + lane], big) : 0.0f;
-    Vb[((long long)bh * kb64 + k) * 64 + ((lane & 3) << 4) + (lane >> 2)] = x;  // dim d at (d % 4) * 16 + d / 4
+    const long long o = ((long long)bh * kb64 + k) * 64 + ((lane & 3) << 4) + (lane >> 2);  // dim d at (d % 4) * 16 + d / 4
+    if (big)
+      reinterpret_cast<uint16_t*>(Vb)[o] = (uint16_t)(__float_as_uint(x) >> 16);
+    else
+      Vb[o] = x;
     tile[r][lane] = x;
   }
   __syncthreads();
   {  // Vt[bh][chunk][dim][pos]: key 4s + j of the chunk at pos 16j + s
-    float* dst = Vt + ((long long)bh * kb64 + k0) * 64;
+    const long long o = ((long long)bh * kb64 + k0) * 64;
     for (int e = tid; e < 4096; e += 256) {
       const int pos = e & 63;
-      dst[e] = tile[4 * (pos & 15) + (pos >> 4)][e >> 6];
+      const float x = tile[4 * (pos & 15) + (pos >> 4)][e >> 6];
+      if (big)
+        reinterpret_cast<uint16_t*>(Vt)[o + e] = (uint16_t)(__float_as_uint(x) >> 16);
+      else
+        Vt[o + e] = x;
     }
   }
   // termk: Mb v_k for the block's 64 keys on the matrix cores, the sum over j in order
@@ -158,6 +168,7 @@ struct RsPvArgs {
   const float* A;   // [BH][q_blk][kb_p] pooled map
   const float* Vt;  // [BH][kb64/64][64 dims][64] big(V) per chunk in operand order, zero past kb_p
   const float* Vb;  // [BH][kb64][64] big(V), zero rows past kb_p; dim d of a row at (d % 4) * 16 + d / 4
+                    // (Vt, Vb: fp32, or bf16 bits when the k-wide tensors are bf16)
   const float* Mop;  // [BH][2][64][64]: big(M), then M, element j of row i at (j % 4) * 16 + j / 4
   uint8_t* drop;    // [BH][q_blk][rs_dstride] 1 = dropped, candidates at rs_dpos
   uint8_t* best;    // [BH][q_blk][rs_dstride] the track-best set, the same order
@@ -193,14 +204,46 @@ constexpr int PW_ROWS = 16;
 constexpr int PW_LD = 68;  // LDS tile row stride
 constexpr int PW_NW = 4;   // waves per 16 rows = SEQK4 chains
 
+// A lane's 16 values of V for one step range of a dims tile (or a candidate row): fp32 in
+// four float4, or bf16 bits in two uint4 (BV); value st as an fp32 operand.
+template <bool BV>
+struct PwV;
+template <>
+struct PwV<false> {
+  float4 v[4];
+  __device__ __forceinline__ void load(const void* base, long long o) {  // o: offset of value 0, in values
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(base) + o)[q];
+  }
+  __device__ __forceinline__ float at(int st) const {
+    const float4 y = v[st >> 2];
+    return (st & 3) == 0 ? y.x : (st & 3) == 1 ? y.y : (st & 3) == 2 ? y.z : y.w;
+  }
+};
+template <>
+struct PwV<true> {
+  uint4 v[2];
+  __device__ __forceinline__ void load(const void* base, long long o) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) v[q] = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(base) + o)[q];
+  }
+  __device__ __forceinline__ float at(int st) const {
+    const uint4 y = v[st >> 3];
+    const int q = (st >> 1) & 3;
+    const uint32_t w = q == 0 ? y.x : q == 1 ? y.y : q == 2 ? y.z : y.w;
+    return __uint_as_float((st & 1) ? (w & 0xffff0000u) : (w << 16));
+  }
+};
+
+template <bool BV>
 struct PwSet {
   float x[PW_ROWS];  // the chunk of the map rows: row e, key k0 + lane
   uint4 dm;
-  float4 v[16];  // tile c, step group q at [4c + q]
+  PwV<BV> v[4];  // dims tile c
 };
 
-template <int MODE>
-__global__ __launch_bounds__(64 * PW_NW, 2) void k_rs_pw(RsPvArgs a) {
+template <int MODE, bool BV>
+__global__ __launch_bounds__(64 * PW_NW, BV ? 3 : 2) void k_rs_pw(RsPvArgs a) {
   __shared__ __align__(16) float T0[PW_ROWS * PW_LD];  // g (or vq in the setup)
   __shared__ __align__(16) float T1[PW_ROWS * PW_LD];  // M g (or X in the setup)
   __shared__ __align__(16) float T2[PW_ROWS * PW_LD];  // vq (rounds)
@@ -232,25 +275,23 @@ __global__ __launch_bounds__(64 * PW_NW, 2) void k_rs_pw(RsPvArgs a) {
   // run; rows past nrow read row nrow - 1, keys past kend key kend - 1, both masked later)
   const float* A0 = a.A + rowbase * a.kb_p;
   // this lane's V: dims 16c + am, positions 16aq.. of each chunk
-  const float4* Vh = reinterpret_cast<const float4*>(a.Vt + (long long)bh * a.kb64 * 64) + am * 16 + aq * 4;
+  const long long vo = (long long)bh * a.kb64 * 64 + am * 64 + aq * 16;
   const int nch = cdiv(kend, 64);
   float* aw = Aw[wv];
-  auto load = [&](PwSet& S, int ch) {
+  auto load = [&](PwSet<BV>& S, int ch) {
     ch = min(ch, nch - 1);  // past the chain's end: a chunk in range, not used
     const int k0 = ch * 64;
 #pragma unroll
     for (int e = 0; e < PW_ROWS; ++e) S.x[e] = A0[(long long)min(e, nrow - 1) * a.kb_p + min(k0 + lane, kend - 1)];
     if (MODE != RS_PV_SETUP) S.dm = *reinterpret_cast<const uint4*>(Dr + k0 + 16 * aq);
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) S.v[4 * c + q] = Vh[(long long)ch * 1024 + c * 256 + q];
+    for (int c = 0; c < 4; ++c) S.v[c].load(a.Vt, vo + (long long)ch * 4096 + c * 1024);
   };
   rs_f4v acc[5];  // [4]: the weight sum
 #pragma unroll
   for (int t = 0; t < 5; ++t) acc[t] = rs_f4v{0.0f, 0.0f, 0.0f, 0.0f};
   const float one = am == 0 ? 1.0f : 0.0f;
-  auto compute = [&](const PwSet& S, int ch) {
+  auto compute = [&](const PwSet<BV>& S, int ch) {
     const int k0 = ch * 64;
     const uint32_t dw[4] = {S.dm.x, S.dm.y, S.dm.z, S.dm.w};
     // through the wave's LDS tile into operand order: lane 16j + r reads keys 4s + j of row r
@@ -269,16 +310,12 @@ __global__ __launch_bounds__(64 * PW_NW, 2) void k_rs_pw(RsPvArgs a) {
                       (MODE == RS_PV_SETUP || ((dw[st >> 2] >> (8 * (st & 3))) & 0xffu));
       const float x = in ? rs_bf(xs[st], big) : 0.0f;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const float4 v4 = S.v[4 * c + (st >> 2)];
-        const float y = (st & 3) == 0 ? v4.x : (st & 3) == 1 ? v4.y : (st & 3) == 2 ? v4.z : v4.w;
-        acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, acc[c], 0, 0, 0);
-      }
+      for (int c = 0; c < 4; ++c) acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, S.v[c].at(st), acc[c], 0, 0, 0);
       acc[4] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, one, acc[4], 0, 0, 0);
     }
   };
   if (wv < nch) {  // uniform per wave: chain wv
-    PwSet s0, s1;
+    PwSet<BV> s0, s1;
     load(s0, wv);
 #pragma unroll 1
     for (int ch = wv; ch < nch; ch += 2 * PW_NW) {
@@ -410,22 +447,13 @@ __global__ __launch_bounds__(64 * PW_NW, 2) void k_rs_pw(RsPvArgs a) {
       xa[st] = MODE == RS_PV_OBJ ? rs_bf(x, big) : x;  // the setup's X is rounded already
     }
     const int nb = cdiv(a.n_cand, 16);
-    const float* Vbh = a.Vb + (long long)bh * a.kb64 * 64;
+    const long long vbo = (long long)bh * a.kb64 * 64 + 16 * aq;
     float* Tg = a.T + rowbase * a.n_cand;
-    auto loadb = [&](float4 (&y)[4], int b) {
-      const float4* src =
-          reinterpret_cast<const float4*>(Vbh + (long long)min(16 * min(b, nb - 1) + am, a.kb64 - 1) * 64 + 16 * aq);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) y[q] = src[q];
-    };
-    auto block = [&](const float4 (&y)[4], int b) {
+    auto loadb = [&](PwV<BV>& y, int b) { y.load(a.Vb, vbo + (long long)min(16 * min(b, nb - 1) + am, a.kb64 - 1) * 64); };
+    auto block = [&](const PwV<BV>& y, int b) {
       rs_f4v o = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int st = 0; st < 16; ++st) {
-        const float4 y4 = y[st >> 2];
-        const float yv = (st & 3) == 0 ? y4.x : (st & 3) == 1 ? y4.y : (st & 3) == 2 ? y4.z : y4.w;
-        o = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[st], yv, o, 0, 0, 0);
-      }
+      for (int st = 0; st < 16; ++st) o = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[st], y.at(st), o, 0, 0, 0);
       const int col = 16 * b + am;
       if (col < a.n_cand)
 #pragma unroll
@@ -434,7 +462,7 @@ __global__ __launch_bounds__(64 * PW_NW, 2) void k_rs_pw(RsPvArgs a) {
     };
     // wave 0's row lanes ran the scalar chains, so the other waves take the blocks
     constexpr int P0 = 1, PS = PW_NW - P0;
-    float4 y0[4], y1[4];
+    PwV<BV> y0, y1;
     int b = wv - P0;
     if (b >= 0 && b < nb) {  // uniform
       loadb(y0, b);
@@ -734,7 +762,11 @@ int rs_select(int BH, const RsSelArgs& s, hipStream_t stream) {
 
 template <int MODE>
 int rs_pv(int BH, const RsPvArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL(k_rs_pw<MODE>, dim3(cdiv(a.q_blk, PW_ROWS) * BH), dim3(64 * PW_NW), 0, stream, a);
+  const dim3 grid(cdiv(a.q_blk, PW_ROWS) * BH), block(64 * PW_NW);
+  if (a.flags & RS_BF16)  // k_rs_head stored big(V) as bf16 bits
+    hipLaunchKernelGGL((k_rs_pw<MODE, true>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((k_rs_pw<MODE, false>), grid, block, 0, stream, a);
   RESS_LAUNCHED("k_rs_pw");
   return 0;
 }
