@@ -100,7 +100,7 @@ class Blocks:
     operands the attention kernel will use:
       "f16"   16-bit operands: the bf16 queries (converted to fp16 per row by the kernel),
               k_pack (fp16 K blocks) and k_scale = each key block's largest key norm
-              (the bound of the kernel's fixed-offset softmax); no codes are written
+              (with |q'| the row's logit bound, which picks the kernel's softmax path); no codes are written
       "i8x2"  two-term INT8 codes (q_i8 + q_lo, k_i8 + k_lo) with per-block scales
       "i8"    the reference's single-term per-block INT8 codes (q_i8, k_i8)"""
 
