@@ -90,11 +90,19 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 __device__ __forceinline__ int k_slot(int r, int c) { return 4 * r + (c ^ (((r >> 1) ^ (r >> 3)) & 3)); }
 __device__ __forceinline__ int v_slot(int r, int c) { return 8 * r + (c ^ ((r ^ (r >> 3)) & 7)); }
 
-// 16 bytes per lane, global -> LDS without a register round trip (gfx950
-// global_load_lds_dwordx4): lane i of the wave writes lds_base + 16*i, lds_base uniform.
-__device__ __forceinline__ void gl_lds16(const void* src, void* lds_base) {
-  __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)src,
-                                   (void __attribute__((address_space(3)))*)lds_base, 16, 0, 0);
+// 16 bytes per lane, global -> LDS without a register round trip (buffer_load_dwordx4 ...
+// lds): lane i of the wave writes lds_base + 16*i (lds_base uniform, taken from M0) with the
+// bytes at soffset + voffset from the descriptor's base. The stage loads address a head's
+// blocks through one descriptor per operand: the block offset is the scalar soffset and the
+// lane's chunk a 32-bit voffset, so a DMA costs no VALU address arithmetic (the flat form's
+// 64-bit lane addresses cost two VALU ops per load in the 16-bit loop).
+#define RESS_BUF_DWORD3 0x00020000  // raw (untyped) buffer: descriptor word 3 of the gfx9 family
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, RESS_BUF_DWORD3);
+}
+__device__ __forceinline__ void buf_lds16(__amdgpu_buffer_rsrc_t rsrc, unsigned voffset, int soffset, void* lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds_base, 16, (int)voffset,
+                                           soffset, 0, 0);
 }
 __device__ __forceinline__ void wait_lds_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // Barrier between pipeline steps. __syncthreads() would also wait for every outstanding
@@ -500,33 +508,26 @@ __device__ __forceinline__ void sparse_attn_row(const AttnArgs& a, const int* __
 
   // Stage loads are LDS-DMA: lane l of wave w fills 16-byte slots 64w+l (K hi, K lo) and
   // 128w+l, 128w+64+l (V), so it fetches the global chunk that the swizzle places there
-  // (the XOR swizzles are their own inverse).
-  // Byte offsets are unsigned 32-bit, so each DMA address is a uniform 64-bit block base
-  // plus a zero-extended lane offset (the SGPR-base form of the load, no 64-bit VALU add).
+  // (the XOR swizzles are their own inverse), through the head's buffer descriptors.
   const unsigned kslot = 64 * w + l;
   const unsigned ksrc = 16 * (4 * (kslot >> 2) + ((kslot & 3) ^ ((((kslot >> 2) >> 1) ^ ((kslot >> 2) >> 3)) & 3)));
   const unsigned vslot0 = 128 * w + l, vslot1 = vslot0 + 64;
   const unsigned vsrc0 = 16 * (8 * (vslot0 >> 3) + ((vslot0 & 7) ^ (((vslot0 >> 3) ^ (vslot0 >> 6)) & 7)));
   const unsigned vsrc1 = 16 * (8 * (vslot1 >> 3) + ((vslot1 & 7) ^ (((vslot1 >> 3) ^ (vslot1 >> 6)) & 7)));
-  const char* kblk0 = reinterpret_cast<const char*>(a.k_i8) + (long long)bh * a.kb_tot * 4096;
-  const char* klblk0 =
-      QK == QK_I8X2 ? reinterpret_cast<const char*>(a.k_lo) + (long long)bh * a.kb_tot * 4096 : nullptr;
-  const char* vblk0 = reinterpret_cast<const char*>(a.v_pack) + (long long)bh * a.kb_tot * 8192;
-  // The block bases pass through an empty asm so that they stay uniform SGPR values:
-  // otherwise the compiler hoists base + lane offset out of the loop as a 64-bit VGPR and
-  // adds the block offset with a VALU op per load.
-  auto uniform_base = [](const char* p) {
-    asm("" : "+s"(p));
-    return p;
-  };
+  const __amdgpu_buffer_rsrc_t krs =
+      head_rsrc(reinterpret_cast<const char*>(a.k_i8) + (long long)bh * a.kb_tot * 4096, a.kb_tot * 4096);
+  const __amdgpu_buffer_rsrc_t klrs =
+      head_rsrc(QK == QK_I8X2 ? reinterpret_cast<const char*>(a.k_lo) + (long long)bh * a.kb_tot * 4096
+                              : reinterpret_cast<const char*>(a.k_i8),
+                QK == QK_I8X2 ? a.kb_tot * 4096 : 0);
+  const __amdgpu_buffer_rsrc_t vrs =
+      head_rsrc(reinterpret_cast<const char*>(a.v_pack) + (long long)bh * a.kb_tot * 8192, a.kb_tot * 8192);
   auto stage_load = [&](uint4* stage, int kb) {
     char* base = reinterpret_cast<char*>(stage);
-    const char* vb = uniform_base(vblk0 + (long long)kb * 8192);
-    gl_lds16(uniform_base(kblk0 + (long long)kb * 4096) + ksrc, base + 1024 * w);
-    if constexpr (QK == QK_I8X2)
-      gl_lds16(uniform_base(klblk0 + (long long)kb * 4096) + ksrc, base + 4096 + 1024 * w);
-    gl_lds16(vb + vsrc0, base + 16 * KCH + 2048 * w);
-    gl_lds16(vb + vsrc1, base + 16 * KCH + 2048 * w + 1024);
+    buf_lds16(krs, ksrc, kb * 4096, base + 1024 * w);
+    if constexpr (QK == QK_I8X2) buf_lds16(klrs, ksrc, kb * 4096, base + 4096 + 1024 * w);
+    buf_lds16(vrs, vsrc0, kb * 8192, base + 16 * KCH + 2048 * w);
+    buf_lds16(vrs, vsrc1, kb * 8192, base + 16 * KCH + 2048 * w + 1024);
   };
   // LDS sources of this lane's K operands, per tile
   int ks0[4], ks1[4];
@@ -835,16 +836,14 @@ __device__ __forceinline__ void attn_row_f16(const AttnArgs& a, const int* __res
   // block, fetching the chunk the XOR swizzle places there (its own inverse)
   const unsigned slot = 64 * w + l;
   const unsigned src = 16 * (8 * (slot >> 3) + ((slot & 7) ^ (((slot >> 3) ^ (slot >> 6)) & 7)));
-  const char* kblk0 = reinterpret_cast<const char*>(a.k_pack) + (long long)bh * a.kb_tot * 8192;
-  const char* vblk0 = reinterpret_cast<const char*>(a.v_pack) + (long long)bh * a.kb_tot * 8192;
-  auto uniform_base = [](const char* p) {
-    asm("" : "+s"(p));
-    return p;
-  };
+  const __amdgpu_buffer_rsrc_t krs =
+      head_rsrc(reinterpret_cast<const char*>(a.k_pack) + (long long)bh * a.kb_tot * 8192, a.kb_tot * 8192);
+  const __amdgpu_buffer_rsrc_t vrs =
+      head_rsrc(reinterpret_cast<const char*>(a.v_pack) + (long long)bh * a.kb_tot * 8192, a.kb_tot * 8192);
   auto stage_load = [&](uint4* stage, int kb) {
     char* base = reinterpret_cast<char*>(stage) + 1024 * w;
-    gl_lds16(uniform_base(kblk0 + (long long)kb * 8192) + src, base);
-    gl_lds16(uniform_base(vblk0 + (long long)kb * 8192) + src, base + 8192);
+    buf_lds16(krs, src, kb * 8192, base);
+    buf_lds16(vrs, src, kb * 8192, base + 8192);
   };
   // LDS byte offsets of this lane's operands within a stage: K chunk 2j+g of key 32kh+qi;
   // V^T chunks 4kh+2h+g of dims qi and 32+qi (the V^T block starts 8 KiB into the stage)
@@ -1163,6 +1162,10 @@ static int attn_args(AttnArgs& a, const void* v_pack, const void* lut, const voi
   a.q_blk_p = cdiv(m.T_p, 128);
   a.q_blk_total = a.q_blk_p + cdiv(m.T_s, 128);
   a.kb_tot = cdiv(Tk, 64);
+  // the kernels address a head's blocks (8 KiB each) through buffer descriptors with a
+  // 32-bit size and scalar byte offsets
+  RESS_REQUIRE((long long)a.kb_tot * 8192 <= 0x7fffffffLL,
+               "sparse attention: %d key blocks per head exceed the 2 GiB a head's K/V blocks may span", a.kb_tot);
   a.Tk = Tk;
   a.sm_scale_log2e = sm_scale * 1.4426950408889634f;
   a.sched = (int*)sched;
