@@ -80,3 +80,15 @@ def test_argument_validation_without_a_gpu(library):
     rc = library.ress_qattn_block_sparse_fwd(*([None] * 3), 0, None, 0, None, None, None, None, None, 1, 1, 128, 64,
                                              0, 0, 0, 0, 0, 0, 0, 0, 1, ctypes.c_float(0.125), 0, None, 0, None)
     assert rc == -1 and b"tensor_layout" in library.ress_last_error()
+
+
+def test_attention_rejects_heads_beyond_the_descriptor_range(library):
+    # the attention kernels address a head's K/V blocks (8 KiB each) through buffer descriptors
+    # with a 32-bit size: a sequence of more than 2^31 / 8192 key blocks is refused on the host,
+    # before any pointer is used (the fake, aligned addresses below are never dereferenced)
+    fake = ctypes.c_void_p(4096)
+    frames, P, S = 12300, 1374, 5  # 16.9 M keys: 264,070 blocks of 64
+    args = (fake, 0, 0, 64, fake, fake, fake, fake, fake, 1, 1, frames, P, S, None, ctypes.c_float(0.125), fake, 0,
+            0, 0, 64, fake, None)
+    assert library.ress_sparse_attn_fwd_f16(*args) == -1
+    assert b"2 GiB" in library.ress_last_error()
