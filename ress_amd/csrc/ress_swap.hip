@@ -586,6 +586,13 @@ struct RsSelArgs {
   float frac;  // the round's fraction of nts (rounds only)
 };
 
+// element i of a row through a 32-bit byte offset from the row's (uniform) base: the
+// scalar-base + zero-extended vector offset form of the access, no 64-bit VALU add
+template <class T>
+__device__ __forceinline__ T& at_u32(T* base, unsigned i) {
+  return *reinterpret_cast<T*>(reinterpret_cast<char*>(const_cast<std::remove_const_t<T>*>(base)) + i * (unsigned)sizeof(T));
+}
+
 // One wave per row (four rows of one head per workgroup); candidate k = lane + 64i in
 // slot i (n_cand <= 64 NPL). The candidates' values come from the raw products T:
 //  INIT:  cr = big(T) = big(Mvq . v_k), qd = big(big(tq - big(2 cr)) + term_k) (>= 0),
@@ -614,22 +621,23 @@ __global__ __launch_bounds__(256) void k_rs_select(RsSelArgs a) {
   uint8_t* dr = a.drop + R * rs_dstride(n);
   float* sr = a.ssq + R * n;
   // every slot's operands first (slots past n_cand read candidate n_cand - 1 and are masked)
+  const float* xr = INIT ? a.termk + (long long)bh * n : sr;
   float tv[NPL], pv[NPL], xv[NPL];
   uint32_t cand = 0u;
 #pragma unroll
   for (int i = 0; i < NPL; ++i) {
     const int k = lane + 64 * i;
     if (k < n) cand |= 1u << i;
-    const int kc = min(k, n - 1);
-    tv[i] = Tr[kc];
-    pv[i] = Ar[kc];
-    xv[i] = INIT ? a.termk[(long long)bh * n + kc] : sr[kc];
+    const unsigned kc = (unsigned)min(k, n - 1);
+    tv[i] = at_u32(Tr, kc);
+    pv[i] = at_u32(Ar, kc);
+    xv[i] = at_u32(xr, kc);
   }
   uint32_t dropb = 0u;
   if constexpr (!INIT) {
 #pragma unroll
     for (int i = 0; i < NPL; ++i)
-      if (dr[rs_dpos(min(lane + 64 * i, n - 1))]) dropb |= 1u << i;
+      if (at_u32(dr, (unsigned)rs_dpos(min(lane + 64 * i, n - 1)))) dropb |= 1u << i;
     dropb &= cand;
   }
   uint32_t key[NPL];
@@ -650,8 +658,8 @@ __global__ __launch_bounds__(256) void k_rs_select(RsSelArgs a) {
       om = rs_bf(om < 1e-4f ? 1e-4f : om, big);
       const float scut = (a.flags & RS_NO_RENORM) ? s : rs_bf(s / om, big);
       if (k < n) {
-        sr[k] = rs_bf(s * s, big);
-        if (a.s_out) a.s_out[R * n + k] = s;
+        at_u32(sr, (unsigned)k) = rs_bf(s * s, big);
+        if (a.s_out) at_u32(a.s_out + R * n, (unsigned)k) = s;
       }
       key[i] = rs_key((a.flags & RS_INVERT_CUT) ? -scut : scut);
     } else {
@@ -688,7 +696,7 @@ __global__ __launch_bounds__(256) void k_rs_select(RsSelArgs a) {
       uint8_t* br = a.best + R * rs_dstride(n);
 #pragma unroll
       for (int i = 0; i < NPL; ++i)  // the row's padding past n (to its 64-byte stride) is never read
-        if (64 * i < rs_dstride(n)) br[rs_dpos(lane + 64 * i)] = (uint8_t)((dropb >> i) & 1u);
+        if (64 * i < rs_dstride(n)) at_u32(br, (unsigned)rs_dpos(lane + 64 * i)) = (uint8_t)((dropb >> i) & 1u);
     }
     // set 0: the dropped candidates (restore the top cnt), set 1: the kept (drop the top cnt)
     rs_top_m_pair<NPL>(key, cand, cand & ~dropb, cnt, cnt, lane, hist[w], sel0, sel1);
@@ -696,7 +704,7 @@ __global__ __launch_bounds__(256) void k_rs_select(RsSelArgs a) {
   }
 #pragma unroll
   for (int i = 0; i < NPL; ++i)  // uniform bound: the row's padding past n is never read
-    if (64 * i < rs_dstride(n)) dr[rs_dpos(lane + 64 * i)] = (uint8_t)((nd >> i) & 1u);
+    if (64 * i < rs_dstride(n)) at_u32(dr, (unsigned)rs_dpos(lane + 64 * i)) = (uint8_t)((nd >> i) & 1u);
 }
 
 // The keep set of each row, one wave per row: the final set, or under track-best the best
