@@ -31,7 +31,19 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #define RESS_API extern "C" __attribute__((visibility("default")))
+
+// Element i of a row through a 32-bit byte offset from the row's base. With a uniform base
+// the access takes the scalar-base + zero-extended vector-offset form; a plain base[i]
+// forms a 64-bit address per lane with a VALU add (i*sizeof(T) is computed in 64 bits).
+// The row must span less than 4 GiB.
+template <class T>
+__device__ __forceinline__ T& at_u32(T* base, unsigned i) {
+  return *reinterpret_cast<T*>(reinterpret_cast<char*>(const_cast<std::remove_const_t<T>*>(base)) +
+                               i * (unsigned)sizeof(T));
+}
 
 // ---- error reporting (defined in capi.hip) --------------------------------
 void ress_set_error(const char* fmt, ...);

@@ -38,8 +38,6 @@
 //    recomputes Pd @ v_bar each round (projected.py:903-907).
 //  * The 64-term products and sums of M (M v_bar_query, M g, ||g||^2_M, the term_q sums,
 //    and term_k once per head) are sequential fp32 chains in index order.
-#include <type_traits>
-
 #include "common.h"
 #include "mfma_gemm.h"
 
@@ -585,13 +583,6 @@ struct RsSelArgs {
   int q_blk, kb_p, n_cand, flags;
   float frac;  // the round's fraction of nts (rounds only)
 };
-
-// element i of a row through a 32-bit byte offset from the row's (uniform) base: the
-// scalar-base + zero-extended vector offset form of the access, no 64-bit VALU add
-template <class T>
-__device__ __forceinline__ T& at_u32(T* base, unsigned i) {
-  return *reinterpret_cast<T*>(reinterpret_cast<char*>(const_cast<std::remove_const_t<T>*>(base)) + i * (unsigned)sizeof(T));
-}
 
 // One wave per row (four rows of one head per workgroup); candidate k = lane + 64i in
 // slot i (n_cand <= 64 NPL). The candidates' values come from the raw products T:
