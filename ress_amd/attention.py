@@ -21,7 +21,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
-from ress_amd import _lib, kernels
+from ress_amd import _lib, kernels, trace
 from ress_amd import criterion as _criterion
 from ress_amd.kernels import KS_K, KS_Q, LayerGrid
 from ress_amd.qkv import combine_special_and_patch, compute_qkv, get_patch_tokens, get_special_tokens, project_out
@@ -233,25 +233,29 @@ def sparse_global_attention(q, k, v, grid, *, num_to_select=None, budget_fn=None
     (src/ress/models/hilbert.py:128-162), but read and written in place.
     Returns a LayerResult whose `out` is (B, H, frames*P, 64) in storage order."""
     sink_lead = sink_lead_blocks(attention_sink, grid)
-    blocks = kernels.prepare_blocks(q, k, v, grid, mode=qk_mode or DEFAULT_QK_MODE, patch_order=patch_order)
-    attn_full, attn_cond = kernels.pooled_scores(blocks)
+    with trace.stage("ress.prepare_blocks"):
+        blocks = kernels.prepare_blocks(q, k, v, grid, mode=qk_mode or DEFAULT_QK_MODE, patch_order=patch_order)
+    with trace.stage("ress.pooled_scores"):
+        attn_full, attn_cond = kernels.pooled_scores(blocks)
     v_bar_full = blocks.pooled_v.view(grid.B, grid.H, grid.kb_p, 64)
     counts = None
     final_map = None
     budget_iters, max_iters = None, None
     if joint_select_fn is not None:
-        final_map = joint_select_fn(attn_cond, v_bar_full[..., :grid.n_cand, :], grid.sink_blocks)
+        with trace.stage("ress.joint_select"):
+            final_map = joint_select_fn(attn_cond, v_bar_full[..., :grid.n_cand, :], grid.sink_blocks)
         if sink_lead and not protect_own_frame:
             final_map = final_map.clone()
             final_map[..., :sink_lead] = True
         lut, nvalid = kernels.lut_from_map(final_map, grid)
     else:
-        if perhead_budget_fn is not None:
-            counts = perhead_budget_fn(attn_cond, v_bar_full[..., :grid.n_cand, :])
-        elif budget_fn is not None:
-            counts = budget_fn(attn_cond)
-        else:
-            counts = num_to_select
+        with trace.stage("ress.budget"):
+            if perhead_budget_fn is not None:
+                counts = perhead_budget_fn(attn_cond, v_bar_full[..., :grid.n_cand, :])
+            elif budget_fn is not None:
+                counts = budget_fn(attn_cond)
+            else:
+                counts = num_to_select
         if counts is None:
             raise AssertionError("num_to_select (or budget_fn/perhead_budget_fn) required unless dense=True "
                                  "or joint_select_fn is given")
@@ -260,11 +264,12 @@ def sparse_global_attention(q, k, v, grid, *, num_to_select=None, budget_fn=None
         if not torch.is_tensor(counts):
             counts = torch.full((grid.B, grid.H, grid.q_blk_p), int(counts), dtype=torch.int32, device=q.device)
         counts = counts.reshape(grid.B, grid.H, grid.q_blk_p)
-        rank = _rank_key(block_criterion, attn_cond, attn_full, v_bar_full,
-                         counts.clamp(min=min(MIN_NUM_TO_SELECT, grid.n_cand)) if block_criterion != "probability"
-                         else counts, grid, M, 64)
-        final_map, lut, nvalid = kernels.select_blocks(rank, counts, grid, min(MIN_NUM_TO_SELECT, grid.n_cand),
-                                                       sink_lead=0 if protect_own_frame else sink_lead)
+        with trace.stage("ress.select"):
+            rank = _rank_key(block_criterion, attn_cond, attn_full, v_bar_full,
+                             counts.clamp(min=min(MIN_NUM_TO_SELECT, grid.n_cand))
+                             if block_criterion != "probability" else counts, grid, M, 64)
+            final_map, lut, nvalid = kernels.select_blocks(rank, counts, grid, min(MIN_NUM_TO_SELECT, grid.n_cand),
+                                                           sink_lead=0 if protect_own_frame else sink_lead)
     if protect_own_frame and grid.q_blk_p:  # after either selection path, as the reference does
         final_map = protect_own_frame_swap(final_map, attn_full[..., :grid.n_cand], grid)
         if sink_lead:  # forced blocks go on last, so the swap never trades one away
@@ -273,7 +278,8 @@ def sparse_global_attention(q, k, v, grid, *, num_to_select=None, budget_fn=None
     if M is not None:  # after every step that can move the map, as the reference records it
         from ress_amd import projected as _projected
         _projected.record_layer_drift(M, attn_full, v_bar_full, final_map, grid.n_cand)
-    o = kernels.sparse_attention(blocks, lut, nvalid, out=out, out_dtype=out_dtype)
+    with trace.stage("ress.sparse_attention"):
+        o = kernels.sparse_attention(blocks, lut, nvalid, out=out, out_dtype=out_dtype)
     res = LayerResult(out=o, final_map=final_map, budget_iters=budget_iters, max_iters=max_iters,
                       attn_status=getattr(o, "ress_attn_status", None))
     if keep_intermediates:
