@@ -78,3 +78,26 @@ def test_layer_stages_are_ranged_in_launch_order(recorder, dev):
     assert pushes == ["ress.prepare_blocks", "ress.pooled_scores", "ress.budget", "ress.select",
                       "ress.sparse_attention"]
     assert sum(op == "pop" for op, _ in recorder.calls) == len(pushes)
+
+
+def _csv(path, header, rows):
+    path.write_text("\n".join([",".join(header)] + [",".join(f'"{v}"' for v in r) for r in rows]) + "\n")
+
+
+def test_stage_times_ties_kernels_to_the_innermost_range_open_at_launch(tmp_path):
+    from ress_amd import stage_times
+
+    _csv(tmp_path / "r_marker_api_trace.csv", ["Function", "Thread_Id", "Start_Timestamp", "End_Timestamp"],
+         [["ress.select", 7, 100, 200], ["ress.inner", 7, 150, 180], ["ress.other_thread", 8, 100, 200]])
+    _csv(tmp_path / "r_hip_api_trace.csv", ["Correlation_Id", "Thread_Id", "Start_Timestamp"],
+         [[1, 7, 120], [2, 7, 160], [3, 7, 250], [4, 8, 130]])
+    _csv(tmp_path / "r_kernel_trace.csv", ["Correlation_Id", "Kernel_Name", "Start_Timestamp", "End_Timestamp"],
+         [[1, "void (anonymous namespace)::k_rs_pw<4>(Args)", 1000, 1010],
+          [2, "k_select(int)", 1020, 1050], [3, "k_late()", 1060, 1061], [4, "void k_x<1>(int)", 1070, 1072],
+          [9, "k_unknown()", 1080, 1084]])
+    t = stage_times.stage_times(str(tmp_path), "r")
+    assert t["ress.select"][:3] == (1, 1, 10) and dict(t["ress.select"][3]) == {"k_rs_pw": 10}
+    assert t["ress.inner"][:3] == (1, 1, 30)
+    assert t["ress.other_thread"][:3] == (1, 1, 2)
+    assert t[stage_times.OUTSIDE][:3] == (0, 2, 5)  # launched after every range, or no launch record
+    assert "ress.inner" in stage_times.report(t)
